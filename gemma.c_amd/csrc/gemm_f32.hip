@@ -1,0 +1,149 @@
+// gemm_f32.hip -- fp32 fallback GEMM for unquantized model files
+// (gemma.c:3304-3399 gemm_fpx), on fp32 MFMA (v_mfma_f32_32x32x2_f32).
+//
+//   dst[i][j] = sum_l src[i][l]*mat[j][l]
+//
+// Same tiling as the int8 GEMM: 256 threads, 2x2 waves, 128x128 block tile,
+// a K step of 16 floats (64 bytes per row) double-buffered in LDS.  A lane
+// owns 8 consecutive k of each step (lane / 32 picks the half) for A and B
+// alike, so each of the 8 MFMA sub-steps pairs matching k.  The reference's
+// fp32 sum has no fixed order (vectorised, KC-chunked, gemma.c:3287-3299), so
+// parity for this path is a tolerance on |y - y_exact| / sum|a*b|.
+#include "gh_arith.h"
+#include "gh_kernels.h"
+
+namespace gh {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 16;                   // floats of K per step
+constexpr int kRowChunks = kBK / 4 + 1;   // float4 chunks per LDS row (+1 pad)
+
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
+    float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
+    const float *__restrict__ src, int sstr, int m, int n, int k) {
+  __shared__ v4f lds_a[2][kBM][kRowChunks];
+  __shared__ v4f lds_b[2][kBN][kRowChunks];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  const int m0 = blockIdx.y * kBM;
+  const int n0 = blockIdx.x * kBN;
+  const int ld_row = tid >> 2;
+  const int ld_chunk = tid & 3;
+
+  v4f ra[2], rb[2];
+  auto load_tiles = [&](int kt) {
+    const int kb = kt * kBK + ld_chunk * 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = ld_row + 64 * h;
+      const int gm = m0 + r;
+      const int gn = n0 + r;
+      ra[h] = (gm < m && kb < k)
+                  ? *reinterpret_cast<const v4f *>(src + (size_t)gm * sstr + kb)
+                  : v4f{0.f, 0.f, 0.f, 0.f};
+      rb[h] = (gn < n && kb < k)
+                  ? *reinterpret_cast<const v4f *>(mat + (size_t)gn * mstr + kb)
+                  : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      lds_a[buf][ld_row + 64 * h][ld_chunk] = ra[h];
+      lds_b[buf][ld_row + 64 * h][ld_chunk] = rb[h];
+    }
+  };
+
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+
+  const int nk = (k + kBK - 1) / kBK;
+  load_tiles(0);
+  store_tiles(0);
+  __syncthreads();
+
+  const int frag_row = lane & 31;
+  const int half = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_tiles(kt + 1);
+    v4f a[2][2], b[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      a[i][0] = lds_a[cur][wm * 64 + i * 32 + frag_row][half * 2];
+      a[i][1] = lds_a[cur][wm * 64 + i * 32 + frag_row][half * 2 + 1];
+      b[i][0] = lds_b[cur][wn * 64 + i * 32 + frag_row][half * 2];
+      b[i][1] = lds_b[cur][wn * 64 + i * 32 + frag_row][half * 2 + 1];
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+              a[i][s >> 2][s & 3], b[j][s >> 2][s & 3], acc[i][j], 0, 0, 0);
+    if (kt + 1 < nk) store_tiles(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+    if (col >= n) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row =
+            m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < m) dst[(size_t)row * dstr + col] = acc[i][j][r];
+      }
+  }
+}
+
+// Any shape, any alignment: one thread per output.
+__global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
+    float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
+    const float *__restrict__ src, int sstr, int m, int n, int k) {
+  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (row >= m || col >= n) return;
+  const float *a = src + (size_t)row * sstr;
+  const float *b = mat + (size_t)col * mstr;
+  float acc = 0.0f;
+  for (int l = 0; l < k; ++l) acc = __builtin_fmaf(a[l], b[l], acc);
+  dst[(size_t)row * dstr + col] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
+                           const float *src, int sstr, int m, int n, int k,
+                           const DeviceInfo &dev, hipStream_t stream) {
+  (void)dev;
+  const bool fast = k % 4 == 0 && mstr % 4 == 0 && sstr % 4 == 0 &&
+                    (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
+  if (fast) {
+    const dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
+    gemm_f32_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src,
+                                                   sstr, m, n, k);
+  } else {
+    const dim3 grid((n + 63) / 64, (m + 3) / 4);
+    gemm_f32_generic_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr,
+                                                           src, sstr, m, n, k);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace gh

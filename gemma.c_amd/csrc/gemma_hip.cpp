@@ -1,0 +1,599 @@
+// gemma_hip.cpp -- the C ABI declared in include/gemma_hip.h.
+//
+// Host-side responsibilities: the error channel (the reference's
+// log_error/get_error, gemma.c:577-587: return 1 and keep a message), the
+// device and stream, the weight registry (host range -> device copy, so the
+// reference's host weight pointers, interior ones included, stay the
+// handles), argument validation (every shape/stride/pointer a kernel's grid
+// relies on is checked here before a launch), and kernel selection: M == 1
+// goes to the bandwidth-bound GEMV, M > 1 to the MFMA GEMM.
+#include "../../include/gemma_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "gh_kernels.h"
+
+namespace {
+
+thread_local char g_err[256] = "";
+
+int fail(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return 1;
+}
+
+int hip_fail(const char *what, hipError_t e) {
+  return fail("%s: %s", what, hipGetErrorString(e));
+}
+
+#define GH_CHECK(what, expr)                  \
+  do {                                        \
+    hipError_t gh_e_ = (expr);                \
+    if (gh_e_ != hipSuccess) return hip_fail(what, gh_e_); \
+  } while (0)
+
+struct Region {
+  size_t bytes;
+  char *device;
+};
+
+struct State {
+  bool ready = false;
+  int device = -1;
+  hipStream_t stream = nullptr;
+  gh::DeviceInfo info{};
+  std::map<uintptr_t, Region> regions;  // keyed by host start address
+  std::mutex lock;
+  // device staging for the _host entry points, grown on demand
+  char *staging = nullptr;
+  size_t staging_bytes = 0;
+};
+
+State g;
+
+hipStream_t pick_stream(void *stream) {
+  return stream != nullptr ? static_cast<hipStream_t>(stream) : g.stream;
+}
+
+int need_init() {
+  if (!g.ready) return fail("gemma_hip: library not initialised (call gemma_hip_init)");
+  return 0;
+}
+
+// Device address of [host, host+bytes) inside a registered range, or null.
+char *resolve(const void *host, size_t bytes) {
+  const uintptr_t h = reinterpret_cast<uintptr_t>(host);
+  std::lock_guard<std::mutex> guard(g.lock);
+  auto it = g.regions.upper_bound(h);
+  if (it == g.regions.begin()) return nullptr;
+  --it;
+  const uintptr_t begin = it->first;
+  if (h + bytes > begin + it->second.bytes) return nullptr;
+  return it->second.device + (h - begin);
+}
+
+int staging_reserve(size_t bytes) {
+  if (bytes <= g.staging_bytes) return 0;
+  if (g.staging != nullptr) {
+    GH_CHECK("gemma_hip staging sync", hipStreamSynchronize(g.stream));
+    GH_CHECK("gemma_hip staging free", hipFree(g.staging));
+    g.staging = nullptr;
+    g.staging_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  GH_CHECK("gemma_hip staging alloc", hipMalloc(&g.staging, want));
+  g.staging_bytes = want;
+  return 0;
+}
+
+// Carves aligned pieces out of the staging buffer.
+struct Carver {
+  size_t used = 0;
+  size_t take(size_t bytes) {
+    size_t at = used;
+    used += (bytes + 255) / 256 * 256;
+    return at;
+  }
+};
+
+int check_matmul_shape(const char *fn, int m, int n, int k, int dstr, int mstr,
+                       int sstr) {
+  if (m < 0 || n <= 0 || k <= 0)
+    return fail("%s: bad shape m=%d n=%d k=%d", fn, m, n, k);
+  if (dstr < n || mstr < k || sstr < k)
+    return fail("%s: stride smaller than row (dstr=%d n=%d mstr=%d sstr=%d k=%d)",
+                fn, dstr, n, mstr, sstr, k);
+  return 0;
+}
+
+int build_jobs(const char *fn, const gemma_hip_job *jobs, int njobs,
+               gh::GemvJobs *out) {
+  if (jobs == nullptr || njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS)
+    return fail("%s: njobs must be 1..%d (got %d)", fn, GEMMA_HIP_MAX_JOBS,
+                njobs);
+  memset(out, 0, sizeof(*out));
+  long total = 0;
+  for (int j = 0; j < njobs; ++j) {
+    if (jobs[j].m < 0) return fail("%s: job %d has m=%d", fn, j, jobs[j].m);
+    if (jobs[j].m > 0 && (jobs[j].w == nullptr || jobs[j].dst == nullptr))
+      return fail("%s: job %d has a null pointer", fn, j);
+    total += jobs[j].m;
+    if (total > (1l << 30)) return fail("%s: too many rows", fn);
+    out->w[j] = jobs[j].w;
+    out->sc[j] = jobs[j].sc;
+    out->dst[j] = jobs[j].dst;
+    out->end[j] = (int)total;
+  }
+  for (int j = njobs; j < gh::kMaxJobs; ++j) out->end[j] = (int)total;
+  out->njobs = njobs;
+  return 0;
+}
+
+constexpr int kMaxGemvK8 = 65536;   // int8 vector staged in 64 KB of LDS
+constexpr int kMaxGemvK32 = 16384;  // fp32 vector staged in 64 KB of LDS
+
+}  // namespace
+
+extern "C" {
+
+int gemma_hip_init(int device) {
+  if (g.ready) {
+    if (device == g.device) return 0;
+    return fail("gemma_hip_init: already initialised on device %d", g.device);
+  }
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail("gemma_hip_init: no HIP device available (%s)",
+                e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+  if (device < 0 || device >= count)
+    return fail("gemma_hip_init: device %d out of range (0..%d)", device,
+                count - 1);
+  hipDeviceProp_t prop;
+  GH_CHECK("gemma_hip_init: hipGetDeviceProperties",
+           hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail("gemma_hip_init: device %d is %s; this library is built for gfx950",
+                device, prop.gcnArchName);
+  GH_CHECK("gemma_hip_init: hipSetDevice", hipSetDevice(device));
+  GH_CHECK("gemma_hip_init: hipStreamCreate",
+           hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+  g.info.cus = prop.multiProcessorCount;
+  g.device = device;
+  g.ready = true;
+  g_err[0] = '\0';
+  return 0;
+}
+
+void gemma_hip_shutdown(void) {
+  if (!g.ready) return;
+  (void)hipStreamSynchronize(g.stream);
+  {
+    std::lock_guard<std::mutex> guard(g.lock);
+    for (auto &kv : g.regions) (void)hipFree(kv.second.device);
+    g.regions.clear();
+  }
+  if (g.staging != nullptr) (void)hipFree(g.staging);
+  g.staging = nullptr;
+  g.staging_bytes = 0;
+  (void)hipStreamDestroy(g.stream);
+  g.stream = nullptr;
+  g.ready = false;
+  g.device = -1;
+}
+
+const char *gemma_hip_last_error(void) { return g_err; }
+
+int gemma_hip_sync(void *stream) {
+  if (need_init()) return 1;
+  GH_CHECK("gemma_hip_sync", hipStreamSynchronize(pick_stream(stream)));
+  return 0;
+}
+
+int gemma_hip_register_weights(const void *host, size_t bytes) {
+  if (need_init()) return 1;
+  if (host == nullptr || bytes == 0)
+    return fail("gemma_hip_register_weights: empty range");
+  const uintptr_t h = reinterpret_cast<uintptr_t>(host);
+  {
+    std::lock_guard<std::mutex> guard(g.lock);
+    auto it = g.regions.upper_bound(h + bytes - 1);
+    if (it != g.regions.begin()) {
+      --it;
+      if (it->first + it->second.bytes > h)
+        return fail("gemma_hip_register_weights: range overlaps a registered one");
+    }
+  }
+  char *device = nullptr;
+  GH_CHECK("gemma_hip_register_weights: hipMalloc", hipMalloc(&device, bytes));
+  hipError_t e = hipMemcpy(device, host, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(device);
+    return hip_fail("gemma_hip_register_weights: upload", e);
+  }
+  std::lock_guard<std::mutex> guard(g.lock);
+  g.regions[h] = Region{bytes, device};
+  return 0;
+}
+
+int gemma_hip_release_weights(const void *host) {
+  if (need_init()) return 1;
+  const uintptr_t h = reinterpret_cast<uintptr_t>(host);
+  char *device = nullptr;
+  {
+    std::lock_guard<std::mutex> guard(g.lock);
+    auto it = g.regions.find(h);
+    if (it == g.regions.end())
+      return fail("gemma_hip_release_weights: %p is not a registered range start",
+                  host);
+    device = it->second.device;
+    g.regions.erase(it);
+  }
+  GH_CHECK("gemma_hip_release_weights: sync", hipStreamSynchronize(g.stream));
+  GH_CHECK("gemma_hip_release_weights: hipFree", hipFree(device));
+  return 0;
+}
+
+void *gemma_hip_device_ptr(const void *host) {
+  if (!g.ready) return nullptr;
+  return resolve(host, 1);
+}
+
+/* ---- device entry points ---------------------------------------------- */
+
+int gemma_hip_quantize(int8_t *dst, float *dsc, const float *src, int sstr,
+                       int m, int n, void *stream) {
+  if (need_init()) return 1;
+  if (sstr == 0) sstr = n;
+  if (m < 0 || n <= 0 || sstr < n)
+    return fail("gemma_hip_quantize: bad shape m=%d n=%d sstr=%d", m, n, sstr);
+  if (m == 0) return 0;
+  if (dst == nullptr || dsc == nullptr || src == nullptr)
+    return fail("gemma_hip_quantize: null pointer");
+  GH_CHECK("gemma_hip_quantize: launch",
+           gh::launch_quantize(dst, dsc, src, sstr, m, n, pick_stream(stream)));
+  return 0;
+}
+
+int gemma_hip_matmul(float *dst, int dstr, const int8_t *mat, int mstr,
+                     const float *matsc, const int8_t *src, int sstr,
+                     const float *ssc, int m, int n, int k, void *stream) {
+  if (need_init()) return 1;
+  if (dstr == 0) dstr = n;
+  if (mstr == 0) mstr = k;
+  if (sstr == 0) sstr = k;
+  if (check_matmul_shape("gemma_hip_matmul", m, n, k, dstr, mstr, sstr)) return 1;
+  if (m == 0) return 0;
+  if (!dst || !mat || !matsc || !src || !ssc)
+    return fail("gemma_hip_matmul: null pointer");
+  hipStream_t s = pick_stream(stream);
+  if (m == 1 && mstr == k && k <= kMaxGemvK8) {
+    gh::GemvJobs jobs{};
+    jobs.w[0] = mat;
+    jobs.sc[0] = matsc;
+    jobs.dst[0] = dst;
+    for (int j = 0; j < gh::kMaxJobs; ++j) jobs.end[j] = n;
+    jobs.njobs = 1;
+    GH_CHECK("gemma_hip_matmul: gemv launch",
+             gh::launch_gemv_i8(jobs, k, src, ssc, nullptr, nullptr, nullptr,
+                                g.info, s));
+    return 0;
+  }
+  GH_CHECK("gemma_hip_matmul: gemm launch",
+           gh::launch_gemm_i8(dst, dstr, 0, mat, mstr, matsc, src, sstr, ssc, m,
+                              n, k, g.info, s));
+  return 0;
+}
+
+int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,
+                           const int8_t *src, const float *ssc, int m,
+                           int heads, int hdim, int k, void *stream) {
+  if (need_init()) return 1;
+  if (m < 0 || heads <= 0 || hdim <= 0 || k <= 0 || (long)heads * hdim > (1l << 30))
+    return fail("gemma_hip_matmul_heads: bad shape m=%d heads=%d hdim=%d k=%d", m,
+                heads, hdim, k);
+  if (m == 0) return 0;
+  if (!dst || !mat || !matsc || !src || !ssc)
+    return fail("gemma_hip_matmul_heads: null pointer");
+  GH_CHECK("gemma_hip_matmul_heads: launch",
+           gh::launch_gemm_i8(dst, hdim, hdim, mat, k, matsc, src, k, ssc, m,
+                              heads * hdim, k, g.info, pick_stream(stream)));
+  return 0;
+}
+
+int gemma_hip_matmul_multi(const gemma_hip_job *jobs, int njobs,
+                           const int8_t *x, const float *xs, int k,
+                           void *stream) {
+  if (need_init()) return 1;
+  gh::GemvJobs gj;
+  if (build_jobs("gemma_hip_matmul_multi", jobs, njobs, &gj)) return 1;
+  if (k <= 0 || k > kMaxGemvK8)
+    return fail("gemma_hip_matmul_multi: k=%d outside 1..%d", k, kMaxGemvK8);
+  if (x == nullptr || xs == nullptr)
+    return fail("gemma_hip_matmul_multi: null activation pointer");
+  for (int j = 0; j < njobs; ++j)
+    if (jobs[j].m > 0 && jobs[j].sc == nullptr)
+      return fail("gemma_hip_matmul_multi: job %d has no scales", j);
+  if (gj.end[njobs - 1] == 0) return 0;
+  GH_CHECK("gemma_hip_matmul_multi: launch",
+           gh::launch_gemv_i8(gj, k, x, xs, nullptr, nullptr, nullptr, g.info,
+                              pick_stream(stream)));
+  return 0;
+}
+
+int gemma_hip_quantize_matmul(const gemma_hip_job *jobs, int njobs,
+                              const float *x, int k, int8_t *xq, float *xs,
+                              void *stream) {
+  if (need_init()) return 1;
+  gh::GemvJobs gj;
+  if (build_jobs("gemma_hip_quantize_matmul", jobs, njobs, &gj)) return 1;
+  if (k <= 0 || k > kMaxGemvK8)
+    return fail("gemma_hip_quantize_matmul: k=%d outside 1..%d", k, kMaxGemvK8);
+  if (x == nullptr) return fail("gemma_hip_quantize_matmul: null activation pointer");
+  for (int j = 0; j < njobs; ++j)
+    if (jobs[j].m > 0 && jobs[j].sc == nullptr)
+      return fail("gemma_hip_quantize_matmul: job %d has no scales", j);
+  hipStream_t s = pick_stream(stream);
+  if (gj.end[njobs - 1] == 0) {
+    // no rows: still produce the quantized vector when asked for
+    if (xq != nullptr && xs != nullptr)
+      GH_CHECK("gemma_hip_quantize_matmul: quantize",
+               gh::launch_quantize(xq, xs, x, k, 1, k, s));
+    return 0;
+  }
+  GH_CHECK("gemma_hip_quantize_matmul: launch",
+           gh::launch_gemv_i8(gj, k, nullptr, nullptr, x, xq, xs, g.info, s));
+  return 0;
+}
+
+int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
+                         const float *src, int sstr, int m, int n, int k,
+                         void *stream) {
+  if (need_init()) return 1;
+  if (dstr == 0) dstr = n;
+  if (mstr == 0) mstr = k;
+  if (sstr == 0) sstr = k;
+  if (check_matmul_shape("gemma_hip_matmul_f32", m, n, k, dstr, mstr, sstr)) return 1;
+  if (m == 0) return 0;
+  if (!dst || !mat || !src) return fail("gemma_hip_matmul_f32: null pointer");
+  hipStream_t s = pick_stream(stream);
+  if (m == 1 && mstr == k && k <= kMaxGemvK32) {
+    gh::GemvJobs jobs{};
+    jobs.w[0] = mat;
+    jobs.dst[0] = dst;
+    for (int j = 0; j < gh::kMaxJobs; ++j) jobs.end[j] = n;
+    jobs.njobs = 1;
+    GH_CHECK("gemma_hip_matmul_f32: gemv launch",
+             gh::launch_gemv_f32(jobs, k, src, g.info, s));
+    return 0;
+  }
+  GH_CHECK("gemma_hip_matmul_f32: gemm launch",
+           gh::launch_gemm_f32(dst, dstr, mat, mstr, src, sstr, m, n, k, g.info, s));
+  return 0;
+}
+
+int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
+                               const float *x, int k, void *stream) {
+  if (need_init()) return 1;
+  gh::GemvJobs gj;
+  if (build_jobs("gemma_hip_matmul_f32_multi", jobs, njobs, &gj)) return 1;
+  if (k <= 0 || k > kMaxGemvK32)
+    return fail("gemma_hip_matmul_f32_multi: k=%d outside 1..%d", k, kMaxGemvK32);
+  if (x == nullptr) return fail("gemma_hip_matmul_f32_multi: null activation pointer");
+  if (gj.end[njobs - 1] == 0) return 0;
+  GH_CHECK("gemma_hip_matmul_f32_multi: launch",
+           gh::launch_gemv_f32(gj, k, x, g.info, pick_stream(stream)));
+  return 0;
+}
+
+/* ---- host drop-ins ------------------------------------------------------ */
+
+int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,
+                                int dim) {
+  if (need_init()) return 1;
+  if (dim <= 0 || !dst || !scale || !vec)
+    return fail("gemma_hip_quantize_act_host: bad arguments (dim=%d)", dim);
+  Carver c;
+  size_t o_src = c.take((size_t)dim * 4), o_q = c.take(dim), o_s = c.take(4);
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  GH_CHECK("quantize_act_host: H2D",
+           hipMemcpyAsync(base + o_src, vec, (size_t)dim * 4, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_quantize((int8_t *)(base + o_q), (float *)(base + o_s),
+                         (const float *)(base + o_src), dim, 1, dim, nullptr))
+    return 1;
+  GH_CHECK("quantize_act_host: D2H",
+           hipMemcpyAsync(dst, base + o_q, dim, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("quantize_act_host: D2H",
+           hipMemcpyAsync(scale, base + o_s, 4, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("quantize_act_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
+                                 int sstr, int m, int n) {
+  if (need_init()) return 1;
+  if (sstr == 0) sstr = n;
+  if (m < 0 || n <= 0 || sstr < n || !dst || !dsc || !src)
+    return fail("gemma_hip_quantize_acts_host: bad arguments");
+  if (m == 0) return 0;
+  const size_t in_floats = (size_t)(m - 1) * sstr + n;
+  Carver c;
+  size_t o_src = c.take(in_floats * 4), o_q = c.take((size_t)m * n),
+         o_s = c.take((size_t)m * 4);
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  GH_CHECK("quantize_acts_host: H2D",
+           hipMemcpyAsync(base + o_src, src, in_floats * 4, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_quantize((int8_t *)(base + o_q), (float *)(base + o_s),
+                         (const float *)(base + o_src), sstr, m, n, nullptr))
+    return 1;
+  GH_CHECK("quantize_acts_host: D2H",
+           hipMemcpyAsync(dst, base + o_q, (size_t)m * n, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("quantize_acts_host: D2H",
+           hipMemcpyAsync(dsc, base + o_s, (size_t)m * 4, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("quantize_acts_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_gemv_int8_host(float *dst, const int8_t *mat, const float *matsc,
+                             const int8_t *vec, float vsc, int m, int n) {
+  gemma_hip_job job{mat, matsc, dst, m};
+  return gemma_hip_gemv_int8_multi_host(&job, 1, vec, vsc, n);
+}
+
+int gemma_hip_gemv_int8_multi_host(const gemma_hip_job *jobs, int njobs,
+                                   const int8_t *vec, float vsc, int n) {
+  if (need_init()) return 1;
+  if (jobs == nullptr || njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS || n <= 0 || !vec)
+    return fail("gemma_hip_gemv_int8_multi_host: bad arguments");
+  gemma_hip_job djobs[GEMMA_HIP_MAX_JOBS];
+  Carver c;
+  size_t o_x = c.take(n), o_s = c.take(4), o_y[GEMMA_HIP_MAX_JOBS];
+  for (int j = 0; j < njobs; ++j) {
+    if (jobs[j].m < 0) return fail("gemma_hip_gemv_int8_multi_host: job %d m<0", j);
+    o_y[j] = c.take((size_t)jobs[j].m * 4);
+  }
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  for (int j = 0; j < njobs; ++j) {
+    const size_t rows = (size_t)jobs[j].m;
+    const void *w = rows ? resolve(jobs[j].w, rows * n) : nullptr;
+    const void *sc = rows ? resolve(jobs[j].sc, rows * 4) : nullptr;
+    if (rows && (w == nullptr || sc == nullptr))
+      return fail("gemma_hip_gemv_int8_multi_host: job %d weights are not registered", j);
+    djobs[j] = gemma_hip_job{w, (const float *)sc, (float *)(base + o_y[j]), jobs[j].m};
+  }
+  GH_CHECK("gemv_int8_host: H2D",
+           hipMemcpyAsync(base + o_x, vec, n, hipMemcpyHostToDevice, g.stream));
+  GH_CHECK("gemv_int8_host: H2D",
+           hipMemcpyAsync(base + o_s, &vsc, 4, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_matmul_multi(djobs, njobs, (const int8_t *)(base + o_x),
+                             (const float *)(base + o_s), n, nullptr))
+    return 1;
+  for (int j = 0; j < njobs; ++j)
+    if (jobs[j].m > 0)
+      GH_CHECK("gemv_int8_host: D2H",
+               hipMemcpyAsync(jobs[j].dst, base + o_y[j], (size_t)jobs[j].m * 4,
+                              hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemv_int8_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_gemm_int8_host(float *dst, int dstr, const int8_t *mat, int mstr,
+                             const float *matsc, const int8_t *src, int sstr,
+                             const float *ssc, int m, int n, int k) {
+  if (need_init()) return 1;
+  if (dstr == 0) dstr = n;
+  if (mstr == 0) mstr = k;
+  if (sstr == 0) sstr = k;
+  if (check_matmul_shape("gemma_hip_gemm_int8_host", m, n, k, dstr, mstr, sstr))
+    return 1;
+  if (m == 0) return 0;
+  if (!dst || !mat || !matsc || !src || !ssc)
+    return fail("gemma_hip_gemm_int8_host: null pointer");
+  const void *dmat = resolve(mat, (size_t)(n - 1) * mstr + k);
+  const void *dsc = resolve(matsc, (size_t)n * 4);
+  if (dmat == nullptr || dsc == nullptr)
+    return fail("gemma_hip_gemm_int8_host: weights are not registered");
+  const size_t src_bytes = (size_t)(m - 1) * sstr + k;
+  Carver c;
+  size_t o_a = c.take(src_bytes), o_as = c.take((size_t)m * 4),
+         o_y = c.take((size_t)m * dstr * 4);
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  GH_CHECK("gemm_int8_host: H2D",
+           hipMemcpyAsync(base + o_a, src, src_bytes, hipMemcpyHostToDevice, g.stream));
+  GH_CHECK("gemm_int8_host: H2D",
+           hipMemcpyAsync(base + o_as, ssc, (size_t)m * 4, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_matmul((float *)(base + o_y), dstr, (const int8_t *)dmat, mstr,
+                       (const float *)dsc, (const int8_t *)(base + o_a), sstr,
+                       (const float *)(base + o_as), m, n, k, nullptr))
+    return 1;
+  GH_CHECK("gemm_int8_host: D2H",
+           hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,
+                            (size_t)n * 4, m, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemm_int8_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_gemv_fpx_host(float *dst, const float *mat, const float *vec,
+                            int m, int n) {
+  gemma_hip_job job{mat, nullptr, dst, m};
+  return gemma_hip_gemv_fpx_multi_host(&job, 1, vec, n);
+}
+
+int gemma_hip_gemv_fpx_multi_host(const gemma_hip_job *jobs, int njobs,
+                                  const float *vec, int n) {
+  if (need_init()) return 1;
+  if (jobs == nullptr || njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS || n <= 0 || !vec)
+    return fail("gemma_hip_gemv_fpx_multi_host: bad arguments");
+  gemma_hip_job djobs[GEMMA_HIP_MAX_JOBS];
+  Carver c;
+  size_t o_x = c.take((size_t)n * 4), o_y[GEMMA_HIP_MAX_JOBS];
+  for (int j = 0; j < njobs; ++j) {
+    if (jobs[j].m < 0) return fail("gemma_hip_gemv_fpx_multi_host: job %d m<0", j);
+    o_y[j] = c.take((size_t)jobs[j].m * 4);
+  }
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  for (int j = 0; j < njobs; ++j) {
+    const size_t rows = (size_t)jobs[j].m;
+    const void *w = rows ? resolve(jobs[j].w, rows * n * 4) : nullptr;
+    if (rows && w == nullptr)
+      return fail("gemma_hip_gemv_fpx_multi_host: job %d weights are not registered", j);
+    djobs[j] = gemma_hip_job{w, nullptr, (float *)(base + o_y[j]), jobs[j].m};
+  }
+  GH_CHECK("gemv_fpx_host: H2D",
+           hipMemcpyAsync(base + o_x, vec, (size_t)n * 4, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_matmul_f32_multi(djobs, njobs, (const float *)(base + o_x), n, nullptr))
+    return 1;
+  for (int j = 0; j < njobs; ++j)
+    if (jobs[j].m > 0)
+      GH_CHECK("gemv_fpx_host: D2H",
+               hipMemcpyAsync(jobs[j].dst, base + o_y[j], (size_t)jobs[j].m * 4,
+                              hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemv_fpx_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
+                            const float *src, int sstr, int m, int n, int k) {
+  if (need_init()) return 1;
+  if (dstr == 0) dstr = n;
+  if (mstr == 0) mstr = k;
+  if (sstr == 0) sstr = k;
+  if (check_matmul_shape("gemma_hip_gemm_fpx_host", m, n, k, dstr, mstr, sstr))
+    return 1;
+  if (m == 0) return 0;
+  if (!dst || !mat || !src) return fail("gemma_hip_gemm_fpx_host: null pointer");
+  const void *dmat = resolve(mat, ((size_t)(n - 1) * mstr + k) * 4);
+  if (dmat == nullptr) return fail("gemma_hip_gemm_fpx_host: weights are not registered");
+  const size_t src_floats = (size_t)(m - 1) * sstr + k;
+  Carver c;
+  size_t o_a = c.take(src_floats * 4), o_y = c.take((size_t)m * dstr * 4);
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  GH_CHECK("gemm_fpx_host: H2D",
+           hipMemcpyAsync(base + o_a, src, src_floats * 4, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_matmul_f32((float *)(base + o_y), dstr, (const float *)dmat, mstr,
+                           (const float *)(base + o_a), sstr, m, n, k, nullptr))
+    return 1;
+  GH_CHECK("gemm_fpx_host: D2H",
+           hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,
+                            (size_t)n * 4, m, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemm_fpx_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,106 @@
+// gh_arith.h -- device arithmetic that reproduces the reference build's fp32
+// results bit for bit on gfx950.
+//
+// The reference (gemma.c, built by gcc with -ffast-math) runs with FTZ and DAZ
+// set in MXCSR and truncates with cvttss2si.  gfx950 keeps fp32 denormals and
+// saturates on conversion, so the differences are written out here:
+//  - DAZ: a subnormal operand is read as a zero of its sign.
+//  - FTZ: x86 flushes a product whose value, rounded to 24 bits with an
+//    unbounded exponent, is below FLT_MIN.  The GPU's gradual underflow gives
+//    the same answer except when its denormal rounding lands on exactly
+//    FLT_MIN; that case is settled with the exact double product.
+//  - cvttss2si returns INT_MIN for NaN and out-of-range values.
+// Files including this header are compiled with -ffp-contract=off, so every
+// a*b and a+b below is one IEEE round-to-nearest operation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gh {
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float daz(float v) {
+  uint32_t bits = __float_as_uint(v);
+  return (bits & 0x7f800000u) == 0 ? __uint_as_float(bits & 0x80000000u) : v;
+}
+
+// a*b under FTZ/DAZ (gemma.c's rescale products, gemma.c:2762, 3629, 3862)
+__device__ __forceinline__ float mul_ftz(float a, float b) {
+  a = daz(a);
+  b = daz(b);
+  float p = a * b;
+  if (fabsf(p) <= 1.17549435e-38f) {
+    double exact = (double)a * (double)b;  // exact: 24+24 bits fit in 53
+    float scaled = (float)(exact * 0x1p64);  // 24-bit rounding, no underflow
+    p = fabsf(scaled) < 0x1p-62f
+            ? (__double_as_longlong(exact) < 0 ? -0.0f : 0.0f)
+            : (float)exact;
+  }
+  return p;
+}
+
+// x86 cvttss2si
+__device__ __forceinline__ int32_t cvtt(float v) {
+  return fabsf(v) < 2147483648.0f ? (int32_t)v : INT32_MIN;
+}
+
+// Scale and reciprocal of one activation row from its amax
+// (gemma.c:2616-2617 as gcc -ffast-math evaluates it: scale = amax*(1/127),
+// inv = 127/amax; both 1 when amax == 0).  The division is done in double:
+// a 53-bit quotient rounded to 24 bits equals the correctly rounded float
+// quotient (double rounding is innocuous for p' >= 2p+2).
+struct QuantParams {
+  float scale;
+  float inv;
+};
+
+__device__ __forceinline__ QuantParams quant_params(float amax) {
+  QuantParams qp;
+  if (amax > 0.0f) {
+    qp.scale = mul_ftz(amax, 1.0f / 127.0f);
+    qp.inv = (float)(127.0 / (double)amax);
+  } else {
+    qp.scale = 1.0f;
+    qp.inv = 1.0f;
+  }
+  return qp;
+}
+
+// One quantized element (gemma.c:2625-2633 and 2642-2646):
+// q = clamp(trunc(v*inv + copysign(0.5, v*inv)), -127, 127)
+__device__ __forceinline__ int32_t quant_one(float v, float inv) {
+  float x = daz(v) * inv;
+  float t = x + copysignf(0.5f, x);
+  int32_t q = cvtt(t);
+  return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
+// |v| with DAZ, for the exact amax reduction (gemma.c:2596-2615)
+__device__ __forceinline__ float abs_daz(float v) { return fabsf(daz(v)); }
+
+// Rescale of one int32 accumulator: (float)acc * (act_scale * w_scale)
+__device__ __forceinline__ float rescale(int32_t acc, float act_scale,
+                                         float w_scale) {
+  return mul_ftz((float)acc, mul_ftz(act_scale, w_scale));
+}
+
+// Packs four quantized values into one little-endian 32-bit word.
+__device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c,
+                                          int32_t d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
+         ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+}
+
+// Wavefront (64 lanes) reductions.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+}  // namespace gh

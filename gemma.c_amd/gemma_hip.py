@@ -1,0 +1,162 @@
+"""ctypes binding of libgemma_hip.so (the C ABI in include/gemma_hip.h).
+
+This is how Python code (the tests, bench.py, __graft_entry__) reaches the
+HIP kernels: every call goes through the exported C functions, exactly as the
+reference's C call sites would.  Device buffers are plain addresses; torch is
+only used by callers to allocate HBM and to name a stream.
+
+A failing call raises ``GemmaHipError`` with the library's message
+(gemma_hip_last_error); the library never falls back to the CPU, so a missing
+or unloadable ``.so`` is an error too.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libgemma_hip.so")
+HEADER_PATH = os.path.join(REPO_DIR, "include", "gemma_hip.h")
+MAX_JOBS = 4
+
+
+class GemmaHipError(RuntimeError):
+    pass
+
+
+class Job(ctypes.Structure):
+    """gemma_hip_job: mirrors the reference's GemvJob (gemma.c:2790-2800)."""
+
+    _fields_ = [("w", ctypes.c_void_p), ("sc", ctypes.c_void_p),
+                ("dst", ctypes.c_void_p), ("m", ctypes.c_int)]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SIGS = {
+    "gemma_hip_init": (_I, [_I]),
+    "gemma_hip_shutdown": (None, []),
+    "gemma_hip_last_error": (ctypes.c_char_p, []),
+    "gemma_hip_sync": (_I, [_P]),
+    "gemma_hip_register_weights": (_I, [_P, ctypes.c_size_t]),
+    "gemma_hip_release_weights": (_I, [_P]),
+    "gemma_hip_device_ptr": (_P, [_P]),
+    "gemma_hip_quantize": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "gemma_hip_matmul": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
+    "gemma_hip_matmul_heads": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "gemma_hip_matmul_multi": (_I, [ctypes.POINTER(Job), _I, _P, _P, _I, _P]),
+    "gemma_hip_quantize_matmul": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P, _P, _P]),
+    "gemma_hip_matmul_f32": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
+    "gemma_hip_matmul_f32_multi": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P]),
+    "gemma_hip_quantize_act_host": (_I, [_P, _P, _P, _I]),
+    "gemma_hip_quantize_acts_host": (_I, [_P, _P, _P, _I, _I, _I]),
+    "gemma_hip_gemv_int8_host": (_I, [_P, _P, _P, _P, ctypes.c_float, _I, _I]),
+    "gemma_hip_gemv_int8_multi_host": (_I, [ctypes.POINTER(Job), _I, _P, ctypes.c_float, _I]),
+    "gemma_hip_gemm_int8_host": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I]),
+    "gemma_hip_gemv_fpx_host": (_I, [_P, _P, _P, _I, _I]),
+    "gemma_hip_gemv_fpx_multi_host": (_I, [ctypes.POINTER(Job), _I, _P, _I]),
+    "gemma_hip_gemm_fpx_host": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I]),
+}
+
+
+def header_symbols(path: str = HEADER_PATH) -> list[str]:
+    """Every function the public header declares."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gemma_hip_\w+)\s*\(", text)))
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise GemmaHipError(f"{path} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def _addr(x) -> int | None:
+    """Device/host address of a torch tensor, numpy array or int (None -> NULL)."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return x.data_ptr()
+    if hasattr(x, "ctypes"):
+        return x.ctypes.data
+    raise TypeError(f"cannot take the address of {type(x)}")
+
+
+class GemmaHip:
+    """Thin object wrapper: each method is one C call; errors raise."""
+
+    def __init__(self, device: int = 0, path: str = LIB_PATH):
+        self.lib = load(path)
+        self._check(self.lib.gemma_hip_init(device))
+        self.device = device
+
+    def _check(self, rc: int) -> None:
+        if rc != 0:
+            raise GemmaHipError(self.lib.gemma_hip_last_error().decode())
+
+    def close(self) -> None:
+        self.lib.gemma_hip_shutdown()
+
+    def sync(self, stream: int | None = None) -> None:
+        self._check(self.lib.gemma_hip_sync(stream))
+
+    @staticmethod
+    def jobs(specs) -> tuple[ctypes.Array, int]:
+        """specs: iterable of (w, sc, dst, m)."""
+        specs = list(specs)
+        arr = (Job * max(1, len(specs)))()
+        for i, (w, sc, dst, m) in enumerate(specs):
+            arr[i] = Job(_addr(w), _addr(sc), _addr(dst), int(m))
+        return arr, len(specs)
+
+    # device entry points ---------------------------------------------------
+    def quantize(self, dst, dsc, src, sstr, m, n, stream=None):
+        self._check(self.lib.gemma_hip_quantize(_addr(dst), _addr(dsc), _addr(src), sstr, m,
+                                                n, stream))
+
+    def matmul(self, dst, dstr, mat, mstr, matsc, src, sstr, ssc, m, n, k, stream=None):
+        self._check(self.lib.gemma_hip_matmul(_addr(dst), dstr, _addr(mat), mstr, _addr(matsc),
+                                              _addr(src), sstr, _addr(ssc), m, n, k, stream))
+
+    def matmul_heads(self, dst, mat, matsc, src, ssc, m, heads, hdim, k, stream=None):
+        self._check(self.lib.gemma_hip_matmul_heads(_addr(dst), _addr(mat), _addr(matsc),
+                                                    _addr(src), _addr(ssc), m, heads, hdim, k,
+                                                    stream))
+
+    def matmul_multi(self, specs, x, xs, k, stream=None):
+        arr, n = self.jobs(specs)
+        self._check(self.lib.gemma_hip_matmul_multi(arr, n, _addr(x), _addr(xs), k, stream))
+
+    def quantize_matmul(self, specs, x, k, xq=None, xs=None, stream=None):
+        arr, n = self.jobs(specs)
+        self._check(self.lib.gemma_hip_quantize_matmul(arr, n, _addr(x), k, _addr(xq),
+                                                       _addr(xs), stream))
+
+    def matmul_f32(self, dst, dstr, mat, mstr, src, sstr, m, n, k, stream=None):
+        self._check(self.lib.gemma_hip_matmul_f32(_addr(dst), dstr, _addr(mat), mstr,
+                                                  _addr(src), sstr, m, n, k, stream))
+
+    def matmul_f32_multi(self, specs, x, k, stream=None):
+        arr, n = self.jobs(specs)
+        self._check(self.lib.gemma_hip_matmul_f32_multi(arr, n, _addr(x), k, stream))
+
+    # weights ---------------------------------------------------------------
+    def register_weights(self, host, nbytes: int):
+        self._check(self.lib.gemma_hip_register_weights(_addr(host), nbytes))
+
+    def release_weights(self, host):
+        self._check(self.lib.gemma_hip_release_weights(_addr(host)))
+
+    def device_ptr(self, host) -> int | None:
+        return self.lib.gemma_hip_device_ptr(_addr(host))

@@ -1,0 +1,187 @@
+/*
+ * gemma_hip.h -- C ABI of the MI355X (gfx950) W8A8 matmul library.
+ *
+ * The library replaces the matmul hot path of Gemma.c's forward passes:
+ * runtime activation quantization, int8 x int8 -> int32 dot products over the
+ * full K row (one fp32 scale per output channel and one per activation row),
+ * the fp32 rescale, and the fp32 GEMV/GEMM fallback used for unquantized
+ * model files.  Every numbered comment names the reference function an entry
+ * point replaces, as /root/reference/gemma.c:<line>.
+ *
+ * Arithmetic contract (bit-exact with the reference built by gcc with
+ * -ffast-math, whose start-up code sets FTZ and DAZ):
+ *   amax  = max |v| over the row (subnormal v count as 0)
+ *   scale = amax * (1/127)   (1 when amax == 0; a result below FLT_MIN is 0)
+ *   inv   = 127 / amax       (1 when amax == 0; correctly rounded)
+ *   x     = v * inv,  t = x + copysign(0.5, x)
+ *   q     = clamp(trunc_x86(t), -127, 127)   (NaN/out of range -> -127)
+ *   acc   = sum_k (int32)a[k] * (int32)w[k]  (exact int32)
+ *   y     = (float)acc * (act_scale * w_scale)   (two roundings, FTZ)
+ * The fp32 fallback has no bit-exact target (the reference's summation order
+ * is whatever its compiler vectorises); it matches within a relative error of
+ * 1e-5 of sum_k |a_k w_k|.
+ *
+ * Conventions shared by every entry point:
+ *  - Return 0 on success and 1 on failure; the failure's message is kept in a
+ *    thread-local buffer read by gemma_hip_last_error() (the reference's
+ *    log_error/get_error convention, gemma.c:577-587).  Nothing aborts.
+ *  - Matrices are row-major.  A stride of 0 means "dense" (the row length),
+ *    as in the reference (gemma.c:3951-3956).
+ *  - "n" of gemv_* is the reference's m (output rows) and "k" its n
+ *    (reduction length): the names here follow the GEMM contract.
+ *  - Entry points without the _host suffix take DEVICE pointers (HBM) and
+ *    enqueue their work on `stream` (a hipStream_t; NULL selects the
+ *    library's own stream) without synchronising.
+ *  - Entry points with the _host suffix take the reference call sites' host
+ *    buffers for activations and outputs, resolve weight pointers through the
+ *    registry below, and return after the result is back in host memory.
+ *  - Calls are made from one host thread at a time.
+ */
+#ifndef GEMMA_HIP_H
+#define GEMMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GEMMA_HIP_MAX_JOBS 4
+
+/* One projection of a fused multi-output GEMV: replaces GemvJob
+ * (gemma.c:2790-2800) field for field.  w is int8 [m][k] (or fp32 [m][k] for
+ * the fp32 entry points), sc its fp32 [m] row scales (unused for fp32),
+ * dst the fp32 [m] output. */
+typedef struct {
+  const void *w;
+  const float *sc;
+  float *dst;
+  int m;
+} gemma_hip_job;
+
+/* ---- lifecycle --------------------------------------------------------- */
+
+/* Select the GPU and create the library's stream.  Replaces nothing in the
+ * reference (its kernels need no set-up); called from setup_gemma_model
+ * (gemma.c:6867). */
+int gemma_hip_init(int device);
+
+/* Free every registered weight and the staging buffers.  Called from
+ * cleanup_gemma_model (gemma.c:6909), next to gemm_free_thread_scratch
+ * (gemma.c:4056-4065). */
+void gemma_hip_shutdown(void);
+
+/* Message of the last failure on this thread (gemma.c:577-587 get_error). */
+const char *gemma_hip_last_error(void);
+
+/* Block until all work the library enqueued on `stream` (NULL: its own
+ * stream) has finished. */
+int gemma_hip_sync(void *stream);
+
+/* ---- weights: uploaded once, addressed by their host pointers ---------- */
+
+/* Copy [host, host+bytes) to a new device allocation.  Registered ranges are
+ * looked up by the _host entry points, which accept any pointer inside a
+ * range (the prefill QKV site passes w->i8.q + hd*hdim*dim, gemma.c:5084).
+ * Called once per QTensor array after read_qtensor/mmap_qtensor
+ * (gemma.c:1134-1171). */
+int gemma_hip_register_weights(const void *host, size_t bytes);
+
+/* Free the device copy of the range that starts at `host`. */
+int gemma_hip_release_weights(const void *host);
+
+/* Device address of a host pointer inside a registered range, or NULL. */
+void *gemma_hip_device_ptr(const void *host);
+
+/* ---- device entry points (the hot path) -------------------------------- */
+
+/* quantize_acts (gemma.c:2652-2674), and quantize_act (gemma.c:2586-2650)
+ * for m == 1: quantize m rows of n values, read with row stride sstr, into
+ * dst [m][n] int8 and dsc [m] fp32 scales. */
+int gemma_hip_quantize(int8_t *dst, float *dsc, const float *src, int sstr,
+                       int m, int n, void *stream);
+
+/* gemm_int8 (gemma.c:3937-4054), and gemv_int8 (gemma.c:2765-2788) when
+ * m == 1: dst[i][j] = (float)sum_l src[i][l]*mat[j][l] * (ssc[i]*matsc[j]).
+ * src int8 [m][sstr], mat int8 [n][mstr], dst fp32 [m][dstr]; cells outside
+ * [m][n] are not written. */
+int gemma_hip_matmul(float *dst, int dstr, const int8_t *mat, int mstr,
+                     const float *matsc, const int8_t *src, int sstr,
+                     const float *ssc, int m, int n, int k, void *stream);
+
+/* The prefill QKV site (gemma.c:5045-5089) as one launch: the same product
+ * as gemma_hip_matmul with n = heads*hdim and dense operands, written
+ * head-major, dst[(h*m + i)*hdim + j] for output column h*hdim + j. */
+int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,
+                           const int8_t *src, const float *ssc, int m,
+                           int heads, int hdim, int k, void *stream);
+
+/* gemv_int8_multi (gemma.c:2813-2837): njobs (<= GEMMA_HIP_MAX_JOBS)
+ * projections of the one quantized vector x [k] with scale xs (a device
+ * pointer to one float). */
+int gemma_hip_matmul_multi(const gemma_hip_job *jobs, int njobs,
+                           const int8_t *x, const float *xs, int k,
+                           void *stream);
+
+/* The decode call sites' quantize_act followed by gemv_int8_multi / gemv_int8
+ * (gemma.c:4768-4773, 4858-4859, 4911-4915, 4929-4930, 4964-4965) in one
+ * launch: x fp32 [k] is quantized inside the kernel.  xq [k] and xs [1]
+ * (both nullable) receive the quantized vector and its scale. */
+int gemma_hip_quantize_matmul(const gemma_hip_job *jobs, int njobs,
+                              const float *x, int k, int8_t *xq, float *xs,
+                              void *stream);
+
+/* gemm_fpx (gemma.c:3304-3399) and gemv_fpx (gemma.c:2730-2752) when
+ * m == 1: dst[i][j] = sum_l src[i][l]*mat[j][l] in fp32. */
+int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
+                         const float *src, int sstr, int m, int n, int k,
+                         void *stream);
+
+/* gemv_fpx_multi (gemma.c:2839-2858). */
+int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
+                               const float *x, int k, void *stream);
+
+/* ---- host drop-ins for the reference call sites ------------------------ */
+/* Same argument order and meaning as the reference functions named; weight
+ * pointers (mat, matsc, job w/sc) must lie in registered ranges, activation
+ * and output pointers are ordinary host memory. */
+
+/* quantize_act (gemma.c:2590); the scale goes to *scale. */
+int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,
+                                int dim);
+
+/* quantize_acts (gemma.c:2656). */
+int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
+                                 int sstr, int m, int n);
+
+/* gemv_int8 (gemma.c:2770): m output rows, reduction length n. */
+int gemma_hip_gemv_int8_host(float *dst, const int8_t *mat, const float *matsc,
+                             const int8_t *vec, float vsc, int m, int n);
+
+/* gemv_int8_multi (gemma.c:2818); job dst pointers are host memory. */
+int gemma_hip_gemv_int8_multi_host(const gemma_hip_job *jobs, int njobs,
+                                   const int8_t *vec, float vsc, int n);
+
+/* gemm_int8 (gemma.c:3943). */
+int gemma_hip_gemm_int8_host(float *dst, int dstr, const int8_t *mat, int mstr,
+                             const float *matsc, const int8_t *src, int sstr,
+                             const float *ssc, int m, int n, int k);
+
+/* gemv_fpx (gemma.c:2734). */
+int gemma_hip_gemv_fpx_host(float *dst, const float *mat, const float *vec,
+                            int m, int n);
+
+/* gemv_fpx_multi (gemma.c:2840). */
+int gemma_hip_gemv_fpx_multi_host(const gemma_hip_job *jobs, int njobs,
+                                  const float *vec, int n);
+
+/* gemm_fpx (gemma.c:3308). */
+int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
+                            const float *src, int sstr, int m, int n, int k);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,380 @@
+"""GPU parity of the HIP library against the oracle and the reference's
+golden fixtures, every call through the C ABI (include/gemma_hip.h).
+
+Bar: bit-exact int8 activations, scales, int32 sums (observed through the
+rescale, which is itself bit-exact) and fp32 outputs for the W8A8 path; for
+the fp32 fallback |y - y_exact| <= 1e-5 * sum|a*b| (TOL_F32).
+Large shapes are checked on sampled rows (exact per element) so the oracle
+finishes in seconds.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import oracle as om
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.int32)
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def outlier_acts(rng, shape):
+    x = rng.standard_normal(shape).astype(np.float32)
+    x[..., rng.random(shape[-1]) < 0.01] *= 20.0
+    return x
+
+
+# --------------------------------------------------------------- quantize
+def test_quantize_golden(gh, golden):
+    g = golden("quantize_act")
+    bounds = np.concatenate([[0], np.cumsum(g["lens"])])
+    for i in range(len(g["lens"])):
+        vec = g["vec"][bounds[i]:bounds[i + 1]]
+        n = len(vec)
+        note(f"quantize golden case {i} n={n}")
+        src = dev(vec)
+        q = torch.empty(n, dtype=torch.int8, device="cuda")
+        s = torch.empty(1, dtype=torch.float32, device="cuda")
+        gh.quantize(q, s, src, n, 1, n, stream())
+        assert np.array_equal(host(q), g["q_gcc"][bounds[i]:bounds[i + 1]]), f"case {i}"
+        assert bits(host(s))[0] == bits(g["scale_gcc"][i]), f"case {i}"
+
+
+def test_quantize_strided_golden(gh, golden):
+    g = golden("quantize_acts")
+    m, sstr = g["src"].shape
+    n = int(g["n"])
+    q = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    s = torch.empty(m, dtype=torch.float32, device="cuda")
+    gh.quantize(q, s, dev(g["src"]), sstr, m, n, stream())
+    assert np.array_equal(host(q), g["q"])
+    assert np.array_equal(bits(host(s)), bits(g["scale"]))
+
+
+@pytest.mark.parametrize("m,n", [(4096, 1152), (4096, 4304), (512, 6912), (3, 13)])
+def test_quantize_rows_vs_oracle(gh, oracle, m, n):
+    note(f"quantize rows m={m} n={n}")
+    rng = np.random.default_rng(m + n)
+    x = outlier_acts(rng, (m, n))
+    q = torch.empty((m, n), dtype=torch.int8, device="cuda")
+    s = torch.empty(m, dtype=torch.float32, device="cuda")
+    gh.quantize(q, s, dev(x), n, m, n, stream())
+    qo, so = oracle.quantize_acts(x)
+    assert np.array_equal(host(q), qo)
+    assert np.array_equal(bits(host(s)), bits(so))
+
+
+# --------------------------------------------------------------- GEMV
+def test_gemv_golden(gh, golden):
+    g = golden("gemv_int8")
+    n, k = g["mat"].shape
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    gh.matmul(y, 0, dev(g["mat"]), 0, dev(g["matsc"]), dev(g["xq"]), 0,
+              dev(np.array([g["xs"]], np.float32)), 1, n, k, stream())
+    assert np.array_equal(bits(host(y)), bits(g["y_gcc"]))
+
+
+def test_quantize_matmul_golden(gh, golden):
+    """fp32 x quantized inside the GEMV kernel (the decode call sites)."""
+    g = golden("gemv_int8")
+    n, k = g["mat"].shape
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    xq = torch.empty(k, dtype=torch.int8, device="cuda")
+    xs = torch.empty(1, dtype=torch.float32, device="cuda")
+    gh.quantize_matmul([(dev(g["mat"]), dev(g["matsc"]), y, n)], dev(g["x"]), k, xq, xs,
+                       stream())
+    assert np.array_equal(host(xq), g["xq"])
+    assert bits(host(xs))[0] == bits(g["xs"])
+    assert np.array_equal(bits(host(y)), bits(g["y_gcc"]))
+
+
+def test_gemv_multi_golden(gh, golden):
+    g = golden("gemv_int8_multi")
+    k = g["xq"].shape[0]
+    outs, specs = [], []
+    for j in range(3):
+        rows = g[f"w{j}"].shape[0]
+        outs.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
+        specs.append((dev(g[f"w{j}"]), dev(g[f"s{j}"]), outs[-1], rows))
+    gh.matmul_multi(specs, dev(g["xq"]), dev(np.array([g["xs"]], np.float32)), k, stream())
+    y = np.concatenate([host(o) for o in outs])
+    assert np.array_equal(bits(y), bits(g["y"]))
+
+
+# the gemma-3-1b decode GEMVs (out rows, in K)
+SWEEP_1B = [("q", 1024, 1152), ("k", 256, 1152), ("v", 256, 1152), ("o", 1152, 1024),
+            ("gate", 6912, 1152), ("up", 6912, 1152), ("down", 1152, 6912),
+            ("lm_head", 262144, 1152)]
+
+
+@pytest.mark.parametrize("name,n,k", SWEEP_1B)
+def test_gemv_sweep_1b_vs_oracle(gh, oracle, name, n, k):
+    note(f"gemv sweep {name} n={n} k={k}")
+    rng = np.random.default_rng(1234 + n + k)
+    W = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    x = outlier_acts(rng, (k,))
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    xq = torch.empty(k, dtype=torch.int8, device="cuda")
+    xs = torch.empty(1, dtype=torch.float32, device="cuda")
+    gh.quantize_matmul([(dev(W), dev(ws), y, n)], dev(x), k, xq, xs, stream())
+    qo, so = oracle.quantize_act(x)
+    yo, _ = oracle.gemv_int8(W, ws, qo, so)
+    assert np.array_equal(host(xq), qo)
+    assert bits(host(xs))[0] == bits(so)
+    assert np.array_equal(bits(host(y)), bits(yo))
+
+
+@pytest.mark.parametrize("rows,k", [((1024, 256, 256), 1152), ((6912, 6912), 1152),
+                                    ((2048, 1024, 1024), 2560), ((40, 3, 17, 64), 656)])
+def test_fused_multi_vs_oracle(gh, oracle, rows, k):
+    """q/k/v and gate/up as one launch (gemma.c:4768-4773, 4911-4915)."""
+    note(f"fused multi rows={rows} k={k}")
+    rng = np.random.default_rng(sum(rows) + k)
+    x = outlier_acts(rng, (k,))
+    qo, so = oracle.quantize_act(x)
+    specs, outs, refs = [], [], []
+    for r in rows:
+        W = rng.integers(-127, 128, (r, k), dtype=np.int8)
+        ws = rng.uniform(1e-3, 1e-2, r).astype(np.float32)
+        outs.append(torch.empty(r, dtype=torch.float32, device="cuda"))
+        specs.append((dev(W), dev(ws), outs[-1], r))
+        refs.append(oracle.gemv_int8(W, ws, qo, so)[0])
+    gh.quantize_matmul(specs, dev(x), k, None, None, stream())
+    for o, r in zip(outs, refs):
+        assert np.array_equal(bits(host(o)), bits(r))
+
+
+def test_gemv_unaligned_rows(gh, oracle):
+    """k % 16 != 0 and an odd base address take the generic path."""
+    rng = np.random.default_rng(5)
+    n, k = 37, 1001
+    W = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    x = outlier_acts(rng, (k,))
+    buf = torch.zeros(n * k + 1, dtype=torch.int8, device="cuda")
+    buf[1:] = torch.from_numpy(W.reshape(-1)).to("cuda")
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    gh.quantize_matmul([(buf.data_ptr() + 1, dev(ws), y, n)], dev(x), k, None, None, stream())
+    qo, so = oracle.quantize_act(x)
+    assert np.array_equal(bits(host(y)), bits(oracle.gemv_int8(W, ws, qo, so)[0]))
+
+
+# --------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("tag", ["tails", "strided", "m1", "blocks"])
+def test_gemm_golden(gh, golden, tag):
+    g = golden("gemm_int8")
+    m, n, k, ds, ms, ss = (int(v) for v in g[tag + "_shape"])
+    dst = dev(np.full((m, ds), -7.0, np.float32))
+    gh.matmul(dst, ds, dev(g[tag + "_b"]), ms, dev(g[tag + "_bs"]), dev(g[tag + "_a"]), ss,
+              dev(g[tag + "_as"]), m, n, k, stream())
+    assert np.array_equal(bits(host(dst)), bits(g[tag + "_dst"]))
+
+
+GEMM_SHAPES = [
+    # (label, M, N, K): prefill at 1b (M=512) and 4b (M=2048), SigLIP (M=4096)
+    ("1b_o", 512, 1152, 1024), ("1b_gate", 512, 6912, 1152), ("1b_down", 512, 1152, 6912),
+    ("siglip_qkv", 4096, 1152, 1152), ("siglip_fc1", 4096, 4304, 1152),
+    ("siglip_fc2", 4096, 1152, 4304), ("siglip_proj", 256, 2560, 1152),
+    ("4b_gate", 2048, 10240, 2560), ("4b_down", 2048, 2560, 10240),
+    ("tiny", 2, 8, 16), ("odd", 77, 333, 112),
+]
+
+
+@pytest.mark.parametrize("label,m,n,k", GEMM_SHAPES)
+def test_gemm_vs_oracle(gh, oracle, label, m, n, k):
+    note(f"gemm {label} m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    A = outlier_acts(rng, (m, k))
+    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    Aq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    As = torch.empty(m, dtype=torch.float32, device="cuda")
+    gh.quantize(Aq, As, dev(A), k, m, k, stream())
+    dst = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.matmul(dst, n, dev(B), k, dev(bs), Aq, k, As, m, n, k, stream())
+    qo, so = oracle.quantize_acts(A)
+    assert np.array_equal(host(Aq), qo)
+    # exact check on sampled rows: first/last tile rows and random ones
+    rows = np.unique(np.concatenate([np.arange(min(m, 8)), np.arange(max(0, m - 8), m),
+                                     rng.integers(0, m, min(m, 48))]))
+    ref, _ = oracle.gemm_int8(B, bs, qo[rows], so[rows])
+    got = host(dst)[rows]
+    assert np.array_equal(bits(got), bits(ref)), f"{(bits(got) != bits(ref)).sum()} mismatches"
+
+
+def test_gemm_heads_vs_oracle(gh, oracle):
+    """The prefill QKV site's head-major output (gemma.c:5045-5089)."""
+    rng = np.random.default_rng(9)
+    m, heads, hdim, k = 300, 4, 256, 1152
+    A = outlier_acts(rng, (m, k))
+    qo, so = oracle.quantize_acts(A)
+    B = rng.integers(-127, 128, (heads * hdim, k), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, heads * hdim).astype(np.float32)
+    dst = torch.empty((heads, m, hdim), dtype=torch.float32, device="cuda")
+    gh.matmul_heads(dst, dev(B), dev(bs), dev(qo), dev(so), m, heads, hdim, k, stream())
+    ref, _ = oracle.gemm_int8(B, bs, qo, so)  # [m][heads*hdim]
+    ref = ref.reshape(m, heads, hdim).transpose(1, 0, 2)
+    assert np.array_equal(bits(host(dst)), bits(np.ascontiguousarray(ref)))
+
+
+# --------------------------------------------------------------- fp32
+def check_f32(got, mat, src, oracle):
+    exact, mag = oracle.gemm_f64(mat, src)
+    err = np.abs(got.astype(np.float64) - exact)
+    worst = float(np.max(err / np.maximum(mag, 1e-300)))
+    assert np.all(err <= TOL_F32 * mag), f"worst relative error {worst:.3e}"
+
+
+def test_f32_golden(gh, golden, oracle):
+    g = golden("fpx")
+    n, k = g["gemv_w"].shape
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    gh.matmul_f32(y, 0, dev(g["gemv_w"]), 0, dev(g["gemv_x"]), 0, 1, n, k, stream())
+    check_f32(host(y)[None, :], g["gemv_w"], g["gemv_x"][None, :], oracle)
+    m, k = g["gemm_a"].shape
+    n = g["gemm_b"].shape[0]
+    d = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.matmul_f32(d, 0, dev(g["gemm_b"]), 0, dev(g["gemm_a"]), 0, m, n, k, stream())
+    check_f32(host(d), g["gemm_b"], g["gemm_a"], oracle)
+    # the reference's own fp32 results agree with ours to the same tolerance
+    exact, mag = oracle.gemm_f64(g["gemm_b"], g["gemm_a"])
+    assert np.all(np.abs(host(d) - g["gemm_dst"]) <= 2 * TOL_F32 * mag)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 6912, 1152), (1, 1152, 6912), (1, 32768, 2560),
+                                   (64, 1152, 588), (300, 640, 2048), (4096, 1152, 588),
+                                   (5, 7, 9)])
+def test_f32_vs_oracle(gh, oracle, m, n, k):
+    note(f"f32 m={m} n={n} k={k}")
+    rng = np.random.default_rng(m + n + k)
+    A = outlier_acts(rng, (m, k))
+    B = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    d = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.matmul_f32(d, n, dev(B), k, dev(A), k, m, n, k, stream())
+    rows = np.unique(rng.integers(0, m, min(m, 32)))
+    check_f32(host(d)[rows], B, A[rows], oracle)
+
+
+def test_f32_multi(gh, oracle):
+    rng = np.random.default_rng(3)
+    k = 1152
+    x = outlier_acts(rng, (k,))
+    mats = [(rng.standard_normal((r, k)) * 0.02).astype(np.float32) for r in (1024, 256, 256)]
+    outs = [torch.empty(len(w), dtype=torch.float32, device="cuda") for w in mats]
+    gh.matmul_f32_multi([(dev(w), None, o, len(w)) for w, o in zip(mats, outs)], dev(x), k,
+                        stream())
+    for w, o in zip(mats, outs):
+        check_f32(host(o)[None, :], w, x[None, :], oracle)
+
+
+# --------------------------------------------------------------- host drop-ins
+def test_host_entry_points(gh, oracle):
+    """The reference-shaped entry points on host buffers, with weights
+    registered once and addressed through interior pointers."""
+    import ctypes
+
+    lib = gh.lib
+    rng = np.random.default_rng(21)
+    heads, hdim, k = 4, 64, 640
+    W = rng.integers(-127, 128, (heads * hdim, k), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, heads * hdim).astype(np.float32)
+    gh.register_weights(W, W.nbytes)
+    gh.register_weights(ws, ws.nbytes)
+    try:
+        assert gh.device_ptr(W) is not None
+        x = outlier_acts(rng, (k,))
+        q = np.empty(k, np.int8)
+        s = np.zeros(1, np.float32)
+        assert lib.gemma_hip_quantize_act_host(q.ctypes.data, s.ctypes.data, x.ctypes.data, k) == 0
+        qo, so = oracle.quantize_act(x)
+        assert np.array_equal(q, qo) and bits(s)[0] == bits(so)
+        # gemv on the rows of head 2 only: an interior pointer
+        y = np.empty(hdim, np.float32)
+        rc = lib.gemma_hip_gemv_int8_host(y.ctypes.data, W[2 * hdim:].ctypes.data,
+                                          ws[2 * hdim:].ctypes.data, q.ctypes.data,
+                                          ctypes.c_float(s[0]), hdim, k)
+        assert rc == 0, lib.gemma_hip_last_error()
+        yo, _ = oracle.gemv_int8(W[2 * hdim:3 * hdim], ws[2 * hdim:3 * hdim], qo, so)
+        assert np.array_equal(bits(y), bits(yo))
+        # gemm with a padded output stride; the gap keeps its contents
+        m = 19
+        A = outlier_acts(rng, (m, k))
+        Aq = np.empty((m, k), np.int8)
+        As = np.empty(m, np.float32)
+        assert lib.gemma_hip_quantize_acts_host(Aq.ctypes.data, As.ctypes.data, A.ctypes.data,
+                                                0, m, k) == 0
+        dst = np.full((m, heads * hdim + 5), -3.0, np.float32)
+        rc = lib.gemma_hip_gemm_int8_host(dst.ctypes.data, dst.shape[1], W.ctypes.data, 0,
+                                          ws.ctypes.data, Aq.ctypes.data, 0, As.ctypes.data,
+                                          m, heads * hdim, k)
+        assert rc == 0, lib.gemma_hip_last_error()
+        ref = np.full_like(dst, -3.0)
+        ref, _ = oracle.gemm_int8(W, ws, Aq, As, dst=ref)
+        assert np.array_equal(bits(dst), bits(ref))
+        # an unregistered weight pointer is an error, not a CPU fallback
+        stray = np.zeros_like(W)
+        rc = lib.gemma_hip_gemv_int8_host(y.ctypes.data, stray.ctypes.data, ws.ctypes.data,
+                                          q.ctypes.data, ctypes.c_float(1.0), 8, k)
+        assert rc == 1 and b"not registered" in lib.gemma_hip_last_error()
+    finally:
+        gh.release_weights(W)
+        gh.release_weights(ws)
+
+
+def test_host_fp32_entry_points(gh, oracle):
+    lib = gh.lib
+    rng = np.random.default_rng(22)
+    n, k, m = 96, 588, 9
+    W = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    gh.register_weights(W, W.nbytes)
+    try:
+        x = outlier_acts(rng, (k,))
+        y = np.empty(n, np.float32)
+        assert lib.gemma_hip_gemv_fpx_host(y.ctypes.data, W.ctypes.data, x.ctypes.data, n, k) == 0
+        check_f32(y[None, :], W, x[None, :], oracle)
+        A = outlier_acts(rng, (m, k))
+        d = np.empty((m, n), np.float32)
+        assert lib.gemma_hip_gemm_fpx_host(d.ctypes.data, 0, W.ctypes.data, 0, A.ctypes.data,
+                                           0, m, n, k) == 0
+        check_f32(d, W, A, oracle)
+    finally:
+        gh.release_weights(W)
+
+
+def test_argument_errors(gh):
+    import gemma_hip
+
+    with pytest.raises(gemma_hip.GemmaHipError, match="njobs"):
+        gh.matmul_multi([], 0, 0, 64)
+    with pytest.raises(gemma_hip.GemmaHipError, match="stride"):
+        gh.matmul(1, 4, 1, 8, 1, 1, 16, 1, 2, 8, 16)
+    with pytest.raises(gemma_hip.GemmaHipError, match="k="):
+        gh.quantize_matmul([(1, 1, 1, 4)], 1, 70000)
