@@ -1,0 +1,461 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 matmul hot path on one MI355X.
+
+Headline (BASELINE.json metric "int8 GEMV HBM GB/s + GEMM TOPS (% roofline);
+decode tok/s at gemma-3-1b shape", workload = BASELINE config 2):
+
+  step  = one pass over the gemma-3-1b decode GEMVs q, k, v, o, gate, up,
+          down and the tied LM head at M = 1, each with fp32 activations
+          quantized inside the GEMV kernel (gemma_hip_quantize_matmul), as
+          the reference's decode call sites do (gemma.c:4768-4966).
+  value = algorithmic HBM bytes of a step x steps / elapsed, in GB/s.
+
+Weights are int8 uniform in [-127, 127], scales U(1e-3, 1e-2), x ~ N(0,1)
+with 1% of channels x20.  Weight copies rotate so that every launch reads
+its matrix from HBM, not from the 256 MB Infinity Cache (see rotate_copies).
+Steps are replayed from a HIP graph (one graph = ROT_STEPS steps) so the
+timed region measures the GPU, not Python's launch overhead.
+
+The JSON line also carries, measured in the same run:
+  roofline      the dominant kernel (the LM-head GEMV launch): algorithmic
+                bytes / its average launch duration (HIP events on its stream)
+  per_gemv      the same for every sweep shape
+  gemm          int8 MFMA GEMM TOPS at the gemma-3-4b prefill shapes (M=2048)
+                and the SigLIP tower shapes (M=4096), % of the 5.0 POPS peak
+  decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
+                decode token (26 layers x {qkv, o, gate/up, down} + LM head)
+  cpu_baseline  the reference's own quantize_act + gemv_int8, compiled from
+                its source (oracle/_ref/gemma_ref_clang), on the host cores
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "gemma.c_amd")
+for _p in (REPO, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
+ROTATE_BYTES = 512 << 20   # > 2x the 256 MB Infinity Cache
+ROT_STEPS = 8              # steps per captured graph
+
+METRIC = ("int8 GEMV HBM GB/s + GEMM TOPS (% roofline); decode tok/s at "
+          "gemma-3-1b shape")
+
+# gemma-3-1b decode GEMVs: (name, out rows N, reduction K)
+SWEEP_1B = [("q", 1024, 1152), ("k", 256, 1152), ("v", 256, 1152), ("o", 1152, 1024),
+            ("gate", 6912, 1152), ("up", 6912, 1152), ("down", 1152, 6912),
+            ("lm_head", 262144, 1152)]
+
+# gemma-3-4b prefill (M = 2048) and SigLIP (M = 4096) GEMMs: (name, M, N, K)
+GEMM_SHAPES = [("4b_q", 2048, 2048, 2560), ("4b_kv", 2048, 1024, 2560),
+               ("4b_o", 2048, 2560, 2048), ("4b_gate_up", 2048, 10240, 2560),
+               ("4b_down", 2048, 2560, 10240),
+               ("siglip_qkvo", 4096, 1152, 1152), ("siglip_fc1", 4096, 4304, 1152),
+               ("siglip_fc2", 4096, 1152, 4304)]
+# per transformer layer, how often each 4b / SigLIP shape occurs
+GEMM_COUNTS = {"4b_q": 1, "4b_kv": 2, "4b_o": 1, "4b_gate_up": 2, "4b_down": 1,
+               "siglip_qkvo": 4, "siglip_fc1": 1, "siglip_fc2": 1}
+
+# gemma-3-1b: hidden 1152, FFN 6912, 26 layers, 4 q heads / 1 kv head, hd 256
+DEC_1B = dict(dim=1152, mlp=6912, layers=26, q=1024, kv=256, vocab=262144)
+
+
+def gemv_bytes(n: int, k: int) -> int:
+    """Algorithmic HBM bytes of one fused quantize+GEMV: int8 W [n][k], fp32
+    row scales [n], fp32 x [k], fp32 y [n]."""
+    return n * k + 4 * n + 4 * k + 4 * n
+
+
+def gemm_ops(m: int, n: int, k: int) -> int:
+    return 2 * m * n * k
+
+
+def rotate_copies(wbytes: int) -> int:
+    """Distinct weight copies per shape: ceil(512 MB / W), capped at the
+    graph's ROT_STEPS.  Within a graph, a copy is reused only after every
+    other shape of ROT_STEPS steps (>= 8 x 330 MB) has been streamed, far
+    beyond the 256 MB Infinity Cache."""
+    return max(1, min(ROT_STEPS, math.ceil(ROTATE_BYTES / wbytes)))
+
+
+def outlier_acts(torch, shape, gen):
+    x = torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32)
+    cols = torch.rand(shape[-1], generator=gen, device="cuda") < 0.01
+    x[..., cols] *= 20.0
+    return x
+
+
+def rand_i8(torch, shape, gen):
+    return torch.randint(-127, 128, shape, generator=gen, device="cuda", dtype=torch.int8)
+
+
+def rand_scales(torch, n, gen):
+    return torch.rand(n, generator=gen, device="cuda") * 9e-3 + 1e-3
+
+
+class Timer:
+    """HIP-event timing on torch's current stream (the stream every launch
+    below is enqueued on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def elapsed_ms(self, fn, busy=None) -> float:
+        torch = self.torch
+        if busy is not None:
+            busy()  # keep the GPU busy so the host enqueues fn ahead of it
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        fn()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end)
+
+
+def capture(torch, fn):
+    """Capture fn(stream_handle) into a HIP graph (after one eager run)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return graph
+
+
+def build_sweep(torch, gh, gen):
+    shapes = []
+    for name, n, k in SWEEP_1B:
+        copies = rotate_copies(n * k)
+        ws = [rand_i8(torch, (n, k), gen) for _ in range(copies)]
+        ss = [rand_scales(torch, n, gen) for _ in range(copies)]
+        x = outlier_acts(torch, (k,), gen)
+        y = torch.empty(n, device="cuda", dtype=torch.float32)
+        jobs = [gh.jobs([(w, s, y, n)]) for w, s in zip(ws, ss)]
+        shapes.append(dict(name=name, n=n, k=k, copies=copies, w=ws, s=ss, x=x, y=y,
+                           jobs=jobs, bytes=gemv_bytes(n, k)))
+    return shapes
+
+
+def launch_gemv(gh, sh, copy, stream):
+    arr, nj = sh["jobs"][copy % sh["copies"]]
+    rc = gh.lib.gemma_hip_quantize_matmul(arr, nj, sh["x"].data_ptr(), sh["k"], None, None,
+                                          stream)
+    if rc != 0:
+        raise RuntimeError(gh.lib.gemma_hip_last_error().decode())
+
+
+def sweep_graph(torch, gh, shapes):
+    def steps(stream):
+        for step in range(ROT_STEPS):
+            for sh in shapes:
+                launch_gemv(gh, sh, step, stream)
+    return capture(torch, steps)
+
+
+def per_gemv(torch, gh, shapes, timer, busy, reps):
+    """Average launch duration of each sweep shape: `reps` back-to-back
+    launches over distinct, cold weight copies (after a busy prefix that also
+    evicts the caches), timed with HIP events."""
+    out = {}
+    stream = torch.cuda.current_stream().cuda_stream
+    for sh in shapes:
+        launches = min(reps, max(sh["copies"], 4))
+
+        def run():
+            for i in range(launches):
+                launch_gemv(gh, sh, i, stream)
+
+        run()
+        best = min(timer.elapsed_ms(run, busy) for _ in range(3)) / launches
+        out[sh["name"]] = dict(n=sh["n"], k=sh["k"], us=round(best * 1e3, 3),
+                               gbs=round(sh["bytes"] / (best * 1e-3) / 1e9, 1),
+                               copies=sh["copies"])
+    return out
+
+
+def bench_gemm(torch, gh, gen, timer, reps):
+    out = {}
+    stream = torch.cuda.current_stream().cuda_stream
+    for name, m, n, k in GEMM_SHAPES:
+        a = rand_i8(torch, (m, k), gen)
+        asc = rand_scales(torch, m, gen)
+        b = rand_i8(torch, (n, k), gen)
+        bsc = rand_scales(torch, n, gen)
+        d = torch.empty((m, n), device="cuda", dtype=torch.float32)
+
+        def run():
+            for _ in range(reps):
+                gh.matmul(d, n, b, k, bsc, a, k, asc, m, n, k, stream)
+
+        run()
+        ms = min(timer.elapsed_ms(run) for _ in range(3)) / reps
+        tops = gemm_ops(m, n, k) / (ms * 1e-3) / 1e12
+        out[name] = dict(m=m, n=n, k=k, us=round(ms * 1e3, 2), tops=round(tops, 1),
+                         frac=round(tops / INT8_PEAK_TOPS, 4))
+        del a, b, d
+    groups = {}
+    for prefix in ("4b", "siglip"):
+        ops = sum(gemm_ops(v["m"], v["n"], v["k"]) * GEMM_COUNTS[kk]
+                  for kk, v in out.items() if kk.startswith(prefix))
+        us = sum(v["us"] * GEMM_COUNTS[kk] for kk, v in out.items() if kk.startswith(prefix))
+        tops = ops / (us * 1e-6) / 1e12
+        groups[prefix + "_layer"] = dict(tops=round(tops, 1), frac=round(tops / INT8_PEAK_TOPS, 4))
+    return dict(peak_tops=INT8_PEAK_TOPS, shapes=out, **groups)
+
+
+def bench_decode_1b(torch, gh, gen, timer, tokens):
+    """The W8A8 matmul path of one gemma-3-1b decode token, device-resident:
+    per layer quantize+{q,k,v} (one launch), quantize+o, quantize+{gate,up}
+    (one launch), quantize+down; then quantize+LM head."""
+    c = DEC_1B
+    x_dim = outlier_acts(torch, (c["dim"],), gen)
+    x_q = outlier_acts(torch, (c["q"],), gen)
+    x_mlp = outlier_acts(torch, (c["mlp"],), gen)
+    bufs = {n: torch.empty(sz, device="cuda") for n, sz in
+            (("q", c["q"]), ("k", c["kv"]), ("v", c["kv"]), ("o", c["dim"]),
+             ("g", c["mlp"]), ("u", c["mlp"]), ("d", c["dim"]), ("logits", c["vocab"]))}
+    layers = []
+    total_bytes = 0
+    for _ in range(c["layers"]):
+        w = {}
+        for name, n, k in (("q", c["q"], c["dim"]), ("k", c["kv"], c["dim"]),
+                           ("v", c["kv"], c["dim"]), ("o", c["dim"], c["q"]),
+                           ("g", c["mlp"], c["dim"]), ("u", c["mlp"], c["dim"]),
+                           ("d", c["dim"], c["mlp"])):
+            w[name] = (rand_i8(torch, (n, k), gen), rand_scales(torch, n, gen), n)
+        qkv = gh.jobs([(w[t][0], w[t][1], bufs[t], w[t][2]) for t in "qkv"])
+        o = gh.jobs([(w["o"][0], w["o"][1], bufs["o"], w["o"][2])])
+        gu = gh.jobs([(w[t][0], w[t][1], bufs[t], w[t][2]) for t in "gu"])
+        d = gh.jobs([(w["d"][0], w["d"][1], bufs["d"], w["d"][2])])
+        layers.append((w, [(qkv, x_dim, c["dim"]), (o, x_q, c["q"]), (gu, x_dim, c["dim"]),
+                           (d, x_mlp, c["mlp"])]))
+        total_bytes += (gemv_bytes(c["q"] + 2 * c["kv"], c["dim"])
+                        + gemv_bytes(c["dim"], c["q"])
+                        + gemv_bytes(2 * c["mlp"], c["dim"])
+                        + gemv_bytes(c["dim"], c["mlp"]))
+    emb = rand_i8(torch, (c["vocab"], c["dim"]), gen)
+    emb_s = rand_scales(torch, c["vocab"], gen)
+    head = gh.jobs([(emb, emb_s, bufs["logits"], c["vocab"])])
+    total_bytes += gemv_bytes(c["vocab"], c["dim"])
+
+    def token(stream):
+        for _, calls in layers:
+            for (arr, nj), x, k in calls:
+                rc = gh.lib.gemma_hip_quantize_matmul(arr, nj, x.data_ptr(), k, None, None,
+                                                      stream)
+                if rc != 0:
+                    raise RuntimeError(gh.lib.gemma_hip_last_error().decode())
+        rc = gh.lib.gemma_hip_quantize_matmul(head[0], head[1], x_dim.data_ptr(), c["dim"],
+                                              None, None, stream)
+        if rc != 0:
+            raise RuntimeError(gh.lib.gemma_hip_last_error().decode())
+
+    graph = capture(torch, token)
+    for _ in range(5):
+        graph.replay()
+
+    def run():
+        for _ in range(tokens):
+            graph.replay()
+
+    ms = min(timer.elapsed_ms(run) for _ in range(3)) / tokens
+    return dict(tok_s=round(1e3 / ms, 1), ms_per_token=round(ms, 4),
+                bytes_per_token=total_bytes,
+                gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
+                launches_per_token=4 * c["layers"] + 1,
+                what="W8A8 matmul path of one decode token (fused quantize+GEMV launches, "
+                     "HIP graph); attention/norms/RoPE are outside this path")
+
+
+def measured_traffic(kernel: str) -> dict | None:
+    """HBM bytes per launch of the LM-head GEMV from the committed rocprofv3
+    --pmc measurement (FETCH_SIZE and WRITE_SIZE, each scaled by what the
+    counter reads for a copy of known size)."""
+    path = os.path.join(REPO, "profiles", "gemv_i8_lm_head_1b.hbm_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return d if d.get("kernel") == kernel else None
+
+
+def cpu_baseline(threads: int, seconds_per_shape: float) -> dict | None:
+    """The reference's own quantize_act + gemv_int8 (compiled from
+    /root/reference/gemma.c by oracle/Makefile; AVX2 clang build) over the
+    same sweep shapes and rotation, on `threads` host cores."""
+    from oracle.oracle import RefHarness
+
+    if not RefHarness.available("clang"):
+        return None
+    ref = RefHarness("clang")
+    total_bytes, total_s, parts = 0, 0.0, {}
+    for name, n, k in SWEEP_1B:
+        copies = max(2, math.ceil(ROTATE_BYTES / (n * k)))
+        est = gemv_bytes(n, k) / 30e9  # rough per-call time, sizes the sample
+        calls = max(4, int(seconds_per_shape / est))
+        r = ref.bench(["gemv_int8", n, k, copies, calls], threads)
+        per_call = r["seconds"] / r["calls"]
+        parts[name] = round(gemv_bytes(n, k) / per_call / 1e9, 2)
+        total_bytes += gemv_bytes(n, k)
+        total_s += per_call
+    return dict(value=round(total_bytes / total_s / 1e9, 2), unit="GB/s", cores=threads,
+                kind="reference",
+                sample=(f"reference quantize_act+gemv_int8 (gemma.c:2590, 2770) built by clang "
+                        f"-O3 -ffast-math -march=x86-64-v3 -fopenmp, {threads} OpenMP threads, "
+                        f"same 8 shapes, >=512 MB weight rotation, ~{seconds_per_shape:.1f} s "
+                        f"per shape"),
+                per_gemv_gbs=parts)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=2.0,
+                    help="CPU-baseline sample time per sweep shape")
+    ap.add_argument("--only", choices=["sweep", "lm_head"], default=None,
+                    help="profiling aid: run just the timed sweep or the LM-head timing")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="profiling aid: 3 dispatches of an elementwise kernel that reads "
+                         "and writes exactly 1 GiB (calibrates FETCH_SIZE / WRITE_SIZE)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print("bench.py: this build targets one GPU; the W8A8 matmul path has no "
+              "multi-GPU part (collectives and sharding are design-only), so --gpus "
+              f"{args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import gemma_hip
+
+    if args.copy_probe:
+        src = torch.ones(1 << 30, dtype=torch.int8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        print("copy probe: 3 x neg over 1 GiB int8", flush=True)
+        return 0
+
+    gh = gemma_hip.GemmaHip(0)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1234)
+    timer = Timer(torch)
+    shapes = build_sweep(torch, gh, gen)
+    step_bytes = sum(sh["bytes"] for sh in shapes)
+    lm = shapes[-1]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def busy():
+        for i in range(8):
+            launch_gemv(gh, lm, i, stream)
+
+    if args.only == "lm_head":
+        per = per_gemv(torch, gh, [lm], timer, busy, reps=8)
+        print(json.dumps(per), flush=True)
+        return 0
+
+    graph = sweep_graph(torch, gh, shapes)
+    replays_w = max(1, math.ceil(args.warmup / ROT_STEPS))
+    replays = max(1, math.ceil(args.steps / ROT_STEPS))
+    steps = replays * ROT_STEPS
+    for _ in range(replays_w):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end)
+    value = step_bytes * steps / (ms * 1e-3) / 1e9
+    print(f"# sweep: {steps} steps in {ms:.2f} ms -> {value:.1f} GB/s", file=sys.stderr,
+          flush=True)
+    if args.only == "sweep":
+        return 0
+
+    per = per_gemv(torch, gh, shapes, timer, busy, reps=64)
+    print(f"# per-gemv: {json.dumps(per)}", file=sys.stderr, flush=True)
+    gemm = bench_gemm(torch, gh, gen, timer, reps=10)
+    print(f"# gemm: {json.dumps(gemm)}", file=sys.stderr, flush=True)
+    dec = bench_decode_1b(torch, gh, gen, timer, tokens=50)
+    print(f"# decode_1b: {json.dumps(dec)}", file=sys.stderr, flush=True)
+
+    lm_us = per["lm_head"]["us"]
+    traffic = measured_traffic("gemv_i8_kernel<8, true, true>")
+    achieved = lm["bytes"] / (lm_us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(threads, args.cpu_seconds)
+        print(f"# cpu_baseline: {json.dumps(cpu)}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": replays_w * ROT_STEPS,
+        "ms_per_step": round(ms / steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 2: W8A8 GEMV sweep at gemma-3-1b shapes, M=1 "
+                        "(q 1152->1024, k/v 1152->256, o 1024->1152, gate/up 1152->6912, "
+                        "down 6912->1152, LM head 1152->262144), fp32 activations quantized "
+                        "in-kernel, weights rotated through >256 MB of copies",
+            "step_bytes": step_bytes,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "gemv_i8_kernel<8,fused> (LM head launch, 262144x1152)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "avg_launch_us": lm_us,
+            "bytes_per_launch": lm["bytes"],
+            "traffic": traffic["traffic_bytes"] if traffic else None,
+            "traffic_source": ("profiles/gemv_i8_lm_head_1b.hbm_traffic.json (rocprofv3 --pmc "
+                               "FETCH_SIZE x%.3f + WRITE_SIZE x%.3f)"
+                               % (traffic["fetch_scale"], traffic["write_scale"])
+                               if traffic else None),
+        },
+        "per_gemv": per,
+        "gemm": gemm,
+        "decode_1b": dec,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    gh.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -61,9 +61,9 @@ struct State {
 
 State g;
 
-hipStream_t pick_stream(void *stream) {
-  return stream != nullptr ? static_cast<hipStream_t>(stream) : g.stream;
-}
+// NULL is HIP's default (null) stream, so work on it is ordered with the
+// caller's own default-stream copies.
+hipStream_t pick_stream(void *stream) { return static_cast<hipStream_t>(stream); }
 
 int need_init() {
   if (!g.ready) return fail("gemma_hip: library not initialised (call gemma_hip_init)");
@@ -410,7 +410,7 @@ int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,
   GH_CHECK("quantize_act_host: H2D",
            hipMemcpyAsync(base + o_src, vec, (size_t)dim * 4, hipMemcpyHostToDevice, g.stream));
   if (gemma_hip_quantize((int8_t *)(base + o_q), (float *)(base + o_s),
-                         (const float *)(base + o_src), dim, 1, dim, nullptr))
+                         (const float *)(base + o_src), dim, 1, dim, g.stream))
     return 1;
   GH_CHECK("quantize_act_host: D2H",
            hipMemcpyAsync(dst, base + o_q, dim, hipMemcpyDeviceToHost, g.stream));
@@ -436,7 +436,7 @@ int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
   GH_CHECK("quantize_acts_host: H2D",
            hipMemcpyAsync(base + o_src, src, in_floats * 4, hipMemcpyHostToDevice, g.stream));
   if (gemma_hip_quantize((int8_t *)(base + o_q), (float *)(base + o_s),
-                         (const float *)(base + o_src), sstr, m, n, nullptr))
+                         (const float *)(base + o_src), sstr, m, n, g.stream))
     return 1;
   GH_CHECK("quantize_acts_host: D2H",
            hipMemcpyAsync(dst, base + o_q, (size_t)m * n, hipMemcpyDeviceToHost, g.stream));
@@ -479,7 +479,7 @@ int gemma_hip_gemv_int8_multi_host(const gemma_hip_job *jobs, int njobs,
   GH_CHECK("gemv_int8_host: H2D",
            hipMemcpyAsync(base + o_s, &vsc, 4, hipMemcpyHostToDevice, g.stream));
   if (gemma_hip_matmul_multi(djobs, njobs, (const int8_t *)(base + o_x),
-                             (const float *)(base + o_s), n, nullptr))
+                             (const float *)(base + o_s), n, g.stream))
     return 1;
   for (int j = 0; j < njobs; ++j)
     if (jobs[j].m > 0)
@@ -518,7 +518,7 @@ int gemma_hip_gemm_int8_host(float *dst, int dstr, const int8_t *mat, int mstr,
            hipMemcpyAsync(base + o_as, ssc, (size_t)m * 4, hipMemcpyHostToDevice, g.stream));
   if (gemma_hip_matmul((float *)(base + o_y), dstr, (const int8_t *)dmat, mstr,
                        (const float *)dsc, (const int8_t *)(base + o_a), sstr,
-                       (const float *)(base + o_as), m, n, k, nullptr))
+                       (const float *)(base + o_as), m, n, k, g.stream))
     return 1;
   GH_CHECK("gemm_int8_host: D2H",
            hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,
@@ -556,7 +556,7 @@ int gemma_hip_gemv_fpx_multi_host(const gemma_hip_job *jobs, int njobs,
   }
   GH_CHECK("gemv_fpx_host: H2D",
            hipMemcpyAsync(base + o_x, vec, (size_t)n * 4, hipMemcpyHostToDevice, g.stream));
-  if (gemma_hip_matmul_f32_multi(djobs, njobs, (const float *)(base + o_x), n, nullptr))
+  if (gemma_hip_matmul_f32_multi(djobs, njobs, (const float *)(base + o_x), n, g.stream))
     return 1;
   for (int j = 0; j < njobs; ++j)
     if (jobs[j].m > 0)
@@ -587,7 +587,7 @@ int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
   GH_CHECK("gemm_fpx_host: H2D",
            hipMemcpyAsync(base + o_a, src, src_floats * 4, hipMemcpyHostToDevice, g.stream));
   if (gemma_hip_matmul_f32((float *)(base + o_y), dstr, (const float *)dmat, mstr,
-                           (const float *)(base + o_a), sstr, m, n, k, nullptr))
+                           (const float *)(base + o_a), sstr, m, n, k, g.stream))
     return 1;
   GH_CHECK("gemm_fpx_host: D2H",
            hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,

@@ -30,8 +30,8 @@
  *  - "n" of gemv_* is the reference's m (output rows) and "k" its n
  *    (reduction length): the names here follow the GEMM contract.
  *  - Entry points without the _host suffix take DEVICE pointers (HBM) and
- *    enqueue their work on `stream` (a hipStream_t; NULL selects the
- *    library's own stream) without synchronising.
+ *    enqueue their work on `stream` (a hipStream_t; NULL is HIP's default
+ *    stream) without synchronising.
  *  - Entry points with the _host suffix take the reference call sites' host
  *    buffers for activations and outputs, resolve weight pointers through the
  *    registry below, and return after the result is back in host memory.
@@ -75,8 +75,8 @@ void gemma_hip_shutdown(void);
 /* Message of the last failure on this thread (gemma.c:577-587 get_error). */
 const char *gemma_hip_last_error(void);
 
-/* Block until all work the library enqueued on `stream` (NULL: its own
- * stream) has finished. */
+/* Block until all work enqueued on `stream` (NULL: HIP's default stream)
+ * has finished. */
 int gemma_hip_sync(void *stream);
 
 /* ---- weights: uploaded once, addressed by their host pointers ---------- */
