@@ -3,22 +3,31 @@
 //
 //   dst[i][j] = (float)sum_l src[i][l]*mat[j][l] * (ssc[i]*matsc[j])
 //
-// Both operands are K-contiguous ("NT"), which is the layout MFMA wants: a
-// lane feeds 16 consecutive int8 of one row to v_mfma_i32_32x32x32_i8.
-// Workgroup: 256 threads = 4 waves in a 2x2 grid, block tile 128x128, K step
-// 64 bytes, LDS double-buffered (one barrier per K step; the next step's
-// global loads are in registers while the current step's MFMAs run).  Each
-// wave owns a 64x64 sub-tile = 2x2 MFMA tiles of 32x32 with int32
-// accumulators, so the sum is exact whatever order the hardware adds in.
-// The epilogue fuses the reference's dequant flush (gemma.c:3854-3865): each
-// accumulator is rescaled with the row and column scales and stored fp32.
-//
-// Operand layout: a lane supplies row (lane % 32) of its 32-row tile and the
-// 16-byte K chunk (lane / 32) of each 32-byte K sub-step, for A and B alike.
-// The A and B k-index maps therefore coincide, and an exact int32 dot product
+// Both operands are K-contiguous ("NT"), the layout MFMA wants: a lane feeds
+// 16 consecutive int8 of one row to v_mfma_i32_32x32x32_i8.  A workgroup is
+// 256 threads = 4 waves in a 2x2 grid; each wave owns WM x WN tiles of 32x32
+// with int32 accumulators, so the sum is exact whatever order the hardware
+// adds in.  Operand layout: a lane supplies row (lane % 32) of its 32-row
+// tile and the 16-byte K chunk (lane / 32) of each 32-byte K sub-step, for A
+// and B alike; the A and B k-index maps coincide, so the exact dot product
 // does not depend on which k the hardware pairs inside one instruction.
 // Output layout (32x32 MFMA): accumulator r of lane l holds row
 // 8*(r/4) + 4*(l/32) + r%4, column l%32.
+//
+// Kernels:
+//  - gemm_i8_dma_kernel (default): operands go global -> LDS by
+//    buffer_load ... lds into an S-stage ring (no VGPRs held, zero fill by
+//    out-of-range offsets), XOR-swizzled so fragment reads are bank-conflict
+//    free; one barrier per K stage.  The epilogue (store_tile) fuses the
+//    reference's dequant flush (gemma.c:3854-3865) with scales loaded at
+//    kernel start and buffer stores whose out-of-range cells are dropped.
+//  - gemm_i8_kernel: register-staged loads into a padded LDS double buffer;
+//    used when an operand is too large for 32-bit buffer offsets.
+//  - gemm_i8_generic_kernel: one thread per output, any shape/alignment.
+// Tile choice and the measurements behind it are in launch_gemm_i8.
+#include <cstdio>
+#include <cstdlib>
+
 #include "gh_arith.h"
 #include "gh_kernels.h"
 
@@ -26,45 +35,73 @@ namespace gh {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBM = 128;
-constexpr int kBN = 128;
 constexpr int kBK = 64;                   // bytes of K per step
 constexpr int kRowChunks = kBK / 16 + 1;  // 16-byte chunks per LDS row (+1 pad)
+constexpr int kXcds = 8;                  // MI355X: 8 XCDs, each with its own L2
+constexpr int kGroupM = 8;                // M tiles per group of the tile order
+constexpr uint32_t kOob = 0x80000000u;    // buffer offset: reads zero, drops stores
 
-// VEC-free requirement: k % 16 == 0 and every row 16-byte aligned (checked
-// by the launcher); rows/columns beyond m/n and K beyond k load as zeros.
-template <bool HEADS>
+// Block -> tile.  The dispatcher hands workgroup b to XCD b % 8, so first
+// give each XCD a contiguous range of tile ids, then walk tiles in groups of
+// kGroupM row-tiles so neighbouring workgroups of one XCD share A rows and B
+// columns in that XCD's L2.
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n,
+                                        int *tm, int *tn) {
+  const int total = tiles_m * tiles_n;
+  const int per = total / kXcds, extra = total % kXcds;
+  const int xcd = b % kXcds, idx = b / kXcds;
+  const int t = xcd * per + (xcd < extra ? xcd : extra) + idx;
+  const int per_group = kGroupM * tiles_n;
+  const int group = t / per_group;
+  const int first_m = group * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int in_group = t - group * per_group;
+  *tm = first_m + in_group % gsize;
+  *tn = in_group / gsize;
+}
+
+// Requirement (checked by the launcher): k % 16 == 0 and every row 16-byte
+// aligned; rows/columns beyond m/n and K beyond k load as zeros.
+// WM x WN: each wave's sub-tile in 32x32 MFMA tiles; waves form a 2x2 grid,
+// so the block tile is (64*WM) x (64*WN).
+template <int WM, int WN, bool HEADS>
 __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(
     float *__restrict__ dst, int dstr, int hdim, const int8_t *__restrict__ mat,
     int mstr, const float *__restrict__ matsc, const int8_t *__restrict__ src,
     int sstr, const float *__restrict__ ssc, int m, int n, int k) {
+  constexpr int kBM = 64 * WM;
+  constexpr int kBN = 64 * WN;
   __shared__ v4i lds_a[2][kBM][kRowChunks];
   __shared__ v4i lds_b[2][kBN][kRowChunks];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1;  // wave's 64-row half of the block tile
-  const int wn = wave & 1;   // wave's 64-column half
-  const int m0 = blockIdx.y * kBM;
-  const int n0 = blockIdx.x * kBN;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int wm = wave >> 1;  // wave's row half of the block tile
+  const int wn = wave & 1;   // wave's column half
+  int tm, tn;
+  tile_of(blockIdx.x, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, &tm, &tn);
+  const int m0 = tm * kBM;
+  const int n0 = tn * kBN;
 
   // global -> register mapping: thread loads chunk (tid % 4) of rows
-  // tid/4 and 64 + tid/4 of both the A and the B tile
+  // tid/4 + 64*h of the A and the B tile
   const int ld_row = tid >> 2;
   const int ld_chunk = tid & 3;
 
-  v4i ra[2], rb[2];
+  v4i ra[WM], rb[WN];
   auto load_tiles = [&](int kt) {
     const int kb = kt * kBK + ld_chunk * 16;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = ld_row + 64 * h;
-      const int gm = m0 + r;
-      const int gn = n0 + r;
+    for (int h = 0; h < WM; ++h) {
+      const int gm = m0 + ld_row + 64 * h;
       ra[h] = (gm < m && kb < k)
                   ? *reinterpret_cast<const v4i *>(src + (size_t)gm * sstr + kb)
                   : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int h = 0; h < WN; ++h) {
+      const int gn = n0 + ld_row + 64 * h;
       rb[h] = (gn < n && kb < k)
                   ? *reinterpret_cast<const v4i *>(mat + (size_t)gn * mstr + kb)
                   : v4i{0, 0, 0, 0};
@@ -72,17 +109,16 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(
   };
   auto store_tiles = [&](int buf) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      lds_a[buf][ld_row + 64 * h][ld_chunk] = ra[h];
-      lds_b[buf][ld_row + 64 * h][ld_chunk] = rb[h];
-    }
+    for (int h = 0; h < WM; ++h) lds_a[buf][ld_row + 64 * h][ld_chunk] = ra[h];
+#pragma unroll
+    for (int h = 0; h < WN; ++h) lds_b[buf][ld_row + 64 * h][ld_chunk] = rb[h];
   };
 
-  v16i acc[2][2];
+  v16i acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+    for (int j = 0; j < WN; ++j) acc[i][j] = v16i{};
 
   const int nk = (k + kBK - 1) / kBK;
   load_tiles(0);
@@ -96,17 +132,17 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(
     if (kt + 1 < nk) load_tiles(kt + 1);
 #pragma unroll
     for (int ks = 0; ks < kBK / 32; ++ks) {
-      v4i a[2], b[2];
+      v4i a[WM], b[WN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = lds_a[cur][wm * 64 + i * 32 + frag_row][ks * 2 + frag_chunk];
+      for (int i = 0; i < WM; ++i)
+        a[i] = lds_a[cur][wm * 32 * WM + i * 32 + frag_row][ks * 2 + frag_chunk];
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = lds_b[cur][wn * 64 + j * 32 + frag_row][ks * 2 + frag_chunk];
+      for (int j = 0; j < WN; ++j)
+        b[j] = lds_b[cur][wn * 32 * WN + j * 32 + frag_row][ks * 2 + frag_chunk];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j],
                                                             acc[i][j], 0, 0, 0);
     }
@@ -116,8 +152,8 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(
 
   // epilogue: rescale and store (gemma.c:3854-3865)
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+  for (int j = 0; j < WN; ++j) {
+    const int col = n0 + wn * 32 * WN + j * 32 + (lane & 31);
     if (col >= n) continue;
     const float wsc = matsc[col];
     float *out_col;
@@ -130,16 +166,276 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_kernel(
       row_stride = dstr;
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < WM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row =
-            m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int row = m0 + wm * 32 * WM + i * 32 + 8 * (r >> 2) +
+                        4 * (lane >> 5) + (r & 3);
         if (row < m)
           out_col[(size_t)row * row_stride] = rescale(acc[i][j][r], ssc[row], wsc);
       }
     }
   }
+}
+
+// ---- epilogue shared by the DMA kernels -----------------------------------
+//
+// Scales are loaded at kernel start (their latency, including address
+// translation, hides under the K loop).  Whether the plain IEEE rescale is
+// exact for every output of the wave is decided once from the scales'
+// extremes; row-major outputs then go out as buffer stores whose row offset
+// is a uniform soffset and whose out-of-range rows/columns the hardware
+// drops, so the common path is cvt + 2 multiplies + 1 store per output.
+template <int WM, int WN>
+struct TileScales {
+  float act[WM][16];
+  float w[WN];
+};
+
+template <int WM, int WN>
+__device__ __forceinline__ void load_tile_scales(TileScales<WM, WN> &sc,
+                                                 const float *__restrict__ ssc,
+                                                 const float *__restrict__ matsc,
+                                                 int m, int n, int m0, int n0,
+                                                 int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < WN; ++j)
+    sc.w[j] = matsc[min(n0 + wn * 32 * WN + j * 32 + (lane & 31), n - 1)];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      sc.act[i][r] = ssc[min(m0 + wm * 32 * WM + i * 32 + 8 * (r >> 2) +
+                                 4 * (lane >> 5) + (r & 3), m - 1)];
+}
+
+template <int WM, int WN, bool HEADS>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[WM][WN],
+                                           const TileScales<WM, WN> &sc,
+                                           float *__restrict__ dst, int dstr,
+                                           int hdim, int m, int n, int m0,
+                                           int n0, int wm, int wn, int lane) {
+  float amin = __builtin_inff(), wmin = __builtin_inff();
+  bool asub = false, wsub = false;
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) scale_extremes(sc.act[i][r], &amin, &asub);
+#pragma unroll
+  for (int j = 0; j < WN; ++j) scale_extremes(sc.w[j], &wmin, &wsub);
+  const bool plain_lane = rescale_all_plain(amin, asub, wmin, wsub);
+  const bool all_plain = __builtin_amdgcn_readfirstlane(__any(!plain_lane) ? 0 : 1) != 0;
+
+  if (!HEADS && all_plain) {
+    // bytes of dst covered by valid cells: any offset at or past it is dropped
+    const uint32_t extent = ((uint32_t)(m - 1) * (uint32_t)dstr + (uint32_t)n) * 4u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        dst, (short)0, (int)extent, 0x00020000);
+    const int row_lane = 4 * (lane >> 5);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int col = n0 + wn * 32 * WN + j * 32 + (lane & 31);
+      const uint32_t voff = col < n ? ((uint32_t)row_lane * dstr + col) * 4u : kOob;
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row_base = m0 + wm * 32 * WM + i * 32 + 8 * (r >> 2) + (r & 3);
+          const float y = (float)acc[i][j][r] * (sc.act[i][r] * sc.w[j]);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rs, voff,
+                                                (uint32_t)row_base * dstr * 4u, 0);
+        }
+      }
+    }
+    return;
+  }
+  // head-major layout, or scales in FTZ/DAZ territory: guarded stores
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int col = n0 + wn * 32 * WN + j * 32 + (lane & 31);
+    float *out_col;
+    size_t row_stride;
+    if (HEADS) {
+      out_col = dst + (size_t)(col / hdim) * m * hdim + (col % hdim);
+      row_stride = hdim;
+    } else {
+      out_col = dst + col;
+      row_stride = dstr;
+    }
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 32 * WM + i * 32 + 8 * (r >> 2) +
+                        4 * (lane >> 5) + (r & 3);
+        const float y = all_plain ? (float)acc[i][j][r] * (sc.act[i][r] * sc.w[j])
+                                  : rescale(acc[i][j][r], sc.act[i][r], sc.w[j]);
+        if (row < m && col < n) out_col[(size_t)row * row_stride] = y;
+      }
+    }
+  }
+}
+
+// ---- LDS-DMA pipelined kernel ------------------------------------------
+//
+// The register-staged kernel above waits one global round trip per 64-byte
+// K step.  Here K steps are fetched S-1 steps ahead straight into an S-stage
+// LDS ring with buffer_load_dwordx4 ... lds (no VGPRs held), so the MFMAs of
+// step kt overlap the loads of steps kt+1 .. kt+S-1.
+//
+// LDS stage layout: 16-byte slots, A rows then B rows, 4 slots (64 bytes of
+// K) per row; chunk c of row r sits in slot 4r + (c ^ ((r >> 2) & 3)).  The
+// XOR swizzle makes the MFMA fragment reads (16 lanes = 16 consecutive rows,
+// one chunk) hit 16 distinct 16-byte bank groups.  A DMA instruction writes
+// 64 consecutive slots (lane i -> slot base + i), so each lane fetches the
+// global chunk that the swizzle assigns to its slot.
+//
+// Zero fill: a lane whose row is past m (or n) or whose chunk is past k gets
+// a buffer offset beyond the descriptor's range, for which the hardware
+// returns zeros.
+//
+// Synchronisation per step kt: wait until this wave's loads of step kt are
+// done (vmcnt = loads issued after them), s_barrier (every wave's loads of
+// kt have landed, and every wave has finished reading step kt-1), issue step
+// kt+S-1 into the slot step kt-1 used, then compute step kt.
+
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <int kPerWave, int kMaxAhead>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+  // ahead in [0, kMaxAhead]: loads still allowed in flight = ahead*kPerWave
+  if constexpr (kMaxAhead >= 4) { if (ahead >= 4) { wait_vmcnt<4 * kPerWave>(); return; } }
+  if constexpr (kMaxAhead >= 3) { if (ahead == 3) { wait_vmcnt<3 * kPerWave>(); return; } }
+  if constexpr (kMaxAhead >= 2) { if (ahead == 2) { wait_vmcnt<2 * kPerWave>(); return; } }
+  if constexpr (kMaxAhead >= 1) { if (ahead == 1) { wait_vmcnt<kPerWave>(); return; } }
+  wait_vmcnt<0>();
+}
+
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int WM, int WN, int S, int BKB, bool HEADS>
+__global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
+    float *__restrict__ dst, int dstr, int hdim, const int8_t *__restrict__ mat,
+    int mstr, const float *__restrict__ matsc, const int8_t *__restrict__ src,
+    int sstr, const float *__restrict__ ssc, int m, int n, int k) {
+  constexpr int kBM = 64 * WM;
+  constexpr int kBN = 64 * WN;
+  constexpr int kC = BKB / 16;                 // 16-byte chunks per row and stage
+  constexpr int kSlots = (kBM + kBN) * kC;
+  constexpr int kPerWave = kSlots / 64 / 4;
+  constexpr int kSub = BKB / 32;               // MFMA K sub-steps per stage
+  static_assert(S >= 2 && S <= 6, "stages");
+  static_assert(BKB == 64 || BKB == 128, "stage depth");
+  __shared__ v4i lds[S][kSlots];
+
+  // chunk c of row r lives in slot r*kC + (c ^ swz(r)): 16 consecutive rows
+  // reading one chunk land in 16 distinct 16-byte bank groups
+  auto swz = [](int r) { return kC == 4 ? ((r >> 2) & 3) : ((r >> 1) & 7); };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, &tm, &tn);
+  const int m0 = tm * kBM;
+  const int n0 = tn * kBN;
+  TileScales<WM, WN> scales;
+  load_tile_scales<WM, WN>(scales, ssc, matsc, m, n, m0, n0, wm, wn, lane);
+
+  const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t *>(src), (short)0, (int)((uint32_t)(m - 1) * sstr + k), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t *>(mat), (short)0, (int)((uint32_t)(n - 1) * mstr + k), 0x00020000);
+
+  // this lane's slot of each of its kPerWave DMA instructions
+  uint32_t row_off[kPerWave];
+  int chunk16[kPerWave];
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int instr = wave * kPerWave + i;
+    const bool is_a = instr * 64 < kBM * kC;  // wave-uniform
+    const int slot = instr * 64 + lane - (is_a ? 0 : kBM * kC);
+    const int row = slot / kC;
+    const int chunk = (slot % kC) ^ swz(row);
+    const int grow = (is_a ? m0 : n0) + row;
+    const bool in = grow < (is_a ? m : n);
+    row_off[i] = in ? (uint32_t)grow * (uint32_t)(is_a ? sstr : mstr) + chunk * 16 : kOob;
+    chunk16[i] = chunk * 16;
+  }
+  auto issue = [&](int kt, int buf) {
+#pragma unroll
+    for (int i = 0; i < kPerWave; ++i) {
+      const int instr = wave * kPerWave + i;
+      const bool is_a = instr * 64 < kBM * kC;
+      const int kb = kt * BKB;
+      const uint32_t voff =
+          (row_off[i] == kOob || kb + chunk16[i] >= k) ? kOob : row_off[i] + kb;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          is_a ? rs_a : rs_b,
+          (__attribute__((address_space(3))) void *)&lds[buf][instr * 64], 16, voff, 0, 0, 0);
+    }
+  };
+
+  v16i acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = v16i{};
+
+  const int nk = (k + BKB - 1) / BKB;
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nk) issue(st, st);
+
+  const int frag_row = lane & 31;
+  const int frag_chunk = lane >> 5;
+  auto load_frags = [&](const v4i *stage, int ks, v4i (&a)[WM], v4i (&b)[WN]) {
+    const int c = ks * 2 + frag_chunk;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int r = wm * 32 * WM + i * 32 + frag_row;
+      a[i] = stage[r * kC + (c ^ swz(r))];
+    }
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int r = wn * 32 * WN + j * 32 + frag_row;
+      b[j] = stage[kBM * kC + r * kC + (c ^ swz(r))];
+    }
+  };
+  for (int kt = 0; kt < nk; ++kt) {
+    const int ahead = min(S - 2, nk - 1 - kt);
+    wait_ahead<kPerWave, S - 2>(ahead);
+    block_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const v4i *stage = lds[kt % S];
+    // fragments of sub-step ks+1 are read while the MFMAs of ks run
+    v4i a[2][WM], b[2][WN];
+    load_frags(stage, 0, a[0], b[0]);
+#pragma unroll
+    for (int ks = 0; ks < kSub; ++ks) {
+      if (ks + 1 < kSub) load_frags(stage, ks + 1, a[(ks + 1) & 1], b[(ks + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[ks & 1][i], b[ks & 1][j],
+                                                            acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // epilogue: rescale and store (gemma.c:3854-3865)
+  store_tile<WM, WN, HEADS>(acc, scales, dst, dstr, hdim, m, n, m0, n0, wm, wn, lane);
 }
 
 // Any shape, any alignment: one thread per output, byte loads.  Used only
@@ -163,24 +459,90 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_generic_kernel(
     dst[(size_t)row * dstr + col] = y;
 }
 
+// Tile shape: GEMMA_HIP_GEMM_TILE=WMxWN (register-staged kernel), WMxWNxS
+// (LDS-DMA kernel, S stages of 64-byte K) or WMxWNxSx128 (128-byte K stages)
+// overrides the choice below (a launch-shape knob like the reference's
+// GEMM_MC/GEMM_NC, gemma.c:458-493).
+int env_tile() {
+  static const int t = [] {
+    const char *e = getenv("GEMMA_HIP_GEMM_TILE");
+    if (e == nullptr) return 0;
+    int a = 0, b = 0, c = 0, d = 0;
+    const int got = sscanf(e, "%dx%dx%dx%d", &a, &b, &c, &d);
+    if (got == 4) return a * 1000 + b * 100 + c * 10 + (d == 128 ? 1 : 0);
+    if (got == 3) return a * 100 + b * 10 + c;
+    if (got == 2) return a * 10 + b;
+    return 0;
+  }();
+  return t;
+}
+
+template <int WM, int WN, int S, int BKB = 64>
+void launch_dma(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
+                const int8_t *mat, int mstr, const float *matsc,
+                const int8_t *src, int sstr, const float *ssc, int m, int n,
+                int k) {
+  const int tiles = ((m + 64 * WM - 1) / (64 * WM)) * ((n + 64 * WN - 1) / (64 * WN));
+  if (heads)
+    gemm_i8_dma_kernel<WM, WN, S, BKB, true><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
+  else
+    gemm_i8_dma_kernel<WM, WN, S, BKB, false><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
+}
+
+template <int WM, int WN>
+void launch_tiled(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
+                  const int8_t *mat, int mstr, const float *matsc,
+                  const int8_t *src, int sstr, const float *ssc, int m, int n,
+                  int k) {
+  const int tiles = ((m + 64 * WM - 1) / (64 * WM)) * ((n + 64 * WN - 1) / (64 * WN));
+  if (heads)
+    gemm_i8_kernel<WM, WN, true><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
+  else
+    gemm_i8_kernel<WM, WN, false><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
+}
+
 }  // namespace
 
 hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
                           int mstr, const float *matsc, const int8_t *src,
                           int sstr, const float *ssc, int m, int n, int k,
                           const DeviceInfo &dev, hipStream_t stream) {
-  (void)dev;
   const bool fast = k % 16 == 0 && mstr % 16 == 0 && sstr % 16 == 0 &&
                     (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
   const bool heads = hdim > 0;
+  // the DMA kernel addresses operands with 32-bit buffer offsets
+  const bool dma_ok = (uint64_t)(m - 1) * sstr + k < kOob &&
+                      (uint64_t)(n - 1) * mstr + k < kOob &&
+                      ((uint64_t)(m - 1) * dstr + n) * 4 < kOob;
   if (fast) {
-    const dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    if (heads)
-      gemm_i8_kernel<true><<<grid, kThreads, 0, stream>>>(
-          dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
-    else
-      gemm_i8_kernel<false><<<grid, kThreads, 0, stream>>>(
-          dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
+    int tile = env_tile();
+    if (tile == 0) {
+      // measured on MI355X at the 1b/4b prefill and SigLIP shapes: 128x128
+      // tiles with two 128-byte K stages are fastest once there is a tile
+      // per CU; below that, 128x64 tiles keep more CUs busy
+      const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+      tile = !dma_ok ? 22 : (tiles128 >= dev.cus ? 2221 : 214);
+    }
+    if (tile >= 100 && !dma_ok) tile = 22;
+    switch (tile) {
+      case 224: launch_dma<2, 2, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 223: launch_dma<2, 2, 3>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 226: launch_dma<2, 2, 6>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 424: launch_dma<4, 2, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 244: launch_dma<2, 4, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 2221: launch_dma<2, 2, 2, 128>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 2231: launch_dma<2, 2, 3, 128>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 4221: launch_dma<4, 2, 2, 128>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 114: launch_dma<1, 1, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 214: launch_dma<2, 1, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 11: launch_tiled<1, 1>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      case 21: launch_tiled<2, 1>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+      default: launch_tiled<2, 2>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
+    }
   } else {
     const dim3 grid((n + 63) / 64, (m + 3) / 4);
     if (heads)

@@ -15,6 +15,8 @@
 //
 // Several weight matrices ("jobs": q/k/v or gate/up) are one flat row range,
 // as in gemma.c:2803-2811, so a fused projection is one launch.
+#include <cstdlib>
+
 #include "gh_arith.h"
 #include "gh_kernels.h"
 
@@ -58,7 +60,7 @@ __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
 // Stage the activation vector in LDS as int8.  FUSED: quantize x fp32 [k]
 // (the quantize_act that precedes every decode GEMV); otherwise copy xq.
 // Returns the activation scale.
-template <bool FUSED>
+template <bool FUSED, int NT = kThreads>
 __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
                                             const int8_t *__restrict__ xq,
                                             const float *__restrict__ xs,
@@ -68,49 +70,72 @@ __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
   const int tid = threadIdx.x;
   if (!FUSED) {
     if (((uintptr_t)xq & 15) == 0 && (k & 15) == 0) {
-      for (int c = tid; c < k / 16; c += kThreads)
+      for (int c = tid; c < k / 16; c += NT)
         reinterpret_cast<v4i *>(lds)[c] =
             reinterpret_cast<const v4i *>(xq)[c];
     } else {
-      for (int c = tid; c < k; c += kThreads) lds[c] = xq[c];
+      for (int c = tid; c < k; c += NT) lds[c] = xq[c];
     }
     __syncthreads();
     return *xs;
   }
 
-  __shared__ float wave_amax[kWaves];
+  __shared__ float wave_amax[NT / 64];
   const bool vec = ((uintptr_t)xf & 15) == 0 && (k & 3) == 0;
+  // x stays in registers between the amax pass and the quantize pass when
+  // it fits in kXRegs float4 per thread (k <= 4096); longer rows re-read it.
+  constexpr int kXRegs = 4;
+  const bool in_regs = vec && k / 4 <= kXRegs * NT;
+  v4f xr[kXRegs];
   float amax = 0.0f;
-  if (vec) {
-    for (int c = tid; c < k / 4; c += kThreads) {
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kXRegs; ++j) {
+      const int c = tid + j * NT;
+      xr[j] = c < k / 4 ? reinterpret_cast<const v4f *>(xf)[c] : v4f{0.f, 0.f, 0.f, 0.f};
+      amax = fmaxf(amax, fmaxf(fmaxf(abs_daz(xr[j].x), abs_daz(xr[j].y)),
+                               fmaxf(abs_daz(xr[j].z), abs_daz(xr[j].w))));
+    }
+  } else if (vec) {
+    for (int c = tid; c < k / 4; c += NT) {
       v4f v = reinterpret_cast<const v4f *>(xf)[c];
       amax = fmaxf(amax, fmaxf(fmaxf(abs_daz(v.x), abs_daz(v.y)),
                                fmaxf(abs_daz(v.z), abs_daz(v.w))));
     }
   } else {
-    for (int c = tid; c < k; c += kThreads) amax = fmaxf(amax, abs_daz(xf[c]));
+    for (int c = tid; c < k; c += NT) amax = fmaxf(amax, abs_daz(xf[c]));
   }
   amax = wave_max(amax);
   if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]),
-               fmaxf(wave_amax[2], wave_amax[3]));
+  amax = wave_amax[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, wave_amax[w]);
   const QuantParams qp = quant_params(amax);
-  if (vec) {
-    for (int c = tid; c < k / 4; c += kThreads) {
+  if (in_regs) {
+#pragma unroll
+    for (int j = 0; j < kXRegs; ++j) {
+      const int c = tid + j * NT;
+      if (c < k / 4)
+        reinterpret_cast<uint32_t *>(lds)[c] =
+            pack4(quant_one(xr[j].x, qp.inv), quant_one(xr[j].y, qp.inv),
+                  quant_one(xr[j].z, qp.inv), quant_one(xr[j].w, qp.inv));
+    }
+  } else if (vec) {
+    for (int c = tid; c < k / 4; c += NT) {
       v4f v = reinterpret_cast<const v4f *>(xf)[c];
       reinterpret_cast<uint32_t *>(lds)[c] =
           pack4(quant_one(v.x, qp.inv), quant_one(v.y, qp.inv),
                 quant_one(v.z, qp.inv), quant_one(v.w, qp.inv));
     }
   } else {
-    for (int c = tid; c < k; c += kThreads)
+    for (int c = tid; c < k; c += NT)
       lds[c] = (int8_t)quant_one(xf[c], qp.inv);
   }
   __syncthreads();
   if (blockIdx.x == 0) {
     if (xq_out != nullptr)
-      for (int c = tid; c < k; c += kThreads) xq_out[c] = lds[c];
+      for (int c = tid; c < k; c += NT) xq_out[c] = lds[c];
     if (xs_out != nullptr && tid == 0) *xs_out = qp.scale;
   }
   return qp.scale;
@@ -158,6 +183,70 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     if (sub == 0 && row < total)
       pick(jobs.dst, j)[r] = rescale(acc, act_scale, pick(jobs.sc, j)[r]);
+  }
+}
+
+// Latency-oriented variant (VEC layout only): each lane owns at most CPL
+// 16-byte chunks of its row, L = 64 / RPW lanes per row.  A lane issues the
+// loads of its first row before the activation is staged, so HBM latency
+// overlaps the quantize prologue, and the loads of its next row before it
+// reduces the current one (register double buffering).
+template <int L, int CPL, bool FUSED, int NT>
+__global__ __launch_bounds__(NT) void gemv_i8_pipelined_kernel(
+    GemvJobs jobs, int total, int k, const int8_t *__restrict__ xq,
+    const float *__restrict__ xs, const float *__restrict__ xf,
+    int8_t *__restrict__ xq_out, float *__restrict__ xs_out) {
+  extern __shared__ v4i lds_x4[];
+  constexpr int kRowsPerWave = 64 / L;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane % L;
+  const int rloc = lane / L;
+  const int kc = k >> 4;
+  constexpr int kBlockWaves = NT / 64;
+  const int stride = gridDim.x * kBlockWaves * kRowsPerWave;
+
+  auto load_row = [&](int row, v4i (&buf)[CPL]) {
+    if (row < total) {
+      int r;
+      const int j = job_of(jobs, row, &r);
+      const v4i *w4 = static_cast<const v4i *>(pick(jobs.w, j)) + (size_t)r * kc;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = sub + i * L;
+        buf[i] = c < kc ? __builtin_nontemporal_load(w4 + c) : v4i{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) buf[i] = v4i{0, 0, 0, 0};
+    }
+  };
+
+  int base = (blockIdx.x * kBlockWaves + wave) * kRowsPerWave;
+  v4i cur[CPL];
+  load_row(base + rloc, cur);
+  const float act_scale = stage_x_i8<FUSED, NT>(reinterpret_cast<int8_t *>(lds_x4), k,
+                                            xq, xs, xf, xq_out, xs_out);
+
+  for (; base < total; base += stride) {
+    const int row = base + rloc;
+    v4i nxt[CPL];
+    load_row(row + stride, nxt);
+    int32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;
+      if (c < kc) acc = dot16(cur[i], lds_x4[c], acc);
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (sub == 0 && row < total) {
+      int r;
+      const int j = job_of(jobs, row, &r);
+      pick(jobs.dst, j)[r] = rescale(acc, act_scale, pick(jobs.sc, j)[r]);
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) cur[i] = nxt[i];
   }
 }
 
@@ -278,6 +367,85 @@ hipError_t gemv_f32_dispatch(int lanes, dim3 grid, size_t lds,
   return hipGetLastError();
 }
 
+// Launch-shape knobs, read once from the environment (the reference tunes
+// its CPU GEMM blocking the same way, GEMM_MC/NC/KC, gemma.c:458-493):
+//   GEMMA_HIP_GEMV_LANES         lanes per row of the pipelined GEMV (8..64)
+//   GEMMA_HIP_GEMV_BLOCKS_PER_CU workgroups per CU of the pipelined GEMV
+//   GEMMA_HIP_GEMV_LOOP=1        use the looping GEMV kernel instead
+//   GEMMA_HIP_GEMV_THREADS       256 or 1024 threads per pipelined workgroup
+struct Tuning {
+  int lanes = 0;
+  int blocks_per_cu = 0;  // 0: 8 for 256-thread, 2 for 1024-thread workgroups
+  int threads = 0;        // 0: chosen per shape
+  bool force_loop = false;
+};
+
+const Tuning &tuning() {
+  static const Tuning t = [] {
+    Tuning v;
+    if (const char *e = getenv("GEMMA_HIP_GEMV_LANES")) {
+      const int l = atoi(e);
+      if (l == 8 || l == 16 || l == 32 || l == 64) v.lanes = l;
+    }
+    if (const char *e = getenv("GEMMA_HIP_GEMV_BLOCKS_PER_CU")) {
+      const int b = atoi(e);
+      if (b >= 1 && b <= 64) v.blocks_per_cu = b;
+    }
+    if (const char *e = getenv("GEMMA_HIP_GEMV_LOOP")) v.force_loop = atoi(e) != 0;
+    if (const char *e = getenv("GEMMA_HIP_GEMV_THREADS")) {
+      const int t = atoi(e);
+      if (t == 256 || t == 1024) v.threads = t;
+    }
+    return v;
+  }();
+  return t;
+}
+
+using PipeFn = void (*)(dim3, size_t, hipStream_t, const GemvJobs &, int, int,
+                        const int8_t *, const float *, const float *, int8_t *,
+                        float *);
+
+template <int L, int CPL, bool FUSED, int NT>
+void launch_pipe(dim3 grid, size_t lds, hipStream_t stream, const GemvJobs &jobs,
+                 int total, int k, const int8_t *xq, const float *xs,
+                 const float *xf, int8_t *xq_out, float *xs_out) {
+  gemv_i8_pipelined_kernel<L, CPL, FUSED, NT><<<grid, NT, lds, stream>>>(
+      jobs, total, k, xq, xs, xf, xq_out, xs_out);
+}
+
+template <int L, bool FUSED, int NT>
+PipeFn pipe_for(int cpl) {
+  switch (cpl) {
+    case 1: return &launch_pipe<L, 1, FUSED, NT>;
+    case 2: return &launch_pipe<L, 2, FUSED, NT>;
+    case 3: return &launch_pipe<L, 3, FUSED, NT>;
+    case 4: return &launch_pipe<L, 4, FUSED, NT>;
+    case 5: return &launch_pipe<L, 5, FUSED, NT>;
+    case 6: return &launch_pipe<L, 6, FUSED, NT>;
+    case 7: return &launch_pipe<L, 7, FUSED, NT>;
+    case 8: return &launch_pipe<L, 8, FUSED, NT>;
+    case 9: return &launch_pipe<L, 9, FUSED, NT>;
+    case 10: return &launch_pipe<L, 10, FUSED, NT>;
+    case 11: case 12: return NT == 1024 ? nullptr : &launch_pipe<L, 12, FUSED, NT>;
+    default: return nullptr;
+  }
+}
+
+template <int NT>
+PipeFn pipe_fn_nt(int lanes, int cpl, bool fused) {
+  switch (lanes) {
+    case 64: return fused ? pipe_for<64, true, NT>(cpl) : pipe_for<64, false, NT>(cpl);
+    case 32: return fused ? pipe_for<32, true, NT>(cpl) : pipe_for<32, false, NT>(cpl);
+    case 16: return fused ? pipe_for<16, true, NT>(cpl) : pipe_for<16, false, NT>(cpl);
+    default: return fused ? pipe_for<8, true, NT>(cpl) : pipe_for<8, false, NT>(cpl);
+  }
+}
+
+PipeFn pipe_fn(int lanes, int cpl, bool fused, int threads) {
+  return threads == 1024 ? pipe_fn_nt<1024>(lanes, cpl, fused)
+                         : pipe_fn_nt<256>(lanes, cpl, fused);
+}
+
 }  // namespace
 
 hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
@@ -286,10 +454,37 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
                           hipStream_t stream) {
   const int total = jobs.end[jobs.njobs - 1];
   const bool vec = rows_aligned(jobs, k, 1, 16);
-  const int lanes = vec ? lanes_for(k / 16) : 64;
-  const dim3 grid(grid_for(total, lanes, dev));
   const size_t lds = (size_t)(k + 15) / 16 * 16;
   const bool fused = xf != nullptr;
+  // Measured on MI355X (1b and 4b decode shapes): up to ~2048 rows the
+  // launch is latency-bound and one row per wave with every load issued up
+  // front wins (q/k/v/o, and down with its 6912-byte rows); above that the
+  // looping kernel's 8 rows per wave amortise the per-row reduction better.
+  // Long rows (k >= 4096) with few of them are latency-bound on the x
+  // prologue: 1024-thread workgroups pay it 4x less often (measured on the
+  // 1b/4b down projections: 8.8 -> 7.9 us and 13.9 -> 10.2 us).
+  const bool long_rows = k >= 4096 && total <= 4096;
+  const bool pipelined =
+      tuning().lanes > 0 || tuning().threads > 0 || total <= 2048 || long_rows;
+  if (vec && pipelined && !tuning().force_loop) {
+    const int kc = k / 16;
+    const int lanes = tuning().lanes > 0 ? tuning().lanes : 64;
+    const int threads = tuning().threads > 0 ? tuning().threads : (long_rows ? 1024 : 256);
+    const int cpl = (kc + lanes - 1) / lanes;
+    PipeFn fn = pipe_fn(lanes, cpl, fused, threads);
+    if (fn != nullptr) {
+      const int rows_per_block = threads / 64 * (64 / lanes);
+      long blocks = (total + rows_per_block - 1) / rows_per_block;
+      const int per_cu = tuning().blocks_per_cu > 0 ? tuning().blocks_per_cu
+                                                    : (threads == 1024 ? 2 : 8);
+      const long cap = (long)dev.cus * per_cu;
+      fn(dim3((unsigned)(blocks < cap ? blocks : cap)), lds, stream, jobs, total, k, xq, xs,
+         xf, xq_out, xs_out);
+      return hipGetLastError();
+    }
+  }
+  const int lanes = vec ? lanes_for(k / 16) : 64;
+  const dim3 grid(grid_for(total, lanes, dev));
   if (fused)
     return vec ? gemv_i8_dispatch<true, true>(lanes, grid, lds, stream, jobs,
                                               total, k, xq, xs, xf, xq_out, xs_out)

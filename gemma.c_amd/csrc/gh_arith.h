@@ -89,6 +89,33 @@ __device__ __forceinline__ float rescale(int32_t acc, float act_scale,
   return mul_ftz((float)acc, mul_ftz(act_scale, w_scale));
 }
 
+// True when act_scale*w_scale can take the plain IEEE path in rescale():
+// neither scale is subnormal (DAZ would zero it) and their product is not a
+// nonzero value at or below FLT_MIN (FTZ territory).  Then for every int32
+// acc, |acc*p| >= |p| (acc == 0 gives an exact signed zero), so
+// (float)acc * p equals the FTZ/DAZ result bit for bit.
+__device__ __forceinline__ bool rescale_is_plain(float act_scale, float w_scale) {
+  const float p = act_scale * w_scale;
+  return daz(act_scale) == act_scale && daz(w_scale) == w_scale &&
+         (p == 0.0f || fabsf(p) > 1.17549435e-38f);
+}
+
+// rescale_is_plain() for every pair of a set of activation scales and a set
+// of weight scales, from their extremes: plain unless some scale is
+// subnormal or the smallest nonzero |product| is at or below FLT_MIN.
+// mins are the smallest nonzero magnitudes (+inf when all are zero) and
+// sub flags a subnormal scale.
+__device__ __forceinline__ bool rescale_all_plain(float act_min, bool act_sub,
+                                                  float w_min, bool w_sub) {
+  return !act_sub && !w_sub && act_min * w_min > 1.17549435e-38f;
+}
+
+__device__ __forceinline__ void scale_extremes(float v, float *min_nz, bool *sub) {
+  const float a = fabsf(v);
+  if (a != 0.0f) *min_nz = fminf(*min_nz, a);
+  *sub = *sub || (a != 0.0f && a < 1.17549435e-38f);
+}
+
 // Packs four quantized values into one little-endian 32-bit word.
 __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c,
                                           int32_t d) {
