@@ -44,6 +44,7 @@ for _p in (REPO, PKG):
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
+FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 ROTATE_BYTES = 512 << 20   # > 2x the 256 MB Infinity Cache
 ROT_STEPS = 8              # steps per captured graph
 
@@ -208,7 +209,24 @@ def bench_gemm(torch, gh, gen, timer, reps):
         out[name] = dict(m=m, n=n, k=k, us=round(ms * 1e3, 2), tops=round(tops, 1),
                          frac=round(tops / INT8_PEAK_TOPS, 4))
         del a, b, d
-    groups = {}
+    # SigLIP patch embedding (gemma.c:4411-4448): fp32 im2col + GEMM, 896 px, P = 14
+    img_px, psize, dim = 896, 14, 1152
+    npatch, kdim = (img_px // psize) ** 2, 3 * psize * psize
+    img = torch.rand((img_px, img_px, 3), generator=gen, device="cuda") * 2 - 1
+    pe = torch.randn((dim, kdim), generator=gen, device="cuda") * 0.02
+    pe_b = torch.randn(dim, generator=gen, device="cuda") * 0.02
+    emb = torch.empty((npatch, dim), device="cuda")
+
+    def run_pe():
+        for _ in range(reps):
+            gh.patch_embed(emb, img, pe, pe_b, img_px, psize, dim, None, stream)
+
+    run_pe()
+    ms = min(timer.elapsed_ms(run_pe) for _ in range(3)) / reps
+    tflops = 2 * npatch * dim * kdim / (ms * 1e-3) / 1e12
+    patch = dict(img_px=img_px, psize=psize, dim=dim, us=round(ms * 1e3, 2),
+                 tflops=round(tflops, 1), frac_fp32=round(tflops / FP32_PEAK_TFLOPS, 4))
+    groups = {"siglip_patch_embed_f32": patch}
     for prefix in ("4b", "siglip"):
         ops = sum(gemm_ops(v["m"], v["n"], v["k"]) * GEMM_COUNTS[kk]
                   for kk, v in out.items() if kk.startswith(prefix))

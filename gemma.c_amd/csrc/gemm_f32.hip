@@ -23,7 +23,8 @@ constexpr int kRowChunks = kBK / 4 + 1;   // float4 chunks per LDS row (+1 pad)
 
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
-    const float *__restrict__ src, int sstr, int m, int n, int k) {
+    const float *__restrict__ src, int sstr, int m, int n, int k,
+    const float *__restrict__ bias, bool clamp) {
   __shared__ v4f lds_a[2][kBM][kRowChunks];
   __shared__ v4f lds_b[2][kBN][kRowChunks];
 
@@ -101,13 +102,16 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
   for (int j = 0; j < 2; ++j) {
     const int col = n0 + wn * 64 + j * 32 + (lane & 31);
     if (col >= n) continue;
+    const float b = bias != nullptr ? bias[col] : 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row =
             m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < m) dst[(size_t)row * dstr + col] = acc[i][j][r];
+        float y = bias != nullptr ? acc[i][j][r] + b : acc[i][j][r];
+        if (clamp) y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y));
+        if (row < m) dst[(size_t)row * dstr + col] = y;
       }
   }
 }
@@ -115,7 +119,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 // Any shape, any alignment: one thread per output.
 __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
     float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
-    const float *__restrict__ src, int sstr, int m, int n, int k) {
+    const float *__restrict__ src, int sstr, int m, int n, int k,
+    const float *__restrict__ bias, bool clamp) {
   const int col = blockIdx.x * 64 + (threadIdx.x & 63);
   const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (row >= m || col >= n) return;
@@ -123,6 +128,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
   const float *b = mat + (size_t)col * mstr;
   float acc = 0.0f;
   for (int l = 0; l < k; ++l) acc = __builtin_fmaf(a[l], b[l], acc);
+  if (bias != nullptr) acc += bias[col];
+  if (clamp) acc = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, acc));
   dst[(size_t)row * dstr + col] = acc;
 }
 
@@ -130,6 +137,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
 
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const float *src, int sstr, int m, int n, int k,
+                           const float *bias, bool clamp,
                            const DeviceInfo &dev, hipStream_t stream) {
   (void)dev;
   const bool fast = k % 4 == 0 && mstr % 4 == 0 && sstr % 4 == 0 &&
@@ -137,11 +145,11 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
   if (fast) {
     const dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
     gemm_f32_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src,
-                                                   sstr, m, n, k);
+                                                   sstr, m, n, k, bias, clamp);
   } else {
     const dim3 grid((n + 63) / 64, (m + 3) / 4);
     gemm_f32_generic_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr,
-                                                           src, sstr, m, n, k);
+                                                           src, sstr, m, n, k, bias, clamp);
   }
   return hipGetLastError();
 }

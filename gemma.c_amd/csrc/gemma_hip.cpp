@@ -57,6 +57,9 @@ struct State {
   // device staging for the _host entry points, grown on demand
   char *staging = nullptr;
   size_t staging_bytes = 0;
+  // im2col workspace of the patch embedding, grown on demand
+  float *work = nullptr;
+  size_t work_bytes = 0;
 };
 
 State g;
@@ -186,6 +189,9 @@ void gemma_hip_shutdown(void) {
   if (g.staging != nullptr) (void)hipFree(g.staging);
   g.staging = nullptr;
   g.staging_bytes = 0;
+  if (g.work != nullptr) (void)hipFree(g.work);
+  g.work = nullptr;
+  g.work_bytes = 0;
   (void)hipStreamDestroy(g.stream);
   g.stream = nullptr;
   g.ready = false;
@@ -378,7 +384,8 @@ int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
     return 0;
   }
   GH_CHECK("gemma_hip_matmul_f32: gemm launch",
-           gh::launch_gemm_f32(dst, dstr, mat, mstr, src, sstr, m, n, k, g.info, s));
+           gh::launch_gemm_f32(dst, dstr, mat, mstr, src, sstr, m, n, k, nullptr, false,
+                               g.info, s));
   return 0;
 }
 
@@ -393,6 +400,43 @@ int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
   if (gj.end[njobs - 1] == 0) return 0;
   GH_CHECK("gemma_hip_matmul_f32_multi: launch",
            gh::launch_gemv_f32(gj, k, x, g.info, pick_stream(stream)));
+  return 0;
+}
+
+int gemma_hip_patch_embed(float *dst, const float *img, const float *pe,
+                          const float *pe_b, int img_px, int psize, int dim,
+                          float *work, void *stream) {
+  if (need_init()) return 1;
+  if (psize <= 0 || img_px <= 0 || dim <= 0 || img_px % psize != 0)
+    return fail("gemma_hip_patch_embed: bad shape img_px=%d psize=%d dim=%d", img_px,
+                psize, dim);
+  if (!dst || !img || !pe || !pe_b) return fail("gemma_hip_patch_embed: null pointer");
+  const long ppi = img_px / psize;
+  const long npatch = ppi * ppi;
+  const long kdim = 3l * psize * psize;
+  if (npatch * kdim > (1l << 30) || npatch * dim > (1l << 30) ||
+      (long)img_px * img_px * 3 > (1l << 30))
+    return fail("gemma_hip_patch_embed: image too large");
+  hipStream_t st = pick_stream(stream);
+  if (work == nullptr) {
+    const size_t need = (size_t)npatch * kdim * sizeof(float);
+    if (need > g.work_bytes) {
+      if (g.work != nullptr) {
+        GH_CHECK("gemma_hip_patch_embed: sync", hipDeviceSynchronize());
+        GH_CHECK("gemma_hip_patch_embed: free", hipFree(g.work));
+        g.work = nullptr;
+        g.work_bytes = 0;
+      }
+      GH_CHECK("gemma_hip_patch_embed: workspace", hipMalloc(&g.work, need));
+      g.work_bytes = need;
+    }
+    work = g.work;
+  }
+  GH_CHECK("gemma_hip_patch_embed: im2col",
+           gh::launch_im2col(work, img, img_px, psize, st));
+  GH_CHECK("gemma_hip_patch_embed: gemm",
+           gh::launch_gemm_f32(dst, dim, pe, (int)kdim, work, (int)kdim, (int)npatch, dim,
+                               (int)kdim, pe_b, true, g.info, st));
   return 0;
 }
 
@@ -593,6 +637,36 @@ int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
            hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,
                             (size_t)n * 4, m, hipMemcpyDeviceToHost, g.stream));
   GH_CHECK("gemm_fpx_host: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+
+int gemma_hip_patch_embed_host(float *dst, const float *img, const float *pe,
+                               const float *pe_b, int img_px, int psize, int dim) {
+  if (need_init()) return 1;
+  if (psize <= 0 || img_px <= 0 || dim <= 0 || img_px % psize != 0 || !dst || !img ||
+      !pe || !pe_b)
+    return fail("gemma_hip_patch_embed_host: bad arguments");
+  const size_t kdim = 3ul * psize * psize;
+  const size_t npatch = (size_t)(img_px / psize) * (img_px / psize);
+  const void *dpe = resolve(pe, (size_t)dim * kdim * 4);
+  const void *db = resolve(pe_b, (size_t)dim * 4);
+  if (dpe == nullptr || db == nullptr)
+    return fail("gemma_hip_patch_embed_host: weights are not registered");
+  const size_t img_bytes = (size_t)img_px * img_px * 3 * 4;
+  Carver c;
+  size_t o_img = c.take(img_bytes), o_y = c.take(npatch * dim * 4);
+  if (staging_reserve(c.used)) return 1;
+  char *base = g.staging;
+  GH_CHECK("patch_embed_host: H2D",
+           hipMemcpyAsync(base + o_img, img, img_bytes, hipMemcpyHostToDevice, g.stream));
+  if (gemma_hip_patch_embed((float *)(base + o_y), (const float *)(base + o_img),
+                            (const float *)dpe, (const float *)db, img_px, psize, dim,
+                            nullptr, g.stream))
+    return 1;
+  GH_CHECK("patch_embed_host: D2H",
+           hipMemcpyAsync(dst, base + o_y, npatch * dim * 4, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("patch_embed_host: sync", hipStreamSynchronize(g.stream));
   return 0;
 }
 

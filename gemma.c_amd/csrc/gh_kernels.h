@@ -49,9 +49,16 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
                           int sstr, const float *ssc, int m, int n, int k,
                           const DeviceInfo &dev, hipStream_t stream);
 
-// gemm_f32.hip: dst = src . mat^T in fp32.
+// gemm_f32.hip: dst = src . mat^T in fp32; bias (nullable) adds bias[col],
+// clamp limits every output to [-FLT_MAX, FLT_MAX] (clamp_fpx).
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const float *src, int sstr, int m, int n, int k,
+                           const float *bias, bool clamp,
                            const DeviceInfo &dev, hipStream_t stream);
+
+// patch.hip: a [npatch][3*psize*psize] = patches of the HWC image, in the K
+// order of the SigLIP patch-embedding weight [dim][3][psize][psize].
+hipError_t launch_im2col(float *a, const float *img, int img_px, int psize,
+                         hipStream_t stream);
 
 }  // namespace gh

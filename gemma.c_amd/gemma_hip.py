@@ -59,6 +59,8 @@ _SIGS = {
     "gemma_hip_gemv_fpx_host": (_I, [_P, _P, _P, _I, _I]),
     "gemma_hip_gemv_fpx_multi_host": (_I, [ctypes.POINTER(Job), _I, _P, _I]),
     "gemma_hip_gemm_fpx_host": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I]),
+    "gemma_hip_patch_embed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
+    "gemma_hip_patch_embed_host": (_I, [_P, _P, _P, _P, _I, _I, _I]),
 }
 
 
@@ -150,6 +152,11 @@ class GemmaHip:
     def matmul_f32_multi(self, specs, x, k, stream=None):
         arr, n = self.jobs(specs)
         self._check(self.lib.gemma_hip_matmul_f32_multi(arr, n, _addr(x), k, stream))
+
+    def patch_embed(self, dst, img, pe, pe_b, img_px, psize, dim, work=None, stream=None):
+        self._check(self.lib.gemma_hip_patch_embed(_addr(dst), _addr(img), _addr(pe),
+                                                   _addr(pe_b), img_px, psize, dim,
+                                                   _addr(work), stream))
 
     # weights ---------------------------------------------------------------
     def register_weights(self, host, nbytes: int):

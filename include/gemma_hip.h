@@ -142,6 +142,17 @@ int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
 int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
                                const float *x, int k, void *stream);
 
+/* The SigLIP patch embedding (gemma.c:4411-4448): the stride-psize,
+ * psize x psize convolution of an HWC fp32 image img [img_px][img_px][3]
+ * with pe [dim][3][psize][psize] plus pe_b [dim], as im2col + fp32 GEMM.
+ * dst [npatch][dim], npatch = (img_px/psize)^2, each value clamped to
+ * [-FLT_MAX, FLT_MAX] (clamp_fpx, gemma.c:2504).  work is a device
+ * workspace of npatch*3*psize*psize floats, or NULL to use one the library
+ * allocates on first need.  fp32: matches within the fp32 tolerance. */
+int gemma_hip_patch_embed(float *dst, const float *img, const float *pe,
+                          const float *pe_b, int img_px, int psize, int dim,
+                          float *work, void *stream);
+
 /* ---- host drop-ins for the reference call sites ------------------------ */
 /* Same argument order and meaning as the reference functions named; weight
  * pointers (mat, matsc, job w/sc) must lie in registered ranges, activation
@@ -179,6 +190,11 @@ int gemma_hip_gemv_fpx_multi_host(const gemma_hip_job *jobs, int njobs,
 /* gemm_fpx (gemma.c:3308). */
 int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
                             const float *src, int sstr, int m, int n, int k);
+
+/* forward_vision's patch embedding (gemma.c:4411-4448) on a host image;
+ * pe and pe_b must be registered. */
+int gemma_hip_patch_embed_host(float *dst, const float *img, const float *pe,
+                               const float *pe_b, int img_px, int psize, int dim);
 
 #ifdef __cplusplus
 }

@@ -186,3 +186,30 @@ void oracle_gemm_f64(double *dst, double *absdst, const float *mat, int mstr,
     }
   }
 }
+
+/* gemma.c:4419-4447: loops patch (oy, ox), out channel, py, px, c */
+void oracle_patch_embed_f64(double *dst, double *absdst, const float *img,
+                            const float *pe, const float *pe_b, int img_px,
+                            int psize, int dim) {
+  int ppi = img_px / psize;
+  int idim = 3 * psize * psize;
+  for (int pi = 0; pi < ppi * ppi; pi++) {
+    int oy = pi / ppi, ox = pi % ppi;
+    for (int oc = 0; oc < dim; oc++) {
+      double sum = 0.0, mag = 0.0;
+      for (int py = 0; py < psize; py++) {
+        for (int px = 0; px < psize; px++) {
+          for (int c = 0; c < 3; c++) {
+            size_t in_idx = ((size_t)(oy * psize + py) * img_px + (ox * psize + px)) * 3 + c;
+            size_t w_idx = (size_t)oc * idim + c * psize * psize + py * psize + px;
+            double prod = (double)pe[w_idx] * (double)img[in_idx];
+            sum += prod;
+            mag += fabs(prod);
+          }
+        }
+      }
+      dst[(size_t)pi * dim + oc] = sum + (double)pe_b[oc];
+      absdst[(size_t)pi * dim + oc] = mag + fabs((double)pe_b[oc]);
+    }
+  }
+}

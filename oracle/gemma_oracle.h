@@ -66,6 +66,14 @@ void oracle_gemm_int8(float *dst, int dstr, int32_t *acc, const int8_t *mat,
 void oracle_gemm_f64(double *dst, double *absdst, const float *mat, int mstr,
                      const float *src, int sstr, int m, int n, int k);
 
+/* gemma.c:4411-4448, the SigLIP patch embedding, in float64: dst and
+ * absdst are [npatch][dim] with npatch = (img_px/psize)^2; dst = bias +
+ * sum over (py, px, c) of pe[oc][c][py][px] * img[oy*P+py][ox*P+px][c],
+ * absdst = |bias| + the sum of |products| (the fp32 rounding bound). */
+void oracle_patch_embed_f64(double *dst, double *absdst, const float *img,
+                            const float *pe, const float *pe_b, int img_px,
+                            int psize, int dim);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,8 @@ class Oracle:
                                          _f32p, _int, _int, _int, _int]
         lib.oracle_gemm_f64.restype = None
         lib.oracle_gemm_f64.argtypes = [_f64p, _f64p, _f32p, _int, _f32p, _int, _int, _int, _int]
+        lib.oracle_patch_embed_f64.restype = None
+        lib.oracle_patch_embed_f64.argtypes = [_f64p, _f64p, _f32p, _f32p, _f32p, _int, _int, _int]
         self.lib = lib
 
     def quantize_act(self, vec: np.ndarray, flavor: int = GCC):
@@ -136,6 +138,20 @@ class Oracle:
         mag = np.empty((m, n), np.float64)
         self.lib.oracle_gemm_f64(_ptr(dst, _f64p), _ptr(mag, _f64p), _ptr(mat, _f32p), mstr,
                                  _ptr(src, _f32p), sstr, m, n, k)
+        return dst, mag
+
+
+    def patch_embed_f64(self, img, pe, pe_b, psize: int):
+        """img [img_px][img_px][3], pe [dim][3][psize][psize], pe_b [dim]"""
+        img = np.ascontiguousarray(img, dtype=np.float32)
+        pe = np.ascontiguousarray(pe, dtype=np.float32)
+        pe_b = np.ascontiguousarray(pe_b, dtype=np.float32)
+        img_px, dim = img.shape[0], pe.shape[0]
+        npatch = (img_px // psize) ** 2
+        dst = np.empty((npatch, dim), np.float64)
+        mag = np.empty((npatch, dim), np.float64)
+        self.lib.oracle_patch_embed_f64(_ptr(dst, _f64p), _ptr(mag, _f64p), _ptr(img, _f32p),
+                                        _ptr(pe, _f32p), _ptr(pe_b, _f32p), img_px, psize, dim)
         return dst, mag
 
 

@@ -378,3 +378,57 @@ def test_argument_errors(gh):
         gh.matmul(1, 4, 1, 8, 1, 1, 16, 1, 2, 8, 16)
     with pytest.raises(gemma_hip.GemmaHipError, match="k="):
         gh.quantize_matmul([(1, 1, 1, 4)], 1, 70000)
+
+
+# --------------------------------------------------------------- SigLIP patch embedding
+@pytest.mark.parametrize("img_px,psize,dim", [(56, 14, 64), (896, 14, 1152), (30, 5, 17)])
+def test_patch_embed_vs_oracle(gh, oracle, img_px, psize, dim):
+    """gemma.c:4411-4448 as im2col + fp32 GEMM (896 px,
+    P = 14, dim 1152); image normalised as gemma.c:4271-4273."""
+    note(f"patch embed img_px={img_px} psize={psize} dim={dim}")
+    rng = np.random.default_rng(img_px + dim)
+    raw = rng.uniform(0, 255, (img_px, img_px, 3)).astype(np.float32)
+    img = ((raw / np.float32(255.0) - np.float32(0.5)) / np.float32(0.5)).astype(np.float32)
+    pe = (rng.standard_normal((dim, 3, psize, psize)) * 0.02).astype(np.float32)
+    pe_b = (rng.standard_normal(dim) * 0.02).astype(np.float32)
+    npatch = (img_px // psize) ** 2
+    dst = torch.empty((npatch, dim), dtype=torch.float32, device="cuda")
+    gh.patch_embed(dst, dev(img), dev(pe), dev(pe_b), img_px, psize, dim, None, stream())
+    got = host(dst)
+    rows = np.unique(np.concatenate([np.arange(min(npatch, 4)), rng.integers(0, npatch, 24)]))
+    # oracle on the sampled patches only: crop those patches into a strip
+    ppi = img_px // psize
+    ref, mag = oracle.patch_embed_f64(img, pe, pe_b, psize) if npatch <= 256 else (None, None)
+    if ref is None:
+        refs, mags = [], []
+        for pi in rows:
+            oy, ox = divmod(int(pi), ppi)
+            tile = np.ascontiguousarray(img[oy * psize:(oy + 1) * psize, ox * psize:(ox + 1) * psize])
+            r, mg = oracle.patch_embed_f64(tile, pe, pe_b, psize)
+            refs.append(r[0])
+            mags.append(mg[0])
+        ref, mag = np.array(refs), np.array(mags)
+        got = got[rows]
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= TOL_F32 * mag), f"worst {np.max(err / mag):.3e}"
+
+
+def test_patch_embed_host(gh, oracle):
+    lib = gh.lib
+    rng = np.random.default_rng(8)
+    img_px, psize, dim = 28, 14, 40
+    img = rng.standard_normal((img_px, img_px, 3)).astype(np.float32)
+    pe = (rng.standard_normal((dim, 3, psize, psize)) * 0.02).astype(np.float32)
+    pe_b = rng.standard_normal(dim).astype(np.float32)
+    gh.register_weights(pe, pe.nbytes)
+    gh.register_weights(pe_b, pe_b.nbytes)
+    try:
+        out = np.empty(((img_px // psize) ** 2, dim), np.float32)
+        rc = lib.gemma_hip_patch_embed_host(out.ctypes.data, img.ctypes.data, pe.ctypes.data,
+                                            pe_b.ctypes.data, img_px, psize, dim)
+        assert rc == 0, lib.gemma_hip_last_error()
+        ref, mag = oracle.patch_embed_f64(img, pe, pe_b, psize)
+        assert np.all(np.abs(out - ref) <= TOL_F32 * mag)
+    finally:
+        gh.release_weights(pe)
+        gh.release_weights(pe_b)

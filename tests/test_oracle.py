@@ -167,3 +167,39 @@ def test_live_against_reference_build(oracle):
         d, _ = oracle.gemm_int8(B, bs, qa, sa)
         dr, st = ref.gemm_int8(B, bs, qa, sa, k, np.zeros((m, n), np.float32))
         assert st == 0 and np.array_equal(bits(d), bits(dr))
+
+
+def test_patch_embed_one_hot_closed_form(oracle):
+    """gemma.c:4411-4448 indexing: a weight that selects one (c, py, px) per
+    output channel makes the output that image pixel plus the bias, so a
+    transposed channel, row or column index fails."""
+    rng = np.random.default_rng(4)
+    img_px, psize, dim = 28, 7, 5
+    img = rng.standard_normal((img_px, img_px, 3)).astype(np.float32)
+    pe = np.zeros((dim, 3, psize, psize), np.float32)
+    picks = [(0, 0, 0), (2, 6, 1), (1, 3, 5), (0, 6, 6), (2, 0, 4)]
+    for oc, (c, py, px) in enumerate(picks):
+        pe[oc, c, py, px] = 1.0
+    bias = rng.standard_normal(dim).astype(np.float32)
+    out, _ = oracle.patch_embed_f64(img, pe, bias, psize)
+    ppi = img_px // psize
+    for pi in range(ppi * ppi):
+        oy, ox = divmod(pi, ppi)
+        for oc, (c, py, px) in enumerate(picks):
+            want = np.float64(img[oy * psize + py, ox * psize + px, c]) + np.float64(bias[oc])
+            assert out[pi, oc] == want
+
+
+def test_patch_embed_linearity(oracle):
+    """Linear in the image: f(a*x + y) - b = a*(f(x) - b) + (f(y) - b)."""
+    rng = np.random.default_rng(5)
+    img_px, psize, dim = 14, 7, 3
+    # integer-valued images so that 2*x + y is exact in float32
+    x = rng.integers(-8, 9, (img_px, img_px, 3)).astype(np.float32)
+    y = rng.integers(-8, 9, (img_px, img_px, 3)).astype(np.float32)
+    pe = rng.standard_normal((dim, 3, psize, psize)).astype(np.float32)
+    b = rng.standard_normal(dim).astype(np.float32)
+    fx, _ = oracle.patch_embed_f64(x, pe, b, psize)
+    fy, _ = oracle.patch_embed_f64(y, pe, b, psize)
+    fz, _ = oracle.patch_embed_f64((2 * x + y).astype(np.float32), pe, b, psize)
+    assert np.allclose(fz - b, 2 * (fx - b) + (fy - b), rtol=1e-12, atol=1e-9)
