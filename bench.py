@@ -2,7 +2,7 @@
 """Benchmark of the W8A8 matmul hot path on one MI355X.
 
 Headline (BASELINE.json metric "int8 GEMV HBM GB/s + GEMM TOPS (% roofline);
-decode tok/s at gemma-3-1b shape", workload = BASELINE config 2):
+decode tok/s at gemma-3-1b shape", workload = BASELINE.json config 2):
 
   step  = one pass over the gemma-3-1b decode GEMVs q, k, v, o, gate, up,
           down and the tied LM head at M = 1, each with fp32 activations
@@ -51,7 +51,7 @@ ROT_STEPS = 8              # steps per captured graph
 METRIC = ("int8 GEMV HBM GB/s + GEMM TOPS (% roofline); decode tok/s at "
           "gemma-3-1b shape")
 
-# gemma-3-1b decode GEMVs: (name, out rows N, reduction K) -- BASELINE config 2
+# gemma-3-1b decode GEMVs: (name, out rows N, reduction K) -- BASELINE.json config 2
 SWEEP_1B = [("q", 1024, 1152), ("k", 256, 1152), ("v", 256, 1152), ("o", 1152, 1024),
             ("gate", 6912, 1152), ("up", 6912, 1152), ("down", 1152, 6912),
             ("lm_head", 262144, 1152)]
@@ -443,7 +443,7 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE config 2: W8A8 GEMV sweep at gemma-3-1b shapes, M=1 "
+            "workload": "BASELINE.json config 2: W8A8 GEMV sweep at gemma-3-1b shapes, M=1 "
                         "(q 1152->1024, k/v 1152->256, o 1024->1152, gate/up 1152->6912, "
                         "down 6912->1152, LM head 1152->262144), fp32 activations quantized "
                         "in-kernel, weights rotated through >256 MB of copies",

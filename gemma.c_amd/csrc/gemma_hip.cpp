@@ -54,6 +54,10 @@ struct State {
   gh::DeviceInfo info{};
   std::map<uintptr_t, Region> regions;  // keyed by host start address
   std::mutex lock;
+  // serialises the _host entry points, which share the staging buffer and
+  // may be called from several threads at once (the reference's prefill QKV
+  // site calls gemm_int8 from inside an OpenMP loop, gemma.c:5050-5089)
+  std::recursive_mutex host;
   // device staging for the _host entry points, grown on demand
   char *staging = nullptr;
   size_t staging_bytes = 0;
@@ -444,6 +448,7 @@ int gemma_hip_patch_embed(float *dst, const float *img, const float *pe,
 
 int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,
                                 int dim) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (dim <= 0 || !dst || !scale || !vec)
     return fail("gemma_hip_quantize_act_host: bad arguments (dim=%d)", dim);
@@ -466,6 +471,7 @@ int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,
 
 int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
                                  int sstr, int m, int n) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (sstr == 0) sstr = n;
   if (m < 0 || n <= 0 || sstr < n || !dst || !dsc || !src)
@@ -498,6 +504,7 @@ int gemma_hip_gemv_int8_host(float *dst, const int8_t *mat, const float *matsc,
 
 int gemma_hip_gemv_int8_multi_host(const gemma_hip_job *jobs, int njobs,
                                    const int8_t *vec, float vsc, int n) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (jobs == nullptr || njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS || n <= 0 || !vec)
     return fail("gemma_hip_gemv_int8_multi_host: bad arguments");
@@ -537,6 +544,7 @@ int gemma_hip_gemv_int8_multi_host(const gemma_hip_job *jobs, int njobs,
 int gemma_hip_gemm_int8_host(float *dst, int dstr, const int8_t *mat, int mstr,
                              const float *matsc, const int8_t *src, int sstr,
                              const float *ssc, int m, int n, int k) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (dstr == 0) dstr = n;
   if (mstr == 0) mstr = k;
@@ -579,6 +587,7 @@ int gemma_hip_gemv_fpx_host(float *dst, const float *mat, const float *vec,
 
 int gemma_hip_gemv_fpx_multi_host(const gemma_hip_job *jobs, int njobs,
                                   const float *vec, int n) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (jobs == nullptr || njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS || n <= 0 || !vec)
     return fail("gemma_hip_gemv_fpx_multi_host: bad arguments");
@@ -613,6 +622,7 @@ int gemma_hip_gemv_fpx_multi_host(const gemma_hip_job *jobs, int njobs,
 
 int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
                             const float *src, int sstr, int m, int n, int k) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (dstr == 0) dstr = n;
   if (mstr == 0) mstr = k;
@@ -643,6 +653,7 @@ int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
 
 int gemma_hip_patch_embed_host(float *dst, const float *img, const float *pe,
                                const float *pe_b, int img_px, int psize, int dim) {
+  std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (psize <= 0 || img_px <= 0 || dim <= 0 || img_px % psize != 0 || !dst || !img ||
       !pe || !pe_b)

@@ -156,7 +156,9 @@ int gemma_hip_patch_embed(float *dst, const float *img, const float *pe,
 /* ---- host drop-ins for the reference call sites ------------------------ */
 /* Same argument order and meaning as the reference functions named; weight
  * pointers (mat, matsc, job w/sc) must lie in registered ranges, activation
- * and output pointers are ordinary host memory. */
+ * and output pointers are ordinary host memory.  They may be called from
+ * several threads at once (the prefill QKV site calls gemm_int8 inside an
+ * OpenMP loop, gemma.c:5050-5089); such calls run one after another. */
 
 /* quantize_act (gemma.c:2590); the scale goes to *scale. */
 int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,

@@ -1,0 +1,140 @@
+"""End-to-end greedy generation through the reference program itself.
+
+oracle/_ref/gemma_e2e_cpu is gemma.c as it is; oracle/_ref/gemma_e2e_hip is
+the same source with its forward passes' quantize_act / quantize_acts /
+gemv_int8 / gemv_int8_multi / gemm_int8 calls going to libgemma_hip's host
+entry points (oracle/e2e_harness.c, oracle/e2e_retarget.sed).  Everything
+else (embedding, norms, RoPE, attention, GELU, argmax) is the reference's
+code in both, built with the same flags, so the bar is bit-identical logits
+at every step -- hashed over all steps -- and the same greedy tokens.
+
+Models are random-init .bin files in the reference's layout
+(gemma.c_amd/model_bin.py), at the BASELINE.json end-to-end shapes: config 1
+(gemma-3-270m, 32 prompt ids, 64 decode steps) and config 3's prefill
+(gemma-3-1b, 512 prompt ids) with a shortened decode.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import struct
+import subprocess
+import sys
+
+import pytest
+
+import model_bin
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+E2E_CPU = os.path.join(REPO, "oracle", "_ref", "gemma_e2e_cpu")
+E2E_HIP = os.path.join(REPO, "oracle", "_ref", "gemma_e2e_hip")
+THREADS = max(1, min(16, os.cpu_count() or 1))
+
+needs_e2e = pytest.mark.skipif(
+    not (os.path.exists(E2E_CPU) and os.path.exists(E2E_HIP)),
+    reason="oracle/_ref e2e harnesses not built (they need /root/reference)")
+
+
+def run_e2e(binary, model, prompt_len, steps, threads=THREADS, chunk=None, seed=1234):
+    cmd = [binary, model, str(prompt_len), str(steps), str(seed), str(threads)]
+    if chunk is not None:
+        cmd.append(str(chunk))
+    print("run:", " ".join(cmd), flush=True)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert out.returncode == 0, f"{binary} exited {out.returncode}: {out.stderr[-2000:]}"
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    summary = {k: res[k] for k in ("build", "prefill_tok_s", "decode_tok_s", "setup_s",
+                                   "logits_fnv")}
+    print(json.dumps(summary), flush=True)
+    sys.stdout.flush()
+    return res
+
+
+# ------------------------------------------------------------------ CPU
+def test_model_bin_header_round_trip(tmp_path):
+    """The writer's header, read back field by field (gemma.c:770-816)."""
+    path = model_bin.write_bin(str(tmp_path / "m.bin"), "gemma-3-1b", seed=3,
+                               nvocab=300, layers=7)
+    with open(path, "rb") as f:
+        assert f.read(8) == b"GEMAf32Q"
+        cfg = struct.unpack(">BBBHHHHHHIIfffff", f.read(43))
+        assert cfg[:11] == (7, 4, 1, 256, 1152, 6912, 256, 512, 256, 32768, 300)
+        assert cfg[11:] == (10000.0, 1000000.0, struct.unpack(">f", struct.pack(">f", 1e-6))[0],
+                            0.0, 0.0)
+        nbytes = f.read(1)[0]
+        swa = f.read(nbytes)
+        bits = [(swa[i // 8] >> (7 - i % 8)) & 1 for i in range(7)]
+        assert bits == [1, 1, 1, 1, 1, 0, 1]  # every sixth layer is global
+        assert f.read(1)[0] == 7
+        words = []
+        for _ in range(300):
+            n = f.read(1)[0]
+            words.append(f.read(n).decode())
+        assert words[:6] == model_bin.SPECIALS and words[299] == "t299"
+        assert struct.unpack(">I", f.read(4))[0] == 1
+        f.read(2 + 2)  # the one merge: "t" + "0"
+        tensors_at = f.tell()
+    dim, q, kv, mlp = 1152, 1024, 256, 6912
+    qt = lambda n, k: n * k + 4 * n  # noqa: E731
+    per_layer = (qt(q, dim) + 2 * qt(kv, dim) + qt(dim, q) + 2 * 256 * 4
+                 + 2 * qt(mlp, dim) + qt(dim, mlp) + 4 * dim * 4)
+    assert os.path.getsize(path) == tensors_at + qt(300, dim) + 7 * per_layer + dim * 4
+
+
+def test_model_bin_weights_quantize_like_export():
+    """Per-row int8 weights: the largest |w| of each row maps to +-127 and the
+    scale is max(amax, 1e-8) / 127 (model.py:151-161)."""
+    import numpy as np
+
+    rng = np.random.default_rng(0)
+    w = rng.standard_normal((64, 96)).astype(np.float32) * np.float32(0.02)
+    w[5] = 0.0
+    q, s = model_bin.quantize_rows(w)
+    amax = np.abs(w).max(axis=1)
+    assert np.all(np.abs(q[np.arange(64) != 5]).max(axis=1) == 127)
+    assert not q[5].any() and s[5] == np.float32(1e-8) / np.float32(127)
+    err = np.abs(q.astype(np.float32) * s[:, None] - w)
+    assert np.all(err <= s[:, None] * 0.5000001)
+    assert np.allclose(s[np.arange(64) != 5], amax[np.arange(64) != 5] / 127, rtol=1e-7)
+
+
+@needs_e2e
+def test_reference_runs_written_model_deterministically(tmp_path):
+    """The reference's loader accepts the writer's file, and its greedy run
+    does not depend on the thread count (the GPU comparison below runs both
+    builds with the same count, but must not hinge on it).  The prefill chunk
+    size does change the reference's fp32 attention order, and so its
+    logits, so both runs use the same chunk."""
+    path = model_bin.write_bin(str(tmp_path / "tiny.bin"), "gemma-3-270m", seed=5,
+                               nvocab=2048, layers=3)
+    a = run_e2e(E2E_CPU, path, 9, 6, threads=2, chunk=4)
+    b = run_e2e(E2E_CPU, path, 9, 6, threads=5, chunk=4)
+    assert a["tokens"] == b["tokens"] and a["logits_fnv"] == b["logits_fnv"]
+    assert len(a["tokens"]) == 7 and all(0 <= t < 2048 for t in a["tokens"])
+
+
+# ------------------------------------------------------------------ GPU
+@pytest.fixture(scope="module")
+def model_dir(tmp_path_factory):
+    return str(tmp_path_factory.mktemp("models"))
+
+
+@pytest.mark.gpu
+@needs_e2e
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("name,prompt_len,steps,chunk", [
+    ("gemma-3-270m", 32, 64, None),   # config 1
+    ("gemma-3-270m", 40, 8, 16),      # chunked prefill: M = 16, 16, 8
+    ("gemma-3-1b", 512, 16, None),    # config 3's prefill (M = 512)
+])
+def test_e2e_hip_build_matches_reference(model_dir, name, prompt_len, steps, chunk):
+    path = model_bin.ensure_bin(model_dir, name)
+    ref = run_e2e(E2E_CPU, path, prompt_len, steps, chunk=chunk)
+    hip = run_e2e(E2E_HIP, path, prompt_len, steps, chunk=chunk)
+    assert hip["prompt"] == ref["prompt"]
+    assert hip["tokens"] == ref["tokens"], "greedy token streams differ"
+    assert hip["logits_fnv"] == ref["logits_fnv"], "logits differ in some bit"
+    # the library really ran: every int8 op of the HIP build went through it
+    assert hip["weight_bytes"] > 0
+    assert "gemm_int8" in hip["ops"]["prefill"] and "gemv_int8" in hip["ops"]["decode"]

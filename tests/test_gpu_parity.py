@@ -128,7 +128,7 @@ def test_gemv_multi_golden(gh, golden):
     assert np.array_equal(bits(y), bits(g["y"]))
 
 
-# BASELINE config 2: the gemma-3-1b decode GEMVs (out rows, in K)
+# BASELINE.json config 2: the gemma-3-1b decode GEMVs (out rows, in K)
 SWEEP_1B = [("q", 1024, 1152), ("k", 256, 1152), ("v", 256, 1152), ("o", 1152, 1024),
             ("gate", 6912, 1152), ("up", 6912, 1152), ("down", 1152, 6912),
             ("lm_head", 262144, 1152)]
@@ -383,7 +383,7 @@ def test_argument_errors(gh):
 # --------------------------------------------------------------- SigLIP patch embedding
 @pytest.mark.parametrize("img_px,psize,dim", [(56, 14, 64), (896, 14, 1152), (30, 5, 17)])
 def test_patch_embed_vs_oracle(gh, oracle, img_px, psize, dim):
-    """gemma.c:4411-4448 as im2col + fp32 GEMM (BASELINE config 4: 896 px,
+    """gemma.c:4411-4448 as im2col + fp32 GEMM (BASELINE.json config 4: 896 px,
     P = 14, dim 1152); image normalised as gemma.c:4271-4273."""
     note(f"patch embed img_px={img_px} psize={psize} dim={dim}")
     rng = np.random.default_rng(img_px + dim)
