@@ -64,6 +64,28 @@ struct State {
   // im2col workspace of the patch embedding, grown on demand
   float *work = nullptr;
   size_t work_bytes = 0;
+  // pinned host staging of the _host entry points: small activations are
+  // read by the kernels and small outputs written by them in place, so a
+  // decode call costs one launch and one synchronisation
+  char *pinned = nullptr;
+  char *pinned_dev = nullptr;  // the same memory as kernels address it
+  size_t pinned_bytes = 0;
+  // the last activations a _host quantize produced: the device copy, and a
+  // pinned mirror of what the caller received.  A following matmul whose
+  // int8 input and scales are byte-equal to (part of) the mirror reads the
+  // device copy instead of uploading them again.
+  struct {
+    bool valid = false;
+    const int8_t *host_q = nullptr;  // the caller's dst
+    int m = 0, n = 0;
+    int8_t *dev_q = nullptr;
+    float *dev_s = nullptr;
+    int8_t *mir_q = nullptr;  // pinned mirror, host view
+    float *mir_s = nullptr;
+    int8_t *mir_q_dev = nullptr;  // pinned mirror, device view
+    float *mir_s_dev = nullptr;
+    size_t cap_q = 0, cap_s = 0;
+  } act;
 };
 
 State g;
@@ -101,6 +123,81 @@ int staging_reserve(size_t bytes) {
   GH_CHECK("gemma_hip staging alloc", hipMalloc(&g.staging, want));
   g.staging_bytes = want;
   return 0;
+}
+
+int pinned_reserve(size_t bytes) {
+  if (bytes <= g.pinned_bytes) return 0;
+  if (g.pinned != nullptr) {
+    GH_CHECK("gemma_hip pinned sync", hipStreamSynchronize(g.stream));
+    GH_CHECK("gemma_hip pinned free", hipHostFree(g.pinned));
+    g.pinned = nullptr;
+    g.pinned_bytes = 0;
+  }
+  size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+  GH_CHECK("gemma_hip pinned alloc",
+           hipHostMalloc((void **)&g.pinned, want, hipHostMallocMapped));
+  g.pinned_bytes = want;
+  GH_CHECK("gemma_hip pinned map",
+           hipHostGetDevicePointer((void **)&g.pinned_dev, g.pinned, 0));
+  return 0;
+}
+
+// Room for m x n quantized activations in the activation cache.
+int act_reserve(int m, int n) {
+  g.act.valid = false;
+  const size_t q = (size_t)m * n, sc = (size_t)m * 4;
+  if (q > g.act.cap_q || sc > g.act.cap_s) {
+    GH_CHECK("gemma_hip act sync", hipStreamSynchronize(g.stream));
+    if (g.act.dev_q != nullptr) GH_CHECK("gemma_hip act free", hipFree(g.act.dev_q));
+    if (g.act.mir_q != nullptr) GH_CHECK("gemma_hip act free", hipHostFree(g.act.mir_q));
+    g.act.dev_q = nullptr;
+    g.act.mir_q = nullptr;
+    g.act.cap_q = g.act.cap_s = 0;
+    const size_t want_q = (q < (1u << 16) ? (1u << 16) : q + 255) / 256 * 256;
+    const size_t want_s = (sc < 4096 ? 4096 : sc + 255) / 256 * 256;
+    char *dev = nullptr, *mir = nullptr;
+    GH_CHECK("gemma_hip act alloc", hipMalloc((void **)&dev, want_q + want_s));
+    char *mir_dev = nullptr;
+    hipError_t e = hipHostMalloc((void **)&mir, want_q + want_s, hipHostMallocMapped);
+    if (e == hipSuccess) e = hipHostGetDevicePointer((void **)&mir_dev, mir, 0);
+    if (e != hipSuccess) {
+      (void)hipFree(dev);
+      if (mir != nullptr) (void)hipHostFree(mir);
+      return hip_fail("gemma_hip act alloc", e);
+    }
+    g.act.dev_q = (int8_t *)dev;
+    g.act.dev_s = (float *)(dev + want_q);
+    g.act.mir_q = (int8_t *)mir;
+    g.act.mir_s = (float *)(mir + want_q);
+    g.act.mir_q_dev = (int8_t *)mir_dev;
+    g.act.mir_s_dev = (float *)(mir_dev + want_q);
+    g.act.cap_q = want_q;
+    g.act.cap_s = want_s;
+  }
+  return 0;
+}
+
+// Row r0 of the cached activations when the caller's int8 rows [src, m rows
+// of stride sstr, k used bytes each] and their scales are byte-equal to what
+// the last _host quantize handed out from rows r0.. of the cache; else -1.
+// `scales` is the caller's scale array, or null with `one_scale` holding the
+// by-value scale of a single row (gemv_int8's vsc).
+int act_lookup(const int8_t *src, int sstr, const float *scales, float one_scale,
+               int m, int k) {
+  const auto &a = g.act;
+  if (!a.valid || src == nullptr || k > a.n || (m > 1 && sstr != a.n)) return -1;
+  const uintptr_t off = (uintptr_t)src - (uintptr_t)a.host_q;
+  if ((uintptr_t)src < (uintptr_t)a.host_q || off % (size_t)a.n != 0) return -1;
+  const size_t r0 = off / (size_t)a.n;
+  if (r0 + (size_t)m > (size_t)a.m) return -1;
+  const size_t span = (size_t)(m - 1) * a.n + k;
+  if (memcmp(src, a.mir_q + r0 * a.n, span) != 0) return -1;
+  if (scales != nullptr) {
+    if (memcmp(scales, a.mir_s + r0, (size_t)m * 4) != 0) return -1;
+  } else if (m != 1 || memcmp(&one_scale, a.mir_s + r0, 4) != 0) {
+    return -1;
+  }
+  return (int)r0;
 }
 
 // Carves aligned pieces out of the staging buffer.
@@ -196,6 +293,13 @@ void gemma_hip_shutdown(void) {
   if (g.work != nullptr) (void)hipFree(g.work);
   g.work = nullptr;
   g.work_bytes = 0;
+  if (g.pinned != nullptr) (void)hipHostFree(g.pinned);
+  g.pinned = nullptr;
+  g.pinned_dev = nullptr;
+  g.pinned_bytes = 0;
+  if (g.act.dev_q != nullptr) (void)hipFree(g.act.dev_q);
+  if (g.act.mir_q != nullptr) (void)hipHostFree(g.act.mir_q);
+  g.act = {};
   (void)hipStreamDestroy(g.stream);
   g.stream = nullptr;
   g.ready = false;
@@ -446,27 +550,17 @@ int gemma_hip_patch_embed(float *dst, const float *img, const float *pe,
 
 /* ---- host drop-ins ------------------------------------------------------ */
 
+// Inputs up to this size are read by the kernels straight from pinned host
+// memory; larger ones are first copied to the device (DMA at full PCIe rate).
+constexpr size_t kZeroCopyIn = 256u << 10;
+
 int gemma_hip_quantize_act_host(int8_t *dst, float *scale, const float *vec,
                                 int dim) {
   std::lock_guard<std::recursive_mutex> serial(g.host);
   if (need_init()) return 1;
   if (dim <= 0 || !dst || !scale || !vec)
     return fail("gemma_hip_quantize_act_host: bad arguments (dim=%d)", dim);
-  Carver c;
-  size_t o_src = c.take((size_t)dim * 4), o_q = c.take(dim), o_s = c.take(4);
-  if (staging_reserve(c.used)) return 1;
-  char *base = g.staging;
-  GH_CHECK("quantize_act_host: H2D",
-           hipMemcpyAsync(base + o_src, vec, (size_t)dim * 4, hipMemcpyHostToDevice, g.stream));
-  if (gemma_hip_quantize((int8_t *)(base + o_q), (float *)(base + o_s),
-                         (const float *)(base + o_src), dim, 1, dim, g.stream))
-    return 1;
-  GH_CHECK("quantize_act_host: D2H",
-           hipMemcpyAsync(dst, base + o_q, dim, hipMemcpyDeviceToHost, g.stream));
-  GH_CHECK("quantize_act_host: D2H",
-           hipMemcpyAsync(scale, base + o_s, 4, hipMemcpyDeviceToHost, g.stream));
-  GH_CHECK("quantize_act_host: sync", hipStreamSynchronize(g.stream));
-  return 0;
+  return gemma_hip_quantize_acts_host(dst, scale, vec, dim, 1, dim);
 }
 
 int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
@@ -477,22 +571,26 @@ int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
   if (m < 0 || n <= 0 || sstr < n || !dst || !dsc || !src)
     return fail("gemma_hip_quantize_acts_host: bad arguments");
   if (m == 0) return 0;
-  const size_t in_floats = (size_t)(m - 1) * sstr + n;
-  Carver c;
-  size_t o_src = c.take(in_floats * 4), o_q = c.take((size_t)m * n),
-         o_s = c.take((size_t)m * 4);
-  if (staging_reserve(c.used)) return 1;
-  char *base = g.staging;
-  GH_CHECK("quantize_acts_host: H2D",
-           hipMemcpyAsync(base + o_src, src, in_floats * 4, hipMemcpyHostToDevice, g.stream));
-  if (gemma_hip_quantize((int8_t *)(base + o_q), (float *)(base + o_s),
-                         (const float *)(base + o_src), sstr, m, n, g.stream))
-    return 1;
-  GH_CHECK("quantize_acts_host: D2H",
-           hipMemcpyAsync(dst, base + o_q, (size_t)m * n, hipMemcpyDeviceToHost, g.stream));
-  GH_CHECK("quantize_acts_host: D2H",
-           hipMemcpyAsync(dsc, base + o_s, (size_t)m * 4, hipMemcpyDeviceToHost, g.stream));
+  const size_t in_bytes = ((size_t)(m - 1) * sstr + n) * 4;
+  if (act_reserve(m, n) || pinned_reserve(in_bytes)) return 1;
+  memcpy(g.pinned, src, in_bytes);
+  const float *in = (const float *)g.pinned_dev;
+  if (in_bytes > kZeroCopyIn) {
+    if (staging_reserve(in_bytes)) return 1;
+    GH_CHECK("quantize_acts_host: H2D",
+             hipMemcpyAsync(g.staging, g.pinned, in_bytes, hipMemcpyHostToDevice, g.stream));
+    in = (const float *)g.staging;
+  }
+  GH_CHECK("quantize_acts_host: launch",
+           gh::launch_quantize(g.act.dev_q, g.act.dev_s, in, sstr, m, n, g.stream,
+                               g.act.mir_q_dev, g.act.mir_s_dev));
   GH_CHECK("quantize_acts_host: sync", hipStreamSynchronize(g.stream));
+  memcpy(dst, g.act.mir_q, (size_t)m * n);
+  memcpy(dsc, g.act.mir_s, (size_t)m * 4);
+  g.act.host_q = dst;
+  g.act.m = m;
+  g.act.n = n;
+  g.act.valid = true;
   return 0;
 }
 
@@ -509,35 +607,47 @@ int gemma_hip_gemv_int8_multi_host(const gemma_hip_job *jobs, int njobs,
   if (jobs == nullptr || njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS || n <= 0 || !vec)
     return fail("gemma_hip_gemv_int8_multi_host: bad arguments");
   gemma_hip_job djobs[GEMMA_HIP_MAX_JOBS];
+  // outputs go straight to pinned memory; the int8 input comes from the
+  // activation cache when it is what the last quantize returned
   Carver c;
-  size_t o_x = c.take(n), o_s = c.take(4), o_y[GEMMA_HIP_MAX_JOBS];
+  size_t o_y[GEMMA_HIP_MAX_JOBS];
   for (int j = 0; j < njobs; ++j) {
     if (jobs[j].m < 0) return fail("gemma_hip_gemv_int8_multi_host: job %d m<0", j);
     o_y[j] = c.take((size_t)jobs[j].m * 4);
   }
-  if (staging_reserve(c.used)) return 1;
-  char *base = g.staging;
+  const size_t o_x = c.take(n), o_s = c.take(4);
+  if (pinned_reserve(c.used)) return 1;
+  char *pin = g.pinned;
   for (int j = 0; j < njobs; ++j) {
     const size_t rows = (size_t)jobs[j].m;
     const void *w = rows ? resolve(jobs[j].w, rows * n) : nullptr;
     const void *sc = rows ? resolve(jobs[j].sc, rows * 4) : nullptr;
     if (rows && (w == nullptr || sc == nullptr))
       return fail("gemma_hip_gemv_int8_multi_host: job %d weights are not registered", j);
-    djobs[j] = gemma_hip_job{w, (const float *)sc, (float *)(base + o_y[j]), jobs[j].m};
+    djobs[j] = gemma_hip_job{w, (const float *)sc, (float *)(g.pinned_dev + o_y[j]),
+                             jobs[j].m};
   }
-  GH_CHECK("gemv_int8_host: H2D",
-           hipMemcpyAsync(base + o_x, vec, n, hipMemcpyHostToDevice, g.stream));
-  GH_CHECK("gemv_int8_host: H2D",
-           hipMemcpyAsync(base + o_s, &vsc, 4, hipMemcpyHostToDevice, g.stream));
-  if (gemma_hip_matmul_multi(djobs, njobs, (const int8_t *)(base + o_x),
-                             (const float *)(base + o_s), n, g.stream))
-    return 1;
-  for (int j = 0; j < njobs; ++j)
-    if (jobs[j].m > 0)
-      GH_CHECK("gemv_int8_host: D2H",
-               hipMemcpyAsync(jobs[j].dst, base + o_y[j], (size_t)jobs[j].m * 4,
-                              hipMemcpyDeviceToHost, g.stream));
+  const int8_t *xq;
+  const float *xs;
+  const int r0 = act_lookup(vec, n, nullptr, vsc, 1, n);
+  if (r0 >= 0) {
+    xq = g.act.dev_q + (size_t)r0 * g.act.n;
+    xs = g.act.dev_s + r0;
+  } else {
+    if (staging_reserve(256 + (size_t)n)) return 1;
+    memcpy(pin + o_x, vec, n);
+    memcpy(pin + o_s, &vsc, 4);
+    GH_CHECK("gemv_int8_host: H2D",
+             hipMemcpyAsync(g.staging + 256, pin + o_x, n, hipMemcpyHostToDevice, g.stream));
+    GH_CHECK("gemv_int8_host: H2D",
+             hipMemcpyAsync(g.staging, pin + o_s, 4, hipMemcpyHostToDevice, g.stream));
+    xq = (const int8_t *)(g.staging + 256);
+    xs = (const float *)g.staging;
+  }
+  if (gemma_hip_matmul_multi(djobs, njobs, xq, xs, n, g.stream)) return 1;
   GH_CHECK("gemv_int8_host: sync", hipStreamSynchronize(g.stream));
+  for (int j = 0; j < njobs; ++j)
+    if (jobs[j].m > 0) memcpy(jobs[j].dst, pin + o_y[j], (size_t)jobs[j].m * 4);
   return 0;
 }
 
@@ -564,13 +674,20 @@ int gemma_hip_gemm_int8_host(float *dst, int dstr, const int8_t *mat, int mstr,
          o_y = c.take((size_t)m * dstr * 4);
   if (staging_reserve(c.used)) return 1;
   char *base = g.staging;
-  GH_CHECK("gemm_int8_host: H2D",
-           hipMemcpyAsync(base + o_a, src, src_bytes, hipMemcpyHostToDevice, g.stream));
-  GH_CHECK("gemm_int8_host: H2D",
-           hipMemcpyAsync(base + o_as, ssc, (size_t)m * 4, hipMemcpyHostToDevice, g.stream));
+  const int8_t *a = (const int8_t *)(base + o_a);
+  const float *as = (const float *)(base + o_as);
+  const int r0 = act_lookup(src, sstr, ssc, 0.0f, m, k);
+  if (r0 >= 0) {
+    a = g.act.dev_q + (size_t)r0 * g.act.n;
+    as = g.act.dev_s + r0;
+  } else {
+    GH_CHECK("gemm_int8_host: H2D",
+             hipMemcpyAsync(base + o_a, src, src_bytes, hipMemcpyHostToDevice, g.stream));
+    GH_CHECK("gemm_int8_host: H2D",
+             hipMemcpyAsync(base + o_as, ssc, (size_t)m * 4, hipMemcpyHostToDevice, g.stream));
+  }
   if (gemma_hip_matmul((float *)(base + o_y), dstr, (const int8_t *)dmat, mstr,
-                       (const float *)dsc, (const int8_t *)(base + o_a), sstr,
-                       (const float *)(base + o_as), m, n, k, g.stream))
+                       (const float *)dsc, a, sstr, as, m, n, k, g.stream))
     return 1;
   GH_CHECK("gemm_int8_host: D2H",
            hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,

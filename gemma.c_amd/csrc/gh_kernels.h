@@ -27,9 +27,11 @@ struct DeviceInfo {
   int cus;  // compute units
 };
 
-// quantize.hip: rows of src [m][sstr] -> dst [m][n] int8 + dsc [m]
+// quantize.hip: rows of src [m][sstr] -> dst [m][n] int8 + dsc [m], and the
+// same into the mirror mdst/mdsc when given (pinned host memory)
 hipError_t launch_quantize(int8_t *dst, float *dsc, const float *src, int sstr,
-                           int m, int n, hipStream_t stream);
+                           int m, int n, hipStream_t stream,
+                           int8_t *mdst = nullptr, float *mdsc = nullptr);
 
 // gemv.hip: int8 GEMV over jobs.  Either xq/xs (already quantized) or xf
 // (fp32, quantized inside the kernel; xq_out/xs_out nullable) is given.

@@ -349,6 +349,66 @@ def test_host_entry_points(gh, oracle):
         gh.release_weights(ws)
 
 
+def test_host_activation_reuse(gh, oracle):
+    """The host entry points reuse the device copy of the last quantized
+    activations only when the caller's int8 rows and scales are byte-equal
+    to what that quantize returned: interior row blocks (the prefill QKV
+    site's token blocks) and single rows hit, edited bytes or scales miss,
+    and every result matches the oracle on the caller's actual inputs."""
+    import ctypes
+
+    lib = gh.lib
+    rng = np.random.default_rng(23)
+    n_out, k = 96, 1152
+    W = rng.integers(-127, 128, (n_out, k), dtype=np.int8)
+    ws = rng.uniform(1e-3, 1e-2, n_out).astype(np.float32)
+    gh.register_weights(W, W.nbytes)
+    gh.register_weights(ws, ws.nbytes)
+
+    def gemm(Aq, As, r0, m):
+        dst = np.zeros((m, n_out), np.float32)
+        rc = lib.gemma_hip_gemm_int8_host(dst.ctypes.data, 0, W.ctypes.data, 0, ws.ctypes.data,
+                                          Aq[r0:].ctypes.data, 0, As[r0:].ctypes.data,
+                                          m, n_out, k)
+        assert rc == 0, lib.gemma_hip_last_error()
+        ref, _ = oracle.gemm_int8(W, ws, Aq[r0:r0 + m], As[r0:r0 + m])
+        assert np.array_equal(bits(dst), bits(ref)), f"rows {r0}..{r0 + m}"
+
+    try:
+        # 160 rows of 1152 floats: larger than the zero-copy limit, and a
+        # source row stride wider than the row
+        m, sstr = 160, k + 8
+        A = outlier_acts(rng, (m, sstr))
+        Aq = np.empty((m, k), np.int8)
+        As = np.empty(m, np.float32)
+        assert lib.gemma_hip_quantize_acts_host(Aq.ctypes.data, As.ctypes.data, A.ctypes.data,
+                                                sstr, m, k) == 0
+        qo, so = oracle.quantize_acts(np.ascontiguousarray(A[:, :k]))
+        assert np.array_equal(Aq, qo) and np.array_equal(bits(As), bits(so))
+        for r0, mm in ((0, 128), (128, 32), (37, 5)):
+            gemm(Aq, As, r0, mm)
+        # one row of the batch as a GEMV input
+        y = np.empty(n_out, np.float32)
+        rc = lib.gemma_hip_gemv_int8_host(y.ctypes.data, W.ctypes.data, ws.ctypes.data,
+                                          Aq[3].ctypes.data, ctypes.c_float(As[3]), n_out, k)
+        assert rc == 0, lib.gemma_hip_last_error()
+        yo, _ = oracle.gemv_int8(W, ws, Aq[3], As[3])
+        assert np.array_equal(bits(y), bits(yo))
+        # the caller edits one int8 value, then one scale: both must be seen
+        Aq[40, 7] = 127 if Aq[40, 7] != 127 else -127
+        gemm(Aq, As, 32, 16)
+        As[45] *= np.float32(2.0)
+        gemm(Aq, As, 32, 16)
+        rc = lib.gemma_hip_gemv_int8_host(y.ctypes.data, W.ctypes.data, ws.ctypes.data,
+                                          Aq[3].ctypes.data, ctypes.c_float(As[3] * 2), n_out, k)
+        assert rc == 0, lib.gemma_hip_last_error()
+        yo, _ = oracle.gemv_int8(W, ws, Aq[3], As[3] * np.float32(2))
+        assert np.array_equal(bits(y), bits(yo))
+    finally:
+        gh.release_weights(W)
+        gh.release_weights(ws)
+
+
 def test_host_fp32_entry_points(gh, oracle):
     lib = gh.lib
     rng = np.random.default_rng(22)
