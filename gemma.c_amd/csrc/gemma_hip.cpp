@@ -11,12 +11,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "gh_kernels.h"
 
@@ -796,6 +798,379 @@ int gemma_hip_patch_embed_host(float *dst, const float *img, const float *pe,
            hipMemcpyAsync(dst, base + o_y, npatch * dim * 4, hipMemcpyDeviceToHost, g.stream));
   GH_CHECK("patch_embed_host: sync", hipStreamSynchronize(g.stream));
   return 0;
+}
+
+}  // extern "C"
+
+/* ---- device-resident decoder -------------------------------------------- */
+
+struct gemma_hip_decoder {
+  gemma_hip_text_config cfg{};
+  std::vector<unsigned char> swa;
+  int clen = 0, block = 64, max_blocks = 0, nparts = 256;
+  struct Layer {
+    const int8_t *w[7];  // wq wk wv wo w1(up) w2(gate) w3(down), device
+    const float *s[7];
+    float *nq, *nk, *n1, *n2, *n3, *n4;  // device copies
+  };
+  std::vector<Layer> layers;
+  const int8_t *emb = nullptr;
+  const float *emb_s = nullptr;
+  float *fnorm = nullptr;
+  char *mem = nullptr;  // every device buffer below lives in this allocation
+  float *x[2]{}, *xq = nullptr, *xk = nullptr, *xv = nullptr, *xo = nullptr;
+  float *yattn = nullptr, *gbuf = nullptr, *ymlp = nullptr, *h = nullptr;
+  float *logits = nullptr, *rope_l = nullptr, *rope_g = nullptr;
+  double *part = nullptr;
+  float *kv = nullptr, *pval = nullptr;
+  int *pidx = nullptr, *step = nullptr, *tokens = nullptr;
+  int *pin = nullptr;  // pinned: step upload [4] and token readback [1]
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+void decoder_free(gemma_hip_decoder *d) {
+  if (d == nullptr) return;
+  if (d->exec != nullptr) (void)hipGraphExecDestroy(d->exec);
+  if (d->graph != nullptr) (void)hipGraphDestroy(d->graph);
+  if (d->mem != nullptr) (void)hipFree(d->mem);
+  if (d->pin != nullptr) (void)hipHostFree(d->pin);
+  delete d;
+}
+
+// Enqueues one decode step on `st` (captured into the decoder's graph).
+hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
+  const gemma_hip_text_config &c = d->cfg;
+  const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim;
+  hipError_t e;
+  gh::DecEmbed em{d->emb, d->emb_s, d->x[0], d->step, c.dim, c.nvocab, d->clen,
+                  c.mlp_pre ? 1.0f : sqrtf((float)c.dim)};
+  if ((e = gh::launch_dec_embed(em, st)) != hipSuccess) return e;
+  int cur = 0;
+  for (int l = 0; l < c.nl; ++l) {
+    const auto &L = d->layers[l];
+    // residual of the previous MLP (post-FFN norm), pre-attention norm, q/k/v
+    gh::DecNorm n1{d->x[cur], l > 0 ? d->ymlp : nullptr,
+                   (l > 0 && c.mlp_pst) ? d->layers[l - 1].n4 : nullptr, L.n1,
+                   d->x[cur ^ 1], nullptr, c.dim, c.eps};
+    gh::GemvJobs qkv{};
+    qkv.w[0] = L.w[0]; qkv.w[1] = L.w[1]; qkv.w[2] = L.w[2];
+    qkv.sc[0] = L.s[0]; qkv.sc[1] = L.s[1]; qkv.sc[2] = L.s[2];
+    qkv.dst[0] = d->xq; qkv.dst[1] = d->xk; qkv.dst[2] = d->xv;
+    qkv.end[0] = q_sz; qkv.end[1] = q_sz + kv_sz; qkv.end[2] = qkv.end[3] = q_sz + 2 * kv_sz;
+    qkv.njobs = 3;
+    if ((e = gh::launch_dec_norm_gemv(n1, qkv, q_sz + 2 * kv_sz, c.dim, false, g.info, st)) !=
+        hipSuccess)
+      return e;
+    cur ^= 1;
+    // attention
+    const size_t cache = (size_t)d->clen * kv_sz;
+    float *kc = d->kv + (size_t)l * 2 * cache;
+    const bool sliding = d->swa[l] != 0;
+    gh::DecAttn at{d->xq, d->xk, d->xv, c.qk_norm ? L.nq : nullptr, c.qk_norm ? L.nk : nullptr,
+                   sliding ? d->rope_l : d->rope_g, kc, kc + cache, d->part, d->xo, d->step,
+                   c.n_heads, c.nkv, c.hdim, d->clen, sliding ? c.slide : 0, d->block,
+                   d->max_blocks, c.nvocab, (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att,
+                   c.eps};
+    if ((e = gh::launch_dec_attention(at, st)) != hipSuccess) return e;
+    // o projection (quantize fused)
+    gh::GemvJobs o{};
+    o.w[0] = L.w[3]; o.sc[0] = L.s[3]; o.dst[0] = d->yattn;
+    for (int j = 0; j < gh::kMaxJobs; ++j) o.end[j] = c.dim;
+    o.njobs = 1;
+    if ((e = gh::launch_gemv_i8(o, q_sz, nullptr, nullptr, d->xo, nullptr, nullptr, g.info, st)) !=
+        hipSuccess)
+      return e;
+    // residual of the attention (post-attention norm), pre-FFN norm, gate/up + GELU
+    gh::DecNorm n3{d->x[cur], d->yattn, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
+                   d->x[cur ^ 1], nullptr, c.dim, c.eps};
+    gh::GemvJobs gu{};
+    gu.w[0] = L.w[5]; gu.w[1] = L.w[4];  // gate (w2), up (w1): gemma.c:4911-4915
+    gu.sc[0] = L.s[5]; gu.sc[1] = L.s[4];
+    gu.dst[0] = d->gbuf; gu.dst[1] = d->gbuf;
+    gu.end[0] = gu.end[1] = gu.end[2] = gu.end[3] = 2 * c.mlp_dim;
+    gu.njobs = 2;
+    if ((e = gh::launch_dec_norm_gemv(n3, gu, 2 * c.mlp_dim, c.dim, true, g.info, st)) !=
+        hipSuccess)
+      return e;
+    cur ^= 1;
+    // down projection (quantize fused)
+    gh::GemvJobs dn{};
+    dn.w[0] = L.w[6]; dn.sc[0] = L.s[6]; dn.dst[0] = d->ymlp;
+    for (int j = 0; j < gh::kMaxJobs; ++j) dn.end[j] = c.dim;
+    dn.njobs = 1;
+    if ((e = gh::launch_gemv_i8(dn, c.mlp_dim, nullptr, nullptr, d->gbuf, nullptr, nullptr,
+                                g.info, st)) != hipSuccess)
+      return e;
+  }
+  // last residual, final norm, LM head (tied embedding), softcap, argmax
+  gh::DecNorm fn{d->x[cur], d->ymlp, c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm,
+                 nullptr, d->h, c.dim, c.eps};
+  if ((e = gh::launch_dec_final_norm(fn, st)) != hipSuccess) return e;
+  gh::GemvJobs lm{};
+  lm.w[0] = d->emb; lm.sc[0] = d->emb_s; lm.dst[0] = d->logits;
+  for (int j = 0; j < gh::kMaxJobs; ++j) lm.end[j] = c.nvocab;
+  lm.njobs = 1;
+  if ((e = gh::launch_gemv_i8(lm, c.dim, nullptr, nullptr, d->h, nullptr, nullptr, g.info, st)) !=
+      hipSuccess)
+    return e;
+  if (c.sc_log != 0.0f &&
+      (e = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st)) != hipSuccess)
+    return e;
+  return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
+                               d->tokens, d->clen, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
+                                            const gemma_hip_layer *layers,
+                                            const int8_t *emb, const float *emb_s,
+                                            const float *fnorm, int clen) {
+  if (need_init()) return nullptr;
+  if (cfg == nullptr || layers == nullptr || emb == nullptr || emb_s == nullptr ||
+      fnorm == nullptr || cfg->swa == nullptr) {
+    fail("gemma_hip_decoder_create: null argument");
+    return nullptr;
+  }
+  const gemma_hip_text_config c = *cfg;
+  if (c.nl <= 0 || c.n_heads <= 0 || c.nkv <= 0 || c.n_heads % c.nkv != 0 || c.hdim <= 0 ||
+      c.hdim % 2 != 0 || c.dim <= 0 || c.dim % 16 != 0 || c.dim > 6144 || c.mlp_dim <= 0 ||
+      c.mlp_dim % 16 != 0 || c.nvocab <= 0 || c.q_scale <= 0 || clen <= 0 || c.slide < 0 ||
+      (c.n_heads * c.hdim) % 16 != 0) {
+    fail("gemma_hip_decoder_create: unsupported config (nl=%d heads=%d/%d hdim=%d dim=%d "
+         "mlp=%d vocab=%d clen=%d)", c.nl, c.n_heads, c.nkv, c.hdim, c.dim, c.mlp_dim, c.nvocab,
+         clen);
+    return nullptr;
+  }
+  for (int l = 0; l < c.nl; ++l)
+    if (c.swa[l] && c.slide <= 0) {
+      fail("gemma_hip_decoder_create: layer %d slides but slide = %d", l, c.slide);
+      return nullptr;
+    }
+  gemma_hip_decoder *d = new gemma_hip_decoder();
+  d->cfg = c;
+  d->swa.assign(c.swa, c.swa + c.nl);
+  d->cfg.swa = nullptr;
+  d->clen = clen;
+  d->max_blocks = (clen + d->block - 1) / d->block;
+  const int hn = c.n_heads / c.nkv;
+  if ((size_t)hn * d->block * 8 + ((size_t)hn * c.hdim + 2 * (size_t)c.hdim) * 4 > 65536) {
+    fail("gemma_hip_decoder_create: attention tile exceeds 64 KB of LDS");
+    decoder_free(d);
+    return nullptr;
+  }
+  const size_t q_sz = (size_t)c.n_heads * c.hdim, kv_sz = (size_t)c.nkv * c.hdim;
+  const size_t dim = c.dim, mlp = c.mlp_dim;
+  // resolve every weight; rows must be 16-byte aligned on the device
+  auto weight = [&](const void *host, size_t bytes, const char *what, const void **out) {
+    const char *p = resolve(host, bytes);
+    if (p == nullptr) return fail("gemma_hip_decoder_create: %s is not registered", what);
+    if ((uintptr_t)p % 16 != 0)
+      return fail("gemma_hip_decoder_create: %s is not 16-byte aligned on the device "
+                  "(register each tensor as its own range)", what);
+    *out = p;
+    return 0;
+  };
+  const void *ptr = nullptr;
+  if (weight(emb, (size_t)c.nvocab * dim, "emb", &ptr)) { decoder_free(d); return nullptr; }
+  d->emb = (const int8_t *)ptr;
+  if (weight(emb_s, (size_t)c.nvocab * 4, "emb scales", &ptr)) { decoder_free(d); return nullptr; }
+  d->emb_s = (const float *)ptr;
+  d->layers.resize(c.nl);
+  for (int l = 0; l < c.nl; ++l) {
+    const gemma_hip_layer &src = layers[l];
+    const int8_t *ws[7] = {src.wq, src.wk, src.wv, src.wo, src.w1, src.w2, src.w3};
+    const float *ss[7] = {src.wq_s, src.wk_s, src.wv_s, src.wo_s, src.w1_s, src.w2_s, src.w3_s};
+    const size_t rows[7] = {q_sz, kv_sz, kv_sz, dim, mlp, mlp, dim};
+    const size_t cols[7] = {dim, dim, dim, q_sz, dim, dim, mlp};
+    static const char *names[7] = {"wq", "wk", "wv", "wo", "w1", "w2", "w3"};
+    for (int t = 0; t < 7; ++t) {
+      if (weight(ws[t], rows[t] * cols[t], names[t], &ptr)) { decoder_free(d); return nullptr; }
+      d->layers[l].w[t] = (const int8_t *)ptr;
+      if (weight(ss[t], rows[t] * 4, names[t], &ptr)) { decoder_free(d); return nullptr; }
+      d->layers[l].s[t] = (const float *)ptr;
+    }
+    if (src.n1 == nullptr || src.n2 == nullptr || (c.qk_norm && (!src.nq || !src.nk)) ||
+        (c.mlp_pre && !src.n3) || (c.mlp_pst && !src.n4)) {
+      fail("gemma_hip_decoder_create: layer %d lacks a norm weight", l);
+      decoder_free(d);
+      return nullptr;
+    }
+  }
+  // one device allocation for norms, activations, tables and the KV cache
+  Carver cv;
+  std::vector<size_t> o_norm(c.nl);
+  const size_t norm_floats = 2 * (size_t)c.hdim + 4 * dim;
+  for (int l = 0; l < c.nl; ++l) o_norm[l] = cv.take(norm_floats * 4);
+  const size_t o_fnorm = cv.take(dim * 4), o_x0 = cv.take(dim * 4), o_x1 = cv.take(dim * 4),
+               o_xq = cv.take(q_sz * 4), o_xk = cv.take(kv_sz * 4), o_xv = cv.take(kv_sz * 4),
+               o_xo = cv.take(q_sz * 4), o_ya = cv.take(dim * 4), o_g = cv.take(mlp * 4),
+               o_ym = cv.take(dim * 4), o_h = cv.take(dim * 4),
+               o_lg = cv.take((size_t)c.nvocab * 4),
+               o_part = cv.take((size_t)c.n_heads * d->max_blocks * (c.hdim + 2) * 8),
+               o_rl = cv.take((size_t)clen * c.hdim * 4), o_rg = cv.take((size_t)clen * c.hdim * 4),
+               o_kv = cv.take((size_t)c.nl * 2 * clen * kv_sz * 4),
+               o_pv = cv.take((size_t)d->nparts * 4), o_pi = cv.take((size_t)d->nparts * 4),
+               o_st = cv.take(16), o_tok = cv.take((size_t)clen * 4);
+  hipError_t e = hipMalloc((void **)&d->mem, cv.used);
+  if (e == hipSuccess) e = hipHostMalloc((void **)&d->pin, 64, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    hip_fail("gemma_hip_decoder_create: alloc", e);
+    decoder_free(d);
+    return nullptr;
+  }
+  char *m = d->mem;
+  d->fnorm = (float *)(m + o_fnorm);
+  d->x[0] = (float *)(m + o_x0);
+  d->x[1] = (float *)(m + o_x1);
+  d->xq = (float *)(m + o_xq);
+  d->xk = (float *)(m + o_xk);
+  d->xv = (float *)(m + o_xv);
+  d->xo = (float *)(m + o_xo);
+  d->yattn = (float *)(m + o_ya);
+  d->gbuf = (float *)(m + o_g);
+  d->ymlp = (float *)(m + o_ym);
+  d->h = (float *)(m + o_h);
+  d->logits = (float *)(m + o_lg);
+  d->part = (double *)(m + o_part);
+  d->rope_l = (float *)(m + o_rl);
+  d->rope_g = (float *)(m + o_rg);
+  d->kv = (float *)(m + o_kv);
+  d->pval = (float *)(m + o_pv);
+  d->pidx = (int *)(m + o_pi);
+  d->step = (int *)(m + o_st);
+  d->tokens = (int *)(m + o_tok);
+  // norms and RoPE tables, staged on the host
+  std::vector<float> host(norm_floats * c.nl + dim, 0.0f);
+  for (int l = 0; l < c.nl; ++l) {
+    float *dst = host.data() + norm_floats * l;
+    const gemma_hip_layer &src = layers[l];
+    const float *parts[6] = {src.nq, src.nk, src.n1, src.n2, src.n3, src.n4};
+    const size_t lens[6] = {(size_t)c.hdim, (size_t)c.hdim, dim, dim, dim, dim};
+    float *devp[6];
+    size_t off = 0;
+    for (int t = 0; t < 6; ++t) {
+      if (parts[t] != nullptr) memcpy(dst + off, parts[t], lens[t] * 4);
+      devp[t] = (float *)(m + o_norm[l]) + off;
+      off += lens[t];
+    }
+    d->layers[l].nq = devp[0];
+    d->layers[l].nk = devp[1];
+    d->layers[l].n1 = devp[2];
+    d->layers[l].n2 = devp[3];
+    d->layers[l].n3 = devp[4];
+    d->layers[l].n4 = devp[5];
+    e = hipMemcpy(m + o_norm[l], dst, norm_floats * 4, hipMemcpyHostToDevice);
+    if (e != hipSuccess) break;
+  }
+  if (e == hipSuccess) e = hipMemcpy(d->fnorm, fnorm, dim * 4, hipMemcpyHostToDevice);
+  // rope_freqs_pos (gemma.c:4178-4196): freq = theta^(-2d/hdim) and the
+  // angle freq*pos as the reference's floats, each rounded once; cos and sin
+  // of that angle rounded once to float
+  if (e == hipSuccess) {
+    std::vector<float> tab((size_t)clen * c.hdim);
+    for (int which = 0; which < 2 && e == hipSuccess; ++which) {
+      const float theta = which == 0 ? c.theta_l : c.theta_g;
+      for (int dd = 0; dd < c.hdim / 2; ++dd) {
+        const float ex = (float)(-2 * dd) / (float)c.hdim;
+        const float freq = (float)pow((double)theta, (double)ex);
+        for (int p = 0; p < clen; ++p) {
+          const float ang = freq * (float)p;
+          tab[(size_t)p * c.hdim + 2 * dd] = (float)cos((double)ang);
+          tab[(size_t)p * c.hdim + 2 * dd + 1] = (float)sin((double)ang);
+        }
+      }
+      e = hipMemcpy(which == 0 ? d->rope_l : d->rope_g, tab.data(), tab.size() * 4,
+                    hipMemcpyHostToDevice);
+    }
+  }
+  if (e != hipSuccess) {
+    hip_fail("gemma_hip_decoder_create: upload", e);
+    decoder_free(d);
+    return nullptr;
+  }
+  // capture the step graph
+  e = hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal);
+  if (e == hipSuccess) {
+    hipError_t le = decoder_enqueue(d, g.stream);
+    e = hipStreamEndCapture(g.stream, &d->graph);
+    if (le != hipSuccess) e = le;
+  }
+  if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hip_fail("gemma_hip_decoder_create: graph capture", e);
+    decoder_free(d);
+    return nullptr;
+  }
+  return d;
+}
+
+void gemma_hip_decoder_destroy(gemma_hip_decoder *dec) {
+  if (dec == nullptr) return;
+  if (g.ready) (void)hipStreamSynchronize(g.stream);
+  decoder_free(dec);
+}
+
+int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos, float *logits,
+                           int *next) {
+  if (need_init()) return 1;
+  if (dec == nullptr) return fail("gemma_hip_decoder_step: null decoder");
+  if (token < 0 || token >= dec->cfg.nvocab || pos < 0 || pos >= dec->clen)
+    return fail("gemma_hip_decoder_step: token %d / pos %d out of range (vocab %d, clen %d)",
+                token, pos, dec->cfg.nvocab, dec->clen);
+  GH_CHECK("gemma_hip_decoder_step: sync", hipStreamSynchronize(g.stream));
+  dec->pin[0] = token;
+  dec->pin[1] = pos;
+  dec->pin[2] = 0;
+  dec->pin[3] = 0;
+  GH_CHECK("gemma_hip_decoder_step: H2D",
+           hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
+  GH_CHECK("gemma_hip_decoder_step: graph", hipGraphLaunch(dec->exec, g.stream));
+  if (logits != nullptr)
+    GH_CHECK("gemma_hip_decoder_step: logits D2H",
+             hipMemcpyAsync(logits, dec->logits, (size_t)dec->cfg.nvocab * 4,
+                            hipMemcpyDeviceToHost, g.stream));
+  if (next != nullptr)
+    GH_CHECK("gemma_hip_decoder_step: D2H",
+             hipMemcpyAsync(dec->pin + 4, dec->tokens, 4, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemma_hip_decoder_step: sync", hipStreamSynchronize(g.stream));
+  if (next != nullptr) *next = dec->pin[4];
+  return 0;
+}
+
+int gemma_hip_decoder_generate(gemma_hip_decoder *dec, int token, int pos, int n,
+                               int *tokens) {
+  if (need_init()) return 1;
+  if (dec == nullptr || tokens == nullptr) return fail("gemma_hip_decoder_generate: null argument");
+  if (token < 0 || token >= dec->cfg.nvocab || pos < 0 || n < 0 || n > dec->clen - pos)
+    return fail("gemma_hip_decoder_generate: token %d / pos %d / n %d out of range", token,
+                pos, n);
+  if (n == 0) return 0;
+  GH_CHECK("gemma_hip_decoder_generate: sync", hipStreamSynchronize(g.stream));
+  dec->pin[0] = token;
+  dec->pin[1] = pos;
+  dec->pin[2] = 0;
+  dec->pin[3] = 0;
+  GH_CHECK("gemma_hip_decoder_generate: H2D",
+           hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
+  for (int i = 0; i < n; ++i)
+    GH_CHECK("gemma_hip_decoder_generate: graph", hipGraphLaunch(dec->exec, g.stream));
+  GH_CHECK("gemma_hip_decoder_generate: D2H",
+           hipMemcpyAsync(tokens, dec->tokens, (size_t)n * 4, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemma_hip_decoder_generate: sync", hipStreamSynchronize(g.stream));
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= dec->cfg.nvocab)
+      return fail("gemma_hip_decoder_generate: step %d produced no token (NaN logits?)", i);
+  return 0;
+}
+
+const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec) {
+  return dec != nullptr ? dec->logits : nullptr;
 }
 
 }  // extern "C"

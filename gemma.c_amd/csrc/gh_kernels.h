@@ -63,4 +63,56 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
 hipError_t launch_im2col(float *a, const float *img, int img_px, int psize,
                          hipStream_t stream);
 
+// decode.hip: the device-resident decode step.
+// Residual update and rmsnorm in front of an int8 GEMV:
+//   x_new = clamp(x_res + (w_post ? rmsnorm(y, w_post) : y))   (x_res when y is null)
+//   h     = rmsnorm(x_new, w_pre)
+// workgroup 0 stores x_new to x_out and h to h_out (each nullable).
+struct DecNorm {
+  const float *x_res;
+  const float *y;
+  const float *w_post;
+  const float *w_pre;
+  float *x_out;
+  float *h_out;
+  int dim;
+  float eps;
+};
+
+// x = emb_q[token] * (esc * emb_s[token]); step = {token, pos, count}
+struct DecEmbed {
+  const int8_t *emb_q;
+  const float *emb_s;
+  float *x;
+  const int *step;
+  int dim, nvocab, clen;
+  float esc;
+};
+
+// One layer's attention: q/k/v rows in, xo out; kc/vc are the layer's cache
+// [nkv][clen][hdim]; rope the table [clen][hdim] (cos, sin interleaved) of
+// the layer's base; part holds [n_heads][max_blocks][hdim + 2] fp64 partials.
+struct DecAttn {
+  const float *xq, *xk, *xv, *nq, *nk, *rope;
+  float *kc, *vc;
+  double *part;
+  float *xo;
+  const int *step;
+  int n_heads, nkv, hdim, clen, slide, block, max_blocks, nvocab;
+  float asc, sc_att, eps;
+};
+
+// norm prologue + int8 GEMV over jobs (gelu: jobs.w[0]/w[1] are gate/up,
+// total = 2 * rows, output gelu(gate) * up to jobs.dst[0]); k % 16 == 0,
+// k <= 8192, rows 16-byte aligned
+hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
+                                bool gelu, const DeviceInfo &dev, hipStream_t stream);
+hipError_t launch_dec_embed(const DecEmbed &a, hipStream_t stream);
+hipError_t launch_dec_final_norm(const DecNorm &na, hipStream_t stream);
+hipError_t launch_dec_attention(const DecAttn &a, hipStream_t stream);
+hipError_t launch_dec_softcap(float *logits, int n, float cap, hipStream_t stream);
+// argmax over logits; writes step[0] = token, step[1] += 1, tokens[step[2]++]
+hipError_t launch_dec_argmax(const float *logits, int n, float *pval, int *pidx, int nparts,
+                             int *step, int *tokens, int max_tokens, hipStream_t stream);
+
 }  // namespace gh

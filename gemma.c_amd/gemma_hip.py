@@ -34,6 +34,25 @@ class Job(ctypes.Structure):
                 ("dst", ctypes.c_void_p), ("m", ctypes.c_int)]
 
 
+class TextConfig(ctypes.Structure):
+    """gemma_hip_text_config: the reference's TextConfig (gemma.c:740-761)."""
+
+    _fields_ = [(n, ctypes.c_int) for n in ("nl", "n_heads", "nkv", "hdim", "dim", "mlp_dim",
+                                            "q_scale", "slide", "nvocab")] + \
+               [(n, ctypes.c_float) for n in ("theta_l", "theta_g", "eps", "sc_att", "sc_log")] + \
+               [(n, ctypes.c_int) for n in ("qk_norm", "mlp_pre", "mlp_pst")] + \
+               [("swa", ctypes.c_void_p)]
+
+
+class Layer(ctypes.Structure):
+    """gemma_hip_layer: one TextDecoderLayer (gemma.c:1173-1195)."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "wq", "wk", "wv", "wo", "w1", "w2", "w3",
+        "wq_s", "wk_s", "wv_s", "wo_s", "w1_s", "w2_s", "w3_s",
+        "nq", "nk", "n1", "n2", "n3", "n4")]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SIGS = {
@@ -61,6 +80,12 @@ _SIGS = {
     "gemma_hip_gemm_fpx_host": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I]),
     "gemma_hip_patch_embed": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "gemma_hip_patch_embed_host": (_I, [_P, _P, _P, _P, _I, _I, _I]),
+    "gemma_hip_decoder_create": (_P, [ctypes.POINTER(TextConfig), ctypes.POINTER(Layer), _P, _P,
+                                      _P, _I]),
+    "gemma_hip_decoder_destroy": (None, [_P]),
+    "gemma_hip_decoder_step": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
+    "gemma_hip_decoder_generate": (_I, [_P, _I, _I, _I, _P]),
+    "gemma_hip_decoder_logits": (_P, [_P]),
 }
 
 
@@ -167,3 +192,88 @@ class GemmaHip:
 
     def device_ptr(self, host) -> int | None:
         return self.lib.gemma_hip_device_ptr(_addr(host))
+
+    # device-resident decoder -----------------------------------------------
+    def decoder(self, model, clen: int) -> "Decoder":
+        """A decoder over a model from model_bin.read_bin(): registers every
+        int8 tensor (each as its own range) and builds the step graph."""
+        return Decoder(self, model, clen)
+
+
+class Decoder:
+    """gemma_hip_decoder_*: forward_gemma_decode (gemma.c:5456) on the GPU."""
+
+    def __init__(self, gh: GemmaHip, model, clen: int):
+        import numpy as np
+
+        self.gh, self.lib = gh, gh.lib
+        c = model["config"]
+        self.nvocab = c["nvocab"]
+        self._keep = []
+        self._registered = []
+
+        def reg(arr):
+            arr = np.asarray(arr)
+            gh.register_weights(arr, arr.nbytes)
+            self._registered.append(arr)
+            return arr.ctypes.data
+
+        def host(arr):
+            arr = np.ascontiguousarray(arr, np.float32)
+            self._keep.append(arr)
+            return arr.ctypes.data
+
+        swa = np.asarray(c["swa"], np.uint8)
+        self._keep.append(swa)
+        cfg = TextConfig(c["nl"], c["n_heads"], c["nkv"], c["hdim"], c["dim"], c["mlp_dim"],
+                         c["q_scale"], c["slide"], c["nvocab"], c["theta_l"], c["theta_g"],
+                         c["eps"], c["sc_att"], c["sc_log"], int(c["qk_norm"]),
+                         int(c["mlp_pre"]), int(c["mlp_pst"]), swa.ctypes.data)
+        layers = (Layer * c["nl"])()
+        try:
+            for i, ly in enumerate(model["layers"]):
+                f = {}
+                for w in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+                    f[w] = reg(ly[w][0])
+                    f[w + "_s"] = reg(ly[w][1])
+                for n in ("nq", "nk", "n1", "n2", "n3", "n4"):
+                    f[n] = host(ly[n]) if ly.get(n) is not None else None
+                layers[i] = Layer(**f)
+            emb_q, emb_s = reg(model["emb"][0]), reg(model["emb"][1])
+            fnorm = host(model["fnorm"])
+            self.handle = self.lib.gemma_hip_decoder_create(ctypes.byref(cfg), layers, emb_q,
+                                                            emb_s, fnorm, clen)
+            if not self.handle:
+                raise GemmaHipError(self.lib.gemma_hip_last_error().decode())
+        except Exception:
+            self._release()
+            raise
+
+    def _release(self):
+        for arr in self._registered:
+            self.gh.release_weights(arr)
+        self._registered = []
+
+    def step(self, token: int, pos: int, logits=None) -> int:
+        nxt = ctypes.c_int(-1)
+        self.gh._check(self.lib.gemma_hip_decoder_step(self.handle, token, pos, _addr(logits),
+                                                       ctypes.byref(nxt)))
+        return nxt.value
+
+    def generate(self, token: int, pos: int, n: int):
+        import numpy as np
+
+        out = np.empty(max(1, n), np.int32)
+        self.gh._check(self.lib.gemma_hip_decoder_generate(self.handle, token, pos, n,
+                                                           out.ctypes.data))
+        return out[:n]
+
+    def logits_ptr(self) -> int:
+        return self.lib.gemma_hip_decoder_logits(self.handle)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.gemma_hip_decoder_destroy(self.handle)
+            self.handle = None
+        self._release()
+

@@ -67,13 +67,19 @@ def _pascal(s: str) -> bytes:
 
 
 def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
-              layers: int | None = None) -> str:
+              layers: int | None = None, slide: int | None = None, sc_att: float = 0.0,
+              sc_log: float = 0.0, flags: int = 4 | 2 | 1, norm_std: float = 0.0) -> str:
     """Write a random-init W8A8 (f32 build) text model of shape `name`;
-    `nvocab` and `layers` shrink it for quick tests."""
-    c = CONFIGS[name]
+    `nvocab` and `layers` shrink it for quick tests, `slide`, the softcaps
+    and the flags byte (4 qk-norm, 2 pre-FFN norm, 1 post-FFN norm) select
+    the other code paths of the reference's decoder; norm_std > 0 draws the
+    norm weights from N(0, norm_std) instead of zeros."""
+    c = dict(CONFIGS[name])
     nl, dim, hdim, mlp = c["nl"], c["dim"], c["hdim"], c["mlp"]
     if layers is not None:
         nl = layers
+    if slide is not None:
+        c["slide"] = slide
     q_sz, kv_sz = c["n_heads"] * hdim, c["nkv"] * hdim
     rng = np.random.default_rng(seed)
     tmp = path + ".tmp"
@@ -81,32 +87,101 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
         f.write(b"GEMA" + b"f32" + b"Q")
         f.write(struct.pack(">BBBHHHHHHIIfffff", nl, c["n_heads"], c["nkv"], hdim, dim, mlp,
                             hdim, c["slide"], 256, 32768, nvocab, 10000.0, 1000000.0, 1e-6,
-                            0.0, 0.0))
+                            sc_att, sc_log))
         nbytes = (nl + 7) // 8
         bits = bytearray(nbytes)
         for i in range(nl):
             if (i + 1) % 6 != 0:  # gemma 3: five sliding-window layers per global one
                 bits[i // 8] |= 1 << (7 - i % 8)
         f.write(bytes([nbytes]) + bytes(bits))
-        f.write(bytes([4 | 2 | 1]))  # qk_norm, pre- and post-FFN norms; text only
+        f.write(bytes([flags & 7]))  # qk_norm, pre- and post-FFN norms; text only
         vocab = SPECIALS + [f"t{i}" for i in range(len(SPECIALS), nvocab)]
         f.write(b"".join(_pascal(s) for s in vocab))
         f.write(struct.pack(">I", 1) + _pascal("t") + _pascal("0"))
-        zeros_dim = np.zeros(dim, np.float32).tobytes()
+
+        def norm(n: int) -> bytes:
+            if norm_std <= 0.0:
+                return np.zeros(n, np.float32).tobytes()
+            return (rng.standard_normal(n, dtype=np.float32) * np.float32(norm_std)).tobytes()
+
         _write_qtensor(f, rng, nvocab, dim)  # emb, also the tied LM head
         for _ in range(nl):
             _write_qtensor(f, rng, q_sz, dim)    # wq
             _write_qtensor(f, rng, kv_sz, dim)   # wk
             _write_qtensor(f, rng, kv_sz, dim)   # wv
             _write_qtensor(f, rng, dim, q_sz)    # wo
-            f.write(np.zeros(hdim, np.float32).tobytes() * 2)  # nq, nk
+            if flags & 4:
+                f.write(norm(hdim) + norm(hdim))  # nq, nk
             _write_qtensor(f, rng, mlp, dim)     # w1 (up)
             _write_qtensor(f, rng, mlp, dim)     # w2 (gate)
             _write_qtensor(f, rng, dim, mlp)     # w3 (down)
-            f.write(zeros_dim * 4)               # n1, n2, n3, n4
-        f.write(zeros_dim)                       # fnorm
+            for _ in range(2 + ((flags & 2) != 0) + ((flags & 1) != 0)):
+                f.write(norm(dim))               # n1 n2 [n3] [n4]
+        f.write(norm(dim))                       # fnorm
     os.replace(tmp, path)
     return path
+
+
+def read_bin(path: str) -> dict:
+    """Map a W8A8 f32 .bin (text decoder) into numpy views, as the reference's
+    mmap loader does (gemma.c:1942-2055, tensor order 1386-1469).  Returns
+    {"config": {...}, "emb": (q, s), "layers": [{"wq": (q, s), ..., "n1": ...}],
+    "fnorm": ...}; int8 tensors are read-only views of the file."""
+    data = np.memmap(path, dtype=np.uint8, mode="r")
+    if bytes(data[:4]) != b"GEMA" or bytes(data[4:7]) != b"f32":
+        raise ValueError(f"{path}: not an f32 Gemma.c model")
+    if bytes(data[7:8]) != b"Q":
+        raise ValueError(f"{path}: not a W8A8 ('Q') model")
+    at = 8
+    (nl, n_heads, nkv, hdim, dim, mlp, q_scale, slide, img_tok, max_seq, nvocab, theta_l,
+     theta_g, eps, sc_att, sc_log) = struct.unpack(">BBBHHHHHHIIfffff", bytes(data[at:at + 43]))
+    at += 43
+    nbytes = int(data[at])
+    bits = bytes(data[at + 1:at + 1 + nbytes])
+    at += 1 + nbytes
+    swa = [(bits[i // 8] >> (7 - i % 8)) & 1 for i in range(nl)]
+    flags = int(data[at])
+    at += 1
+    multimodal = bool(flags & 8)
+    if multimodal:
+        at += 14  # vision config (gemma.c:726-729)
+    for _ in range(nvocab + (1 if multimodal else 0)):
+        at += 1 + int(data[at])
+    (nmerges,) = struct.unpack(">I", bytes(data[at:at + 4]))
+    at += 4
+    for _ in range(2 * nmerges):
+        at += 1 + int(data[at])
+
+    def f32(n):
+        nonlocal at
+        v = np.frombuffer(data, np.float32, n, at)
+        at += 4 * n
+        return v
+
+    def qt(rows, cols):
+        nonlocal at
+        q = np.frombuffer(data, np.int8, rows * cols, at).reshape(rows, cols)
+        at += rows * cols
+        return q, f32(rows)
+
+    cfg = dict(nl=nl, n_heads=n_heads, nkv=nkv, hdim=hdim, dim=dim, mlp_dim=mlp,
+               q_scale=q_scale, slide=slide, nvocab=nvocab, theta_l=theta_l, theta_g=theta_g,
+               eps=eps, sc_att=sc_att, sc_log=sc_log, qk_norm=bool(flags & 4),
+               mlp_pre=bool(flags & 2), mlp_pst=bool(flags & 1), swa=swa, max_seq=max_seq)
+    q_sz, kv_sz = n_heads * hdim, nkv * hdim
+    emb = qt(nvocab, dim)
+    layers = []
+    for _ in range(nl):
+        ly = {"wq": qt(q_sz, dim), "wk": qt(kv_sz, dim), "wv": qt(kv_sz, dim),
+              "wo": qt(dim, q_sz)}
+        ly["nq"], ly["nk"] = (f32(hdim), f32(hdim)) if cfg["qk_norm"] else (None, None)
+        ly["w1"], ly["w2"], ly["w3"] = qt(mlp, dim), qt(mlp, dim), qt(dim, mlp)
+        ly["n1"], ly["n2"] = f32(dim), f32(dim)
+        ly["n3"] = f32(dim) if cfg["mlp_pre"] else None
+        ly["n4"] = f32(dim) if cfg["mlp_pst"] else None
+        layers.append(ly)
+    fnorm = f32(dim)
+    return {"config": cfg, "emb": emb, "layers": layers, "fnorm": fnorm, "end": at}
 
 
 def ensure_bin(directory: str, name: str, seed: int = 1234) -> str:

@@ -35,7 +35,8 @@
  *  - Entry points with the _host suffix take the reference call sites' host
  *    buffers for activations and outputs, resolve weight pointers through the
  *    registry below, and return after the result is back in host memory.
- *  - Calls are made from one host thread at a time.
+ *  - Device entry points and the decoder are called from one host thread at
+ *    a time; the _host entry points serialise among themselves.
  */
 #ifndef GEMMA_HIP_H
 #define GEMMA_HIP_H
@@ -197,6 +198,62 @@ int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
  * pe and pe_b must be registered. */
 int gemma_hip_patch_embed_host(float *dst, const float *img, const float *pe,
                                const float *pe_b, int img_px, int psize, int dim);
+
+/* ---- device-resident decoder ------------------------------------------- */
+/* One greedy decode step with every tensor resident in HBM: the embedding
+ * lookup, all layers (norms, q/k/v, q/k norm, RoPE, KV cache, attention,
+ * o, gate/up, GELU, down, residuals), the final norm, the LM head and the
+ * argmax run on the GPU, captured once into a HIP graph.  Replaces
+ * forward_gemma_decode (gemma.c:5456) + forward_text_decode (4727) for W8A8
+ * model files, and argmax (5600) for greedy sampling.  The int8 products are
+ * bit-exact as above; the fp32 glue (norms, RoPE, softmax, GELU) follows
+ * the reference's formulas in its own summation order, so logits agree with
+ * the reference to fp32 rounding amplified by int8 requantization, not bit
+ * for bit. */
+
+/* The reference's TextConfig (gemma.c:740-761) as plain fields. */
+typedef struct {
+  int nl, n_heads, nkv, hdim, dim, mlp_dim, q_scale, slide, nvocab;
+  float theta_l, theta_g, eps, sc_att, sc_log;
+  int qk_norm, mlp_pre, mlp_pst; /* flags, 0 or 1 */
+  const unsigned char *swa;      /* nl flags: 1 = sliding-window layer */
+} gemma_hip_text_config;
+
+/* One TextDecoderLayer (gemma.c:1173-1195) of a W8A8 file: int8 weights and
+ * their row scales are host pointers inside registered ranges; the norm
+ * weights (stored as w, applied as w + 1) are host arrays the decoder copies
+ * (nq/nk only read when qk_norm, n3 when mlp_pre, n4 when mlp_pst). */
+typedef struct {
+  const int8_t *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+  const float *wq_s, *wk_s, *wv_s, *wo_s, *w1_s, *w2_s, *w3_s;
+  const float *nq, *nk, *n1, *n2, *n3, *n4;
+} gemma_hip_layer;
+
+typedef struct gemma_hip_decoder gemma_hip_decoder;
+
+/* Builds a decoder for a context of clen positions: resolves the registered
+ * weights (emb int8 [nvocab][dim] + emb_s [nvocab] is also the tied LM head),
+ * copies the norms, allocates the KV cache [nl][2][nkv][clen][hdim] and the
+ * activations, and captures the step graph.  NULL on failure. */
+gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
+                                            const gemma_hip_layer *layers,
+                                            const int8_t *emb, const float *emb_s,
+                                            const float *fnorm, int clen);
+void gemma_hip_decoder_destroy(gemma_hip_decoder *dec);
+
+/* One step at position pos (0 <= pos < clen, token < nvocab): logits (host,
+ * nvocab floats) and next (the argmax) are written when non-NULL. */
+int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos,
+                           float *logits, int *next);
+
+/* n greedy steps without host round trips: step i consumes the token step
+ * i-1 produced (the first consumes `token` at `pos`); tokens[i] receives the
+ * argmax of step i (host, n ints).  pos + n <= clen. */
+int gemma_hip_decoder_generate(gemma_hip_decoder *dec, int token, int pos, int n,
+                               int *tokens);
+
+/* Device pointer of the last step's logits (nvocab floats). */
+const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,144 @@
+"""CPU restatement of the reference's decode step, the checker of the
+device-resident decoder.  TEST INFRASTRUCTURE ONLY: tests/ use it; nothing in
+the product imports it.
+
+Follows forward_gemma_decode (gemma.c:5456-5499) and forward_text_decode
+(4727-4983) step by step.  The int8 parts are the pinned oracle's: quantize_act
+from oracle/gemma_oracle.c and int32 sums in int64 numpy (exact), rescaled as
+(float)acc * (xs * ws) in float32 (IEEE, the gcc -ffast-math order; no
+operand here is near the FTZ range).  The fp32 glue -- rmsnorm (2508-2521),
+clamp_fpx (2504-2506), RoPE (4178-4246), scores, att_finalize/softmax
+(4091-4131), values, gelu_tanh (4139-4170) -- is computed in float64 from the
+reference's formulas and rounded to float32 where the reference stores a
+float32 tensor.  The reference leaves the fp32 summation order to its
+compiler, so no bit pattern is canonical for the glue; float64 is the exact
+value the GPU's and the CPU's float32 results are both checked against.
+
+Pins: the int8 pieces are the pinned oracle functions; the glue formulas are
+pinned by closed-form tests in tests/test_decoder.py (a one-hot attention,
+RoPE's rotation invariants, rmsnorm of a constant vector) and by the
+comparison with the reference program's own logits (tests/test_e2e.py).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+F64 = np.float64
+
+
+def rmsnorm(x, w, eps):
+    """gemma.c:2508-2521: x * rsqrt(mean(x^2) + eps) * (w + 1)."""
+    x = np.asarray(x, F64)
+    rms = 1.0 / np.sqrt(np.mean(x * x) + F64(F32(eps)))
+    return (x * rms * (np.asarray(w, F64) + 1.0)).astype(F32)
+
+
+def clamp_f32(x):
+    """clamp_fpx (gemma.c:2504-2506) for fp32."""
+    m = F64(np.finfo(F32).max)
+    return np.clip(np.asarray(x, F64), -m, m).astype(F32)
+
+
+def gelu_tanh(x):
+    """gemma.c:4139-4145."""
+    x = np.asarray(x, F64)
+    return 0.5 * x * (1.0 + np.tanh(F64(F32(0.79788456080287)) * (x + F64(F32(0.044715)) * x ** 3)))
+
+
+def rope_table(theta, hdim, pos):
+    """rope_freqs_pos (gemma.c:4178-4196): freq = theta^(-2d/hdim) and the
+    angle freq*pos rounded to float32 as the reference computes them."""
+    d = np.arange(hdim // 2)
+    ex = (F32(-2) * d.astype(F32)) / F32(hdim)
+    freq = np.power(F64(F32(theta)), ex.astype(F64)).astype(F32)
+    ang = (freq * F32(pos)).astype(F32)
+    return np.cos(ang.astype(F64)).astype(F32), np.sin(ang.astype(F64)).astype(F32)
+
+
+def rope(x, cos, sin):
+    """rope_apply (gemma.c:4223-4246) on one head vector."""
+    h = len(x) // 2
+    a, b = np.asarray(x[:h], F64), np.asarray(x[h:], F64)
+    c, s = cos.astype(F64), sin.astype(F64)
+    return np.concatenate([a * c - b * s, a * s + b * c]).astype(F32)
+
+
+def attend(q, keys, vals, asc, sc_att):
+    """One query head over its keys (gemma.c:4826-4851): scores k.q * asc,
+    optional tanh softcap, softmax (att_finalize 4119-4131), value sum."""
+    s = np.asarray(keys, F64) @ np.asarray(q, F64) * F64(asc)
+    if sc_att != 0.0:
+        s = np.tanh(s / F64(sc_att)) * F64(sc_att)
+    p = np.exp(s - s.max())
+    p /= p.sum()
+    return (p @ np.asarray(vals, F64)).astype(F32)
+
+
+class DecodeOracle:
+    """One model's decode state (KV cache) on the CPU."""
+
+    def __init__(self, model, oracle, clen: int):
+        self.m = model
+        self.c = model["config"]
+        self.o = oracle
+        c = self.c
+        self.kc = np.zeros((c["nl"], c["nkv"], clen, c["hdim"]), F32)
+        self.vc = np.zeros_like(self.kc)
+        self.clen = clen
+
+    def gemv(self, w, x_f32):
+        """quantize_act + gemv_int8 (gemma.c:2590-2788): exact."""
+        q, xs = self.o.quantize_act(np.ascontiguousarray(x_f32, F32))
+        acc = np.asarray(w[0], np.int64) @ q.astype(np.int64)
+        return acc.astype(np.int32).astype(F32) * (F32(xs) * np.asarray(w[1], F32))
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        c, m = self.c, self.m
+        dim, hd, nh, nkv = c["dim"], c["hdim"], c["n_heads"], c["nkv"]
+        eps = c["eps"]
+        esc = F32(1.0) if c["mlp_pre"] else F32(np.sqrt(F32(dim)))
+        esc = F32(esc * m["emb"][1][token])
+        x = (m["emb"][0][token].astype(F32) * esc).astype(F32)
+        asc = F32(1.0) / F32(np.sqrt(F32(c["q_scale"])))
+        for li, ly in enumerate(m["layers"]):
+            resid = x
+            h = rmsnorm(x, ly["n1"], eps)
+            q = self.gemv(ly["wq"], h).reshape(nh, hd)
+            k = self.gemv(ly["wk"], h).reshape(nkv, hd)
+            v = self.gemv(ly["wv"], h).reshape(nkv, hd)
+            if c["qk_norm"]:
+                q = np.stack([rmsnorm(qh, ly["nq"], eps) for qh in q])
+                k = np.stack([rmsnorm(kh, ly["nk"], eps) for kh in k])
+            sliding = bool(c["swa"][li])
+            cos, sin = rope_table(c["theta_l"] if sliding else c["theta_g"], hd, pos)
+            q = np.stack([rope(qh, cos, sin) for qh in q])
+            k = np.stack([rope(kh, cos, sin) for kh in k])
+            self.kc[li, :, pos] = k
+            self.vc[li, :, pos] = v
+            spos = pos + 1 - c["slide"] if (sliding and pos >= c["slide"]) else 0
+            hn = nh // nkv
+            xo = np.empty((nh, hd), F32)
+            for hh in range(nh):
+                kvh = hh // hn
+                xo[hh] = attend(q[hh], self.kc[li, kvh, spos:pos + 1],
+                                self.vc[li, kvh, spos:pos + 1], asc, c["sc_att"])
+            y = self.gemv(ly["wo"], xo.reshape(-1))
+            if c["mlp_pre"]:
+                y = rmsnorm(y, ly["n2"], eps)
+            x = clamp_f32(y.astype(F64) + resid.astype(F64))
+            resid = x
+            h = rmsnorm(x, ly["n3"] if c["mlp_pre"] else ly["n2"], eps)
+            gate = self.gemv(ly["w2"], h)
+            up = self.gemv(ly["w1"], h)
+            g = (gelu_tanh(gate) * up.astype(F64)).astype(F32)
+            y = self.gemv(ly["w3"], g)
+            if c["mlp_pst"]:
+                y = rmsnorm(y, ly["n4"], eps)
+            x = clamp_f32(y.astype(F64) + resid.astype(F64))
+        h = rmsnorm(x, m["fnorm"], eps)
+        logits = self.gemv(m["emb"], h)
+        if c["sc_log"] != 0.0:
+            logits = (np.tanh(logits.astype(F64) / c["sc_log"]) * c["sc_log"]).astype(F32)
+        return logits
