@@ -24,6 +24,11 @@ The JSON line also carries, measured in the same run:
                 and the SigLIP tower shapes (M=4096), % of the 5.0 POPS peak
   decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
                 decode token (26 layers x {qkv, o, gate/up, down} + LM head)
+  decoder       tokens/s of the whole device-resident greedy decode step
+                (gemma_hip_decoder_generate: embedding, norms, q/k/v, RoPE,
+                KV cache, attention, o, GELU, down, LM head, argmax) at the
+                decode phase of BASELINE.json configs 3 (gemma-3-1b, context
+                512 -> 768) and 5 (gemma-3-4b, context 2048 -> 2560)
   cpu_baseline  the reference's own quantize_act + gemv_int8, compiled from
                 its source (oracle/_ref/gemma_ref_clang), on the host cores
 """
@@ -300,6 +305,47 @@ def bench_decode_1b(torch, gh, gen, timer, tokens):
                      "HIP graph); attention/norms/RoPE are outside this path")
 
 
+def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
+    """Greedy decode fully on the GPU: the KV cache is filled by `prompt`
+    untimed decode steps, then `steps` steps are timed (one HIP graph launch
+    each, tokens fed back on the device, one readback at the end)."""
+    import time
+
+    import model_bin
+
+    model = model_bin.synth_model(name, seed=1234)
+    c = model["config"]
+    dec = gh.decoder(model, prompt + steps + 1)
+    try:
+        dec.generate(2, 0, prompt)
+        torch.cuda.synchronize()
+        best = None
+        for _ in range(2):
+            t0 = time.perf_counter()
+            toks = dec.generate(7, prompt, steps)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+    finally:
+        dec.close()
+    q_sz, kv_sz = c["n_heads"] * c["hdim"], c["nkv"] * c["hdim"]
+    per_layer = (gemv_bytes(q_sz + 2 * kv_sz, c["dim"]) + gemv_bytes(c["dim"], q_sz)
+                 + gemv_bytes(2 * c["mlp_dim"], c["dim"]) + gemv_bytes(c["dim"], c["mlp_dim"]))
+    weights = c["nl"] * per_layer + gemv_bytes(c["nvocab"], c["dim"])
+    kv = 0
+    for pos in range(prompt, prompt + steps):
+        for sw in c["swa"]:
+            keys = min(pos + 1, c["slide"]) if sw else pos + 1
+            kv += 2 * kv_sz * 4 * keys
+    per_token = weights + kv / steps
+    tok_s = steps / best
+    gbs = per_token * tok_s / 1e9
+    return dict(model=name, context=f"{prompt}->{prompt + steps}", tok_s=round(tok_s, 1),
+                ms_per_token=round(1e3 * best / steps, 4), bytes_per_token=int(per_token),
+                gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                hbm_bound_tok_s=round(HBM_PEAK_GBS * 1e9 / per_token, 1),
+                distinct_tokens=int(len(set(toks.tolist()))))
+
+
 def measured_traffic(kernel: str) -> dict | None:
     """HBM bytes per launch of the LM-head GEMV from the committed rocprofv3
     --pmc measurement (FETCH_SIZE and WRITE_SIZE, each scaled by what the
@@ -348,8 +394,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=2.0,
                     help="CPU-baseline sample time per sweep shape")
-    ap.add_argument("--only", choices=["sweep", "lm_head"], default=None,
-                    help="profiling aid: run just the timed sweep or the LM-head timing")
+    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder"], default=None,
+                    help="profiling aid: run just the timed sweep, the LM-head timing or "
+                         "the device-resident decoder")
     ap.add_argument("--copy-probe", action="store_true",
                     help="profiling aid: 3 dispatches of an elementwise kernel that reads "
                          "and writes exactly 1 GiB (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -375,6 +422,11 @@ def main() -> int:
         return 0
 
     gh = gemma_hip.GemmaHip(0)
+    if args.only == "decoder":
+        for name, prompt, nsteps in (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512)):
+            print(json.dumps(bench_decoder(torch, gh, name, prompt, nsteps)), flush=True)
+        gh.close()
+        return 0
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
     timer = Timer(torch)
@@ -419,6 +471,10 @@ def main() -> int:
     print(f"# gemm: {json.dumps(gemm)}", file=sys.stderr, flush=True)
     dec = bench_decode_1b(torch, gh, gen, timer, tokens=50)
     print(f"# decode_1b: {json.dumps(dec)}", file=sys.stderr, flush=True)
+    decoder = {}
+    for name, prompt, nsteps in (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512)):
+        decoder[name] = bench_decoder(torch, gh, name, prompt, nsteps)
+        print(f"# decoder: {json.dumps(decoder[name])}", file=sys.stderr, flush=True)
 
     lm_us = per["lm_head"]["us"]
     traffic = measured_traffic("gemv_i8_kernel<8, true, true>")
@@ -468,6 +524,7 @@ def main() -> int:
         "per_gemv": per,
         "gemm": gemm,
         "decode_1b": dec,
+        "decoder": decoder,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -41,27 +41,32 @@ namespace {
 
 constexpr int kNT = 256;
 constexpr int kWaves = kNT / 64;
+constexpr int kAttB = kDecAttnBlock;  // keys per attention workgroup
 
+// Workgroup sum / max, the same bits in every thread (and in every
+// workgroup that reduces the same values): wave reductions in a fixed DPP
+// order, then the waves' results in wave order.
+template <int NT = kNT>
 __device__ __forceinline__ double block_sum(double v, double *red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  v = wave_sum_f64(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   double s = red[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) s += red[w];
+  for (int w = 1; w < NT / 64; ++w) s += red[w];
   return s;
 }
 
+template <int NT = kNT>
 __device__ __forceinline__ float block_max(float v, float *red) {
-  v = wave_max(v);
+  v = wave_max_dpp(v);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   float s = red[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) s = fmaxf(s, red[w]);
+  for (int w = 1; w < NT / 64; ++w) s = fmaxf(s, red[w]);
   return s;
 }
 
@@ -96,52 +101,92 @@ __device__ __forceinline__ bool step_ok(const int *step, int nvocab, int clen,
   return *token >= 0 && *token < nvocab && *pos >= 0 && *pos < clen;
 }
 
-// x_new = clamp(x_res + post(y)), then h = rmsnorm(x_new, w_pre) into xs.
-// Every thread handles elements i = tid, tid + 256, ...; workgroup 0 stores
-// x_new (and h when h_out is given).
-__device__ void norm_prologue(const DecNorm &a, float *xs, double *red) {
+// x_new = clamp(x_res + post(y)), h = rmsnorm(x_new, w_pre), and h
+// quantized into xq (LDS, int8) exactly as quantize_act does (gemma.c:
+// 2590-2650).  Split in two so the caller can issue its own (HBM) loads
+// between them: norm_load issues every load the prologue needs (NPT
+// 16-byte chunks per vector per thread, dim <= NPT * 4 * NT); vector loads
+// return in issue order, so loads issued after it do not delay it.
+template <int NPT>
+struct NormIn {
+  v4f y[NPT], xr[NPT], wp[NPT], wq[NPT];
+};
+
+template <int NPT, int NT>
+__device__ __forceinline__ void norm_load(const DecNorm &a, NormIn<NPT> &in) {
   const int tid = threadIdx.x;
-  const int dim = a.dim;
+  const int n4 = a.dim >> 2;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int c = tid + j * NT;
+    const bool ok = c < n4;
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    in.xr[j] = ok ? reinterpret_cast<const v4f *>(a.x_res)[c] : zero;
+    in.wq[j] = ok ? reinterpret_cast<const v4f *>(a.w_pre)[c] : zero;
+    in.y[j] = (ok && a.y != nullptr) ? reinterpret_cast<const v4f *>(a.y)[c] : zero;
+    in.wp[j] = (ok && a.w_post != nullptr) ? reinterpret_cast<const v4f *>(a.w_post)[c] : zero;
+  }
+}
+
+// The arithmetic of the prologue; returns the activation scale.  Workgroup 0
+// stores x_new to x_out and h to h_out (each nullable); xq may be null (the
+// final norm only stores h).
+template <int NPT, int NT>
+__device__ float norm_quant(const DecNorm &a, NormIn<NPT> &in, int8_t *xq, double *red,
+                            float *redf) {
+  const int tid = threadIdx.x;
+  const int n4 = a.dim >> 2;
   if (a.y != nullptr) {
     double rms = 1.0;
     if (a.w_post != nullptr) {
       double ss = 0.0;
-      for (int i = tid; i < dim; i += kNT) {
-        const double v = a.y[i];
-        ss += v * v;
+#pragma unroll
+      for (int j = 0; j < NPT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += (double)in.y[j][e] * (double)in.y[j][e];
+      rms = rms_of(block_sum<NT>(ss, red), a.dim, a.eps);
+    }
+#pragma unroll
+    for (int j = 0; j < NPT; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float t = a.w_post != nullptr ? norm_one(in.y[j][e], rms, in.wp[j][e]) : in.y[j][e];
+        in.xr[j][e] = clamp_f32(t + in.xr[j][e]);
       }
-      rms = rms_of(block_sum(ss, red), dim, a.eps);
-    }
-    for (int i = tid; i < dim; i += kNT) {
-      const float t = a.w_post != nullptr ? norm_one(a.y[i], rms, a.w_post[i]) : a.y[i];
-      xs[i] = clamp_f32(t + a.x_res[i]);
-    }
-  } else {
-    for (int i = tid; i < dim; i += kNT) xs[i] = a.x_res[i];
   }
   if (blockIdx.x == 0 && a.x_out != nullptr)
-    for (int i = tid; i < dim; i += kNT) a.x_out[i] = xs[i];
+#pragma unroll
+    for (int j = 0; j < NPT; ++j)
+      if (tid + j * NT < n4) reinterpret_cast<v4f *>(a.x_out)[tid + j * NT] = in.xr[j];
   double ss = 0.0;
-  for (int i = tid; i < dim; i += kNT) ss += (double)xs[i] * (double)xs[i];
-  const double rms = rms_of(block_sum(ss, red), dim, a.eps);
-  for (int i = tid; i < dim; i += kNT) xs[i] = norm_one(xs[i], rms, a.w_pre[i]);
-  if (blockIdx.x == 0 && a.h_out != nullptr)
-    for (int i = tid; i < dim; i += kNT) a.h_out[i] = xs[i];
-  __syncthreads();
-}
-
-// Quantizes xs[0..k) into xq (LDS) exactly as quantize_act does
-// (gemma.c:2590-2650); returns the activation scale.
-__device__ float quantize_lds(const float *xs, int8_t *xq, int k, float *red) {
-  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss += (double)in.xr[j][e] * (double)in.xr[j][e];
+  const double rms = rms_of(block_sum<NT>(ss, red), a.dim, a.eps);
   float amax = 0.0f;
-  for (int i = tid; i < k; i += kNT) amax = fmaxf(amax, abs_daz(xs[i]));
-  amax = block_max(amax, red);
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      in.y[j][e] = norm_one(in.xr[j][e], rms, in.wq[j][e]);  // h; padding lanes stay 0
+      amax = fmaxf(amax, abs_daz(in.y[j][e]));
+    }
+  if (blockIdx.x == 0 && a.h_out != nullptr)
+#pragma unroll
+    for (int j = 0; j < NPT; ++j)
+      if (tid + j * NT < n4) reinterpret_cast<v4f *>(a.h_out)[tid + j * NT] = in.y[j];
+  if (xq == nullptr) return 1.0f;
+  amax = block_max<NT>(amax, redf);
   const QuantParams qp = quant_params(amax);
-  for (int c = tid; c < k / 4; c += kNT)
-    reinterpret_cast<uint32_t *>(xq)[c] =
-        pack4(quant_one(xs[4 * c], qp.inv), quant_one(xs[4 * c + 1], qp.inv),
-              quant_one(xs[4 * c + 2], qp.inv), quant_one(xs[4 * c + 3], qp.inv));
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int c = tid + j * NT;
+    if (c < n4)
+      reinterpret_cast<uint32_t *>(xq)[c] =
+          pack4(quant_one(in.y[j].x, qp.inv), quant_one(in.y[j].y, qp.inv),
+                quant_one(in.y[j].z, qp.inv), quant_one(in.y[j].w, qp.inv));
+  }
   __syncthreads();
   return qp.scale;
 }
@@ -162,14 +207,14 @@ __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
 //                 (jobs.w[1]); both sit in one wave (L <= 32), and the lanes
 //                 of the gate row store gelu(gate) * up to jobs.dst[0][r].
 // Requires k % 16 == 0, 16-byte aligned weight rows, k <= L * CPL * 16.
-template <int L, int CPL, bool GELU>
-__global__ __launch_bounds__(kNT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs jobs,
-                                                            int total, int k) {
-  extern __shared__ v4i lds4[];
-  __shared__ double red[kWaves];
-  __shared__ float redf[kWaves];
-  float *xs = reinterpret_cast<float *>(lds4);
-  v4i *xq4 = lds4 + (k * 4 + 15) / 16;
+template <int L, int CPL, bool GELU, int NT>
+__global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs jobs,
+                                                           int total, int k) {
+  extern __shared__ v4i xq4[];
+  constexpr int kW = NT / 64;
+  __shared__ double red[kW];
+  __shared__ float redf[kW];
+  constexpr int kNpt = (CPL * L * 16 + NT * 4 - 1) / (NT * 4);
   static_assert(!GELU || L <= 32, "gate and up rows must share a wave");
   constexpr int kRowsPerWave = 64 / L;
   const int lane = threadIdx.x & 63;
@@ -177,7 +222,7 @@ __global__ __launch_bounds__(kNT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs
   const int sub = lane % L;
   const int rloc = lane / L;
   const int kc = k >> 4;
-  const int stride = gridDim.x * kWaves * kRowsPerWave;
+  const int stride = gridDim.x * kW * kRowsPerWave;
 
   auto locate = [&](int row, int *r) -> int {
     if (GELU) {
@@ -231,11 +276,13 @@ __global__ __launch_bounds__(kNT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs
     }
   };
 
-  int base = (blockIdx.x * kWaves + wave) * kRowsPerWave;
+  int base = (blockIdx.x * kW + wave) * kRowsPerWave;
+  NormIn<kNpt> in;
+  norm_load<kNpt, NT>(na, in);
   v4i cur[CPL];
   load_row(base + rloc, cur);
-  norm_prologue(na, xs, red);
-  const float act_scale = quantize_lds(xs, reinterpret_cast<int8_t *>(xq4), k, redf);
+  const float act_scale =
+      norm_quant<kNpt, NT>(na, in, reinterpret_cast<int8_t *>(xq4), red, redf);
 
   for (; base < total; base += stride) {
     const int row = base + rloc;
@@ -274,168 +321,256 @@ __global__ __launch_bounds__(kNT) void dec_embed_kernel(DecEmbed a) {
 }
 
 // Final residual add + final norm (gemma.c:4950-4955): one workgroup writes h.
+template <int NPT>
 __global__ __launch_bounds__(kNT) void dec_final_norm_kernel(DecNorm na) {
-  extern __shared__ v4i lds4[];
   __shared__ double red[kWaves];
-  norm_prologue(na, reinterpret_cast<float *>(lds4), red);
+  __shared__ float redf[kWaves];
+  NormIn<NPT> in;
+  norm_load<NPT, kNT>(na, in);
+  norm_quant<NPT, kNT>(na, in, nullptr, red, redf);
 }
 
 // Attention of one kv head over one block of keys (gemma.c:4776-4851):
-// grid (max blocks, nkv).  The workgroup prepares the q heads of its group
-// (q norm, RoPE) and the new k (k norm, RoPE) and v rows in LDS; block 0
-// appends k and v to the cache.  Keys before the step's position are read
-// from the cache, the key at the position from LDS, so no workgroup waits
-// for another.  Output per (q head, block), in fp64: the block's max score
-// m, l = sum exp(s - m) and acc[d] = sum exp(s - m) v[d]; the combine kernel
-// merges the blocks.
+// grid (max blocks, nkv), kAttB keys per block.  The workgroup prepares the
+// q heads of its group (q norm, RoPE) and the new k (k norm, RoPE) and v
+// rows, loads its block's K and V rows into LDS with all loads in flight at
+// once (the key at the step's position comes from the new rows, so no
+// workgroup waits for another; block 0 appends them to the cache), then
+// computes scores, the block softmax and the value sums.  Output per (q head,
+// block), in fp64: the block's max score m, l = sum exp(s - m) and
+// acc[d] = sum exp(s - m) v[d]; the combine kernel merges the blocks.
+template <int HD>
 __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
   extern __shared__ double smem_d[];
-  __shared__ double red[kWaves];
   int token, pos;
   if (!step_ok(a.step, a.nvocab, a.clen, &token, &pos)) return;
-  const int hd = a.hdim;
+  constexpr int hd = HD;
   const int hk = blockIdx.y;
   const int hn = a.n_heads / a.nkv;
   const int h0 = hk * hn;
   const int spos = (a.slide > 0 && pos >= a.slide) ? pos + 1 - a.slide : 0;
-  const int t0 = spos + blockIdx.x * a.block;
+  const int t0 = spos + blockIdx.x * kAttB;
   if (t0 > pos) return;
-  const int t1 = min(t0 + a.block, pos + 1);
-  const int nt = t1 - t0;
+  const int nt = min(kAttB, pos + 1 - t0);
   const int tid = threadIdx.x;
 
-  double *s = smem_d;                                  // [hn][block]
-  float *q = reinterpret_cast<float *>(s + hn * a.block);  // [hn][hd]
-  float *kn = q + hn * hd;                             // [hd]
-  float *vn = kn + hd;                                 // [hd]
-  const float *cs = a.rope + (size_t)pos * hd;         // cos, sin interleaved
-
-  // q heads: optional rmsnorm with nq, then RoPE (gemma.c:4778-4800)
-  for (int g = 0; g < hn; ++g) {
-    const float *src = a.xq + (size_t)(h0 + g) * hd;
-    double rms = 1.0;
-    if (a.nq != nullptr) {
-      double ss = 0.0;
-      for (int d = tid; d < hd; d += kNT) ss += (double)src[d] * (double)src[d];
-      rms = rms_of(block_sum(ss, red), hd, a.eps);
-    }
-    for (int d = tid; d < hd; d += kNT)
-      q[g * hd + d] = a.nq != nullptr ? norm_one(src[d], rms, a.nq[d]) : src[d];
-    __syncthreads();
-    for (int d = tid; d < hd / 2; d += kNT) {
-      const double c = cs[2 * d], sn = cs[2 * d + 1];
-      const double x0 = q[g * hd + d], x1 = q[g * hd + d + hd / 2];
-      q[g * hd + d] = (float)(x0 * c - x1 * sn);
-      q[g * hd + d + hd / 2] = (float)(x0 * sn + x1 * c);
-    }
-    __syncthreads();
-  }
-  // the new key (k norm, RoPE) and value rows
-  {
-    const float *src = a.xk + (size_t)hk * hd;
-    double rms = 1.0;
-    if (a.nk != nullptr) {
-      double ss = 0.0;
-      for (int d = tid; d < hd; d += kNT) ss += (double)src[d] * (double)src[d];
-      rms = rms_of(block_sum(ss, red), hd, a.eps);
-    }
-    for (int d = tid; d < hd; d += kNT) {
-      kn[d] = a.nk != nullptr ? norm_one(src[d], rms, a.nk[d]) : src[d];
-      vn[d] = a.xv[(size_t)hk * hd + d];
-    }
-    __syncthreads();
-    for (int d = tid; d < hd / 2; d += kNT) {
-      const double c = cs[2 * d], sn = cs[2 * d + 1];
-      const double x0 = kn[d], x1 = kn[d + hd / 2];
-      kn[d] = (float)(x0 * c - x1 * sn);
-      kn[d + hd / 2] = (float)(x0 * sn + x1 * c);
-    }
-    __syncthreads();
-  }
+  double *e = smem_d;                                       // [hn][kAttB]
+  float *q = reinterpret_cast<float *>(e + hn * kAttB);     // [hn][hd]
+  float *kn = q + hn * hd;                                  // [hd]
+  float *vn = kn + hd;                                      // [hd]
+  constexpr int KS = HD + 4;  // padded K rows: the score reads hit distinct banks
+  float *kt = vn + hd;                                      // [kAttB][KS]
+  float *vt = kt + kAttB * KS;                              // [kAttB][hd]
+  const float *cs = a.rope + (size_t)pos * hd;              // cos, sin interleaved
   float *kc = a.kc + (size_t)hk * a.clen * hd;
   float *vc = a.vc + (size_t)hk * a.clen * hd;
+
+  // Loads, in the order their data is needed (vector loads return in issue
+  // order): this wave's first prologue row, the new value row, then the
+  // block's cached K and V rows (all but the step's own key).
+  const int lane = tid & 63, wave = tid >> 6;
+  constexpr int NJ = HD / 64, NH = NJ / 2;
+  struct Row {
+    float v[NJ], w[NJ], c[NH], s[NH];
+  };
+  auto load_row = [&](int r, Row &row) {
+    const float *src = r < hn ? a.xq + (size_t)(h0 + r) * hd : a.xk + (size_t)hk * hd;
+    const float *w = r < hn ? a.nq : a.nk;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      row.v[jj] = src[lane + 64 * jj];
+      row.w[jj] = w != nullptr ? w[lane + 64 * jj] : 0.0f;
+    }
+#pragma unroll
+    for (int jj = 0; jj < NH; ++jj) {
+      row.c[jj] = cs[2 * (lane + 64 * jj)];
+      row.s[jj] = cs[2 * (lane + 64 * jj) + 1];
+    }
+  };
+  Row first;
+  if (wave <= hn) load_row(wave, first);
+  constexpr int kVn = (HD + kNT - 1) / kNT;
+  float vnr[kVn];
+#pragma unroll
+  for (int u = 0; u < kVn; ++u)
+    vnr[u] = tid + u * kNT < hd ? a.xv[(size_t)hk * hd + tid + u * kNT] : 0.0f;
+
+  const int ncached = min(nt, pos - t0);  // keys t0 .. t0+ncached-1 are cached
+  const int vec = hd / 4;
+  const int ntile = ncached * vec;
+  constexpr int kTileV = kAttB * HD / 4 / kNT;  // 16-byte loads per thread per tile
+  v4f kr[kTileV], vr[kTileV];
+#pragma unroll
+  for (int u = 0; u < kTileV; ++u) {
+    const int i = tid + u * kNT;
+    if (i < ntile) {
+      const int t = i / vec, c = i - t * vec;
+      kr[u] = reinterpret_cast<const v4f *>(kc + (size_t)(t0 + t) * hd)[c];
+      vr[u] = reinterpret_cast<const v4f *>(vc + (size_t)(t0 + t) * hd)[c];
+    }
+  }
+
+  // q heads and the new key: optional rmsnorm (nq / nk), then RoPE
+  // (gemma.c:4778-4800).  One wave per row; lane l holds d = l + 64 j, so
+  // the RoPE pair (d, d + HD/2) is (j, j + HD/128) in the same lane.
+  for (int r = wave; r <= hn; r += kWaves) {
+    Row row;
+    if (r == wave) {
+      row = first;
+    } else {
+      load_row(r, row);
+    }
+    const bool has_w = (r < hn ? a.nq : a.nk) != nullptr;
+    if (has_w) {
+      double ss = 0.0;
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) ss += (double)row.v[jj] * (double)row.v[jj];
+      const double rms = rms_of(wave_sum_f64(ss), hd, a.eps);
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) row.v[jj] = norm_one(row.v[jj], rms, row.w[jj]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < NH; ++jj) {
+      const double c = row.c[jj], sv = row.s[jj];
+      const double x0 = row.v[jj], x1 = row.v[jj + NH];
+      row.v[jj] = (float)(x0 * c - x1 * sv);
+      row.v[jj + NH] = (float)(x0 * sv + x1 * c);
+    }
+    float *dst = r < hn ? q + (size_t)r * hd : kn;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) dst[lane + 64 * jj] = row.v[jj];
+  }
+#pragma unroll
+  for (int u = 0; u < kVn; ++u)
+    if (tid + u * kNT < hd) vn[tid + u * kNT] = vnr[u];
+#pragma unroll
+  for (int u = 0; u < kTileV; ++u) {
+    const int i = tid + u * kNT;
+    if (i < ntile) {
+      const int t = i / vec, c = i - t * vec;
+      *reinterpret_cast<v4f *>(kt + t * KS + 4 * c) = kr[u];
+      reinterpret_cast<v4f *>(vt)[i] = vr[u];
+    }
+  }
+  __syncthreads();
   if (blockIdx.x == 0)
     for (int d = tid; d < hd; d += kNT) {
       kc[(size_t)pos * hd + d] = kn[d];
       vc[(size_t)pos * hd + d] = vn[d];
     }
+  if (ncached < nt)  // the block holds the step's position: its rows from LDS
+    for (int d = tid; d < hd; d += kNT) {
+      kt[ncached * KS + d] = kn[d];
+      vt[ncached * hd + d] = vn[d];
+    }
+  __syncthreads();
 
-  // scores: one key per wave at a time, lanes split the head dimension
-  const int lane = tid & 63, wave = tid >> 6;
-  for (int t = wave; t < nt; t += kWaves) {
-    const int key = t0 + t;
-    const float *kr = key == pos ? kn : kc + (size_t)key * hd;
-    for (int g = 0; g < hn; ++g) {
-      double part = 0.0;
-      for (int d = lane; d < hd; d += 64) part += (double)q[g * hd + d] * (double)kr[d];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
-      if (lane == 0) {
-        double sc = part * (double)a.asc;
-        if (a.sc_att != 0.0f) sc = tanh(sc / (double)a.sc_att) * (double)a.sc_att;
-        s[g * a.block + t] = sc;
+  // scores: four threads per (head, key) pair, each summing every fourth
+  // element of the head dimension, then a quad reduction
+  const int npair = hn * nt;
+  for (int p0 = 0; p0 < npair; p0 += kNT / 4) {
+    const int pr = p0 + (tid >> 2), c = tid & 3;
+    double a0 = 0.0, a1 = 0.0;
+    if (pr < npair) {
+      const int g = pr / nt, t = pr - g * nt;
+      const float *qg = q + g * hd + c;
+      const float *kr = kt + t * KS + c;
+#pragma unroll 8
+      for (int i = 0; i < HD / 4; i += 2) {
+        a0 += (double)qg[4 * i] * (double)kr[4 * i];
+        a1 += (double)qg[4 * i + 4] * (double)kr[4 * i + 4];
       }
+    }
+    double part = a0 + a1;
+    part += dpp_f64<kDppXor1>(part);
+    part += dpp_f64<kDppXor2>(part);
+    if (pr < npair && c == 0) {
+      const int g = pr / nt, t = pr - g * nt;
+      double sc = part * (double)a.asc;
+      if (a.sc_att != 0.0f) sc = tanh(sc / (double)a.sc_att) * (double)a.sc_att;
+      e[g * kAttB + t] = sc;
     }
   }
   __syncthreads();
-  // per head: max, exp, sum, and the value sum
-  for (int g = 0; g < hn; ++g) {
-    double m = -DBL_MAX;
-    for (int t = tid; t < nt; t += kNT) m = fmax(m, s[g * a.block + t]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmax(m, __shfl_xor(m, off, 64));
-    __syncthreads();
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    m = red[0];
-#pragma unroll
-    for (int w = 1; w < kWaves; ++w) m = fmax(m, red[w]);
-    double l = 0.0;
-    for (int t = tid; t < nt; t += kNT) {
-      const double e = exp(s[g * a.block + t] - m);
-      s[g * a.block + t] = e;
-      l += e;
+  // block softmax: one wave per head, lane t holds key t (nt <= 16 lanes:
+  // one DPP row)
+  double *out_base = a.part + ((size_t)h0 * a.max_blocks + blockIdx.x) * (hd + 2);
+  const size_t head_stride = (size_t)a.max_blocks * (hd + 2);
+  for (int g = wave; g < hn; g += kWaves) {
+    const bool live = lane < nt;
+    double sv = live ? e[g * kAttB + lane] : -DBL_MAX;
+    double m = sv;
+    m = fmax(m, dpp_f64<kDppXor1>(m));
+    m = fmax(m, dpp_f64<kDppXor2>(m));
+    m = fmax(m, dpp_f64<kDppHalfMirror>(m));
+    m = fmax(m, dpp_f64<kDppMirror>(m));
+    m = readlane_f64(m, 0);
+    const double x = live ? exp(sv - m) : 0.0;
+    double l = x;
+    l += dpp_f64<kDppXor1>(l);
+    l += dpp_f64<kDppXor2>(l);
+    l += dpp_f64<kDppHalfMirror>(l);
+    l += dpp_f64<kDppMirror>(l);
+    if (live) e[g * kAttB + lane] = x;
+    if (lane == 0) {
+      out_base[g * head_stride + hd] = m;
+      out_base[g * head_stride + hd + 1] = l;
     }
-    l = block_sum(l, red);
-    double *out = a.part + ((size_t)(h0 + g) * a.max_blocks + blockIdx.x) * (hd + 2);
-    for (int d = tid; d < hd; d += kNT) {
-      double acc = 0.0;
-      for (int t = 0; t < nt; ++t) {
-        const int key = t0 + t;
-        const double v = key == pos ? vn[d] : vc[(size_t)key * hd + d];
-        acc += s[g * a.block + t] * v;
+  }
+  __syncthreads();
+  // value sums: thread d, every head of the group, four chains over the keys
+  for (int d = tid; d < hd; d += kNT) {
+    for (int g = 0; g < hn; ++g) {
+      const double *eg = e + g * kAttB;
+      double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+      int t = 0;
+      for (; t + 4 <= nt; t += 4) {
+        a0 += eg[t] * (double)vt[t * hd + d];
+        a1 += eg[t + 1] * (double)vt[(t + 1) * hd + d];
+        a2 += eg[t + 2] * (double)vt[(t + 2) * hd + d];
+        a3 += eg[t + 3] * (double)vt[(t + 3) * hd + d];
       }
-      out[d] = acc;
+      for (; t < nt; ++t) a0 += eg[t] * (double)vt[t * hd + d];
+      out_base[g * head_stride + d] = (a0 + a1) + (a2 + a3);
     }
-    if (tid == 0) {
-      out[hd] = m;
-      out[hd + 1] = l;
-    }
-    __syncthreads();
   }
 }
 
-// xo[h] = sum_b exp(m_b - M) acc_b / sum_b exp(m_b - M) l_b: grid n_heads
+// xo[h] = sum_b exp(m_b - M) acc_b / sum_b exp(m_b - M) l_b: grid n_heads;
+// the block weights exp(m_b - M) are computed once into LDS
 __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
+  extern __shared__ double wts[];
+  __shared__ double red[kWaves];
   int token, pos;
   if (!step_ok(a.step, a.nvocab, a.clen, &token, &pos)) return;
-  const int hd = a.hdim, h = blockIdx.x;
+  const int hd = a.hdim, h = blockIdx.x, tid = threadIdx.x;
   const int spos = (a.slide > 0 && pos >= a.slide) ? pos + 1 - a.slide : 0;
-  const int nb = (pos + 1 - spos + a.block - 1) / a.block;
+  const int nb = (pos + 1 - spos + kAttB - 1) / kAttB;
   const double *p = a.part + (size_t)h * a.max_blocks * (hd + 2);
   double m = -DBL_MAX;
-  for (int b = 0; b < nb; ++b) m = fmax(m, p[(size_t)b * (hd + 2) + hd]);
+  for (int b = tid; b < nb; b += kNT) m = fmax(m, p[(size_t)b * (hd + 2) + hd]);
+  m = fmax(m, dpp_f64<kDppXor1>(m));
+  m = fmax(m, dpp_f64<kDppXor2>(m));
+  m = fmax(m, dpp_f64<kDppHalfMirror>(m));
+  m = fmax(m, dpp_f64<kDppMirror>(m));
+  m = fmax(fmax(readlane_f64(m, 0), readlane_f64(m, 16)),
+           fmax(readlane_f64(m, 32), readlane_f64(m, 48)));
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) m = fmax(m, red[w]);
   double den = 0.0;
-  for (int b = 0; b < nb; ++b) {
-    const double *pb = p + (size_t)b * (hd + 2);
-    den += exp(pb[hd] - m) * pb[hd + 1];
+  for (int b = tid; b < nb; b += kNT) {
+    const double w = exp(p[(size_t)b * (hd + 2) + hd] - m);
+    wts[b] = w;
+    den += w * p[(size_t)b * (hd + 2) + hd + 1];
   }
-  for (int d = threadIdx.x; d < hd; d += kNT) {
+  den = block_sum(den, red);
+  __syncthreads();
+  for (int d = tid; d < hd; d += kNT) {
     double num = 0.0;
-    for (int b = 0; b < nb; ++b) {
-      const double *pb = p + (size_t)b * (hd + 2);
-      num += exp(pb[hd] - m) * pb[d];
-    }
+    for (int b = 0; b < nb; ++b) num += wts[b] * p[(size_t)b * (hd + 2) + d];
     a.xo[(size_t)h * hd + d] = (float)(num / den);
   }
 }
@@ -522,15 +657,22 @@ __global__ __launch_bounds__(kNT) void dec_argmax_final_kernel(const float *pval
   }
 }
 
+// 1024-thread workgroups, one per CU: the prologue is paid once per CU and
+// each workgroup streams its rows with one row per row group in flight
+// ahead (measured on the 1b/4b q/k/v and gate/up shapes against 256-thread
+// workgroups at up to 8 per CU, which pay the prologue up to 8 times).
+constexpr int kNormNT = 1024;
+
 template <int L, int CPL, bool GELU>
 hipError_t launch_norm_gemv_t(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                               const DeviceInfo &dev, hipStream_t stream) {
-  constexpr int rows_per_block = kWaves * (64 / L);
+  constexpr int rows_per_block = kNormNT / 64 * (64 / L);
   long blocks = (total + rows_per_block - 1) / rows_per_block;
-  const long cap = (long)dev.cus * 8;
-  const size_t lds = (size_t)(k * 4 + 15) / 16 * 16 + (size_t)k;
-  dec_norm_gemv_kernel<L, CPL, GELU>
-      <<<dim3((unsigned)(blocks < cap ? blocks : cap)), kNT, lds, stream>>>(na, jobs, total, k);
+  const long cap = (long)dev.cus;
+  const size_t lds = (size_t)(k + 15) / 16 * 16;
+  dec_norm_gemv_kernel<L, CPL, GELU, kNormNT>
+      <<<dim3((unsigned)(blocks < cap ? blocks : cap)), kNormNT, lds, stream>>>(na, jobs, total,
+                                                                             k);
   return hipGetLastError();
 }
 
@@ -571,17 +713,31 @@ hipError_t launch_dec_embed(const DecEmbed &a, hipStream_t stream) {
 }
 
 hipError_t launch_dec_final_norm(const DecNorm &na, hipStream_t stream) {
-  dec_final_norm_kernel<<<1, kNT, (size_t)na.dim * 4, stream>>>(na);
+  switch ((na.dim + kNT * 4 - 1) / (kNT * 4)) {
+    case 1: dec_final_norm_kernel<1><<<1, kNT, 0, stream>>>(na); break;
+    case 2: dec_final_norm_kernel<2><<<1, kNT, 0, stream>>>(na); break;
+    case 3: dec_final_norm_kernel<3><<<1, kNT, 0, stream>>>(na); break;
+    case 4: dec_final_norm_kernel<4><<<1, kNT, 0, stream>>>(na); break;
+    case 5: dec_final_norm_kernel<5><<<1, kNT, 0, stream>>>(na); break;
+    case 6: dec_final_norm_kernel<6><<<1, kNT, 0, stream>>>(na); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_dec_attention(const DecAttn &a, hipStream_t stream) {
-  const int hn = a.n_heads / a.nkv;
-  const size_t lds = (size_t)hn * a.block * 8 + ((size_t)hn * a.hdim + 2 * (size_t)a.hdim) * 4;
-  dec_attn_kernel<<<dim3(a.max_blocks, a.nkv), kNT, lds, stream>>>(a);
+  const dim3 grid(a.max_blocks, a.nkv);
+  const size_t lds = dec_attn_lds(a.n_heads / a.nkv, a.hdim);
+  switch (a.hdim) {
+    case 128: dec_attn_kernel<128><<<grid, kNT, lds, stream>>>(a); break;
+    case 256: dec_attn_kernel<256><<<grid, kNT, lds, stream>>>(a); break;
+    case 384: dec_attn_kernel<384><<<grid, kNT, lds, stream>>>(a); break;
+    case 512: dec_attn_kernel<512><<<grid, kNT, lds, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dec_attn_combine_kernel<<<a.n_heads, kNT, 0, stream>>>(a);
+  dec_attn_combine_kernel<<<a.n_heads, kNT, (size_t)a.max_blocks * 8, stream>>>(a);
   return hipGetLastError();
 }
 

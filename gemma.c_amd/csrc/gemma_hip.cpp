@@ -807,7 +807,7 @@ int gemma_hip_patch_embed_host(float *dst, const float *img, const float *pe,
 struct gemma_hip_decoder {
   gemma_hip_text_config cfg{};
   std::vector<unsigned char> swa;
-  int clen = 0, block = 64, max_blocks = 0, nparts = 256;
+  int clen = 0, max_blocks = 0, nparts = 256;
   struct Layer {
     const int8_t *w[7];  // wq wk wv wo w1(up) w2(gate) w3(down), device
     const float *s[7];
@@ -871,7 +871,7 @@ hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
     const bool sliding = d->swa[l] != 0;
     gh::DecAttn at{d->xq, d->xk, d->xv, c.qk_norm ? L.nq : nullptr, c.qk_norm ? L.nk : nullptr,
                    sliding ? d->rope_l : d->rope_g, kc, kc + cache, d->part, d->xo, d->step,
-                   c.n_heads, c.nkv, c.hdim, d->clen, sliding ? c.slide : 0, d->block,
+                   c.n_heads, c.nkv, c.hdim, d->clen, sliding ? c.slide : 0,
                    d->max_blocks, c.nvocab, (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att,
                    c.eps};
     if ((e = gh::launch_dec_attention(at, st)) != hipSuccess) return e;
@@ -957,10 +957,12 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   d->swa.assign(c.swa, c.swa + c.nl);
   d->cfg.swa = nullptr;
   d->clen = clen;
-  d->max_blocks = (clen + d->block - 1) / d->block;
+  d->max_blocks = (clen + gh::kDecAttnBlock - 1) / gh::kDecAttnBlock;
   const int hn = c.n_heads / c.nkv;
-  if ((size_t)hn * d->block * 8 + ((size_t)hn * c.hdim + 2 * (size_t)c.hdim) * 4 > 65536) {
-    fail("gemma_hip_decoder_create: attention tile exceeds 64 KB of LDS");
+  if (gh::dec_attn_lds(hn, c.hdim) > 65536 || (size_t)d->max_blocks * 8 > 65536 ||
+      c.hdim % 128 != 0 || c.hdim > 512) {
+    fail("gemma_hip_decoder_create: unsupported attention shape (head dim %d must be a "
+         "multiple of 128 up to 512; %d q heads per kv head; context %d)", c.hdim, hn, clen);
     decoder_free(d);
     return nullptr;
   }

@@ -57,6 +57,59 @@ __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
   return acc;
 }
 
+// The fused activation staging in two phases, for x that fits in
+// registers (16-byte aligned, k % 4 == 0, k/4 <= kXRegs * NT): x_load issues
+// the loads; x_quantize reduces amax, quantizes x into LDS as int8 and
+// returns the scale (block 0 also stores xq_out / xs_out when given).
+// Vector loads return in issue order, so a caller that issues its weight
+// loads between the two phases does not delay the activation behind them.
+constexpr int kXRegs = 4;
+
+template <int NT>
+__device__ __forceinline__ void x_load(int k, const float *__restrict__ xf, v4f (&xr)[kXRegs]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < kXRegs; ++j) {
+    const int c = tid + j * NT;
+    xr[j] = c < k / 4 ? reinterpret_cast<const v4f *>(xf)[c] : v4f{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ float x_quantize(int8_t *lds, int k, const v4f (&xr)[kXRegs],
+                                            int8_t *__restrict__ xq_out,
+                                            float *__restrict__ xs_out) {
+  __shared__ float wave_amax[NT / 64];
+  const int tid = threadIdx.x;
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kXRegs; ++j)
+    amax = fmaxf(amax, fmaxf(fmaxf(abs_daz(xr[j].x), abs_daz(xr[j].y)),
+                             fmaxf(abs_daz(xr[j].z), abs_daz(xr[j].w))));
+  amax = wave_max_dpp(amax);
+  if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
+  __syncthreads();
+  amax = wave_amax[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, wave_amax[w]);
+  const QuantParams qp = quant_params(amax);
+#pragma unroll
+  for (int j = 0; j < kXRegs; ++j) {
+    const int c = tid + j * NT;
+    if (c < k / 4)
+      reinterpret_cast<uint32_t *>(lds)[c] =
+          pack4(quant_one(xr[j].x, qp.inv), quant_one(xr[j].y, qp.inv),
+                quant_one(xr[j].z, qp.inv), quant_one(xr[j].w, qp.inv));
+  }
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    if (xq_out != nullptr)
+      for (int c = tid; c < k; c += NT) xq_out[c] = lds[c];
+    if (xs_out != nullptr && tid == 0) *xs_out = qp.scale;
+  }
+  return qp.scale;
+}
+
 // Stage the activation vector in LDS as int8.  FUSED: quantize x fp32 [k]
 // (the quantize_act that precedes every decode GEMV); otherwise copy xq.
 // Returns the activation scale.
@@ -79,24 +132,16 @@ __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
     __syncthreads();
     return *xs;
   }
-
-  __shared__ float wave_amax[NT / 64];
   const bool vec = ((uintptr_t)xf & 15) == 0 && (k & 3) == 0;
-  // x stays in registers between the amax pass and the quantize pass when
-  // it fits in kXRegs float4 per thread (k <= 4096); longer rows re-read it.
-  constexpr int kXRegs = 4;
-  const bool in_regs = vec && k / 4 <= kXRegs * NT;
-  v4f xr[kXRegs];
+  if (vec && k / 4 <= kXRegs * NT) {
+    v4f xr[kXRegs];
+    x_load<NT>(k, xf, xr);
+    return x_quantize<NT>(lds, k, xr, xq_out, xs_out);
+  }
+  // long or unaligned rows: two passes over x (the second from L2)
+  __shared__ float wave_amax[NT / 64];
   float amax = 0.0f;
-  if (in_regs) {
-#pragma unroll
-    for (int j = 0; j < kXRegs; ++j) {
-      const int c = tid + j * NT;
-      xr[j] = c < k / 4 ? reinterpret_cast<const v4f *>(xf)[c] : v4f{0.f, 0.f, 0.f, 0.f};
-      amax = fmaxf(amax, fmaxf(fmaxf(abs_daz(xr[j].x), abs_daz(xr[j].y)),
-                               fmaxf(abs_daz(xr[j].z), abs_daz(xr[j].w))));
-    }
-  } else if (vec) {
+  if (vec) {
     for (int c = tid; c < k / 4; c += NT) {
       v4f v = reinterpret_cast<const v4f *>(xf)[c];
       amax = fmaxf(amax, fmaxf(fmaxf(abs_daz(v.x), abs_daz(v.y)),
@@ -105,23 +150,14 @@ __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
   } else {
     for (int c = tid; c < k; c += NT) amax = fmaxf(amax, abs_daz(xf[c]));
   }
-  amax = wave_max(amax);
+  amax = wave_max_dpp(amax);
   if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
   __syncthreads();
   amax = wave_amax[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, wave_amax[w]);
   const QuantParams qp = quant_params(amax);
-  if (in_regs) {
-#pragma unroll
-    for (int j = 0; j < kXRegs; ++j) {
-      const int c = tid + j * NT;
-      if (c < k / 4)
-        reinterpret_cast<uint32_t *>(lds)[c] =
-            pack4(quant_one(xr[j].x, qp.inv), quant_one(xr[j].y, qp.inv),
-                  quant_one(xr[j].z, qp.inv), quant_one(xr[j].w, qp.inv));
-    }
-  } else if (vec) {
+  if (vec) {
     for (int c = tid; c < k / 4; c += NT) {
       v4f v = reinterpret_cast<const v4f *>(xf)[c];
       reinterpret_cast<uint32_t *>(lds)[c] =
@@ -224,9 +260,18 @@ __global__ __launch_bounds__(NT) void gemv_i8_pipelined_kernel(
 
   int base = (blockIdx.x * kBlockWaves + wave) * kRowsPerWave;
   v4i cur[CPL];
-  load_row(base + rloc, cur);
-  const float act_scale = stage_x_i8<FUSED, NT>(reinterpret_cast<int8_t *>(lds_x4), k,
-                                            xq, xs, xf, xq_out, xs_out);
+  float act_scale;
+  if (FUSED && ((uintptr_t)xf & 15) == 0 && (k & 3) == 0 && k / 4 <= kXRegs * NT) {
+    // activation loads first, then the first weight row, then the quantize
+    v4f xr[kXRegs];
+    x_load<NT>(k, xf, xr);
+    load_row(base + rloc, cur);
+    act_scale = x_quantize<NT>(reinterpret_cast<int8_t *>(lds_x4), k, xr, xq_out, xs_out);
+  } else {
+    load_row(base + rloc, cur);
+    act_scale = stage_x_i8<FUSED, NT>(reinterpret_cast<int8_t *>(lds_x4), k, xq, xs, xf, xq_out,
+                                      xs_out);
+  }
 
   for (; base < total; base += stride) {
     const int row = base + rloc;

@@ -89,6 +89,13 @@ struct DecEmbed {
   float esc;
 };
 
+// Keys per attention workgroup, and its LDS bytes for hn q heads per kv head.
+constexpr int kDecAttnBlock = 16;
+inline size_t dec_attn_lds(int hn, int hdim) {
+  return (size_t)hn * kDecAttnBlock * 8 +
+         ((size_t)hn * hdim + 2 * (size_t)hdim + (size_t)kDecAttnBlock * (2 * hdim + 4)) * 4;
+}
+
 // One layer's attention: q/k/v rows in, xo out; kc/vc are the layer's cache
 // [nkv][clen][hdim]; rope the table [clen][hdim] (cos, sin interleaved) of
 // the layer's base; part holds [n_heads][max_blocks][hdim + 2] fp64 partials.
@@ -98,7 +105,7 @@ struct DecAttn {
   double *part;
   float *xo;
   const int *step;
-  int n_heads, nkv, hdim, clen, slide, block, max_blocks, nvocab;
+  int n_heads, nkv, hdim, clen, slide, max_blocks, nvocab;
   float asc, sc_att, eps;
 };
 

@@ -184,6 +184,44 @@ def read_bin(path: str) -> dict:
     return {"config": cfg, "emb": emb, "layers": layers, "fnorm": fnorm, "end": at}
 
 
+def synth_model(name: str, seed: int = 1234, nvocab: int = NVOCAB) -> dict:
+    """A random W8A8 model of shape `name` in memory, in read_bin()'s layout,
+    for throughput runs where writing a multi-GB file would dominate: int8
+    weights are tiles of one 64 MB random block (each tensor starting at its
+    own offset), row scales U(4e-4, 8e-4) (the scale of N(0, 0.02) weights
+    quantized per row), norm weights 0."""
+    c = CONFIGS[name]
+    nl, dim, hdim, mlp = c["nl"], c["dim"], c["hdim"], c["mlp"]
+    q_sz, kv_sz = c["n_heads"] * hdim, c["nkv"] * hdim
+    rng = np.random.default_rng(seed)
+    block = np.frombuffer(rng.bytes(64 << 20), np.int8)
+    block = np.where(block == -128, np.int8(127), block).astype(np.int8)
+    twice = np.concatenate([block, block])
+
+    def qt(rows, cols):
+        n = rows * cols
+        q = np.empty(n, np.int8)
+        start, done = int(rng.integers(0, len(block))), 0
+        while done < n:
+            take = min(n - done, len(block))
+            q[done:done + take] = twice[start:start + take]
+            done += take
+        return q.reshape(rows, cols), rng.uniform(4e-4, 8e-4, rows).astype(np.float32)
+
+    zeros = lambda n: np.zeros(n, np.float32)  # noqa: E731
+    cfg = dict(nl=nl, n_heads=c["n_heads"], nkv=c["nkv"], hdim=hdim, dim=dim, mlp_dim=mlp,
+               q_scale=hdim, slide=c["slide"], nvocab=nvocab, theta_l=10000.0,
+               theta_g=1000000.0, eps=float(np.float32(1e-6)), sc_att=0.0, sc_log=0.0,
+               qk_norm=True, mlp_pre=True, mlp_pst=True,
+               swa=[int((i + 1) % 6 != 0) for i in range(nl)], max_seq=32768)
+    layers = [{"wq": qt(q_sz, dim), "wk": qt(kv_sz, dim), "wv": qt(kv_sz, dim),
+               "wo": qt(dim, q_sz), "nq": zeros(hdim), "nk": zeros(hdim),
+               "w1": qt(mlp, dim), "w2": qt(mlp, dim), "w3": qt(dim, mlp),
+               "n1": zeros(dim), "n2": zeros(dim), "n3": zeros(dim), "n4": zeros(dim)}
+              for _ in range(nl)]
+    return {"config": cfg, "emb": qt(nvocab, dim), "layers": layers, "fnorm": zeros(dim)}
+
+
 def ensure_bin(directory: str, name: str, seed: int = 1234) -> str:
     """Path of the random-init model `name`, written on first use."""
     os.makedirs(directory, exist_ok=True)
