@@ -32,6 +32,14 @@
  * prints one JSON line: the generated tokens, an FNV-1a hash of the bits of
  * every step's logits, and the wall time of each phase.
  *
+ * Environment:
+ *   GEMMA_E2E_DECODE_ONLY=1  feed <bos> and the prompt one token at a time
+ *                            through forward_gemma_decode instead of the
+ *                            chunked prefill (the decode path at every
+ *                            position, as the device-resident decoder runs)
+ *   GEMMA_E2E_LOGITS=<path>  write every step's logits (nvocab float32 each,
+ *                            in step order) to <path>
+ *
  * Everything below the include uses identifiers of three characters or more
  * (the stb blob at the end of gemma.c defines one- and two-letter macros,
  * among them `x`), and touches no struct field of one or two letters that
@@ -247,37 +255,76 @@ int main(int argc, char **argv) {
   memset(&perf, 0, sizeof(perf));
   int pos = 0;
   int bos_tok = model->tok->bos;
-
-  double tic = now_sec();
-  if (forward_gemma_prefill(model, buf, &bos_tok, 1, &pos, chunk, NULL, false,
-                            threads, &perf) != 0) {
-    die_with("prefill <bos>", get_error());
+  const char *only = getenv("GEMMA_E2E_DECODE_ONLY");
+  const bool decode_only = only != NULL && only[0] == '1';
+  const char *dump_path = getenv("GEMMA_E2E_LOGITS");
+  FILE *dump = NULL;
+  if (dump_path != NULL && (dump = fopen(dump_path, "wb")) == NULL) {
+    die_with("logits file", dump_path);
   }
-  double bos_sec = now_sec() - tic;
-
-  tic = now_sec();
-  if (forward_gemma_prefill(model, buf, prompt, prompt_len, &pos, chunk, NULL,
-                            true, threads, &perf) != 0) {
-    die_with("prefill", get_error());
-  }
-  double prefill_sec = now_sec() - tic;
-
   uint64_t hash = 0xCBF29CE484222325ull;
-  hash = fnv_chain(hash, buf->logits, (size_t)nvocab);
+  double bos_sec = 0.0, prefill_sec = 0.0;
+
+  if (decode_only) {
+    /* every position through the decode path, <bos> first */
+    double tic = now_sec();
+    for (int idx = 0; idx <= prompt_len; idx++) {
+      int tok = idx == 0 ? bos_tok : prompt[idx - 1];
+      if (forward_gemma_decode(model, buf, tok, pos, threads, &perf) != 0) {
+        die_with("decode (prompt)", get_error());
+      }
+      pos++;
+      if (dump != NULL) {
+        fwrite(buf->logits, sizeof(float), (size_t)nvocab, dump);
+      }
+      if (idx == 0) {
+        bos_sec = now_sec() - tic;
+        tic = now_sec();
+      } else {
+        hash = fnv_chain(hash, buf->logits, (size_t)nvocab);
+      }
+    }
+    prefill_sec = now_sec() - tic;
+  } else {
+    double tic = now_sec();
+    if (forward_gemma_prefill(model, buf, &bos_tok, 1, &pos, chunk, NULL, false,
+                              threads, &perf) != 0) {
+      die_with("prefill <bos>", get_error());
+    }
+    bos_sec = now_sec() - tic;
+
+    tic = now_sec();
+    if (forward_gemma_prefill(model, buf, prompt, prompt_len, &pos, chunk, NULL,
+                              true, threads, &perf) != 0) {
+      die_with("prefill", get_error());
+    }
+    prefill_sec = now_sec() - tic;
+    hash = fnv_chain(hash, buf->logits, (size_t)nvocab);
+    if (dump != NULL) {
+      fwrite(buf->logits, sizeof(float), (size_t)nvocab, dump);
+    }
+  }
+
   int token = argmax(buf->logits, nvocab, threads);
   generated[0] = token;
 
-  tic = now_sec();
+  double tic = now_sec();
   for (int step = 0; step < decode_steps; step++) {
     if (forward_gemma_decode(model, buf, token, pos, threads, &perf) != 0) {
       die_with("decode", get_error());
     }
     pos++;
     hash = fnv_chain(hash, buf->logits, (size_t)nvocab);
+    if (dump != NULL) {
+      fwrite(buf->logits, sizeof(float), (size_t)nvocab, dump);
+    }
     token = argmax(buf->logits, nvocab, threads);
     generated[step + 1] = token;
   }
   double decode_sec = now_sec() - tic;
+  if (dump != NULL) {
+    fclose(dump);
+  }
 
   printf("{\"build\": \"%s\", \"model\": \"%s\", \"nl\": %d, \"dim\": %d, "
          "\"prompt_len\": %d, \"decode_steps\": %d, \"seed\": %" PRIu64
@@ -286,10 +333,10 @@ int main(int argc, char **argv) {
          decode_steps, seed, threads, chunk);
   printf("\"setup_s\": %.6f, \"weight_bytes\": %zu, \"bos_s\": %.6f, "
          "\"prefill_s\": %.6f, \"decode_s\": %.6f, \"prefill_tok_s\": %.3f, "
-         "\"decode_tok_s\": %.3f, ",
+         "\"decode_tok_s\": %.3f, \"decode_only\": %d, ",
          setup_sec, weight_bytes, bos_sec, prefill_sec, decode_sec,
          prompt_len / prefill_sec,
-         decode_steps > 0 ? decode_steps / decode_sec : 0.0);
+         decode_steps > 0 ? decode_steps / decode_sec : 0.0, (int)decode_only);
   printf("\"ops\": {");
   for (int phase = 0; phase < 2; phase++) {
     printf("%s\"%s\": {", phase ? ", " : "", phase ? "decode" : "prefill");
@@ -304,7 +351,8 @@ int main(int argc, char **argv) {
     }
     printf("}");
   }
-  printf("}, \"logits_fnv\": \"%016" PRIx64 "\", \"prompt\": [", hash);
+  printf("}, \"bos\": %d, \"logits_fnv\": \"%016" PRIx64 "\", \"prompt\": [",
+         bos_tok, hash);
   for (int idx = 0; idx < prompt_len; idx++) {
     printf("%s%d", idx ? ", " : "", prompt[idx]);
   }
