@@ -305,6 +305,10 @@ def bench_decode_1b(torch, gh, gen, timer, tokens):
                      "HIP graph); attention/norms/RoPE are outside this path")
 
 
+# decode phases of BASELINE.json configs 3 and 5: (model, context before, timed steps)
+DECODER_RUNS = (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512))
+
+
 def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     """Greedy decode fully on the GPU: the KV cache is filled by `prompt`
     untimed decode steps, then `steps` steps are timed (one HIP graph launch
@@ -397,6 +401,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["sweep", "lm_head", "decoder"], default=None,
                     help="profiling aid: run just the timed sweep, the LM-head timing or "
                          "the device-resident decoder")
+    ap.add_argument("--decoder-models", default="gemma-3-1b,gemma-3-4b",
+                    help="models of the decoder timing (comma list of gemma-3-1b, gemma-3-4b)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="profiling aid: 3 dispatches of an elementwise kernel that reads "
                          "and writes exactly 1 GiB (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -422,8 +428,9 @@ def main() -> int:
         return 0
 
     gh = gemma_hip.GemmaHip(0)
+    decoder_runs = [r for r in DECODER_RUNS if r[0] in args.decoder_models.split(",")]
     if args.only == "decoder":
-        for name, prompt, nsteps in (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512)):
+        for name, prompt, nsteps in decoder_runs:
             print(json.dumps(bench_decoder(torch, gh, name, prompt, nsteps)), flush=True)
         gh.close()
         return 0
@@ -472,7 +479,7 @@ def main() -> int:
     dec = bench_decode_1b(torch, gh, gen, timer, tokens=50)
     print(f"# decode_1b: {json.dumps(dec)}", file=sys.stderr, flush=True)
     decoder = {}
-    for name, prompt, nsteps in (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512)):
+    for name, prompt, nsteps in decoder_runs:
         decoder[name] = bench_decoder(torch, gh, name, prompt, nsteps)
         print(f"# decoder: {json.dumps(decoder[name])}", file=sys.stderr, flush=True)
 
