@@ -49,9 +49,9 @@ constexpr int kAttB = kDecAttnBlock;  // keys per attention workgroup
 template <int NT = kNT>
 __device__ __forceinline__ double block_sum(double v, double *red) {
   v = wave_sum_f64(v);
-  __syncthreads();
+  lds_barrier();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_barrier();
   double s = red[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) s += red[w];
@@ -61,9 +61,9 @@ __device__ __forceinline__ double block_sum(double v, double *red) {
 template <int NT = kNT>
 __device__ __forceinline__ float block_max(float v, float *red) {
   v = wave_max_dpp(v);
-  __syncthreads();
+  lds_barrier();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  lds_barrier();
   float s = red[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) s = fmaxf(s, red[w]);
@@ -187,7 +187,7 @@ __device__ float norm_quant(const DecNorm &a, NormIn<NPT> &in, int8_t *xq, doubl
           pack4(quant_one(in.y[j].x, qp.inv), quant_one(in.y[j].y, qp.inv),
                 quant_one(in.y[j].z, qp.inv), quant_one(in.y[j].w, qp.inv));
   }
-  __syncthreads();
+  lds_barrier();
   return qp.scale;
 }
 
@@ -200,14 +200,22 @@ __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
 }
 
 // The int8 GEMV behind the norm prologue.  L lanes per row, CPL 16-byte
-// chunks per lane; each lane issues the loads of its first row before the
-// prologue so HBM latency overlaps it.
+// chunks per lane, 64 / L rows per wave; a wave's rows sit `stride` apart,
+// in groups g = 0, 1, ... (row base + g * stride + lane / L).
 //  GELU == false: rows are the flat row range of `jobs` (q, k, v).
 //  GELU == true:  virtual row 2r is gate row r (jobs.w[0]), 2r+1 is up row r
 //                 (jobs.w[1]); both sit in one wave (L <= 32), and the lanes
 //                 of the gate row store gelu(gate) * up to jobs.dst[0][r].
+//  G >= 1: every wave has at most G groups, all loaded before the norm
+//          prologue so the weight stream runs under it.
+//  G == 0: any number of groups, loaded two ahead of their use.
+// Every weight load is issued unconditionally (a row past the end reads a
+// row of the wave's own first group, or the last row, and is not used):
+// the compiler's wait counts merge the paths of a conditional load by the
+// path without it, which would make the prologue wait for every weight load
+// issued before its own inputs arrive.
 // Requires k % 16 == 0, 16-byte aligned weight rows, k <= L * CPL * 16.
-template <int L, int CPL, bool GELU, int NT>
+template <int L, int CPL, bool GELU, int G, int NT>
 __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs jobs,
                                                            int total, int k) {
   extern __shared__ v4i xq4[];
@@ -218,11 +226,13 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
   static_assert(!GELU || L <= 32, "gate and up rows must share a wave");
   constexpr int kRowsPerWave = 64 / L;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane % L;
   const int rloc = lane / L;
   const int kc = k >> 4;
   const int stride = gridDim.x * kW * kRowsPerWave;
+  const int base = (blockIdx.x * kW + wave) * kRowsPerWave;  // wave-uniform
+  const int own = base + rloc < total ? base + rloc : total - 1;
 
   auto locate = [&](int row, int *r) -> int {
     if (GELU) {
@@ -239,75 +249,66 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
     *r = row - start;
     return j;
   };
-  auto pick_w = [&](int j) {
-    const void *v = jobs.w[0];
-#pragma unroll
-    for (int t = 1; t < kMaxJobs; ++t)
-      if (j == t) v = jobs.w[t];
-    return static_cast<const v4i *>(v);
+  struct Row {
+    v4i w[CPL];
+    float sc;  // loaded with the weights: loads complete in issue order
   };
-  auto pick_sc = [&](int j) {
-    const float *v = jobs.sc[0];
+  auto load_group = [&](int g, Row &buf) {
+    const int row = base + g * stride + rloc;
+    int r;
+    const int j = locate(row < total ? row : own, &r);
+    const gptr<const v4i> w4 =
+        as_global(static_cast<const v4i *>(pick4(jobs.w, j))) + (size_t)r * kc;
 #pragma unroll
-    for (int t = 1; t < kMaxJobs; ++t)
-      if (j == t) v = jobs.sc[t];
-    return v;
-  };
-  auto pick_dst = [&](int j) {
-    float *v = jobs.dst[0];
-#pragma unroll
-    for (int t = 1; t < kMaxJobs; ++t)
-      if (j == t) v = jobs.dst[t];
-    return v;
-  };
-  auto load_row = [&](int row, v4i (&buf)[CPL]) {
-    if (row < total) {
-      int r;
-      const int j = locate(row, &r);
-      const v4i *w4 = pick_w(j) + (size_t)r * kc;
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = sub + i * L;
-        buf[i] = c < kc ? __builtin_nontemporal_load(w4 + c) : v4i{0, 0, 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) buf[i] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;
+      buf.w[i] = __builtin_nontemporal_load(w4 + (c < kc ? c : 0));
     }
+    buf.sc = as_global(pick4(jobs.sc, j))[r];
   };
 
-  int base = (blockIdx.x * kW + wave) * kRowsPerWave;
   NormIn<kNpt> in;
   norm_load<kNpt, NT>(na, in);
-  v4i cur[CPL];
-  load_row(base + rloc, cur);
+  constexpr int kDepth = G > 0 ? G : 2;
+  Row rows[kDepth];
+#pragma unroll
+  for (int g = 0; g < kDepth; ++g) load_group(g, rows[g]);
   const float act_scale =
       norm_quant<kNpt, NT>(na, in, reinterpret_cast<int8_t *>(xq4), red, redf);
 
-  for (; base < total; base += stride) {
-    const int row = base + rloc;
-    v4i nxt[CPL];
-    load_row(row + stride, nxt);
+  auto process = [&](int g, const Row &w) {
+    const int row = base + g * stride + rloc;
     int32_t acc = 0;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = sub + i * L;
-      if (c < kc) acc = dot16(cur[i], xq4[c], acc);
+      if (c < kc) acc = dot16(w.w[i], xq4[c], acc);
     }
 #pragma unroll
     for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    const float val = row < total ? rescale(acc, act_scale, w.sc) : 0.0f;
     int r = 0;
     const int j = locate(row < total ? row : 0, &r);
-    const float val = row < total ? rescale(acc, act_scale, pick_sc(j)[r]) : 0.0f;
     if (GELU) {
       const float up = __shfl_xor(val, L, 64);
       if (sub == 0 && (rloc & 1) == 0 && row < total)
-        jobs.dst[0][r] = (float)(gelu_tanh((double)val) * (double)up);
+        as_global(pick4(jobs.dst, 0))[r] = (float)(gelu_tanh((double)val) * (double)up);
     } else if (sub == 0 && row < total) {
-      pick_dst(j)[r] = val;
+      as_global(pick4(jobs.dst, j))[r] = val;
     }
+  };
+  if (G > 0) {
+    // groups past the wave's last are skipped whole (g * stride is uniform)
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) cur[i] = nxt[i];
+    for (int g = 0; g < kDepth; ++g)
+      if (base + g * stride < total) process(g, rows[g]);
+  } else {
+    for (int g = 0; base + g * stride < total; g += 2) {
+      process(g, rows[0]);
+      load_group(g + 2, rows[0]);
+      if (base + (g + 1) * stride < total) process(g + 1, rows[1]);
+      load_group(g + 3, rows[1]);
+    }
   }
 }
 
@@ -452,7 +453,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
       reinterpret_cast<v4f *>(vt)[i] = vr[u];
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (blockIdx.x == 0)
     for (int d = tid; d < hd; d += kNT) {
       kc[(size_t)pos * hd + d] = kn[d];
@@ -463,7 +464,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
       kt[ncached * KS + d] = kn[d];
       vt[ncached * hd + d] = vn[d];
     }
-  __syncthreads();
+  lds_barrier();
 
   // scores: four threads per (head, key) pair, each summing every fourth
   // element of the head dimension, then a quad reduction
@@ -491,7 +492,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
       e[g * kAttB + t] = sc;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // block softmax: one wave per head, lane t holds key t (nt <= 16 lanes:
   // one DPP row)
   double *out_base = a.part + ((size_t)h0 * a.max_blocks + blockIdx.x) * (hd + 2);
@@ -517,7 +518,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
       out_base[g * head_stride + hd + 1] = l;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // value sums: thread d, every head of the group, four chains over the keys
   for (int d = tid; d < hd; d += kNT) {
     for (int g = 0; g < hn; ++g) {
@@ -556,7 +557,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   m = fmax(fmax(readlane_f64(m, 0), readlane_f64(m, 16)),
            fmax(readlane_f64(m, 32), readlane_f64(m, 48)));
   if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
+  lds_barrier();
   m = red[0];
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) m = fmax(m, red[w]);
@@ -567,7 +568,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
     den += w * p[(size_t)b * (hd + 2) + hd + 1];
   }
   den = block_sum(den, red);
-  __syncthreads();
+  lds_barrier();
   for (int d = tid; d < hd; d += kNT) {
     double num = 0.0;
     for (int b = 0; b < nb; ++b) num += wts[b] * p[(size_t)b * (hd + 2) + d];
@@ -597,7 +598,7 @@ __global__ __launch_bounds__(kNT) void dec_argmax_partial_kernel(const float *lo
   __shared__ int si[kNT];
   sv[threadIdx.x] = best;
   si[threadIdx.x] = bi;
-  __syncthreads();
+  lds_barrier();
   for (int w = kNT / 2; w > 0; w >>= 1) {
     if (threadIdx.x < w) {
       const float ov = sv[threadIdx.x + w];
@@ -608,7 +609,7 @@ __global__ __launch_bounds__(kNT) void dec_argmax_partial_kernel(const float *lo
         si[threadIdx.x] = oi;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (threadIdx.x == 0) {
     pval[blockIdx.x] = sv[0];
@@ -635,7 +636,7 @@ __global__ __launch_bounds__(kNT) void dec_argmax_final_kernel(const float *pval
   }
   sv[threadIdx.x] = best;
   si[threadIdx.x] = bi;
-  __syncthreads();
+  lds_barrier();
   for (int w = kNT / 2; w > 0; w >>= 1) {
     if (threadIdx.x < w) {
       const float ov = sv[threadIdx.x + w];
@@ -646,7 +647,7 @@ __global__ __launch_bounds__(kNT) void dec_argmax_final_kernel(const float *pval
         si[threadIdx.x] = oi;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
   if (threadIdx.x == 0) {
     const int count = step[2];
@@ -663,48 +664,61 @@ __global__ __launch_bounds__(kNT) void dec_argmax_final_kernel(const float *pval
 // workgroups at up to 8 per CU, which pay the prologue up to 8 times).
 constexpr int kNormNT = 1024;
 
-template <int L, int CPL, bool GELU>
+template <int L, int CPL, bool GELU, int G>
 hipError_t launch_norm_gemv_t(const DecNorm &na, const GemvJobs &jobs, int total, int k,
-                              const DeviceInfo &dev, hipStream_t stream) {
-  constexpr int rows_per_block = kNormNT / 64 * (64 / L);
-  long blocks = (total + rows_per_block - 1) / rows_per_block;
-  const long cap = (long)dev.cus;
+                              int blocks, hipStream_t stream) {
   const size_t lds = (size_t)(k + 15) / 16 * 16;
-  dec_norm_gemv_kernel<L, CPL, GELU, kNormNT>
-      <<<dim3((unsigned)(blocks < cap ? blocks : cap)), kNormNT, lds, stream>>>(na, jobs, total,
-                                                                             k);
+  dec_norm_gemv_kernel<L, CPL, GELU, G, kNormNT>
+      <<<dim3((unsigned)blocks), kNormNT, lds, stream>>>(na, jobs, total, k);
   return hipGetLastError();
 }
 
-template <int L, bool GELU>
+// Groups per wave with one workgroup per CU; the weight registers of all
+// groups (G * CPL * 4 per lane) are kept within 64 where G > 0.
+template <int L, int CPL, bool GELU>
+hipError_t norm_gemv_groups(const DecNorm &na, const GemvJobs &jobs, int total, int k,
+                            const DeviceInfo &dev, hipStream_t stream) {
+  constexpr int rows_per_block = kNormNT / 64 * (64 / L);
+  const long need = (total + rows_per_block - 1) / rows_per_block;
+  const int blocks = (int)(need < dev.cus ? need : dev.cus);
+  const long stride = (long)blocks * rows_per_block;
+  const long groups = (total + stride - 1) / stride;
+  if (groups <= 1) return launch_norm_gemv_t<L, CPL, GELU, 1>(na, jobs, total, k, blocks, stream);
+  if (groups == 2 && 2 * CPL <= 16)
+    return launch_norm_gemv_t<L, CPL, GELU, (2 * CPL <= 16 ? 2 : 0)>(na, jobs, total, k, blocks,
+                                                                     stream);
+  if (groups == 3 && 3 * CPL <= 16)
+    return launch_norm_gemv_t<L, CPL, GELU, (3 * CPL <= 16 ? 3 : 0)>(na, jobs, total, k, blocks,
+                                                                     stream);
+  if (groups == 4 && 4 * CPL <= 16)
+    return launch_norm_gemv_t<L, CPL, GELU, (4 * CPL <= 16 ? 4 : 0)>(na, jobs, total, k, blocks,
+                                                                     stream);
+  return launch_norm_gemv_t<L, CPL, GELU, 0>(na, jobs, total, k, blocks, stream);
+}
+
+template <int L, bool GELU, int C, int CMAX>
 hipError_t norm_gemv_cpl(int cpl, const DecNorm &na, const GemvJobs &jobs, int total, int k,
                          const DeviceInfo &dev, hipStream_t stream) {
-  switch (cpl) {
-    case 1: return launch_norm_gemv_t<L, 1, GELU>(na, jobs, total, k, dev, stream);
-    case 2: return launch_norm_gemv_t<L, 2, GELU>(na, jobs, total, k, dev, stream);
-    case 3: return launch_norm_gemv_t<L, 3, GELU>(na, jobs, total, k, dev, stream);
-    case 4: return launch_norm_gemv_t<L, 4, GELU>(na, jobs, total, k, dev, stream);
-    case 5: return launch_norm_gemv_t<L, 5, GELU>(na, jobs, total, k, dev, stream);
-    case 6: return launch_norm_gemv_t<L, 6, GELU>(na, jobs, total, k, dev, stream);
-    case 7: return launch_norm_gemv_t<L, 7, GELU>(na, jobs, total, k, dev, stream);
-    case 8: return launch_norm_gemv_t<L, 8, GELU>(na, jobs, total, k, dev, stream);
-    default: return hipErrorInvalidValue;
-  }
+  if (cpl == C) return norm_gemv_groups<L, C, GELU>(na, jobs, total, k, dev, stream);
+  if constexpr (C < CMAX)
+    return norm_gemv_cpl<L, GELU, C + 1, CMAX>(cpl, na, jobs, total, k, dev, stream);
+  return hipErrorInvalidValue;
 }
 
 }  // namespace
 
 hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                                 bool gelu, const DeviceInfo &dev, hipStream_t stream) {
+  if (total <= 0 || k <= 0 || k % 16 != 0 || k > 6144) return hipErrorInvalidValue;
   const int kc = k / 16;
   // 32 lanes per row (two rows per wave, as the gate/up pairing needs) up to
   // 256 chunks (k = 4096); 64 lanes beyond that for plain rows
   if (kc <= 32 * 8 || gelu) {
     const int cpl = (kc + 31) / 32;
-    return gelu ? norm_gemv_cpl<32, true>(cpl, na, jobs, total, k, dev, stream)
-                : norm_gemv_cpl<32, false>(cpl, na, jobs, total, k, dev, stream);
+    return gelu ? norm_gemv_cpl<32, true, 1, 8>(cpl, na, jobs, total, k, dev, stream)
+                : norm_gemv_cpl<32, false, 1, 8>(cpl, na, jobs, total, k, dev, stream);
   }
-  return norm_gemv_cpl<64, false>((kc + 63) / 64, na, jobs, total, k, dev, stream);
+  return norm_gemv_cpl<64, false, 5, 6>((kc + 63) / 64, na, jobs, total, k, dev, stream);
 }
 
 hipError_t launch_dec_embed(const DecEmbed &a, hipStream_t stream) {

@@ -40,15 +40,6 @@ __device__ __forceinline__ int job_of(const GemvJobs &jobs, int row,
   return j;
 }
 
-template <class T>
-__device__ __forceinline__ T pick(const T (&arr)[kMaxJobs], int j) {
-  T v = arr[0];
-#pragma unroll
-  for (int t = 1; t < kMaxJobs; ++t)
-    if (j == t) v = arr[t];
-  return v;
-}
-
 __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
   acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
   acc = __builtin_amdgcn_sdot4(w.y, x.y, acc, false);
@@ -88,7 +79,7 @@ __device__ __forceinline__ float x_quantize(int8_t *lds, int k, const v4f (&xr)[
                              fmaxf(abs_daz(xr[j].z), abs_daz(xr[j].w))));
   amax = wave_max_dpp(amax);
   if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
-  __syncthreads();
+  lds_barrier();
   amax = wave_amax[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, wave_amax[w]);
@@ -101,7 +92,7 @@ __device__ __forceinline__ float x_quantize(int8_t *lds, int k, const v4f (&xr)[
           pack4(quant_one(xr[j].x, qp.inv), quant_one(xr[j].y, qp.inv),
                 quant_one(xr[j].z, qp.inv), quant_one(xr[j].w, qp.inv));
   }
-  __syncthreads();
+  lds_barrier();
   if (blockIdx.x == 0) {
     if (xq_out != nullptr)
       for (int c = tid; c < k; c += NT) xq_out[c] = lds[c];
@@ -129,7 +120,7 @@ __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
     } else {
       for (int c = tid; c < k; c += NT) lds[c] = xq[c];
     }
-    __syncthreads();
+    lds_barrier();
     return *xs;
   }
   const bool vec = ((uintptr_t)xf & 15) == 0 && (k & 3) == 0;
@@ -152,7 +143,7 @@ __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
   }
   amax = wave_max_dpp(amax);
   if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
-  __syncthreads();
+  lds_barrier();
   amax = wave_amax[0];
 #pragma unroll
   for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, wave_amax[w]);
@@ -168,7 +159,7 @@ __device__ __forceinline__ float stage_x_i8(int8_t *lds, int k,
     for (int c = tid; c < k; c += NT)
       lds[c] = (int8_t)quant_one(xf[c], qp.inv);
   }
-  __syncthreads();
+  lds_barrier();
   if (blockIdx.x == 0) {
     if (xq_out != nullptr)
       for (int c = tid; c < k; c += NT) xq_out[c] = lds[c];
@@ -202,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
     int j = 0, r = 0;
     if (row < total) {
       j = job_of(jobs, row, &r);
-      const int8_t *w = static_cast<const int8_t *>(pick(jobs.w, j));
+      const int8_t *w = static_cast<const int8_t *>(pick4(jobs.w, j));
       if (VEC) {
         const int kc = k >> 4;
         const v4i *w4 = reinterpret_cast<const v4i *>(w) + (size_t)r * kc;
@@ -218,15 +209,21 @@ __global__ __launch_bounds__(kThreads) void gemv_i8_kernel(
 #pragma unroll
     for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     if (sub == 0 && row < total)
-      pick(jobs.dst, j)[r] = rescale(acc, act_scale, pick(jobs.sc, j)[r]);
+      pick4(jobs.dst, j)[r] = rescale(acc, act_scale, pick4(jobs.sc, j)[r]);
   }
 }
 
 // Latency-oriented variant (VEC layout only): each lane owns at most CPL
 // 16-byte chunks of its row, L = 64 / RPW lanes per row.  A lane issues the
-// loads of its first row before the activation is staged, so HBM latency
-// overlaps the quantize prologue, and the loads of its next row before it
+// loads of its first row (weights, then its scale) before the activation is
+// staged, so HBM latency overlaps the quantize prologue.  When the grid
+// covers every row in one pass (the launch shapes this kernel is chosen
+// for) that is all; otherwise each pass loads the next row before it
 // reduces the current one (register double buffering).
+// Weight loads are issued unconditionally (a row past the end reads the
+// wave's own first row, or the last row, and is not used): the compiler's
+// wait counts merge the paths of a conditional load by the path without it,
+// which would make the prologue wait for the weights issued before it.
 template <int L, int CPL, bool FUSED, int NT>
 __global__ __launch_bounds__(NT) void gemv_i8_pipelined_kernel(
     GemvJobs jobs, int total, int k, const int8_t *__restrict__ xq,
@@ -235,63 +232,71 @@ __global__ __launch_bounds__(NT) void gemv_i8_pipelined_kernel(
   extern __shared__ v4i lds_x4[];
   constexpr int kRowsPerWave = 64 / L;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = lane % L;
   const int rloc = lane / L;
   const int kc = k >> 4;
   constexpr int kBlockWaves = NT / 64;
   const int stride = gridDim.x * kBlockWaves * kRowsPerWave;
+  const int base0 = (blockIdx.x * kBlockWaves + wave) * kRowsPerWave;  // wave-uniform
+  const int own = base0 + rloc < total ? base0 + rloc : total - 1;
 
-  auto load_row = [&](int row, v4i (&buf)[CPL]) {
-    if (row < total) {
-      int r;
-      const int j = job_of(jobs, row, &r);
-      const v4i *w4 = static_cast<const v4i *>(pick(jobs.w, j)) + (size_t)r * kc;
+  struct Row {
+    v4i w[CPL];
+    float sc;
+  };
+  auto load_row = [&](int row, Row &buf) {
+    int r;
+    const int j = job_of(jobs, row < total ? row : own, &r);
+    const gptr<const v4i> w4 =
+        as_global(static_cast<const v4i *>(pick4(jobs.w, j))) + (size_t)r * kc;
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = sub + i * L;
-        buf[i] = c < kc ? __builtin_nontemporal_load(w4 + c) : v4i{0, 0, 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) buf[i] = v4i{0, 0, 0, 0};
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;
+      buf.w[i] = __builtin_nontemporal_load(w4 + (c < kc ? c : 0));
     }
+    buf.sc = as_global(pick4(jobs.sc, j))[r];
   };
 
-  int base = (blockIdx.x * kBlockWaves + wave) * kRowsPerWave;
-  v4i cur[CPL];
+  Row cur;
   float act_scale;
   if (FUSED && ((uintptr_t)xf & 15) == 0 && (k & 3) == 0 && k / 4 <= kXRegs * NT) {
     // activation loads first, then the first weight row, then the quantize
     v4f xr[kXRegs];
     x_load<NT>(k, xf, xr);
-    load_row(base + rloc, cur);
+    load_row(base0 + rloc, cur);
     act_scale = x_quantize<NT>(reinterpret_cast<int8_t *>(lds_x4), k, xr, xq_out, xs_out);
   } else {
-    load_row(base + rloc, cur);
+    load_row(base0 + rloc, cur);
     act_scale = stage_x_i8<FUSED, NT>(reinterpret_cast<int8_t *>(lds_x4), k, xq, xs, xf, xq_out,
                                       xs_out);
   }
 
-  for (; base < total; base += stride) {
+  auto process = [&](int base, const Row &w) {
     const int row = base + rloc;
-    v4i nxt[CPL];
-    load_row(row + stride, nxt);
     int32_t acc = 0;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = sub + i * L;
-      if (c < kc) acc = dot16(cur[i], lds_x4[c], acc);
+      if (c < kc) acc = dot16(w.w[i], lds_x4[c], acc);
     }
 #pragma unroll
     for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
     if (sub == 0 && row < total) {
       int r;
       const int j = job_of(jobs, row, &r);
-      pick(jobs.dst, j)[r] = rescale(acc, act_scale, pick(jobs.sc, j)[r]);
+      as_global(pick4(jobs.dst, j))[r] = rescale(acc, act_scale, w.sc);
     }
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) cur[i] = nxt[i];
+  };
+  if (total <= stride) {  // one pass: every row was loaded above
+    if (base0 < total) process(base0, cur);
+    return;
+  }
+  for (int base = base0; base < total; base += stride) {
+    Row nxt;
+    load_row(base + stride + rloc, nxt);
+    process(base, cur);
+    cur = nxt;
   }
 }
 
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(
   extern __shared__ v4f lds_f4[];
   float *lds_f = reinterpret_cast<float *>(lds_f4);
   for (int c = threadIdx.x; c < k; c += kThreads) lds_f[c] = x[c];
-  __syncthreads();
+  lds_barrier();
 
   constexpr int kRowsPerWave = 64 / L;
   const int lane = threadIdx.x & 63;
@@ -317,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(
     int j = 0, r = 0;
     if (row < total) {
       j = job_of(jobs, row, &r);
-      const float *w = static_cast<const float *>(pick(jobs.w, j));
+      const float *w = static_cast<const float *>(pick4(jobs.w, j));
       if (VEC) {
         const int kc = k >> 2;
         const v4f *w4 = reinterpret_cast<const v4f *>(w) + (size_t)r * kc;
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(
     }
 #pragma unroll
     for (int off = L / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (sub == 0 && row < total) pick(jobs.dst, j)[r] = acc;
+    if (sub == 0 && row < total) pick4(jobs.dst, j)[r] = acc;
   }
 }
 
@@ -498,6 +503,7 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
                           float *xs_out, const DeviceInfo &dev,
                           hipStream_t stream) {
   const int total = jobs.end[jobs.njobs - 1];
+  if (total <= 0 || k <= 0) return hipErrorInvalidValue;
   const bool vec = rows_aligned(jobs, k, 1, 16);
   const size_t lds = (size_t)(k + 15) / 16 * 16;
   const bool fused = xf != nullptr;

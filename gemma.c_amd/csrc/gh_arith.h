@@ -123,6 +123,49 @@ __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c,
          ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
+// Workgroup barrier for LDS traffic only: this wave's LDS operations are
+// complete (lgkmcnt(0)) before the barrier, and nothing moves across it.
+// __syncthreads() also waits for the wave's outstanding global loads
+// (vmcnt(0)), which would stall a kernel that has weight loads in flight
+// behind a reduction over LDS.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt not waited on
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Pins a wave-uniform value to scalar registers.  Choosing one of several
+// kernel-argument pointers by a per-lane index otherwise compiles to a
+// per-lane load from the argument segment, and its wait also drains every
+// global load issued before it.
+template <class T>
+__device__ __forceinline__ T in_sgpr(T v) {
+  asm("" : "+s"(v));
+  return v;
+}
+
+// a[j] of a four-entry kernel-argument array for a per-lane j, as a chain of
+// v_cndmask over copies of the entries pinned to scalar registers.  A select
+// over the argument array itself is folded into a per-lane load from the
+// argument segment, whose wait drains every global load issued before it.
+template <class T>
+__device__ __forceinline__ T pick4(T const (&a)[4], int j) {
+  T v0 = a[0], v1 = a[1], v2 = a[2], v3 = a[3];
+  asm("" : "+s"(v0), "+s"(v1), "+s"(v2), "+s"(v3));
+  return j == 3 ? v3 : j == 2 ? v2 : j == 1 ? v1 : v0;
+}
+
+// The global-memory view of a pointer.  After in_sgpr the compiler no longer
+// knows a pointer is global, and flat accesses through it count against both
+// vmcnt and lgkmcnt, so waits for them cannot be partial.
+template <class T>
+using gptr = T __attribute__((address_space(1))) *;
+template <class T>
+__device__ __forceinline__ gptr<T> as_global(T *p) {
+  return (gptr<T>)p;
+}
+
 // Wavefront (64 lanes) reductions.
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -12,7 +12,7 @@
 
 namespace gh {
 
-constexpr int kMaxJobs = 4;
+constexpr int kMaxJobs = 4;  // Pick4 (gh_arith.h) selects among exactly four
 
 // A fused multi-output GEMV: jobs[j] owns output rows [end[j-1], end[j]).
 struct GemvJobs {
@@ -111,7 +111,7 @@ struct DecAttn {
 
 // norm prologue + int8 GEMV over jobs (gelu: jobs.w[0]/w[1] are gate/up,
 // total = 2 * rows, output gelu(gate) * up to jobs.dst[0]); k % 16 == 0,
-// k <= 8192, rows 16-byte aligned
+// k <= 6144 (k <= 4096 for gelu), rows 16-byte aligned
 hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                                 bool gelu, const DeviceInfo &dev, hipStream_t stream);
 hipError_t launch_dec_embed(const DecEmbed &a, hipStream_t stream);

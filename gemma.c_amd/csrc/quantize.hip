@@ -40,7 +40,7 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_kernel(
   }
   amax = wave_max(amax);
   if ((tid & 63) == 0) wave_amax[tid >> 6] = amax;
-  __syncthreads();
+  lds_barrier();
   amax = fmaxf(fmaxf(wave_amax[0], wave_amax[1]),
                fmaxf(wave_amax[2], wave_amax[3]));
   const QuantParams qp = quant_params(amax);
