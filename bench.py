@@ -4,10 +4,11 @@
 Headline (BASELINE.json metric "int8 GEMV HBM GB/s + GEMM TOPS (% roofline);
 decode tok/s at gemma-3-1b shape", workload = BASELINE.json config 2):
 
-  step  = one pass over the gemma-3-1b decode GEMVs q, k, v, o, gate, up,
-          down and the tied LM head at M = 1, each with fp32 activations
-          quantized inside the GEMV kernel (gemma_hip_quantize_matmul), as
-          the reference's decode call sites do (gemma.c:4768-4966).
+  step  = one pass over the gemma-3-1b decode GEMVs at M = 1, grouped as the
+          reference's decode call sites issue them (gemma.c:4768-4966):
+          q/k/v as one gemv_int8_multi, o, gate/up as one gemv_int8_multi,
+          down and the tied LM head; each launch quantizes the fp32
+          activation inside the GEMV kernel (gemma_hip_quantize_matmul).
   value = algorithmic HBM bytes of a step x steps / elapsed, in GB/s.
 
 Weights are int8 uniform in [-127, 127], scales U(1e-3, 1e-2), x ~ N(0,1)
@@ -19,7 +20,7 @@ timed region measures the GPU, not Python's launch overhead.
 The JSON line also carries, measured in the same run:
   roofline      the dominant kernel (the LM-head GEMV launch): algorithmic
                 bytes / its average launch duration (HIP events on its stream)
-  per_gemv      the same for every sweep shape
+  per_gemv      the same for every launch of the sweep
   gemm          int8 MFMA GEMM TOPS at the gemma-3-4b prefill shapes (M=2048)
                 and the SigLIP tower shapes (M=4096), % of the 5.0 POPS peak
   decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
@@ -29,8 +30,8 @@ The JSON line also carries, measured in the same run:
                 KV cache, attention, o, GELU, down, LM head, argmax) at the
                 decode phase of BASELINE.json configs 3 (gemma-3-1b, context
                 512 -> 768) and 5 (gemma-3-4b, context 2048 -> 2560)
-  cpu_baseline  the reference's own quantize_act + gemv_int8, compiled from
-                its source (oracle/_ref/gemma_ref_clang), on the host cores
+  cpu_baseline  the reference's own quantize_act + gemv_int8(_multi), compiled
+                from its source (oracle/_ref/gemma_ref_clang), on the host cores
 """
 
 from __future__ import annotations
@@ -48,6 +49,8 @@ for _p in (REPO, PKG):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+# the kernel the LM-head launch runs (as rocprofv3 names it)
+LM_KERNEL = "gemv_i8_stream_kernel<8, 9, 1, true, 256>"
 INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 ROTATE_BYTES = 512 << 20   # > 2x the 256 MB Infinity Cache
@@ -56,10 +59,12 @@ ROT_STEPS = 8              # steps per captured graph
 METRIC = ("int8 GEMV HBM GB/s + GEMM TOPS (% roofline); decode tok/s at "
           "gemma-3-1b shape")
 
-# gemma-3-1b decode GEMVs: (name, out rows N, reduction K)
-SWEEP_1B = [("q", 1024, 1152), ("k", 256, 1152), ("v", 256, 1152), ("o", 1152, 1024),
-            ("gate", 6912, 1152), ("up", 6912, 1152), ("down", 1152, 6912),
-            ("lm_head", 262144, 1152)]
+# gemma-3-1b decode GEMV launches: (name, out rows of each job, reduction K) --
+# BASELINE.json config 2; q/k/v and gate/up share one quantized activation and
+# one launch, as gemv_int8_multi does at gemma.c:4768-4773 and 4911-4915
+SWEEP_1B = [("qkv", (1024, 256, 256), 1152), ("o", (1152,), 1024),
+            ("gate_up", (6912, 6912), 1152), ("down", (1152,), 6912),
+            ("lm_head", (262144,), 1152)]
 
 # gemma-3-4b prefill (M = 2048) and SigLIP (M = 4096) GEMMs: (name, M, N, K)
 GEMM_SHAPES = [("4b_q", 2048, 2048, 2560), ("4b_kv", 2048, 1024, 2560),
@@ -76,8 +81,9 @@ DEC_1B = dict(dim=1152, mlp=6912, layers=26, q=1024, kv=256, vocab=262144)
 
 
 def gemv_bytes(n: int, k: int) -> int:
-    """Algorithmic HBM bytes of one fused quantize+GEMV: int8 W [n][k], fp32
-    row scales [n], fp32 x [k], fp32 y [n]."""
+    """Algorithmic HBM bytes of one fused quantize+GEMV over n output rows (of
+    one or several jobs sharing x): int8 W [n][k], fp32 row scales [n], fp32
+    x [k], fp32 y [n]."""
     return n * k + 4 * n + 4 * k + 4 * n
 
 
@@ -145,14 +151,16 @@ def capture(torch, fn):
 
 def build_sweep(torch, gh, gen):
     shapes = []
-    for name, n, k in SWEEP_1B:
+    for name, ns, k in SWEEP_1B:
+        n = sum(ns)
         copies = rotate_copies(n * k)
-        ws = [rand_i8(torch, (n, k), gen) for _ in range(copies)]
-        ss = [rand_scales(torch, n, gen) for _ in range(copies)]
+        ws = [[rand_i8(torch, (r, k), gen) for r in ns] for _ in range(copies)]
+        ss = [[rand_scales(torch, r, gen) for r in ns] for _ in range(copies)]
         x = outlier_acts(torch, (k,), gen)
-        y = torch.empty(n, device="cuda", dtype=torch.float32)
-        jobs = [gh.jobs([(w, s, y, n)]) for w, s in zip(ws, ss)]
-        shapes.append(dict(name=name, n=n, k=k, copies=copies, w=ws, s=ss, x=x, y=y,
+        ys = [torch.empty(r, device="cuda", dtype=torch.float32) for r in ns]
+        jobs = [gh.jobs([(w, s, y, r) for w, s, y, r in zip(wc, sc, ys, ns)])
+                for wc, sc in zip(ws, ss)]
+        shapes.append(dict(name=name, n=list(ns), k=k, copies=copies, w=ws, s=ss, x=x, y=ys,
                            jobs=jobs, bytes=gemv_bytes(n, k)))
     return shapes
 
@@ -372,21 +380,25 @@ def cpu_baseline(threads: int, seconds_per_shape: float) -> dict | None:
         return None
     ref = RefHarness("clang")
     total_bytes, total_s, parts = 0, 0.0, {}
-    for name, n, k in SWEEP_1B:
+    for name, ns, k in SWEEP_1B:
+        n = sum(ns)
         copies = max(2, math.ceil(ROTATE_BYTES / (n * k)))
         est = gemv_bytes(n, k) / 30e9  # rough per-call time, sizes the sample
         calls = max(4, int(seconds_per_shape / est))
-        r = ref.bench(["gemv_int8", n, k, copies, calls], threads)
+        if len(ns) == 1:
+            r = ref.bench(["gemv_int8", n, k, copies, calls], threads)
+        else:
+            r = ref.bench(["gemv_int8_multi", k, copies, calls, len(ns), *ns], threads)
         per_call = r["seconds"] / r["calls"]
         parts[name] = round(gemv_bytes(n, k) / per_call / 1e9, 2)
         total_bytes += gemv_bytes(n, k)
         total_s += per_call
     return dict(value=round(total_bytes / total_s / 1e9, 2), unit="GB/s", cores=threads,
                 kind="reference",
-                sample=(f"reference quantize_act+gemv_int8 (gemma.c:2590, 2770) built by clang "
-                        f"-O3 -ffast-math -march=x86-64-v3 -fopenmp, {threads} OpenMP threads, "
-                        f"same 8 shapes, >=512 MB weight rotation, ~{seconds_per_shape:.1f} s "
-                        f"per shape"),
+                sample=(f"reference quantize_act + gemv_int8 / gemv_int8_multi (gemma.c:2590, "
+                        f"2770, 2808) built by clang -O3 -ffast-math -march=x86-64-v3 -fopenmp, "
+                        f"{threads} OpenMP threads, the same {len(SWEEP_1B)} launches, >=512 MB "
+                        f"weight rotation, ~{seconds_per_shape:.1f} s per launch shape"),
                 per_gemv_gbs=parts)
 
 
@@ -484,7 +496,7 @@ def main() -> int:
         print(f"# decoder: {json.dumps(decoder[name])}", file=sys.stderr, flush=True)
 
     lm_us = per["lm_head"]["us"]
-    traffic = measured_traffic("gemv_i8_kernel<8, true, true>")
+    traffic = measured_traffic(LM_KERNEL)
     achieved = lm["bytes"] / (lm_us * 1e-6) / 1e9
     cpu = None
     if not args.no_cpu_baseline:
@@ -506,15 +518,17 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE.json config 2: W8A8 GEMV sweep at gemma-3-1b shapes, M=1 "
-                        "(q 1152->1024, k/v 1152->256, o 1024->1152, gate/up 1152->6912, "
-                        "down 6912->1152, LM head 1152->262144), fp32 activations quantized "
-                        "in-kernel, weights rotated through >256 MB of copies",
+            "workload": "BASELINE.json config 2: W8A8 GEMV sweep at gemma-3-1b shapes, M=1, "
+                        "as the reference's decode call sites issue it (q/k/v 1152->1024+256+256 "
+                        "as one multi-job launch, o 1024->1152, gate/up 1152->2x6912 as one "
+                        "multi-job launch, down 6912->1152, LM head 1152->262144), fp32 "
+                        "activations quantized in-kernel, weights rotated through >256 MB of "
+                        "copies",
             "step_bytes": step_bytes,
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "gemv_i8_kernel<8,fused> (LM head launch, 262144x1152)",
+            "kernel": LM_KERNEL + " (LM head launch, 262144x1152)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

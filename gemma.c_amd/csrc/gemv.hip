@@ -300,6 +300,131 @@ __global__ __launch_bounds__(NT) void gemv_i8_pipelined_kernel(
   }
 }
 
+// Streaming variant for long row ranges (VEC layout only).  Rows are taken
+// in groups of R = 64 / L consecutive rows of one job, so the job, and with
+// it every base pointer, is wave-uniform; groups are dealt to the waves of
+// an all-resident grid round robin.  Each wave keeps D groups in flight in
+// registers: it loads group i + D, then reduces group i.  Loads are raw
+// buffer loads: a row past its job's end, a chunk past k and a group past
+// the last are given an offset beyond the buffer, which returns zeros
+// without touching memory, so every load is issued unconditionally and the
+// waits stay exact.  Requires every job's m * k < 2^31.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+// cache policy of the weight loads: nontemporal (each weight byte is read
+// once per launch)
+constexpr int kStreamPolicy = 2;
+
+template <int L, int CPL, int D, bool FUSED, int NT>
+__global__ __launch_bounds__(NT) void gemv_i8_stream_kernel(
+    GemvJobs jobs, int ngroups, int k, const int8_t *__restrict__ xq,
+    const float *__restrict__ xs, const float *__restrict__ xf,
+    int8_t *__restrict__ xq_out, float *__restrict__ xs_out) {
+  extern __shared__ v4i lds_x4[];
+  constexpr int R = 64 / L;
+  constexpr int kBlockWaves = NT / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane % L;
+  const int rloc = lane / L;
+  const int kc = k >> 4;
+  const int nwaves = gridDim.x * kBlockWaves;
+  const int w0 = blockIdx.x * kBlockWaves + wave;
+
+  // first group of each job (scalar)
+  int gend[kMaxJobs];
+  {
+    int prev = 0, g = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxJobs; ++t) {
+      if (t < jobs.njobs) g += (jobs.end[t] - prev + R - 1) / R;
+      gend[t] = g;
+      prev = jobs.end[t];
+    }
+  }
+  struct Where {
+    int job, row, m;  // row within the job (per lane), rows of the job
+  };
+  auto where = [&](int g) {
+    int j = 0, gs = 0, rs = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxJobs - 1; ++t)
+      if (t + 1 < jobs.njobs && g >= gend[t]) {
+        j = t + 1;
+        gs = gend[t];
+        rs = jobs.end[t];
+      }
+    return Where{j, (g - gs) * R + rloc, jobs.end[j] - rs};
+  };
+  auto pick_s = [&](auto const (&a)[kMaxJobs], int j) {  // j is wave-uniform
+    auto v = a[0];
+#pragma unroll
+    for (int t = 1; t < kMaxJobs; ++t)
+      if (j == t) v = a[t];
+    return v;
+  };
+
+  struct Slot {
+    v4i w[CPL];
+    int32_t sc;
+  };
+  auto load = [&](int g, Slot &s) {
+    const Where at = where(g);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(pick_s(jobs.w, at.job)), (short)0, at.m * k, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(pick_s(jobs.sc, at.job)), (short)0, at.m * 4, 0x00020000);
+    const bool ok = g < ngroups && at.row < at.m;
+    const uint32_t row_off = ok ? (uint32_t)at.row * (uint32_t)k : kOutOfRange;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;
+      s.w[i] = __builtin_amdgcn_raw_buffer_load_b128(
+          rw, c < kc ? row_off + (uint32_t)c * 16u : kOutOfRange, 0, kStreamPolicy);
+    }
+    s.sc = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? (uint32_t)at.row * 4u : kOutOfRange, 0,
+                                                0);
+  };
+
+  Slot ring[D];
+  float act_scale;
+  if (FUSED && ((uintptr_t)xf & 15) == 0 && (k & 3) == 0 && k / 4 <= kXRegs * NT) {
+    // activation loads first, then the first D groups, then the quantize
+    v4f xr[kXRegs];
+    x_load<NT>(k, xf, xr);
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(w0 + d * nwaves, ring[d]);
+    act_scale = x_quantize<NT>(reinterpret_cast<int8_t *>(lds_x4), k, xr, xq_out, xs_out);
+  } else {
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(w0 + d * nwaves, ring[d]);
+    act_scale = stage_x_i8<FUSED, NT>(reinterpret_cast<int8_t *>(lds_x4), k, xq, xs, xf, xq_out,
+                                      xs_out);
+  }
+
+  auto process = [&](int g, const Slot &s) {
+    int32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;  // chunks past k hold zeros
+      acc = dot16(s.w[i], lds_x4[c < kc ? c : 0], acc);
+    }
+    acc = group_sum_i32<L>(acc);
+    const Where at = where(g);
+    if (sub == 0 && g < ngroups && at.row < at.m)
+      pick_s(jobs.dst, at.job)[at.row] = rescale(acc, act_scale, __int_as_float(s.sc));
+  };
+  // groups of this wave: w0, w0 + nwaves, ...
+  const int mine = w0 < ngroups ? (ngroups - 1 - w0) / nwaves + 1 : 0;
+  for (int i = 0; i < mine; i += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int g = w0 + (i + d) * nwaves;
+      process(g, ring[d]);
+      load(g + D * nwaves, ring[d]);
+    }
+  }
+}
+
 template <int L, bool VEC>
 __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(
     GemvJobs jobs, int total, int k, const float *__restrict__ x) {
@@ -420,7 +545,8 @@ hipError_t gemv_f32_dispatch(int lanes, dim3 grid, size_t lds,
 // Launch-shape knobs, read once from the environment (the reference tunes
 // its CPU GEMM blocking the same way, GEMM_MC/NC/KC, gemma.c:458-493):
 //   GEMMA_HIP_GEMV_LANES         lanes per row of the pipelined GEMV (8..64)
-//   GEMMA_HIP_GEMV_BLOCKS_PER_CU workgroups per CU of the pipelined GEMV
+//   GEMMA_HIP_GEMV_BLOCKS_PER_CU workgroups per CU of the pipelined GEMV (a
+//                                cap below the occupancy for the streaming one)
 //   GEMMA_HIP_GEMV_LOOP=1        use the looping GEMV kernel instead
 //   GEMMA_HIP_GEMV_THREADS       256 or 1024 threads per pipelined workgroup
 struct Tuning {
@@ -491,6 +617,62 @@ PipeFn pipe_fn_nt(int lanes, int cpl, bool fused) {
   }
 }
 
+// The streaming kernel: L lanes per row, the smallest L with at most 10
+// chunks per lane, one group in flight per wave (measured at the 1b and 4b
+// LM heads and gate/up: a deeper register ring costs more in resident waves
+// than it gains).
+using StreamFn = hipError_t (*)(const DeviceInfo &, hipStream_t, const GemvJobs &, int, int,
+                                const int8_t *, const float *, const float *, int8_t *,
+                                float *);
+constexpr int kStreamNT = 256;
+constexpr int kStreamMaxCpl = 10;
+
+template <int L, int CPL, bool FUSED>
+hipError_t launch_stream(const DeviceInfo &dev, hipStream_t stream, const GemvJobs &jobs,
+                         int ngroups, int k, const int8_t *xq, const float *xs,
+                         const float *xf, int8_t *xq_out, float *xs_out) {
+  constexpr int D = 1;
+  auto kern = gemv_i8_stream_kernel<L, CPL, D, FUSED, kStreamNT>;
+  const size_t lds = (size_t)(k + 15) / 16 * 16;
+  // every workgroup resident at once: the groups are dealt round robin, so
+  // a second round of workgroups would run as a tail
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStreamNT, lds) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  if (tuning().blocks_per_cu > 0 && tuning().blocks_per_cu < per_cu)
+    per_cu = tuning().blocks_per_cu;
+  const long need = (ngroups + kStreamNT / 64 - 1) / (kStreamNT / 64);
+  const long cap = (long)dev.cus * per_cu;
+  kern<<<dim3((unsigned)(need < cap ? need : cap)), kStreamNT, lds, stream>>>(
+      jobs, ngroups, k, xq, xs, xf, xq_out, xs_out);
+  return hipGetLastError();
+}
+
+template <int L, bool FUSED, int C>
+StreamFn stream_for(int cpl) {
+  if (cpl == C) return &launch_stream<L, C, FUSED>;
+  if constexpr (C < kStreamMaxCpl) return stream_for<L, FUSED, C + 1>(cpl);
+  return nullptr;
+}
+
+// chunks per lane: up to 10 at L = 8; above 80 chunks a wider L has 6..10
+StreamFn stream_fn(int kc, bool fused, int *lanes) {
+  for (int l = 8; l <= 64; l *= 2) {
+    const int cpl = (kc + l - 1) / l;
+    if (cpl > kStreamMaxCpl) continue;
+    *lanes = l;
+    switch (l) {
+      case 8: return fused ? stream_for<8, true, 1>(cpl) : stream_for<8, false, 1>(cpl);
+      case 16: return fused ? stream_for<16, true, 6>(cpl) : stream_for<16, false, 6>(cpl);
+      case 32: return fused ? stream_for<32, true, 6>(cpl) : stream_for<32, false, 6>(cpl);
+      default: return fused ? stream_for<64, true, 6>(cpl) : stream_for<64, false, 6>(cpl);
+    }
+  }
+  return nullptr;
+}
+
 PipeFn pipe_fn(int lanes, int cpl, bool fused, int threads) {
   return threads == 1024 ? pipe_fn_nt<1024>(lanes, cpl, fused)
                          : pipe_fn_nt<256>(lanes, cpl, fused);
@@ -532,6 +714,20 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
       fn(dim3((unsigned)(blocks < cap ? blocks : cap)), lds, stream, jobs, total, k, xq, xs,
          xf, xq_out, xs_out);
       return hipGetLastError();
+    }
+  }
+  if (vec && !tuning().force_loop) {
+    bool fits = true;  // buffer offsets are 32-bit
+    for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
+      fits = fits && (long)(jobs.end[j] - prev) * k < (long)kOutOfRange;
+    int lanes = 0;
+    StreamFn fn = fits ? stream_fn(k / 16, fused, &lanes) : nullptr;
+    if (fn != nullptr) {
+      const int rows = 64 / lanes;
+      int ngroups = 0;
+      for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
+        ngroups += (jobs.end[j] - prev + rows - 1) / rows;
+      return fn(dev, stream, jobs, ngroups, k, xq, xs, xf, xq_out, xs_out);
     }
   }
   const int lanes = vec ? lanes_for(k / 16) : 64;

@@ -209,6 +209,21 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// Sum over each aligned group of L lanes (L = 8, 16, 32 or 64), the same
+// value in every lane of the group.  Integer sums are exact, so the order
+// of the additions does not matter.
+template <int L>
+__device__ __forceinline__ int32_t group_sum_i32(int32_t v) {
+  static_assert(L == 8 || L == 16 || L == 32 || L == 64, "L is 8, 16, 32 or 64");
+  v += __builtin_amdgcn_update_dpp(0, v, kDppXor1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppXor2, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, kDppHalfMirror, 0xF, 0xF, false);
+  if (L >= 16) v += __builtin_amdgcn_update_dpp(0, v, kDppMirror, 0xF, 0xF, false);
+  if (L >= 32) v += __shfl_xor(v, 16, 64);
+  if (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Max over the 64 lanes of a wave, the same value in every lane.
 __device__ __forceinline__ float wave_max_dpp(float v) {
   v = fmaxf(v, dpp_f32<kDppXor1>(v));

@@ -264,6 +264,9 @@ static void fill_float(float *ptr, size_t count, float low, float high) {
  * bench gemv_int8 <nout> <kin> <copies> <min_calls>
  *   W8A8 GEMV (quantize_act + gemv_int8, as at the decode call sites
  *   gemma.c:4858-4859) over `copies` distinct weight matrices in rotation.
+ * bench gemv_int8_multi <kin> <copies> <min_calls> <njobs> <nout_0> ...
+ *   quantize_act + gemv_int8_multi over njobs matrices, as at the decode q/k/v
+ *   and gate/up call sites (gemma.c:4768-4773, 4911-4915).
  * bench gemm_int8 <rows> <nout> <kin> <min_calls>
  *   quantize_acts + gemm_int8 (prefill call sites gemma.c:5365-5370).
  * Prints {"op":..., "calls":..., "seconds":..., "threads":...}.
@@ -302,6 +305,49 @@ static int run_bench(int argc, char **argv) {
     printf("{\"op\": \"gemv_int8\", \"nout\": %d, \"kin\": %d, \"calls\": %d, "
            "\"seconds\": %.6f, \"threads\": %d, \"checksum\": %.6e}\n",
            nout, kin, calls, seconds, threads, (double)dst[nout / 2]);
+    return 0;
+  }
+  if (strcmp(what, "gemv_int8_multi") == 0) {
+    int kin = param_at(argc, argv, 3), copies = param_at(argc, argv, 4);
+    int min_calls = param_at(argc, argv, 5), njobs = param_at(argc, argv, 6);
+    if (njobs < 1 || njobs > 8 || copies < 1) {
+      fprintf(stderr, "gemma_ref: njobs or copies out of range\n");
+      return 2;
+    }
+    int nouts[8], total = 0;
+    for (int job = 0; job < njobs; job++) {
+      nouts[job] = param_at(argc, argv, 7 + job);
+      total += nouts[job];
+    }
+    int8_t *weights = alloc_or_die((size_t)copies * total * kin);
+    float *scales = alloc_or_die((size_t)copies * total * 4);
+    float *activ = alloc_or_die((size_t)kin * 4);
+    int8_t *qact = alloc_or_die((size_t)kin);
+    float *dst = alloc_or_die((size_t)total * 4);
+    fill_int8(weights, (size_t)copies * total * kin);
+    fill_float(scales, (size_t)copies * total, 1e-3f, 1e-2f);
+    fill_float(activ, (size_t)kin, -3.0f, 3.0f);
+    GemvJob jobs[8];
+    double start = 0.0;
+    int calls = 0;
+    for (int iter = -2; iter < min_calls; iter++) {  /* two warm-up calls */
+      if (iter == 0) start = now_sec();
+      int copy = (iter + 2) % copies, row = 0;
+      for (int job = 0; job < njobs; job++) {
+        jobs[job].w = weights + ((size_t)copy * total + row) * kin;
+        jobs[job].sc = scales + (size_t)copy * total + row;
+        jobs[job].dst = dst + row;
+        jobs[job].m = nouts[job];
+        row += nouts[job];
+      }
+      float vsc = quantize_act(qact, activ, kin, NULL);
+      gemv_int8_multi(jobs, njobs, qact, vsc, kin, threads, NULL);
+      if (iter >= 0) calls++;
+    }
+    double seconds = now_sec() - start;
+    printf("{\"op\": \"gemv_int8_multi\", \"kin\": %d, \"njobs\": %d, \"calls\": %d, "
+           "\"seconds\": %.6f, \"threads\": %d, \"checksum\": %.6e}\n",
+           kin, njobs, calls, seconds, threads, (double)dst[total / 2]);
     return 0;
   }
   if (strcmp(what, "gemm_int8") == 0) {

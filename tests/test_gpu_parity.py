@@ -172,6 +172,34 @@ def test_fused_multi_vs_oracle(gh, oracle, rows, k):
         assert np.array_equal(bits(host(o)), bits(r))
 
 
+# Above 2048 rows (and below 4096-byte rows) the GEMV streams row groups of one
+# job per wave with bounds-checked loads; ragged jobs, an empty job and a group
+# that ends inside a job exercise the edges of that decomposition.
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("rows,k", [((3001, 5, 0, 2999), 1152), ((4099, 1), 2560),
+                                    ((5000,), 6912), ((2049,), 16)])
+def test_stream_ragged_jobs_vs_oracle(gh, oracle, rows, k, fused):
+    note(f"stream ragged rows={rows} k={k} fused={fused}")
+    rng = np.random.default_rng(sum(rows) * 7 + k)
+    x = outlier_acts(rng, (k,))
+    qo, so = oracle.quantize_act(x)
+    specs, outs, refs = [], [], []
+    for r in rows:
+        W = rng.integers(-127, 128, (max(r, 1), k), dtype=np.int8)
+        ws = rng.uniform(1e-3, 1e-2, max(r, 1)).astype(np.float32)
+        outs.append(torch.full((max(r, 1),), 7.0, dtype=torch.float32, device="cuda"))
+        specs.append((dev(W), dev(ws), outs[-1], r))
+        refs.append(oracle.gemv_int8(W[:r], ws[:r], qo, so)[0])
+    if fused:
+        gh.quantize_matmul(specs, dev(x), k, None, None, stream())
+    else:
+        gh.matmul_multi(specs, dev(qo), dev(np.array([so], np.float32)), k, stream())
+    for o, r, ref in zip(outs, rows, refs):
+        got = host(o)
+        assert np.array_equal(bits(got[:r]), bits(ref))
+        assert np.all(got[r:] == 7.0)  # nothing written past a job's rows
+
+
 def test_gemv_unaligned_rows(gh, oracle):
     """k % 16 != 0 and an odd base address take the generic path."""
     rng = np.random.default_rng(5)
