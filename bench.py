@@ -21,6 +21,8 @@ The JSON line also carries, measured in the same run:
   roofline      the dominant kernel (the LM-head GEMV launch): algorithmic
                 bytes / its average launch duration (HIP events on its stream)
   per_gemv      the same for every launch of the sweep
+  per_gemv_4b   the same at the gemma-3-4b decode shapes (config 5), and
+                their sum ("all": bytes of the five launches / summed time)
   gemm          int8 MFMA GEMM TOPS at the gemma-3-4b prefill shapes (M=2048)
                 and the SigLIP tower shapes (M=4096), % of the 5.0 POPS peak
   decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
@@ -65,6 +67,12 @@ METRIC = ("int8 GEMV HBM GB/s + GEMM TOPS (% roofline); decode tok/s at "
 SWEEP_1B = [("qkv", (1024, 256, 256), 1152), ("o", (1152,), 1024),
             ("gate_up", (6912, 6912), 1152), ("down", (1152,), 6912),
             ("lm_head", (262144,), 1152)]
+
+# gemma-3-4b decode GEMV launches (BASELINE.json config 5's decode phase), the
+# shapes the decode-GEMV target is stated at; reported beside the headline
+SWEEP_4B = [("qkv", (2048, 1024, 1024), 2560), ("o", (2560,), 2048),
+            ("gate_up", (10240, 10240), 2560), ("down", (2560,), 10240),
+            ("lm_head", (262144,), 2560)]
 
 # gemma-3-4b prefill (M = 2048) and SigLIP (M = 4096) GEMMs: (name, M, N, K)
 GEMM_SHAPES = [("4b_q", 2048, 2048, 2560), ("4b_kv", 2048, 1024, 2560),
@@ -149,9 +157,9 @@ def capture(torch, fn):
     return graph
 
 
-def build_sweep(torch, gh, gen):
+def build_sweep(torch, gh, gen, sweep=SWEEP_1B):
     shapes = []
-    for name, ns, k in SWEEP_1B:
+    for name, ns, k in sweep:
         n = sum(ns)
         copies = rotate_copies(n * k)
         ws = [[rand_i8(torch, (r, k), gen) for r in ns] for _ in range(copies)]
@@ -486,6 +494,17 @@ def main() -> int:
 
     per = per_gemv(torch, gh, shapes, timer, busy, reps=64)
     print(f"# per-gemv: {json.dumps(per)}", file=sys.stderr, flush=True)
+    del graph, shapes
+    torch.cuda.empty_cache()
+    shapes_4b = build_sweep(torch, gh, gen, SWEEP_4B)
+    per_4b = per_gemv(torch, gh, shapes_4b, timer, busy, reps=16)
+    per_4b["all"] = dict(
+        us=round(sum(v["us"] for v in per_4b.values()), 3),
+        gbs=round(sum(sh["bytes"] for sh in shapes_4b)
+                  / (sum(v["us"] for v in per_4b.values()) * 1e-6) / 1e9, 1))
+    print(f"# per-gemv 4b: {json.dumps(per_4b)}", file=sys.stderr, flush=True)
+    del shapes_4b
+    torch.cuda.empty_cache()
     gemm = bench_gemm(torch, gh, gen, timer, reps=10)
     print(f"# gemm: {json.dumps(gemm)}", file=sys.stderr, flush=True)
     dec = bench_decode_1b(torch, gh, gen, timer, tokens=50)
@@ -543,6 +562,7 @@ def main() -> int:
                                if traffic else None),
         },
         "per_gemv": per,
+        "per_gemv_4b": per_4b,
         "gemm": gemm,
         "decode_1b": dec,
         "decoder": decoder,
