@@ -27,11 +27,14 @@ The JSON line also carries, measured in the same run:
                 and the SigLIP tower shapes (M=4096), % of the 5.0 POPS peak
   decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
                 decode token (26 layers x {qkv, o, gate/up, down} + LM head)
-  decoder       tokens/s of the whole device-resident greedy decode step
-                (gemma_hip_decoder_generate: embedding, norms, q/k/v, RoPE,
-                KV cache, attention, o, GELU, down, LM head, argmax) at the
-                decode phase of BASELINE.json configs 3 (gemma-3-1b, context
-                512 -> 768) and 5 (gemma-3-4b, context 2048 -> 2560)
+  decoder       configs 3 (gemma-3-1b: 512 prompt tokens, then 256 decode
+                steps) and 5 (gemma-3-4b: 2048, then 512) fully on the GPU:
+                the batched prefill (gemma_hip_decoder_prefill: the int8
+                projections as GEMMs, causal attention, norms, GELU) in
+                tokens/s and int8 TOPS of its GEMMs, then tokens/s of the
+                device-resident greedy decode step (gemma_hip_decoder_generate:
+                embedding, norms, q/k/v, RoPE, KV cache, attention, o, GELU,
+                down, LM head, argmax)
   cpu_baseline  the reference's own quantize_act + gemv_int8(_multi), compiled
                 from its source (oracle/_ref/gemma_ref_clang), on the host cores
 """
@@ -326,28 +329,43 @@ DECODER_RUNS = (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512))
 
 
 def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
-    """Greedy decode fully on the GPU: the KV cache is filled by `prompt`
-    untimed decode steps, then `steps` steps are timed (one HIP graph launch
-    each, tokens fed back on the device, one readback at the end)."""
+    """The prompt and the greedy decode fully on the GPU: `prompt` random token
+    ids go through the batched prefill (gemma_hip_decoder_prefill; timed once
+    after a warm-up call that allocates its row buffers), then `steps` decode
+    steps from the KV cache it filled are timed (one HIP graph launch each,
+    tokens fed back on the device, one readback at the end)."""
     import time
+
+    import numpy as np
 
     import model_bin
 
     model = model_bin.synth_model(name, seed=1234)
     c = model["config"]
+    ids = np.random.default_rng(1234).integers(0, c["nvocab"], prompt).astype(np.int32)
     dec = gh.decoder(model, prompt + steps + 1)
     try:
-        dec.generate(2, 0, prompt)
+        dec.prefill(ids, 0)
         torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        first = dec.prefill(ids, 0)
+        t_pf = time.perf_counter() - t0
         best = None
         for _ in range(2):
             t0 = time.perf_counter()
-            toks = dec.generate(7, prompt, steps)
+            toks = dec.generate(first, prompt, steps)
             dt = time.perf_counter() - t0
             best = dt if best is None else min(best, dt)
     finally:
         dec.close()
     q_sz, kv_sz = c["n_heads"] * c["hdim"], c["nkv"] * c["hdim"]
+    pf_ops = c["nl"] * (gemm_ops(prompt, q_sz + 2 * kv_sz, c["dim"])
+                        + gemm_ops(prompt, c["dim"], q_sz)
+                        + gemm_ops(prompt, 2 * c["mlp_dim"], c["dim"])
+                        + gemm_ops(prompt, c["dim"], c["mlp_dim"]))
+    prefill = dict(tokens=prompt, ms=round(1e3 * t_pf, 3), tok_s=round(prompt / t_pf, 1),
+                   int8_tops=round(pf_ops / t_pf / 1e12, 1),
+                   int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4))
     per_layer = (gemv_bytes(q_sz + 2 * kv_sz, c["dim"]) + gemv_bytes(c["dim"], q_sz)
                  + gemv_bytes(2 * c["mlp_dim"], c["dim"]) + gemv_bytes(c["dim"], c["mlp_dim"]))
     weights = c["nl"] * per_layer + gemv_bytes(c["nvocab"], c["dim"])
@@ -359,7 +377,8 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     per_token = weights + kv / steps
     tok_s = steps / best
     gbs = per_token * tok_s / 1e9
-    return dict(model=name, context=f"{prompt}->{prompt + steps}", tok_s=round(tok_s, 1),
+    return dict(model=name, context=f"{prompt}->{prompt + steps}", prefill=prefill,
+                tok_s=round(tok_s, 1),
                 ms_per_token=round(1e3 * best / steps, 4), bytes_per_token=int(per_token),
                 gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
                 hbm_bound_tok_s=round(HBM_PEAK_GBS * 1e9 / per_token, 1),

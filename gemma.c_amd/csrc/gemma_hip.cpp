@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -827,6 +828,13 @@ struct gemma_hip_decoder {
   int *pin = nullptr;  // pinned: step upload [4] and token readback [1]
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // row buffers of the batched prefill, allocated on first use for pf_rows rows
+  char *pf_mem = nullptr;
+  int pf_rows = 0;
+  float *pf_x = nullptr, *pf_y = nullptr, *pf_qkv = nullptr, *pf_xo = nullptr, *pf_g = nullptr;
+  float *pf_as = nullptr;
+  int8_t *pf_a8 = nullptr;
+  int *pf_tok = nullptr;
 };
 
 namespace {
@@ -836,8 +844,119 @@ void decoder_free(gemma_hip_decoder *d) {
   if (d->exec != nullptr) (void)hipGraphExecDestroy(d->exec);
   if (d->graph != nullptr) (void)hipGraphDestroy(d->graph);
   if (d->mem != nullptr) (void)hipFree(d->mem);
+  if (d->pf_mem != nullptr) (void)hipFree(d->pf_mem);
   if (d->pin != nullptr) (void)hipHostFree(d->pin);
   delete d;
+}
+
+// Row buffers of the batched prefill for n rows (kept, and regrown only for
+// a larger n): x, y [n][dim]; q/k/v [n][q_sz + 2 kv_sz]; attention output
+// [n][q_sz]; gate|up [n][2 mlp]; quantized rows [n][max K] + their scales.
+int prefill_reserve(gemma_hip_decoder *d, int n) {
+  if (n <= d->pf_rows) return 0;
+  const gemma_hip_text_config &c = d->cfg;
+  const size_t rows = (size_t)n, q_sz = (size_t)c.n_heads * c.hdim,
+               kv_sz = (size_t)c.nkv * c.hdim, dim = c.dim, mlp = c.mlp_dim;
+  const size_t kmax = std::max(dim, std::max(q_sz, mlp));
+  Carver cv;
+  const size_t o_x = cv.take(rows * dim * 4), o_y = cv.take(rows * dim * 4),
+               o_qkv = cv.take(rows * (q_sz + 2 * kv_sz) * 4), o_xo = cv.take(rows * q_sz * 4),
+               o_g = cv.take(rows * 2 * mlp * 4), o_a8 = cv.take(rows * kmax),
+               o_as = cv.take(rows * 4), o_tok = cv.take(rows * 4);
+  if (d->pf_mem != nullptr) {
+    (void)hipStreamSynchronize(g.stream);
+    (void)hipFree(d->pf_mem);
+    d->pf_mem = nullptr;
+    d->pf_rows = 0;
+  }
+  hipError_t e = hipMalloc((void **)&d->pf_mem, cv.used);
+  if (e != hipSuccess) return hip_fail("gemma_hip_decoder_prefill: alloc", e);
+  char *m = d->pf_mem;
+  d->pf_x = (float *)(m + o_x);
+  d->pf_y = (float *)(m + o_y);
+  d->pf_qkv = (float *)(m + o_qkv);
+  d->pf_xo = (float *)(m + o_xo);
+  d->pf_g = (float *)(m + o_g);
+  d->pf_a8 = (int8_t *)(m + o_a8);
+  d->pf_as = (float *)(m + o_as);
+  d->pf_tok = (int *)(m + o_tok);
+  d->pf_rows = n;
+  return 0;
+}
+
+// Enqueues the prompt pass of rows pos .. pos+n-1 (forward_text_chunk,
+// gemma.c:4985-5453) and the decode step's tail on the last row.  The step
+// record must hold {last token, pos + n - 1, 0} (the argmax advances it).
+hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st) {
+  const gemma_hip_text_config &c = d->cfg;
+  const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim, dim = c.dim, mlp = c.mlp_dim;
+  const int stride = q_sz + 2 * kv_sz;
+  const size_t cache = (size_t)d->clen * kv_sz;
+  hipError_t e;
+  auto gemm = [&](float *dst, int dstr, const int8_t *w, const float *ws, int nout, int k) {
+    return gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, d->pf_a8, k, d->pf_as, n, nout, k, g.info,
+                              st);
+  };
+  if ((e = gh::launch_pf_embed(d->pf_tok, n, d->emb, d->emb_s, d->pf_x, dim,
+                               c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
+    return e;
+  for (int l = 0; l < c.nl; ++l) {
+    const auto &L = d->layers[l];
+    // residual of the previous MLP (post-FFN norm), pre-attention norm, quantize
+    const gh::PfNorm n1{d->pf_x, l > 0 ? d->pf_y : nullptr,
+                        (l > 0 && c.mlp_pst) ? d->layers[l - 1].n4 : nullptr, L.n1, d->pf_a8,
+                        d->pf_as, dim, c.eps};
+    if ((e = gh::launch_pf_norm_rows(n1, n, st)) != hipSuccess) return e;
+    // q, k, v rows (gemma.c:5045-5089)
+    if ((e = gemm(d->pf_qkv, stride, L.w[0], L.s[0], q_sz, dim)) != hipSuccess ||
+        (e = gemm(d->pf_qkv + q_sz, stride, L.w[1], L.s[1], kv_sz, dim)) != hipSuccess ||
+        (e = gemm(d->pf_qkv + q_sz + kv_sz, stride, L.w[2], L.s[2], kv_sz, dim)) != hipSuccess)
+      return e;
+    // q/k norm, RoPE, KV append, attention
+    const bool sliding = d->swa[l] != 0;
+    float *kc = d->kv + (size_t)l * 2 * cache;
+    const gh::PfRope rp{d->pf_qkv, stride, q_sz, c.qk_norm ? L.nq : nullptr,
+                        c.qk_norm ? L.nk : nullptr, sliding ? d->rope_l : d->rope_g, kc,
+                        kc + cache, d->clen, pos, c.n_heads, c.nkv, c.eps};
+    if ((e = gh::launch_pf_qk_rope(rp, n, c.hdim, st)) != hipSuccess) return e;
+    const gh::PfAttn at{d->pf_qkv, stride, kc, kc + cache, d->pf_xo, q_sz, n, pos, c.n_heads,
+                        c.nkv, d->clen, sliding ? c.slide : 0,
+                        (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att};
+    if ((e = gh::launch_pf_attention(at, c.hdim, st)) != hipSuccess) return e;
+    // o projection
+    if ((e = gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st)) !=
+            hipSuccess ||
+        (e = gemm(d->pf_y, dim, L.w[3], L.s[3], dim, q_sz)) != hipSuccess)
+      return e;
+    // residual of the attention (post-attention norm), pre-FFN norm, quantize
+    const gh::PfNorm n3{d->pf_x, d->pf_y, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
+                        d->pf_a8, d->pf_as, dim, c.eps};
+    if ((e = gh::launch_pf_norm_rows(n3, n, st)) != hipSuccess) return e;
+    // gate (w2), up (w1) (gemma.c:5365-5373), GELU(gate) * up, quantize, down
+    if ((e = gemm(d->pf_g, 2 * mlp, L.w[5], L.s[5], mlp, dim)) != hipSuccess ||
+        (e = gemm(d->pf_g + mlp, 2 * mlp, L.w[4], L.s[4], mlp, dim)) != hipSuccess ||
+        (e = gh::launch_pf_gelu_quant(d->pf_g, n, mlp, d->pf_a8, d->pf_as, st)) != hipSuccess ||
+        (e = gemm(d->pf_y, dim, L.w[6], L.s[6], dim, mlp)) != hipSuccess)
+      return e;
+  }
+  // the last row: last residual, final norm, LM head, softcap, argmax
+  const size_t last = (size_t)(n - 1) * dim;
+  gh::DecNorm fn{d->pf_x + last, d->pf_y + last,
+                 c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm, nullptr, d->h, dim,
+                 c.eps};
+  if ((e = gh::launch_dec_final_norm(fn, st)) != hipSuccess) return e;
+  gh::GemvJobs lm{};
+  lm.w[0] = d->emb; lm.sc[0] = d->emb_s; lm.dst[0] = d->logits;
+  for (int j = 0; j < gh::kMaxJobs; ++j) lm.end[j] = c.nvocab;
+  lm.njobs = 1;
+  if ((e = gh::launch_gemv_i8(lm, dim, nullptr, nullptr, d->h, nullptr, nullptr, g.info, st)) !=
+      hipSuccess)
+    return e;
+  if (c.sc_log != 0.0f &&
+      (e = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st)) != hipSuccess)
+    return e;
+  return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
+                               d->tokens, d->clen, st);
 }
 
 // Enqueues one decode step on `st` (captured into the decoder's graph).
@@ -1168,6 +1287,48 @@ int gemma_hip_decoder_generate(gemma_hip_decoder *dec, int token, int pos, int n
   for (int i = 0; i < n; ++i)
     if (tokens[i] < 0 || tokens[i] >= dec->cfg.nvocab)
       return fail("gemma_hip_decoder_generate: step %d produced no token (NaN logits?)", i);
+  return 0;
+}
+
+int gemma_hip_decoder_prefill(gemma_hip_decoder *dec, const int *tokens, int n, int pos,
+                              float *logits, int *next) {
+  if (need_init()) return 1;
+  if (dec == nullptr || tokens == nullptr)
+    return fail("gemma_hip_decoder_prefill: null argument");
+  const gemma_hip_text_config &c = dec->cfg;
+  if (n < 1 || pos < 0 || pos > dec->clen - n)
+    return fail("gemma_hip_decoder_prefill: %d tokens at pos %d out of range (clen %d)", n, pos,
+                dec->clen);
+  for (int i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= c.nvocab)
+      return fail("gemma_hip_decoder_prefill: token %d at %d out of range (vocab %d)", tokens[i],
+                  i, c.nvocab);
+  const int hn = c.n_heads / c.nkv;
+  if ((c.hdim != 128 && c.hdim != 256) || 32 % hn != 0 ||
+      c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt)
+    return fail("gemma_hip_decoder_prefill: unsupported shape (head dim %d must be 128 or 256, "
+                "%d q heads per kv head must divide 32, mlp %d at most %d)",
+                c.hdim, hn, c.mlp_dim, 4 * 1024 * gh::kPfMaxNpt);
+  GH_CHECK("gemma_hip_decoder_prefill: sync", hipStreamSynchronize(g.stream));
+  if (prefill_reserve(dec, n)) return 1;
+  GH_CHECK("gemma_hip_decoder_prefill: tokens H2D",
+           hipMemcpyAsync(dec->pf_tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, g.stream));
+  dec->pin[0] = tokens[n - 1];
+  dec->pin[1] = pos + n - 1;
+  dec->pin[2] = 0;
+  dec->pin[3] = 0;
+  GH_CHECK("gemma_hip_decoder_prefill: step H2D",
+           hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
+  GH_CHECK("gemma_hip_decoder_prefill: launch", prefill_enqueue(dec, n, pos, g.stream));
+  if (logits != nullptr)
+    GH_CHECK("gemma_hip_decoder_prefill: logits D2H",
+             hipMemcpyAsync(logits, dec->logits, (size_t)c.nvocab * 4, hipMemcpyDeviceToHost,
+                            g.stream));
+  if (next != nullptr)
+    GH_CHECK("gemma_hip_decoder_prefill: D2H",
+             hipMemcpyAsync(dec->pin + 4, dec->tokens, 4, hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemma_hip_decoder_prefill: sync", hipStreamSynchronize(g.stream));
+  if (next != nullptr) *next = dec->pin[4];
   return 0;
 }
 

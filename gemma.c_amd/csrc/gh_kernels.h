@@ -122,4 +122,48 @@ hipError_t launch_dec_softcap(float *logits, int n, float cap, hipStream_t strea
 hipError_t launch_dec_argmax(const float *logits, int n, float *pval, int *pidx, int nparts,
                              int *step, int *tokens, int max_tokens, hipStream_t stream);
 
+// prefill.hip: the batched prompt pass (forward_text_chunk).
+// Rows of x [n][dim] (in place), y [n][dim] nullable: the per-row form of
+// DecNorm; h of every row is quantized into xq [n][dim] + xs [n].
+struct PfNorm {
+  float *x;
+  const float *y;
+  const float *w_post;
+  const float *w_pre;
+  int8_t *xq;
+  float *xs;
+  int dim;
+  float eps;
+};
+// qkv [n][stride]: q heads at column h*hdim, k heads from q_sz, v heads from
+// q_sz + kv_sz; rows sit at positions pos0 .. pos0+n-1; kc/vc [nkv][clen][hdim]
+struct PfRope {
+  float *qkv;
+  int stride, q_sz;
+  const float *nq, *nk, *rope;
+  float *kc, *vc;
+  int clen, pos0, n_heads, nkv;
+  float eps;
+};
+// attention of the n rows of qkv (q part) over kc/vc; xo [n][q_sz]
+struct PfAttn {
+  const float *qkv;
+  int stride;
+  const float *kc, *vc;
+  float *xo;
+  int q_sz, n, pos0, n_heads, nkv, clen, slide;
+  float asc, sc_att;
+};
+// float4 chunks per thread of the row kernels: dim <= 6144 (256 threads),
+// mlp <= 24576 (1024 threads)
+constexpr int kPfMaxNpt = 6;
+hipError_t launch_pf_embed(const int *tokens, int n, const int8_t *emb_q, const float *emb_s,
+                           float *x, int dim, float esc, hipStream_t stream);
+hipError_t launch_pf_norm_rows(const PfNorm &a, int n, hipStream_t stream);
+hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t stream);
+// hdim 128 or 256; the q heads per kv head must divide 32
+hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream);
+hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
+                                hipStream_t stream);
+
 }  // namespace gh

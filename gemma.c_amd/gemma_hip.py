@@ -85,6 +85,7 @@ _SIGS = {
     "gemma_hip_decoder_destroy": (None, [_P]),
     "gemma_hip_decoder_step": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_generate": (_I, [_P, _I, _I, _I, _P]),
+    "gemma_hip_decoder_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_logits": (_P, [_P]),
 }
 
@@ -258,6 +259,18 @@ class Decoder:
         nxt = ctypes.c_int(-1)
         self.gh._check(self.lib.gemma_hip_decoder_step(self.handle, token, pos, _addr(logits),
                                                        ctypes.byref(nxt)))
+        return nxt.value
+
+    def prefill(self, tokens, pos: int, logits=None) -> int:
+        """The prompt pass (forward_gemma_prefill, gemma.c:5501) over `tokens` at
+        positions pos .. pos+len-1; returns the argmax after the last one."""
+        import numpy as np
+
+        toks = np.ascontiguousarray(tokens, np.int32)
+        nxt = ctypes.c_int(-1)
+        self.gh._check(self.lib.gemma_hip_decoder_prefill(self.handle, toks.ctypes.data,
+                                                          int(toks.size), pos, _addr(logits),
+                                                          ctypes.byref(nxt)))
         return nxt.value
 
     def generate(self, token: int, pos: int, n: int):

@@ -246,6 +246,17 @@ void gemma_hip_decoder_destroy(gemma_hip_decoder *dec);
 int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos,
                            float *logits, int *next);
 
+/* The prompt pass: n tokens (host array) at positions pos .. pos+n-1 go
+ * through every layer as one batch, as forward_gemma_prefill (gemma.c:5501)
+ * with forward_text_chunk (4985-5453) does -- the int8 projections as GEMMs,
+ * causal (sliding-window) attention over the KV cache -- filling the KV
+ * cache, so step/generate continue at pos + n.  logits and next (nullable)
+ * receive the last token's logits and argmax.  n >= 1, pos + n <= clen; head
+ * dim 128 or 256, q heads per kv head dividing 32, mlp_dim <= 24576.  Its
+ * row buffers are allocated on the first call (regrown for a larger n). */
+int gemma_hip_decoder_prefill(gemma_hip_decoder *dec, const int *tokens, int n, int pos,
+                              float *logits, int *next);
+
 /* n greedy steps without host round trips: step i consumes the token step
  * i-1 produced (the first consumes `token` at `pos`); tokens[i] receives the
  * argmax of step i (host, n ints).  pos + n <= clen. */

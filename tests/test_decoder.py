@@ -121,6 +121,92 @@ def test_decoder_matches_oracle(gh, oracle, models, case, steps, clen):
         dec.close()
 
 
+def _check_logits(got, want, what):
+    scale = float(np.abs(want).max())
+    diff = float(np.abs(got - want).max())
+    assert diff <= LOGIT_TOL * scale, f"{what}: |d| {diff:.3g} vs {scale:.3g}"
+    return diff / scale
+
+
+@pytest.fixture(scope="module")
+def gqa_model(tmp_path_factory):
+    """gemma-3-4b widths (8 q heads over 4 kv heads: two q heads per kv head),
+    two layers, sliding window 8 on the first."""
+    d = tmp_path_factory.mktemp("gqa")
+    return model_bin.read_bin(model_bin.write_bin(str(d / "gqa.bin"), "gemma-3-4b", seed=5,
+                                                  nvocab=1024, layers=2, slide=8, flags=7,
+                                                  norm_std=0.1))
+
+
+def _prefill_vs_oracle(gh, oracle, model, n, more, clen, chunks=None):
+    """The batched prompt pass (in `chunks`, default one) against the oracle fed
+    the same tokens one at a time: the last prompt token's logits, then `more`
+    decode steps on the KV cache the prefill filled."""
+    nv = model["config"]["nvocab"]
+    prompt = np.random.default_rng(n * 31 + clen).integers(0, nv, n).astype(np.int32)
+    dec = gh.decoder(model, clen)
+    try:
+        ref = dorc.DecodeOracle(model, oracle, clen)
+        for pos, t in enumerate(prompt):
+            want = ref.step(int(t), pos)
+        logits = np.empty(nv, np.float32)
+        cuts = [0] + list(chunks or []) + [n]
+        for a, b in zip(cuts[:-1], cuts[1:]):
+            nxt = dec.prefill(prompt[a:b], a, logits)
+        worst = _check_logits(logits, want, f"prefill of {n}")
+        assert nxt == int(np.argmax(want)) == int(np.argmax(logits))
+        token = nxt
+        for pos in range(n, n + more):
+            nxt = dec.step(token, pos, logits)
+            want = ref.step(token, pos)
+            worst = max(worst, _check_logits(logits, want, f"step at {pos} after prefill"))
+            assert nxt == int(np.argmax(want))
+            token = nxt
+        return worst
+    finally:
+        dec.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case,n,more,clen", [("gemma3", 40, 8, 64), ("softcap", 20, 4, 32),
+                                              ("plain", 20, 4, 32)])
+def test_prefill_matches_oracle(gh, oracle, models, case, n, more, clen):
+    worst = _prefill_vs_oracle(gh, oracle, models[case], n, more, clen)
+    print(f"prefill {case}: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
+@pytest.mark.gpu
+def test_prefill_gqa_matches_oracle(gh, oracle, gqa_model):
+    """Two q heads per kv head (16 rows per attention workgroup) and 4 kv heads."""
+    worst = _prefill_vs_oracle(gh, oracle, gqa_model, 37, 3, 48)
+    print(f"prefill gqa: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
+@pytest.mark.gpu
+def test_prefill_in_chunks(gh, oracle, models):
+    """Chunks continue one another through the KV cache (forward_gemma_prefill
+    feeds long prompts chunk by chunk): a 1-token chunk, a chunk that ends
+    inside an attention tile, and one that starts past the sliding window."""
+    _prefill_vs_oracle(gh, oracle, models["gemma3"], 45, 2, 64, chunks=[1, 13, 30])
+
+
+@pytest.mark.gpu
+def test_prefill_argument_errors(gh, models):
+    from gemma_hip import GemmaHipError
+
+    model = models["plain"]
+    dec = gh.decoder(model, 16)
+    try:
+        with pytest.raises(GemmaHipError, match="out of range"):
+            dec.prefill(np.zeros(0, np.int32), 0)
+        with pytest.raises(GemmaHipError, match="out of range"):
+            dec.prefill(np.zeros(5, np.int32), 12)
+        with pytest.raises(GemmaHipError, match="out of range"):
+            dec.prefill(np.array([1, model["config"]["nvocab"]], np.int32), 0)
+    finally:
+        dec.close()
+
+
 @pytest.mark.gpu
 def test_decoder_generate_equals_steps(gh, models):
     model = models["gemma3"]
