@@ -121,24 +121,35 @@ __global__ __launch_bounds__(64) void pf_qk_rope_kernel(PfRope a) {
 // running max and sum and the value sums are fp64 (an online softmax: on a
 // new max the partial sums are rescaled by exp(m_old - m_new)); each output
 // element is rounded to fp32 once at the end.
+//
+// Scores: thread (c, qg, kg) = (tid & 3, (tid >> 2) & 7, tid >> 5) sums
+// quarter c of the head dimension for queries 4qg..4qg+3 and keys 2kg,
+// 2kg+1 (8 products per 6 LDS vector reads), then the four quarters are
+// added across lanes.  LDS rows are padded so that the 32 (qg, c) and 8
+// (kg, c) addresses of one read fall in distinct 16-byte bank groups as far
+// as 64 banks allow.
 constexpr int kPfQ = 32;     // query vectors per workgroup
 constexpr int kPfKeys = 16;  // keys per tile
 
 template <int HD>
 __global__ __launch_bounds__(kNT) void pf_attn_kernel(PfAttn a) {
-  constexpr int KS = HD + 4;           // padded K rows: the score reads hit distinct banks
+  constexpr int QQ = HD / 4 + 4;       // one padded quarter of a row
+  constexpr int KS = 4 * QQ;           // K row
+  constexpr int QS = 4 * QQ + 4;       // q row
+  constexpr int PS = kPfQ + 2;         // probabilities row (one key)
   constexpr int QPT = kPfQ * HD / kNT; // query vectors per thread in the value sums
-  __shared__ float qs[kPfQ][HD];
-  __shared__ float kt[kPfKeys][KS];
+  __shared__ __attribute__((aligned(16))) float qs[kPfQ * QS];
+  __shared__ __attribute__((aligned(16))) float kt[kPfKeys * KS];
   __shared__ float vt[kPfKeys][HD];
-  __shared__ double p[kPfQ][kPfKeys];
+  __shared__ __attribute__((aligned(16))) double pp[kPfKeys * PS];
   __shared__ double alpha[kPfQ], run_m[kPfQ], run_l[kPfQ];
 
   const int tid = threadIdx.x;
   const int hn = a.n_heads / a.nkv;
   const int qb = kPfQ / hn;                 // rows per workgroup
   const int hk = blockIdx.y;
-  const int r0 = blockIdx.x * qb;
+  // the longest rows (most keys) first
+  const int r0 = (gridDim.x - 1 - blockIdx.x) * qb;
   const int rows = min(qb, a.n - r0);
   // query vector v: head h0 + v / qb, row r0 + v % qb
   auto q_row = [&](int v) { return r0 + v % qb; };
@@ -147,9 +158,14 @@ __global__ __launch_bounds__(kNT) void pf_attn_kernel(PfAttn a) {
     return (a.slide > 0 && p_abs >= a.slide) ? p_abs + 1 - a.slide : 0;
   };
 
-  for (int i = tid; i < kPfQ * HD; i += kNT) {
-    const int v = i / HD, d = i - v * HD;
-    qs[v][d] = v % qb < rows ? a.qkv[(size_t)q_row(v) * a.stride + q_head(v) * HD + d] : 0.0f;
+  for (int i = tid; i < kPfQ * HD / 4; i += kNT) {
+    const int v = i / (HD / 4), c4 = i - v * (HD / 4);  // 4 floats at d = 4 c4
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    const v4f x = v % qb < rows ? reinterpret_cast<const v4f *>(
+                                      a.qkv + (size_t)q_row(v) * a.stride + q_head(v) * HD)[c4]
+                                : zero;
+    const int d = 4 * c4;
+    *reinterpret_cast<v4f *>(&qs[v * QS + (d / (HD / 4)) * QQ + d % (HD / 4)]) = x;
   }
   if (tid < kPfQ) {
     run_m[tid] = -DBL_MAX;
@@ -165,6 +181,7 @@ __global__ __launch_bounds__(kNT) void pf_attn_kernel(PfAttn a) {
   for (int u = 0; u < QPT; ++u) acc[u] = 0.0;
   const int d_own = tid % HD;           // this thread's dimension in the value sums
   const int v_own = (tid / HD) * QPT;   // and its first query vector
+  const int sc_c = tid & 3, sc_qg = (tid >> 2) & 7, sc_kg = tid >> 5;
 
   for (int t0 = k_lo; t0 <= p_last; t0 += kPfKeys) {
     lds_barrier();  // the previous tile's K, V and p are no longer read
@@ -176,54 +193,68 @@ __global__ __launch_bounds__(kNT) void pf_attn_kernel(PfAttn a) {
                                    : zero;
       const v4f vv4 = kp <= p_last ? reinterpret_cast<const v4f *>(vc + (size_t)kp * HD)[c4]
                                    : zero;
-      *reinterpret_cast<v4f *>(&kt[t][4 * c4]) = kv4;
-      *reinterpret_cast<v4f *>(&vt[t][4 * c4]) = vv4;
+      const int d = 4 * c4;
+      *reinterpret_cast<v4f *>(&kt[t * KS + (d / (HD / 4)) * QQ + d % (HD / 4)]) = kv4;
+      *reinterpret_cast<v4f *>(&vt[t][d]) = vv4;
     }
     lds_barrier();
-    // scores: four threads per (query, key) pair, each summing every fourth
-    // element, then a quad reduction
-    for (int p0 = 0; p0 < kPfQ * kPfKeys; p0 += kNT / 4) {
-      const int pr = p0 + (tid >> 2), c = tid & 3;
-      const int v = pr / kPfKeys, t = pr - v * kPfKeys;
-      const float *qv = &qs[v][c];
-      const float *kr = &kt[t][c];
-      double a0 = 0.0, a1 = 0.0;
-#pragma unroll 8
-      for (int i = 0; i < HD / 4; i += 2) {
-        a0 += (double)qv[4 * i] * (double)kr[4 * i];
-        a1 += (double)qv[4 * i + 4] * (double)kr[4 * i + 4];
+    {
+      const float *qb4 = &qs[(4 * sc_qg) * QS + sc_c * QQ];
+      const float *kb2 = &kt[(2 * sc_kg) * KS + sc_c * QQ];
+      double s[4][2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[j][0] = s[j][1] = 0.0;
+#pragma unroll 4
+      for (int i = 0; i < HD / 4; i += 4) {
+        const v4f k0 = *reinterpret_cast<const v4f *>(kb2 + i);
+        const v4f k1 = *reinterpret_cast<const v4f *>(kb2 + KS + i);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4f q = *reinterpret_cast<const v4f *>(qb4 + j * QS + i);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[j][0] = fma((double)q[e], (double)k0[e], s[j][0]);
+            s[j][1] = fma((double)q[e], (double)k1[e], s[j][1]);
+          }
+        }
       }
-      double part = a0 + a1;
-      part += dpp_f64<kDppXor1>(part);
-      part += dpp_f64<kDppXor2>(part);
-      if (c == 0) {
-        const int p_abs = a.pos0 + q_row(v);
-        const int kp = t0 + t;
-        const bool live = v % qb < rows && kp <= p_abs && kp >= window_start(p_abs);
-        double sc = part * (double)a.asc;
-        if (a.sc_att != 0.0f) sc = tanh(sc / (double)a.sc_att) * (double)a.sc_att;
-        p[v][t] = live ? sc : -DBL_MAX;
-      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          double part = s[j][kk];
+          part += dpp_f64<kDppXor1>(part);
+          part += dpp_f64<kDppXor2>(part);
+          const int v = 4 * sc_qg + j, t = 2 * sc_kg + kk;
+          if (sc_c == 0) {
+            const int p_abs = a.pos0 + q_row(v);
+            const int kp = t0 + t;
+            const bool live = v % qb < rows && kp <= p_abs && kp >= window_start(p_abs);
+            double sc = part * (double)a.asc;
+            if (a.sc_att != 0.0f) sc = tanh(sc / (double)a.sc_att) * (double)a.sc_att;
+            pp[t * PS + v] = live ? sc : -DBL_MAX;
+          }
+        }
     }
     lds_barrier();
     // online softmax: 16 lanes (one DPP row) per query vector, lane t = key t
     for (int v = tid / kPfKeys; v < kPfQ; v += kNT / kPfKeys) {
       const int t = tid % kPfKeys;
-      const double s = p[v][t];
-      double m = s;
+      const double sv = pp[t * PS + v];
+      double m = sv;
       m = fmax(m, dpp_f64<kDppXor1>(m));
       m = fmax(m, dpp_f64<kDppXor2>(m));
       m = fmax(m, dpp_f64<kDppHalfMirror>(m));
       m = fmax(m, dpp_f64<kDppMirror>(m));
       const double m_old = run_m[v];
       const double m_new = fmax(m_old, m);
-      const double e = s == -DBL_MAX ? 0.0 : exp(s - m_new);
+      const double e = sv == -DBL_MAX ? 0.0 : exp(sv - m_new);
       double l = e;
       l += dpp_f64<kDppXor1>(l);
       l += dpp_f64<kDppXor2>(l);
       l += dpp_f64<kDppHalfMirror>(l);
       l += dpp_f64<kDppMirror>(l);
-      p[v][t] = e;
+      pp[t * PS + v] = e;
       if (t == 0) {
         const double al = exp(m_old - m_new);
         alpha[v] = al;
@@ -232,17 +263,20 @@ __global__ __launch_bounds__(kNT) void pf_attn_kernel(PfAttn a) {
       }
     }
     lds_barrier();
-    // value sums: thread (d, queries v_own .. v_own + QPT - 1)
+    // value sums: thread (d, queries v_own .. v_own + QPT - 1); the key's
+    // probabilities of two queries are one 16-byte broadcast read
 #pragma unroll
-    for (int u = 0; u < QPT; ++u) {
-      const int v = v_own + u;
-      double s0 = 0.0, s1 = 0.0;
+    for (int u = 0; u < QPT; ++u) acc[u] *= alpha[v_own + u];
+#pragma unroll 4
+    for (int t = 0; t < kPfKeys; ++t) {
+      const double vv = (double)vt[t][d_own];
+      const double *pt = &pp[t * PS + v_own];
 #pragma unroll
-      for (int t = 0; t < kPfKeys; t += 2) {
-        s0 += p[v][t] * (double)vt[t][d_own];
-        s1 += p[v][t + 1] * (double)vt[t + 1][d_own];
+      for (int u = 0; u < QPT; u += 2) {
+        const double2 pr = *reinterpret_cast<const double2 *>(pt + u);
+        acc[u] = fma(pr.x, vv, acc[u]);
+        acc[u + 1] = fma(pr.y, vv, acc[u + 1]);
       }
-      acc[u] = acc[u] * alpha[v] + (s0 + s1);
     }
   }
 #pragma unroll
