@@ -256,3 +256,54 @@ def test_device_decoder_follows_reference_program(gh, tmp_path):
     # test_decode_oracle_follows_reference_program's, and the decoder equals
     # the oracle bit for bit (tests/test_decoder.py)
     assert_close_to_reference(rel, agree, "device decoder vs reference (270m)", flip_free=0)
+
+
+def run_reference_prefill(model_path, prompt_len, steps, tmp_path):
+    """The reference program's own path: <bos> and the prompt through
+    forward_gemma_prefill (GEMMs, blockwise causal attention in fp32), then
+    `steps` greedy decode steps; logits after the prompt and after each step."""
+    import numpy as np
+
+    dump = str(tmp_path / "ref_prefill_logits.bin")
+    env = dict(os.environ, GEMMA_E2E_LOGITS=dump)
+    env.pop("GEMMA_E2E_DECODE_ONLY", None)
+    cmd = [E2E_CPU, model_path, str(prompt_len), str(steps), "1234", str(THREADS)]
+    out = subprocess.run(cmd, env=env, capture_output=True, text=True, timeout=600)
+    assert out.returncode == 0, out.stderr[-2000:]
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    nvocab = model_bin.read_bin(model_path)["config"]["nvocab"]
+    logits = np.fromfile(dump, np.float32).reshape(-1, nvocab)
+    assert logits.shape[0] == 1 + steps
+    return res, logits
+
+
+@pytest.mark.gpu
+@needs_e2e
+@pytest.mark.timeout(600)
+def test_device_prefill_follows_reference_program(gh, tmp_path):
+    """BASELINE.json config 1 (gemma-3-270m, 32 prompt ids): the device's
+    batched prefill (gemma_hip_decoder_prefill) against the reference's own
+    chunked prefill, then 16 decode steps teacher-forced on the reference's
+    tokens.  The reference evaluates the prefill attention in fp32 in its own
+    blockwise order, the device in fp64 (the decode oracle's arithmetic), so
+    the flip-level bounds of the decoder comparison apply."""
+    import numpy as np
+
+    path = model_bin.write_bin(str(tmp_path / "m270.bin"), "gemma-3-270m", seed=1234)
+    res, ref = run_reference_prefill(path, 32, 16, tmp_path)
+    model = model_bin.read_bin(path)
+    prompt, toks = res["prompt"], res["tokens"]
+    dec = gh.decoder(model, len(prompt) + len(toks) + 2)
+    try:
+        lg = np.empty(model["config"]["nvocab"], np.float32)
+        dec.prefill(np.array([res["bos"]], np.int32), 0)
+        dec.prefill(np.array(prompt, np.int32), 1, lg)
+        got = [lg.copy()]
+        for i in range(16):
+            dec.step(toks[i], 1 + len(prompt) + i, lg)
+            got.append(lg.copy())
+    finally:
+        dec.close()
+    rel, agree = compare_to_reference(got, ref)
+    assert_close_to_reference(rel, agree, "device prefill vs reference prefill (270m)",
+                              flip_free=0)
