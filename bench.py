@@ -35,6 +35,8 @@ The JSON line also carries, measured in the same run:
                 device-resident greedy decode step (gemma_hip_decoder_generate:
                 embedding, norms, q/k/v, RoPE, KV cache, attention, o, GELU,
                 down, LM head, argmax)
+  vision        config 4 end to end: one 896x896 image through the SigLIP
+                tower on the GPU (gemma_hip_vision_forward), ms per image
   cpu_baseline  the reference's own quantize_act + gemv_int8(_multi), compiled
                 from its source (oracle/_ref/gemma_ref_clang), on the host cores
 """
@@ -385,6 +387,39 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
                 distinct_tokens=int(len(set(toks.tolist()))))
 
 
+def bench_vision(torch, gh) -> dict:
+    """BASELINE.json config 4 end to end on the GPU: one 896x896 image through
+    the whole SigLIP tower (gemma_hip_vision_forward: patch and position
+    embedding, 27 encoder layers, post norm, pooling to 256 tokens, RMSNorm,
+    projection to the gemma-3-4b width), random weights of that shape; the
+    best of two timed images after one untimed."""
+    import time
+
+    import model_bin
+
+    vis = model_bin.synth_vision(seed=1234, text_dim=2560)
+    img = model_bin.synth_image(vis["config"]["img_px"], seed=1234)
+    c = vis["config"]
+    tower = gh.vision(vis)
+    try:
+        tower.forward(img)
+        best = None
+        for _ in range(2):
+            t0 = time.perf_counter()
+            tower.forward(img)
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+    finally:
+        tower.close()
+    n = (c["img_px"] // c["psize"]) ** 2
+    ops = c["nl"] * (4 * gemm_ops(n, c["dim"], c["dim"]) + gemm_ops(n, c["mlp_dim"], c["dim"])
+                     + gemm_ops(n, c["dim"], c["mlp_dim"])) \
+        + gemm_ops(c["img_tok"], c["text_dim"], c["dim"])
+    return dict(model="siglip (27 layers, 896 px, 4096 patches -> 256 tokens)",
+                ms_per_image=round(1e3 * best, 2), images_s=round(1 / best, 2),
+                int8_ops=ops, int8_tops_over_tower=round(ops / best / 1e12, 1))
+
+
 def measured_traffic(kernel: str) -> dict | None:
     """HBM bytes per launch of the LM-head GEMV from the committed rocprofv3
     --pmc measurement (FETCH_SIZE and WRITE_SIZE, each scaled by what the
@@ -437,9 +472,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=2.0,
                     help="CPU-baseline sample time per sweep shape")
-    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder"], default=None,
-                    help="profiling aid: run just the timed sweep, the LM-head timing or "
-                         "the device-resident decoder")
+    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder", "vision"], default=None,
+                    help="profiling aid: run just the timed sweep, the LM-head timing, "
+                         "the device-resident decoder or the vision tower")
     ap.add_argument("--decoder-models", default="gemma-3-1b,gemma-3-4b",
                     help="models of the decoder timing (comma list of gemma-3-1b, gemma-3-4b)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -471,6 +506,10 @@ def main() -> int:
     if args.only == "decoder":
         for name, prompt, nsteps in decoder_runs:
             print(json.dumps(bench_decoder(torch, gh, name, prompt, nsteps)), flush=True)
+        gh.close()
+        return 0
+    if args.only == "vision":
+        print(json.dumps(bench_vision(torch, gh)), flush=True)
         gh.close()
         return 0
     gen = torch.Generator(device="cuda")
@@ -533,6 +572,9 @@ def main() -> int:
         decoder[name] = bench_decoder(torch, gh, name, prompt, nsteps)
         print(f"# decoder: {json.dumps(decoder[name])}", file=sys.stderr, flush=True)
 
+    vision = bench_vision(torch, gh)
+    print(f"# vision: {json.dumps(vision)}", file=sys.stderr, flush=True)
+
     lm_us = per["lm_head"]["us"]
     traffic = measured_traffic(LM_KERNEL)
     achieved = lm["bytes"] / (lm_us * 1e-6) / 1e9
@@ -585,6 +627,7 @@ def main() -> int:
         "gemm": gemm,
         "decode_1b": dec,
         "decoder": decoder,
+        "vision": vision,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

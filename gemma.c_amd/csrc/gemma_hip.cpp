@@ -1337,3 +1337,253 @@ const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec) {
 }
 
 }  // extern "C"
+
+// ---- vision tower ----------------------------------------------------------
+
+struct gemma_hip_vision {
+  gemma_hip_vision_config cfg{};
+  int npatch = 0, ppi = 0, ksize = 0, hdim = 0;
+  struct Layer {
+    const int8_t *w[6];  // wq wk wv wo w1 w2, device
+    const float *s[6];
+    float *bqkv, *bo, *b1, *b2, *n1, *n1b, *n2, *n2b;  // device copies
+  };
+  std::vector<Layer> layers;
+  const int8_t *pos_q = nullptr, *proj = nullptr;
+  const float *pos_s = nullptr, *proj_s = nullptr;
+  float *pe = nullptr, *pe_b = nullptr, *post_n = nullptr, *post_nb = nullptr, *norm = nullptr;
+  char *mem = nullptr;  // parameters and activations
+  float *img = nullptr, *patches = nullptr, *x = nullptr, *y = nullptr, *qkv = nullptr;
+  float *att = nullptr, *hbuf = nullptr, *hln = nullptr, *out = nullptr, *as = nullptr;
+  int8_t *a8 = nullptr;
+};
+
+namespace {
+
+void vision_free(gemma_hip_vision *v) {
+  if (v == nullptr) return;
+  if (v->mem != nullptr) (void)hipFree(v->mem);
+  delete v;
+}
+
+// forward_vision (gemma.c:4394-4725) on `st`; the image is already in v->img
+hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
+  const gemma_hip_vision_config &c = v->cfg;
+  const int n = v->npatch, dim = c.dim, mlp = c.mlp_dim;
+  hipError_t e;
+  auto gemm = [&](float *dst, int dstr, const int8_t *w, const float *ws, int m, int nout,
+                  int k) {
+    return gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, v->a8, k, v->as, m, nout, k, g.info, st);
+  };
+  // patch embedding + position embedding (4411-4468)
+  if ((e = gh::launch_im2col(v->patches, v->img, c.img_px, c.psize, st)) != hipSuccess)
+    return e;
+  const gh::VisPatch pa{v->patches, v->pe, v->pe_b, v->pos_q, v->pos_s, v->x, n,
+                        3 * c.psize * c.psize, dim};
+  if ((e = gh::launch_vis_patch(pa, st)) != hipSuccess) return e;
+  for (int l = 0; l < c.nl; ++l) {
+    const auto &L = v->layers[l];
+    // residual of the previous layer's MLP (fc2 bias), first layer norm (4474-4484)
+    const gh::VisLn n1{v->x, l > 0 ? v->y : nullptr, l > 0 ? v->layers[l - 1].b2 : nullptr,
+                       L.n1, L.n1b, v->a8, v->as, nullptr, dim, c.eps};
+    if ((e = gh::launch_vis_ln_rows(n1, n, st)) != hipSuccess) return e;
+    // q, k, v (4487-4511); their biases are added inside the attention
+    if ((e = gemm(v->qkv, 3 * dim, L.w[0], L.s[0], n, dim, dim)) != hipSuccess ||
+        (e = gemm(v->qkv + dim, 3 * dim, L.w[1], L.s[1], n, dim, dim)) != hipSuccess ||
+        (e = gemm(v->qkv + 2 * dim, 3 * dim, L.w[2], L.s[2], n, dim, dim)) != hipSuccess)
+      return e;
+    const gh::VisAttn at{v->qkv, 3 * dim, L.bqkv, v->att, n, c.n_heads, dim,
+                         1.0f / sqrtf((float)v->hdim)};
+    if ((e = gh::launch_vis_attention(at, v->hdim, st)) != hipSuccess) return e;
+    // o (4563-4573), then its bias, the residual and the second layer norm
+    if ((e = gh::launch_quantize(v->a8, v->as, v->att, dim, n, dim, st)) != hipSuccess ||
+        (e = gemm(v->y, dim, L.w[3], L.s[3], n, dim, dim)) != hipSuccess)
+      return e;
+    const gh::VisLn n2{v->x, v->y, L.bo, L.n2, L.n2b, v->a8, v->as, nullptr, dim, c.eps};
+    if ((e = gh::launch_vis_ln_rows(n2, n, st)) != hipSuccess) return e;
+    // fc1, bias + GELU, fc2 (4604-4644)
+    if ((e = gemm(v->hbuf, mlp, L.w[4], L.s[4], n, mlp, dim)) != hipSuccess ||
+        (e = gh::launch_vis_gelu_quant(v->hbuf, L.b1, n, mlp, v->a8, v->as, st)) !=
+            hipSuccess ||
+        (e = gemm(v->y, dim, L.w[5], L.s[5], n, dim, mlp)) != hipSuccess)
+      return e;
+  }
+  // last residual, post layer norm (4660-4668), pooling + RMSNorm (4673-4704),
+  // projection (4708-4721)
+  const gh::VisLn pn{v->x, v->y, v->layers[c.nl - 1].b2, v->post_n, v->post_nb, nullptr,
+                     nullptr, v->hln, dim, c.eps};
+  if ((e = gh::launch_vis_ln_rows(pn, n, st)) != hipSuccess) return e;
+  const gh::VisPool po{v->hln, v->norm, v->a8, v->as, dim, v->ppi, v->ksize, c.eps};
+  if ((e = gh::launch_vis_pool(po, c.img_tok, st)) != hipSuccess) return e;
+  return gemm(v->out, c.text_dim, v->proj, v->proj_s, c.img_tok, c.text_dim, dim);
+}
+
+}  // namespace
+
+extern "C" {
+
+gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
+                                          const gemma_hip_vision_layer *layers,
+                                          const float *pe, const float *pe_b,
+                                          const int8_t *pos_q, const float *pos_s,
+                                          const float *post_n, const float *post_nb,
+                                          const float *norm, const int8_t *proj,
+                                          const float *proj_s) {
+  if (need_init()) return nullptr;
+  if (cfg == nullptr || layers == nullptr || pe == nullptr || pe_b == nullptr ||
+      pos_q == nullptr || pos_s == nullptr || post_n == nullptr || post_nb == nullptr ||
+      norm == nullptr || proj == nullptr || proj_s == nullptr) {
+    fail("gemma_hip_vision_create: null argument");
+    return nullptr;
+  }
+  const gemma_hip_vision_config c = *cfg;
+  const int hdim = c.n_heads > 0 ? c.dim / c.n_heads : 0;
+  const int ppi = c.psize > 0 ? c.img_px / c.psize : 0;
+  int side = 0;
+  while (side * side < c.img_tok) ++side;
+  if (c.nl <= 0 || c.n_heads <= 0 || c.dim <= 0 || c.dim % 16 != 0 || c.dim > 6144 ||
+      c.dim % c.n_heads != 0 ||
+      (hdim != 16 && hdim != 32 && hdim != 64 && hdim != 72 && hdim != 128) ||
+      c.mlp_dim <= 0 || c.mlp_dim % 16 != 0 || c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt ||
+      c.psize <= 0 || c.img_px <= 0 || c.img_px % c.psize != 0 || c.img_tok <= 0 ||
+      side * side != c.img_tok || ppi % side != 0 || c.text_dim <= 0 || c.text_dim % 16 != 0) {
+    fail("gemma_hip_vision_create: unsupported config (nl=%d heads=%d dim=%d mlp=%d img=%d "
+         "patch=%d img_tok=%d text_dim=%d)", c.nl, c.n_heads, c.dim, c.mlp_dim, c.img_px,
+         c.psize, c.img_tok, c.text_dim);
+    return nullptr;
+  }
+  gemma_hip_vision *v = new gemma_hip_vision();
+  v->cfg = c;
+  v->hdim = hdim;
+  v->ppi = ppi;
+  v->npatch = ppi * ppi;
+  v->ksize = ppi / side;
+  const size_t dim = c.dim, mlp = c.mlp_dim, n = v->npatch, kpe = 3 * (size_t)c.psize * c.psize;
+  auto weight = [&](const void *host, size_t bytes, const char *what, const void **out) {
+    const char *p = resolve(host, bytes);
+    if (p == nullptr) return fail("gemma_hip_vision_create: %s is not registered", what);
+    if ((uintptr_t)p % 16 != 0)
+      return fail("gemma_hip_vision_create: %s is not 16-byte aligned on the device", what);
+    *out = p;
+    return 0;
+  };
+  const void *ptr = nullptr;
+  v->layers.resize(c.nl);
+  for (int l = 0; l < c.nl; ++l) {
+    const gemma_hip_vision_layer &src = layers[l];
+    const int8_t *ws[6] = {src.wq, src.wk, src.wv, src.wo, src.w1, src.w2};
+    const float *ss[6] = {src.wq_s, src.wk_s, src.wv_s, src.wo_s, src.w1_s, src.w2_s};
+    const size_t rows[6] = {dim, dim, dim, dim, mlp, dim};
+    const size_t cols[6] = {dim, dim, dim, dim, dim, mlp};
+    static const char *names[6] = {"wq", "wk", "wv", "wo", "w1", "w2"};
+    for (int t = 0; t < 6; ++t) {
+      if (weight(ws[t], rows[t] * cols[t], names[t], &ptr)) { vision_free(v); return nullptr; }
+      v->layers[l].w[t] = (const int8_t *)ptr;
+      if (weight(ss[t], rows[t] * 4, names[t], &ptr)) { vision_free(v); return nullptr; }
+      v->layers[l].s[t] = (const float *)ptr;
+    }
+    if (!src.bq || !src.bk || !src.bv || !src.bo || !src.b1 || !src.b2 || !src.n1 ||
+        !src.n1_b || !src.n2 || !src.n2_b) {
+      fail("gemma_hip_vision_create: layer %d lacks a bias or norm weight", l);
+      vision_free(v);
+      return nullptr;
+    }
+  }
+  if (weight(pos_q, n * dim, "pos_emb", &ptr)) { vision_free(v); return nullptr; }
+  v->pos_q = (const int8_t *)ptr;
+  if (weight(pos_s, n * 4, "pos_emb scales", &ptr)) { vision_free(v); return nullptr; }
+  v->pos_s = (const float *)ptr;
+  if (weight(proj, (size_t)c.text_dim * dim, "proj", &ptr)) { vision_free(v); return nullptr; }
+  v->proj = (const int8_t *)ptr;
+  if (weight(proj_s, (size_t)c.text_dim * 4, "proj scales", &ptr)) {
+    vision_free(v);
+    return nullptr;
+  }
+  v->proj_s = (const float *)ptr;
+  // one device allocation: copied parameters, then the activations
+  Carver cv;
+  const size_t per_layer = 3 * dim + dim + mlp + dim + 4 * dim;  // bqkv bo b1 b2 n1 n1b n2 n2b
+  const size_t o_par = cv.take((kpe * dim + dim + 3 * dim + per_layer * c.nl) * 4);
+  const size_t o_img = cv.take((size_t)c.img_px * c.img_px * 3 * 4),
+               o_pat = cv.take(n * kpe * 4), o_x = cv.take(n * dim * 4),
+               o_y = cv.take(n * dim * 4), o_qkv = cv.take(n * 3 * dim * 4),
+               o_att = cv.take(n * dim * 4), o_h = cv.take(n * mlp * 4),
+               o_hln = cv.take(n * dim * 4), o_out = cv.take((size_t)c.img_tok * c.text_dim * 4),
+               o_a8 = cv.take(n * std::max(dim, mlp)), o_as = cv.take(n * 4);
+  hipError_t e = hipMalloc((void **)&v->mem, cv.used);
+  if (e != hipSuccess) {
+    hip_fail("gemma_hip_vision_create: alloc", e);
+    vision_free(v);
+    return nullptr;
+  }
+  char *m = v->mem;
+  std::vector<float> host;
+  host.reserve((kpe * dim + dim + 3 * dim + per_layer * c.nl));
+  auto put = [&](const float *src, size_t len) {
+    float *at = (float *)(m + o_par) + host.size();
+    host.insert(host.end(), src, src + len);
+    return at;
+  };
+  v->pe = put(pe, kpe * dim);
+  v->pe_b = put(pe_b, dim);
+  v->post_n = put(post_n, dim);
+  v->post_nb = put(post_nb, dim);
+  v->norm = put(norm, dim);
+  for (int l = 0; l < c.nl; ++l) {
+    const gemma_hip_vision_layer &src = layers[l];
+    auto &L = v->layers[l];
+    L.bqkv = put(src.bq, dim);
+    put(src.bk, dim);
+    put(src.bv, dim);
+    L.bo = put(src.bo, dim);
+    L.b1 = put(src.b1, mlp);
+    L.b2 = put(src.b2, dim);
+    L.n1 = put(src.n1, dim);
+    L.n1b = put(src.n1_b, dim);
+    L.n2 = put(src.n2, dim);
+    L.n2b = put(src.n2_b, dim);
+  }
+  e = hipMemcpy(m + o_par, host.data(), host.size() * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    hip_fail("gemma_hip_vision_create: upload", e);
+    vision_free(v);
+    return nullptr;
+  }
+  v->img = (float *)(m + o_img);
+  v->patches = (float *)(m + o_pat);
+  v->x = (float *)(m + o_x);
+  v->y = (float *)(m + o_y);
+  v->qkv = (float *)(m + o_qkv);
+  v->att = (float *)(m + o_att);
+  v->hbuf = (float *)(m + o_h);
+  v->hln = (float *)(m + o_hln);
+  v->out = (float *)(m + o_out);
+  v->a8 = (int8_t *)(m + o_a8);
+  v->as = (float *)(m + o_as);
+  return v;
+}
+
+void gemma_hip_vision_destroy(gemma_hip_vision *vis) {
+  if (vis == nullptr) return;
+  if (g.ready) (void)hipStreamSynchronize(g.stream);
+  vision_free(vis);
+}
+
+int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out) {
+  if (need_init()) return 1;
+  if (vis == nullptr || img == nullptr || out == nullptr)
+    return fail("gemma_hip_vision_forward: null argument");
+  const gemma_hip_vision_config &c = vis->cfg;
+  GH_CHECK("gemma_hip_vision_forward: sync", hipStreamSynchronize(g.stream));
+  GH_CHECK("gemma_hip_vision_forward: image H2D",
+           hipMemcpyAsync(vis->img, img, (size_t)c.img_px * c.img_px * 3 * 4,
+                          hipMemcpyHostToDevice, g.stream));
+  GH_CHECK("gemma_hip_vision_forward: launch", vision_enqueue(vis, g.stream));
+  GH_CHECK("gemma_hip_vision_forward: D2H",
+           hipMemcpyAsync(out, vis->out, (size_t)c.img_tok * c.text_dim * 4,
+                          hipMemcpyDeviceToHost, g.stream));
+  GH_CHECK("gemma_hip_vision_forward: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+}  // extern "C"

@@ -166,4 +166,49 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream);
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
                                 hipStream_t stream);
 
+// vision.hip: the SigLIP tower (forward_vision).
+// x [m][dim] = clamp(patches [m][k] . pe [dim][k] + pe_b) + pos_q * pos_s, in fp64
+struct VisPatch {
+  const float *patches, *pe, *pe_b;
+  const int8_t *pos_q;
+  const float *pos_s;
+  float *x;
+  int m, k, dim;
+};
+// per row: x = clamp((y + bias) + x) when y is given; LayerNorm(x; w, b) into
+// xq/xs (quantized) or, when xq is null, into h
+struct VisLn {
+  float *x;
+  const float *y, *bias, *w, *b;
+  int8_t *xq;
+  float *xs;
+  float *h;
+  int dim;
+  float eps;
+};
+// qkv [n][stride] (q | k | v, head h at column h*hdim of each), bias [3*dim]
+struct VisAttn {
+  const float *qkv;
+  int stride;
+  const float *bias;
+  float *out;
+  int n, n_heads, dim;
+  float scale;
+};
+// h [ppi*ppi][dim] -> xq/xs [(ppi/ksize)^2][dim]: mean pooling, RMSNorm(w)
+struct VisPool {
+  const float *h, *w;
+  int8_t *xq;
+  float *xs;
+  int dim, ppi, ksize;
+  float eps;
+};
+hipError_t launch_vis_patch(const VisPatch &a, hipStream_t stream);
+hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream);
+// head dim 16, 32, 64, 72 or 128
+hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream);
+hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int mlp, int8_t *xq,
+                                 float *xs, hipStream_t stream);
+hipError_t launch_vis_pool(const VisPool &a, int ntok, hipStream_t stream);
+
 }  // namespace gh

@@ -53,6 +53,24 @@ class Layer(ctypes.Structure):
         "nq", "nk", "n1", "n2", "n3", "n4")]
 
 
+class VisionConfig(ctypes.Structure):
+    """gemma_hip_vision_config: the reference's VisionConfig (gemma.c:713-721)
+    plus TextConfig's img_tok and dim (here text_dim)."""
+
+    _fields_ = [(n, ctypes.c_int) for n in ("nl", "n_heads", "img_px", "psize", "dim",
+                                            "mlp_dim")] + \
+               [("eps", ctypes.c_float), ("img_tok", ctypes.c_int), ("text_dim", ctypes.c_int)]
+
+
+class VisionLayer(ctypes.Structure):
+    """gemma_hip_vision_layer: one VisionEncoderLayer (gemma.c:1234-1256)."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "wq", "wk", "wv", "wo", "w1", "w2",
+        "wq_s", "wk_s", "wv_s", "wo_s", "w1_s", "w2_s",
+        "bq", "bk", "bv", "bo", "b1", "b2", "n1", "n1_b", "n2", "n2_b")]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SIGS = {
@@ -87,6 +105,9 @@ _SIGS = {
     "gemma_hip_decoder_generate": (_I, [_P, _I, _I, _I, _P]),
     "gemma_hip_decoder_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_logits": (_P, [_P]),
+    "gemma_hip_vision_create": (_P, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "gemma_hip_vision_destroy": (None, [_P]),
+    "gemma_hip_vision_forward": (_I, [_P, _P, _P]),
 }
 
 
@@ -195,6 +216,11 @@ class GemmaHip:
         return self.lib.gemma_hip_device_ptr(_addr(host))
 
     # device-resident decoder -----------------------------------------------
+    def vision(self, vis) -> "Vision":
+        """A vision tower over a dict of VisionEncoder weights
+        (model_bin.synth_vision's layout): registers every int8 tensor."""
+        return Vision(self, vis)
+
     def decoder(self, model, clen: int) -> "Decoder":
         """A decoder over a model from model_bin.read_bin(): registers every
         int8 tensor (each as its own range) and builds the step graph."""
@@ -290,3 +316,72 @@ class Decoder:
             self.handle = None
         self._release()
 
+
+
+class Vision:
+    """gemma_hip_vision_*: forward_vision (gemma.c:4394) on the GPU."""
+
+    def __init__(self, gh: GemmaHip, vis):
+        import numpy as np
+
+        self.gh, self.lib = gh, gh.lib
+        c = vis["config"]
+        self.out_shape = (c["img_tok"], c["text_dim"])
+        self.img_shape = (c["img_px"], c["img_px"], 3)
+        self._keep, self._registered = [], []
+
+        def reg(arr):
+            arr = np.ascontiguousarray(arr)
+            gh.register_weights(arr, arr.nbytes)
+            self._registered.append(arr)
+            return arr.ctypes.data
+
+        def host(arr):
+            arr = np.ascontiguousarray(arr, np.float32)
+            self._keep.append(arr)
+            return arr.ctypes.data
+
+        cfg = VisionConfig(c["nl"], c["n_heads"], c["img_px"], c["psize"], c["dim"],
+                           c["mlp_dim"], c["eps"], c["img_tok"], c["text_dim"])
+        layers = (VisionLayer * c["nl"])()
+        try:
+            for i, ly in enumerate(vis["layers"]):
+                f = {}
+                for w in ("wq", "wk", "wv", "wo", "w1", "w2"):
+                    f[w] = reg(ly[w][0])
+                    f[w + "_s"] = reg(ly[w][1])
+                for b in ("bq", "bk", "bv", "bo", "b1", "b2", "n1", "n1_b", "n2", "n2_b"):
+                    f[b] = host(ly[b])
+                layers[i] = VisionLayer(**f)
+            self.handle = self.lib.gemma_hip_vision_create(
+                ctypes.byref(cfg), layers, host(vis["pe"]), host(vis["pe_b"]),
+                reg(vis["pos"][0]), reg(vis["pos"][1]), host(vis["post_n"]),
+                host(vis["post_nb"]), host(vis["norm"]), reg(vis["proj"][0]),
+                reg(vis["proj"][1]))
+            if not self.handle:
+                raise GemmaHipError(self.lib.gemma_hip_last_error().decode())
+        except Exception:
+            self._release()
+            raise
+
+    def _release(self):
+        for arr in self._registered:
+            self.gh.release_weights(arr)
+        self._registered = []
+
+    def forward(self, img):
+        """img [img_px][img_px][3] float32 -> soft tokens [img_tok][text_dim]."""
+        import numpy as np
+
+        img = np.ascontiguousarray(img, np.float32)
+        assert img.shape == self.img_shape
+        out = np.empty(self.out_shape, np.float32)
+        self.gh._check(self.lib.gemma_hip_vision_forward(self.handle, img.ctypes.data,
+                                                         out.ctypes.data))
+        return out
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.gemma_hip_vision_destroy(self.handle)
+            self.handle = None
+        self._release()

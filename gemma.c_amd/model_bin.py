@@ -222,6 +222,53 @@ def synth_model(name: str, seed: int = 1234, nvocab: int = NVOCAB) -> dict:
     return {"config": cfg, "emb": qt(nvocab, dim), "layers": layers, "fnorm": zeros(dim)}
 
 
+# SigLIP (the Gemma 3 vision tower): VisionConfig
+# (gemma.c:713-721) plus the pooled token count TextConfig carries
+VISION_CONFIGS = {
+    "siglip": dict(nl=27, n_heads=16, img_px=896, psize=14, dim=1152, mlp_dim=4304, img_tok=256),
+}
+
+
+def synth_vision(seed: int = 1234, text_dim: int = 2560, eps: float = 1e-6, **shape) -> dict:
+    """Random W8A8 VisionEncoder weights (gemma.c:1565-1585) in memory: int8
+    tensors uniform in [-127, 127] with row scales U(4e-4, 8e-4), the fp32
+    patch embedding and biases N(0, 0.02), layer-norm weights N(1, 0.05) and
+    biases N(0, 0.05), the soft-embedding RMSNorm weight N(0, 0.1) (applied as
+    w + 1).  `shape` overrides VISION_CONFIGS["siglip"]'s fields."""
+    c = dict(VISION_CONFIGS["siglip"], **shape)
+    rng = np.random.default_rng(seed)
+    dim, mlp, p = c["dim"], c["mlp_dim"], c["psize"]
+    npatch = (c["img_px"] // p) ** 2
+
+    def qt(rows, cols):
+        q = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
+        return q, rng.uniform(4e-4, 8e-4, rows).astype(np.float32)
+
+    def nrm(n, mean, std):
+        return (mean + std * rng.standard_normal(n)).astype(np.float32)
+
+    layers = [{"wq": qt(dim, dim), "wk": qt(dim, dim), "wv": qt(dim, dim), "wo": qt(dim, dim),
+               "w1": qt(mlp, dim), "w2": qt(dim, mlp),
+               "bq": nrm(dim, 0, 0.02), "bk": nrm(dim, 0, 0.02), "bv": nrm(dim, 0, 0.02),
+               "bo": nrm(dim, 0, 0.02), "b1": nrm(mlp, 0, 0.02), "b2": nrm(dim, 0, 0.02),
+               "n1": nrm(dim, 1, 0.05), "n1_b": nrm(dim, 0, 0.05),
+               "n2": nrm(dim, 1, 0.05), "n2_b": nrm(dim, 0, 0.05)}
+              for _ in range(c["nl"])]
+    cfg = dict(c, eps=float(np.float32(eps)), text_dim=text_dim)
+    return {"config": cfg, "pe": nrm(dim * 3 * p * p, 0, 0.02).reshape(dim, 3 * p * p),
+            "pe_b": nrm(dim, 0, 0.02), "pos": qt(npatch, dim), "layers": layers,
+            "post_n": nrm(dim, 1, 0.05), "post_nb": nrm(dim, 0, 0.05), "norm": nrm(dim, 0, 0.1),
+            "proj": qt(text_dim, dim)}
+
+
+def synth_image(img_px: int, seed: int = 1234) -> np.ndarray:
+    """An image ~U(0, 255) per channel, normalized as gemma.c:4271-4273
+    ((p / 255 - 0.5) / 0.5), HWC float32."""
+    rng = np.random.default_rng(seed)
+    pix = rng.integers(0, 256, (img_px, img_px, 3)).astype(np.float32)
+    return ((pix / np.float32(255.0) - np.float32(0.5)) / np.float32(0.5)).astype(np.float32)
+
+
 def ensure_bin(directory: str, name: str, seed: int = 1234) -> str:
     """Path of the random-init model `name`, written on first use."""
     os.makedirs(directory, exist_ok=True)

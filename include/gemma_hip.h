@@ -266,6 +266,57 @@ int gemma_hip_decoder_generate(gemma_hip_decoder *dec, int token, int pos, int n
 /* Device pointer of the last step's logits (nvocab floats). */
 const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec);
 
+/* ---- device-resident vision tower --------------------------------------- */
+/* forward_vision (gemma.c:4394-4725) with every tensor resident in HBM: the
+ * patch embedding, the position embedding, all SigLIP encoder layers (layer
+ * norms, q/k/v/o with biases, attention over all patches, fc1 + GELU, fc2,
+ * residuals), the post layer norm, average pooling to the image tokens, the
+ * soft-embedding RMSNorm and the projection to the text width.  W8A8 files:
+ * the int8 products are bit-exact as above; the fp32 glue follows the
+ * reference's formulas, evaluated in fp64 and rounded once. */
+
+/* The reference's VisionConfig (gemma.c:713-721), plus the two TextConfig
+ * fields the tower feeds: img_tok (a square number of pooled tokens) and the
+ * text model's dim (the projection's width). */
+typedef struct {
+  int nl, n_heads, img_px, psize, dim, mlp_dim;
+  float eps;
+  int img_tok, text_dim;
+} gemma_hip_vision_config;
+
+/* One VisionEncoderLayer (gemma.c:1234-1256) of a W8A8 file: int8 weights and
+ * their row scales are host pointers inside registered ranges (wq..wo
+ * [dim][dim], w1 [mlp_dim][dim], w2 [dim][mlp_dim]); biases and layer-norm
+ * weights are host arrays the tower copies. */
+typedef struct {
+  const int8_t *wq, *wk, *wv, *wo, *w1, *w2;
+  const float *wq_s, *wk_s, *wv_s, *wo_s, *w1_s, *w2_s;
+  const float *bq, *bk, *bv, *bo, *b1, *b2;
+  const float *n1, *n1_b, *n2, *n2_b;
+} gemma_hip_vision_layer;
+
+typedef struct gemma_hip_vision gemma_hip_vision;
+
+/* Builds the tower of a VisionEncoder (gemma.c:1565-1585): pe [dim][3][psize]
+ * [psize] and pe_b [dim] (fp32), post_n/post_nb/norm [dim] are copied;
+ * pos_q [npatch][dim] + pos_s [npatch] and proj [text_dim][dim] + proj_s
+ * [text_dim] must be registered.  Head dim (dim / n_heads) 16, 32, 64, 72 or
+ * 128; dim and mlp_dim multiples of 16 (dim <= 6144, mlp_dim <= 24576).
+ * NULL on failure. */
+gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
+                                          const gemma_hip_vision_layer *layers,
+                                          const float *pe, const float *pe_b,
+                                          const int8_t *pos_q, const float *pos_s,
+                                          const float *post_n, const float *post_nb,
+                                          const float *norm, const int8_t *proj,
+                                          const float *proj_s);
+void gemma_hip_vision_destroy(gemma_hip_vision *vis);
+
+/* One image: img (host, [img_px][img_px][3] fp32, normalized as gemma.c:
+ * 4271-4273 leaves it) in, out (host, [img_tok][text_dim] fp32: the image's
+ * soft tokens, what forward_vision leaves in tb->x) out. */
+int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out);
+
 #ifdef __cplusplus
 }
 #endif
