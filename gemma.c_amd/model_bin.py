@@ -68,12 +68,18 @@ def _pascal(s: str) -> bytes:
 
 def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
               layers: int | None = None, slide: int | None = None, sc_att: float = 0.0,
-              sc_log: float = 0.0, flags: int = 4 | 2 | 1, norm_std: float = 0.0) -> str:
+              sc_log: float = 0.0, flags: int = 4 | 2 | 1, norm_std: float = 0.0,
+              vision: dict | None = None) -> str:
     """Write a random-init W8A8 (f32 build) text model of shape `name`;
     `nvocab` and `layers` shrink it for quick tests, `slide`, the softcaps
     and the flags byte (4 qk-norm, 2 pre-FFN norm, 1 post-FFN norm) select
     the other code paths of the reference's decoder; norm_std > 0 draws the
-    norm weights from N(0, norm_std) instead of zeros."""
+    norm weights from N(0, norm_std) instead of zeros.  `vision`, a
+    synth_vision() dict whose text_dim is this model's dim, makes the file
+    multimodal (flag 8): its VisionConfig follows the flags byte (gemma.c:
+    723-733), the vocabulary gains the image soft token (905-913) and the
+    tower's tensors follow the text decoder's in read_vision_encoder's order
+    (1688-1762)."""
     c = dict(CONFIGS[name])
     nl, dim, hdim, mlp = c["nl"], c["dim"], c["hdim"], c["mlp"]
     if layers is not None:
@@ -85,8 +91,12 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
     tmp = path + ".tmp"
     with open(tmp, "wb") as f:
         f.write(b"GEMA" + b"f32" + b"Q")
+        vc = vision["config"] if vision is not None else None
+        if vc is not None and vc["text_dim"] != dim:
+            raise ValueError("the vision tower's text_dim must be the model's dim")
+        img_tok = vc["img_tok"] if vc is not None else 256
         f.write(struct.pack(">BBBHHHHHHIIfffff", nl, c["n_heads"], c["nkv"], hdim, dim, mlp,
-                            hdim, c["slide"], 256, 32768, nvocab, 10000.0, 1000000.0, 1e-6,
+                            hdim, c["slide"], img_tok, 32768, nvocab, 10000.0, 1000000.0, 1e-6,
                             sc_att, sc_log))
         nbytes = (nl + 7) // 8
         bits = bytearray(nbytes)
@@ -94,8 +104,13 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
             if (i + 1) % 6 != 0:  # gemma 3: five sliding-window layers per global one
                 bits[i // 8] |= 1 << (7 - i % 8)
         f.write(bytes([nbytes]) + bytes(bits))
-        f.write(bytes([flags & 7]))  # qk_norm, pre- and post-FFN norms; text only
+        f.write(bytes([(flags & 7) | (8 if vc is not None else 0)]))
+        if vc is not None:
+            f.write(struct.pack(">BBHHHHf", vc["nl"], vc["n_heads"], vc["mlp_dim"], vc["dim"],
+                                vc["img_px"], vc["psize"], vc["eps"]))
         vocab = SPECIALS + [f"t{i}" for i in range(len(SPECIALS), nvocab)]
+        if vc is not None:
+            vocab.append("<image_soft_token>")
         f.write(b"".join(_pascal(s) for s in vocab))
         f.write(struct.pack(">I", 1) + _pascal("t") + _pascal("0"))
 
@@ -118,8 +133,36 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
             for _ in range(2 + ((flags & 2) != 0) + ((flags & 1) != 0)):
                 f.write(norm(dim))               # n1 n2 [n3] [n4]
         f.write(norm(dim))                       # fnorm
+        if vision is not None:
+            _write_vision(f, vision)
     os.replace(tmp, path)
     return path
+
+
+def _write_vision(f, v: dict) -> None:
+    """The VisionEncoder's tensors in read_vision_encoder's order (gemma.c:
+    1688-1762): pe, pe_b, pos_emb, per layer n1 n1_b wq wk wv wo bq bk bv bo n2
+    n2_b w1 w2 b1 b2, then post_n post_nb norm proj; int8 tensors as int8 rows
+    then their fp32 row scales."""
+    def t(a):
+        f.write(np.ascontiguousarray(a, np.float32).tobytes())
+
+    def q(w):
+        f.write(np.ascontiguousarray(w[0], np.int8).tobytes())
+        t(w[1])
+
+    t(v["pe"])
+    t(v["pe_b"])
+    q(v["pos"])
+    for ly in v["layers"]:
+        t(ly["n1"]); t(ly["n1_b"])
+        for w in ("wq", "wk", "wv", "wo"):
+            q(ly[w])
+        for b in ("bq", "bk", "bv", "bo", "n2", "n2_b"):
+            t(ly[b])
+        q(ly["w1"]); q(ly["w2"]); t(ly["b1"]); t(ly["b2"])
+    t(v["post_n"]); t(v["post_nb"]); t(v["norm"])
+    q(v["proj"])
 
 
 def read_bin(path: str) -> dict:
@@ -143,8 +186,13 @@ def read_bin(path: str) -> dict:
     flags = int(data[at])
     at += 1
     multimodal = bool(flags & 8)
-    if multimodal:
-        at += 14  # vision config (gemma.c:726-729)
+    vcfg = None
+    if multimodal:  # vision config (gemma.c:723-733)
+        vnl, vheads, vmlp, vdim, img_px, psize, veps = struct.unpack(
+            ">BBHHHHf", bytes(data[at:at + 14]))
+        vcfg = dict(nl=vnl, n_heads=vheads, img_px=img_px, psize=psize, dim=vdim,
+                    mlp_dim=vmlp, img_tok=img_tok, eps=veps)
+        at += 14
     for _ in range(nvocab + (1 if multimodal else 0)):
         at += 1 + int(data[at])
     (nmerges,) = struct.unpack(">I", bytes(data[at:at + 4]))
@@ -181,7 +229,29 @@ def read_bin(path: str) -> dict:
         ly["n4"] = f32(dim) if cfg["mlp_pst"] else None
         layers.append(ly)
     fnorm = f32(dim)
-    return {"config": cfg, "emb": emb, "layers": layers, "fnorm": fnorm, "end": at}
+    out = {"config": cfg, "emb": emb, "layers": layers, "fnorm": fnorm}
+    if vcfg is not None:
+        vd, vm, p = vcfg["dim"], vcfg["mlp_dim"], vcfg["psize"]
+        npatch = (vcfg["img_px"] // p) ** 2
+        vis = {"config": dict(vcfg, text_dim=dim)}
+        vis["pe"] = f32(vd * 3 * p * p).reshape(vd, 3 * p * p)
+        vis["pe_b"] = f32(vd)
+        vis["pos"] = qt(npatch, vd)
+        vis["layers"] = []
+        for _ in range(vcfg["nl"]):
+            ly = {"n1": f32(vd), "n1_b": f32(vd)}
+            for w in ("wq", "wk", "wv", "wo"):
+                ly[w] = qt(vd, vd)
+            for b in ("bq", "bk", "bv", "bo", "n2", "n2_b"):
+                ly[b] = f32(vd)
+            ly["w1"], ly["w2"] = qt(vm, vd), qt(vd, vm)
+            ly["b1"], ly["b2"] = f32(vm), f32(vd)
+            vis["layers"].append(ly)
+        vis["post_n"], vis["post_nb"], vis["norm"] = f32(vd), f32(vd), f32(vd)
+        vis["proj"] = qt(dim, vd)
+        out["vision"] = vis
+    out["end"] = at
+    return out
 
 
 def synth_model(name: str, seed: int = 1234, nvocab: int = NVOCAB) -> dict:

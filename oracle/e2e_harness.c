@@ -39,6 +39,13 @@
  *                            position, as the device-resident decoder runs)
  *   GEMMA_E2E_LOGITS=<path>  write every step's logits (nvocab float32 each,
  *                            in step order) to <path>
+ *   GEMMA_E2E_VISION_IMAGE=<path>, GEMMA_E2E_VISION_OUT=<path>
+ *                            (CPU build, multimodal model) instead of the text
+ *                            run: read the image (float32 [img_px][img_px][3],
+ *                            normalized as gemma.c:4271-4273 leaves it) from the
+ *                            first file, run forward_vision (4394-4725) and
+ *                            write the image's soft tokens (float32 [img_tok]
+ *                            [dim], tb->x) to the second
  *
  * Everything below the include uses identifiers of three characters or more
  * (the stb blob at the end of gemma.c defines one- and two-letter macros,
@@ -200,7 +207,63 @@ static uint64_t fnv_chain(uint64_t hash, const float *vals, size_t count) {
   return hash;
 }
 
+/* The reference's vision tower on one image (see GEMMA_E2E_VISION_IMAGE).
+ * The stb blob's `x` macro is no longer needed here: TextBuffer's field x
+ * (gemma.c's soft-token output) is reached through it. */
+#undef x
+static int run_vision(const char *model_path, const char *img_path,
+                      const char *out_path, int threads) {
+  GemmaModel *model = mmap_gemma_model(model_path, true);
+  if (model == NULL || model->encoder == NULL) {
+    die_with("load (multimodal)", model == NULL ? get_error() : "no vision tower");
+  }
+  TextConfig *cfg = model->decoder->config;
+  VisionConfig *vcfg = model->encoder->config;
+  int img_tok = (int)cfg->img_tok;
+  TextBuffer *buf = malloc_text_buffer(cfg, vcfg, img_tok + 1, img_tok, true,
+                                       model->quant);
+  VisionBuffer *vbuf = malloc_vision_buffer(vcfg, model->quant);
+  if (buf == NULL || vbuf == NULL) {
+    die_with("buffers", get_error());
+  }
+  size_t npix = (size_t)vcfg->img_px * vcfg->img_px * 3;
+  float *img = malloc(npix * sizeof(float));
+  FILE *fin = fopen(img_path, "rb");
+  if (img == NULL || fin == NULL || fread(img, sizeof(float), npix, fin) != npix) {
+    die_with("image", img_path);
+  }
+  fclose(fin);
+  PerfBench perf;
+  memset(&perf, 0, sizeof(perf));
+  double tic = now_sec();
+  if (forward_vision(model->encoder, cfg, buf, vbuf, img, model->quant, threads,
+                     &perf) != 0) {
+    die_with("forward_vision", get_error());
+  }
+  double vision_sec = now_sec() - tic;
+  FILE *fout = fopen(out_path, "wb");
+  if (fout == NULL ||
+      fwrite(buf->x, sizeof(float), (size_t)img_tok * cfg->dim, fout) !=
+          (size_t)img_tok * cfg->dim) {
+    die_with("output", out_path);
+  }
+  fclose(fout);
+  printf("{\"build\": \"cpu\", \"model\": \"%s\", \"vision_s\": %.6f, "
+         "\"img_tok\": %d, \"dim\": %d, \"threads\": %d}\n",
+         model_path, vision_sec, img_tok, (int)cfg->dim, threads);
+  free(img);
+  free_vision_buffer(vbuf, model->quant);
+  free_text_buffer(buf, model->quant);
+  munmap_gemma_model(model);
+  return 0;
+}
+
 int main(int argc, char **argv) {
+  const char *vis_img = getenv("GEMMA_E2E_VISION_IMAGE");
+  const char *vis_out = getenv("GEMMA_E2E_VISION_OUT");
+  if (vis_img != NULL && vis_out != NULL && argc >= 2) {
+    return run_vision(argv[1], vis_img, vis_out, argc > 5 ? atoi(argv[5]) : 1);
+  }
   if (argc < 6) {
     fprintf(stderr, "usage: %s <model.bin> <prompt_len> <decode_steps> "
                     "<seed> <threads> [chunk]\n", argv[0]);

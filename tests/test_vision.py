@@ -12,6 +12,10 @@ reassociation anywhere upstream of an int8 requantization would fail.
 
 from __future__ import annotations
 
+import copy
+import os
+import subprocess
+
 import numpy as np
 import pytest
 
@@ -19,6 +23,11 @@ import model_bin
 from oracle import vision_oracle as vorc
 
 TOL = 1e-5
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+E2E_CPU = os.path.join(REPO, "oracle", "_ref", "gemma_e2e_cpu")
+needs_e2e = pytest.mark.skipif(not os.path.exists(E2E_CPU),
+                               reason="oracle/_ref/gemma_e2e_cpu not built (needs /root/reference)")
 
 
 # ------------------------------------------------------------ oracle pins (CPU)
@@ -96,3 +105,93 @@ def test_vision_argument_errors(gh):
     stray = np.zeros(64, np.float32)
     h = gh.lib.gemma_hip_vision_create(ctypes.byref(cfg), layers, *([stray.ctypes.data] * 9))
     assert not h and b"not registered" in gh.lib.gemma_hip_last_error()
+
+
+# ------------------------------------------------- against the reference program
+# forward_vision itself (compiled from the reference's source by oracle/Makefile,
+# run by oracle/e2e_harness.c on a multimodal .bin written by model_bin) on the
+# same weights and image.  The reference evaluates the glue in fp32; below the
+# first int8 requantization flip the two agree to ~2e-7 of the largest output
+# (measured: 1e-7 .. 3e-7 over 12 seeds at head dim 72), which is the bound
+# here, on seeds measured flip-free.  The planted-mistake test shows the bound
+# is sharp: a dropped bias, a squared attention scale or transposed pooling
+# moves the output by 1.5% to 100%.
+REL_PRE_FLIP = 1e-5
+REF_CASES = {"hd72": ("hd72", 1, 101), "hd16": ("hd16", 3, 8)}  # shape, weight seed, image seed
+
+
+def run_reference_vision(tmp_path, case):
+    shape, seed, img_seed = REF_CASES[case]
+    vis = model_bin.synth_vision(seed=seed, text_dim=640, **SHAPES[shape])
+    path = model_bin.write_bin(str(tmp_path / f"mm_{case}.bin"), "gemma-3-270m", seed=5,
+                               nvocab=512, layers=2, vision=vis)
+    img = model_bin.synth_image(SHAPES[shape]["img_px"], seed=img_seed)
+    img_path, out_path = str(tmp_path / "img.f32"), str(tmp_path / "soft.f32")
+    img.tofile(img_path)
+    env = dict(os.environ, GEMMA_E2E_VISION_IMAGE=img_path, GEMMA_E2E_VISION_OUT=out_path)
+    out = subprocess.run([E2E_CPU, path, "1", "0", "1", "4"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    ref = np.fromfile(out_path, np.float32).reshape(SHAPES[shape]["img_tok"], 640)
+    return model_bin.read_bin(path)["vision"], img, ref
+
+
+def rel_to(ref, got):
+    return float(np.abs(got - ref).max() / np.abs(ref).max())
+
+
+def test_multimodal_bin_round_trip(tmp_path):
+    vis = model_bin.synth_vision(seed=2, text_dim=640, **SHAPES["hd16"])
+    path = model_bin.write_bin(str(tmp_path / "mm.bin"), "gemma-3-270m", seed=5, nvocab=512,
+                               layers=2, vision=vis)
+    back = model_bin.read_bin(path)
+    assert back["end"] == os.path.getsize(path)
+    v = back["vision"]
+    assert v["config"] == dict(vis["config"])
+    assert np.array_equal(v["pe"], vis["pe"]) and np.array_equal(v["pos"][0], vis["pos"][0])
+    for a, b in zip(v["layers"], vis["layers"]):
+        for key in ("wq", "w1", "w2"):
+            assert np.array_equal(a[key][0], b[key][0]) and np.array_equal(a[key][1], b[key][1])
+        for key in ("bv", "b1", "n2_b"):
+            assert np.array_equal(a[key], b[key])
+    assert np.array_equal(v["proj"][1], vis["proj"][1]) and np.array_equal(v["norm"], vis["norm"])
+
+
+@needs_e2e
+@pytest.mark.parametrize("case", sorted(REF_CASES))
+def test_vision_oracle_follows_reference_program(tmp_path, oracle, case):
+    vis, img, ref = run_reference_vision(tmp_path, case)
+    rel = rel_to(ref, vorc.VisionOracle(vis, oracle).forward(img))
+    print(f"vision oracle vs reference ({case}): {rel:.3g}", flush=True)
+    assert rel <= REL_PRE_FLIP
+
+
+@needs_e2e
+def test_vision_comparison_catches_planted_mistakes(tmp_path, oracle, monkeypatch):
+    vis, img, ref = run_reference_vision(tmp_path, "hd16")
+    bad = copy.deepcopy(vis)
+    bad["post_nb"] = np.zeros_like(bad["post_nb"])
+    assert rel_to(ref, vorc.VisionOracle(bad, oracle).forward(img)) > 100 * REL_PRE_FLIP
+    attention = vorc.attention
+    monkeypatch.setattr(vorc, "attention", lambda q, k, v, s: attention(q, k, v, s * s))
+    assert rel_to(ref, vorc.VisionOracle(vis, oracle).forward(img)) > 100 * REL_PRE_FLIP
+    monkeypatch.setattr(vorc, "attention", attention)
+    pool = vorc.avg_pool
+    monkeypatch.setattr(vorc, "avg_pool", lambda h, ppi, k: pool(
+        h.reshape(ppi, ppi, -1).transpose(1, 0, 2).reshape(ppi * ppi, -1), ppi, k))
+    assert rel_to(ref, vorc.VisionOracle(vis, oracle).forward(img)) > 100 * REL_PRE_FLIP
+
+
+@pytest.mark.gpu
+@needs_e2e
+@pytest.mark.parametrize("case", sorted(REF_CASES))
+def test_device_vision_follows_reference_program(gh, tmp_path, case):
+    vis, img, ref = run_reference_vision(tmp_path, case)
+    tower = gh.vision(vis)
+    try:
+        got = tower.forward(img)
+    finally:
+        tower.close()
+    rel = rel_to(ref, got)
+    print(f"device vision vs reference ({case}): {rel:.3g}", flush=True)
+    assert rel <= REL_PRE_FLIP
