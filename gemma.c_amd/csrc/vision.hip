@@ -153,157 +153,140 @@ __global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
 // Full (non-causal) attention of every patch over every patch, per head
 // (gemma.c:4533-4561): q, k and v are the GEMM outputs plus their biases
 // (single fp32 additions, 4517-4526), scores q.k * scale with scale =
-// 1 / sqrtf(hdim) in fp32, softmax over all patches, value sums.  A
-// workgroup takes 32 patches of one head and walks every patch in tiles of
-// kVaKeys, with the fp64 online softmax and tiling of the prefill attention
-// (prefill.hip): thread (c, qg, kg) sums every fourth 16-byte chunk of the
-// head dimension starting at chunk c for queries 4qg..4qg+3 and keys 2kg,
-// 2kg+1; in the value sums thread (v, d4) owns query v and the chunks
-// d4, d4 + 8, ... of its output.
-constexpr int kVaQ = 32, kVaKeys = 16;
+// 1 / sqrtf(hdim) in fp32, softmax over all patches, value sums -- on the
+// fp64 matrix cores.  v_mfma_f64_16x16x4f64 takes A[16][4] as lane l ->
+// A[l%16][l/16], B[4][16] as lane l -> B[l/16][l%16], and leaves D[16][16]
+// as lane l, element r -> D[4r + l/16][l%16] (checked on this GPU).
+//
+// A workgroup is 4 waves x 16 patches of one head; each wave holds its 16
+// query rows as fp64 A operands in registers for the whole kernel.  Per tile
+// of 32 keys (K and V staged in LDS as fp32, biases added): two 16x16 score
+// blocks (HD/4 MFMA steps each); an online softmax in fp64 on the score
+// registers -- the 16 lanes of a DPP row hold one query row, so row maxima
+// and sums are DPP reductions; the probabilities go through LDS (16 x 32 per
+// wave) to become A operands; the output block O[16][16 * NB] is rescaled by
+// exp(m_old - m_new) and accumulates P . V (8 MFMA steps per 16 dims).  Every
+// sum is fp64; each output is rounded to fp32 once at the end.
+constexpr int kVaKeys = 32;  // keys per tile
 
 template <int HD>
 __global__ __launch_bounds__(kNT) void vis_attn_kernel(VisAttn a) {
   static_assert(HD % 4 == 0 && HD <= 128, "head dim");
-  constexpr int C4 = HD / 4;          // 16-byte chunks per row
-  constexpr int RS = HD + 4;          // padded LDS row
-  constexpr int PS = kVaQ + 2;        // probabilities row (one key)
-  constexpr int VCH = (C4 + 7) / 8;   // value chunks per thread
-  __shared__ __attribute__((aligned(16))) float qs[kVaQ * RS];
-  __shared__ __attribute__((aligned(16))) float kt[kVaKeys * RS];
-  __shared__ __attribute__((aligned(16))) float vt[kVaKeys * RS];
-  __shared__ double pp[kVaKeys * PS];
-  __shared__ double alpha[kVaQ], run_m[kVaQ], run_l[kVaQ];
+  constexpr int KS = HD / 4;              // MFMA steps of the scores
+  constexpr int NB = (HD + 15) / 16;      // 16-wide output blocks
+  constexpr int RK = HD + 1;              // K row in LDS (odd: the B reads spread)
+  constexpr int RP = kVaKeys + 4;         // P row (doubles)
+  __shared__ float kt[kVaKeys * RK];
+  __shared__ float vt[kVaKeys * (16 * NB + 16)];
+  __shared__ double pw[4][16 * RP];
 
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.y;
-  const int r0 = blockIdx.x * kVaQ;
-  const int rows = min(kVaQ, a.n - r0);
-  const float *bq = a.bias + h * HD;
+  const int q0 = blockIdx.x * 64 + wave * 16;  // this wave's first query row
+  const int col = lane & 15, grp = lane >> 4;  // A/B: row/col col, k grp; D: col, rows 4r+grp
+  constexpr int VS = 16 * NB + 16;             // V row stride in LDS (floats)
+
+  // q rows as A operands: qa[s] = Q[q0 + col][4 s + grp] + bq
+  double qa[KS];
+  {
+    const int qr = q0 + col;
+    const float *qrow = a.qkv + (size_t)qr * a.stride + h * HD;
+    const float *bq = a.bias + h * HD;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qa[s] = qr < a.n ? (double)(qrow[4 * s + grp] + bq[4 * s + grp]) : 0.0;
+  }
+  typedef double v4d __attribute__((ext_vector_type(4)));
+  v4d o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4d{0.0, 0.0, 0.0, 0.0};
+  double run_m[4], run_l[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    run_m[r] = -DBL_MAX;
+    run_l[r] = 0.0;
+  }
   const float *bk = a.bias + a.dim + h * HD;
   const float *bv = a.bias + 2 * a.dim + h * HD;
-  const v4f zero = {0.f, 0.f, 0.f, 0.f};
-
-  for (int i = tid; i < kVaQ * C4; i += kNT) {
-    const int v = i / C4, c4 = i - v * C4;
-    v4f x = zero;
-    if (v < rows) {
-      x = reinterpret_cast<const v4f *>(a.qkv + (size_t)(r0 + v) * a.stride + h * HD)[c4];
-      x += reinterpret_cast<const v4f *>(bq)[c4];
-    }
-    *reinterpret_cast<v4f *>(&qs[v * RS + 4 * c4]) = x;
-  }
-  if (tid < kVaQ) {
-    run_m[tid] = -DBL_MAX;
-    run_l[tid] = 0.0;
-  }
-  const int sc_c = tid & 3, sc_qg = (tid >> 2) & 7, sc_kg = tid >> 5;
-  const int va_v = tid >> 3, va_d4 = tid & 7;
-  double acc[VCH][4];
-#pragma unroll
-  for (int u = 0; u < VCH; ++u)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[u][e] = 0.0;
 
   for (int t0 = 0; t0 < a.n; t0 += kVaKeys) {
-    lds_barrier();  // the previous tile is no longer read
-    for (int i = tid; i < kVaKeys * C4; i += kNT) {
-      const int t = i / C4, c4 = i - t * C4;
-      v4f kx = zero, vx = zero;
+    lds_barrier();  // the previous tile's K, V and P are no longer read
+    for (int i = tid; i < kVaKeys * (HD / 4); i += kNT) {
+      const int t = i / (HD / 4), c4 = i - t * (HD / 4);
+      v4f kx = {0.f, 0.f, 0.f, 0.f}, vx = kx;
       if (t0 + t < a.n) {
         const v4f *row = reinterpret_cast<const v4f *>(a.qkv + (size_t)(t0 + t) * a.stride);
         kx = row[(a.dim + h * HD) / 4 + c4] + reinterpret_cast<const v4f *>(bk)[c4];
         vx = row[(2 * a.dim + h * HD) / 4 + c4] + reinterpret_cast<const v4f *>(bv)[c4];
       }
-      *reinterpret_cast<v4f *>(&kt[t * RS + 4 * c4]) = kx;
-      *reinterpret_cast<v4f *>(&vt[t * RS + 4 * c4]) = vx;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kt[t * RK + 4 * c4 + e] = kx[e];
+      *reinterpret_cast<v4f *>(&vt[t * VS + 4 * c4]) = vx;
     }
-    lds_barrier();
-    {
-      double s[4][2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) s[j][0] = s[j][1] = 0.0;
-      for (int c4 = sc_c; c4 < C4; c4 += 4) {
-        const v4f k0 = *reinterpret_cast<const v4f *>(&kt[(2 * sc_kg) * RS + 4 * c4]);
-        const v4f k1 = *reinterpret_cast<const v4f *>(&kt[(2 * sc_kg + 1) * RS + 4 * c4]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v4f q = *reinterpret_cast<const v4f *>(&qs[(4 * sc_qg + j) * RS + 4 * c4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s[j][0] = fma((double)q[e], (double)k0[e], s[j][0]);
-            s[j][1] = fma((double)q[e], (double)k1[e], s[j][1]);
-          }
-        }
+    if (16 * NB > HD)  // zero the padding columns of V (read by the last output block)
+      for (int i = tid; i < kVaKeys * (16 * NB - HD); i += kNT) {
+        const int t = i / (16 * NB - HD), c = i - t * (16 * NB - HD);
+        vt[t * VS + HD + c] = 0.0f;
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          double part = s[j][kk];
-          part += dpp_f64<kDppXor1>(part);
-          part += dpp_f64<kDppXor2>(part);
-          const int v = 4 * sc_qg + j, t = 2 * sc_kg + kk;
-          if (sc_c == 0)
-            pp[t * PS + v] = (t0 + t < a.n) ? part * (double)a.scale : -DBL_MAX;
-        }
-    }
     lds_barrier();
-    for (int v = tid / kVaKeys; v < kVaQ; v += kNT / kVaKeys) {
-      const int t = tid % kVaKeys;
-      const double sv = pp[t * PS + v];
-      double m = sv;
+    // scores: block b covers keys t0 + 16 b + col
+    v4d sc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      sc[b] = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        sc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+            qa[s], (double)kt[(16 * b + col) * RK + 4 * s + grp], sc[b], 0, 0, 0);
+    }
+    // online softmax on rows 4r + grp (the 16 lanes of this DPP row)
+    double alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      double s0 = t0 + col < a.n ? sc[0][r] * (double)a.scale : -DBL_MAX;
+      double s1 = t0 + 16 + col < a.n ? sc[1][r] * (double)a.scale : -DBL_MAX;
+      double m = fmax(s0, s1);
       m = fmax(m, dpp_f64<kDppXor1>(m));
       m = fmax(m, dpp_f64<kDppXor2>(m));
       m = fmax(m, dpp_f64<kDppHalfMirror>(m));
       m = fmax(m, dpp_f64<kDppMirror>(m));
-      const double m_old = run_m[v];
-      const double m_new = fmax(m_old, m);
-      const double e = sv == -DBL_MAX ? 0.0 : exp(sv - m_new);
-      double l = e;
+      const double m_new = fmax(run_m[r], m);
+      const double p0 = s0 == -DBL_MAX ? 0.0 : exp(s0 - m_new);
+      const double p1 = s1 == -DBL_MAX ? 0.0 : exp(s1 - m_new);
+      double l = p0 + p1;
       l += dpp_f64<kDppXor1>(l);
       l += dpp_f64<kDppXor2>(l);
       l += dpp_f64<kDppHalfMirror>(l);
       l += dpp_f64<kDppMirror>(l);
-      pp[t * PS + v] = e;
-      if (t == 0) {
-        const double al = exp(m_old - m_new);
-        alpha[v] = al;
-        run_l[v] = run_l[v] * al + l;
-        run_m[v] = m_new;
-      }
+      alpha[r] = exp(run_m[r] - m_new);
+      run_l[r] = run_l[r] * alpha[r] + l;
+      run_m[r] = m_new;
+      pw[wave][(4 * r + grp) * RP + col] = p0;
+      pw[wave][(4 * r + grp) * RP + 16 + col] = p1;
     }
-    lds_barrier();
-    const double al = alpha[va_v];
 #pragma unroll
-    for (int u = 0; u < VCH; ++u)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[u][e] *= al;
-#pragma unroll 4
-    for (int t = 0; t < kVaKeys; ++t) {
-      const double pv = pp[t * PS + va_v];
+      for (int r = 0; r < 4; ++r) o[nb][r] *= alpha[r];
+    lds_barrier();  // P is read back in the A layout
 #pragma unroll
-      for (int u = 0; u < VCH; ++u) {
-        const int c4 = va_d4 + 8 * u;
-        if (c4 < C4) {
-          const v4f x = *reinterpret_cast<const v4f *>(&vt[t * RS + 4 * c4]);
+    for (int s = 0; s < kVaKeys / 4; ++s) {
+      const double pa = pw[wave][col * RP + 4 * s + grp];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc[u][e] = fma(pv, (double)x[e], acc[u][e]);
-        }
-      }
+      for (int nb = 0; nb < NB; ++nb)
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+            pa, (double)vt[(4 * s + grp) * VS + 16 * nb + col], o[nb], 0, 0, 0);
     }
   }
-  if (va_v < rows) {
-    const double l = run_l[va_v];
 #pragma unroll
-    for (int u = 0; u < VCH; ++u) {
-      const int c4 = va_d4 + 8 * u;
-      if (c4 < C4) {
-        v4f o;
+  for (int r = 0; r < 4; ++r) {
+    const int qr = q0 + 4 * r + grp;
+    if (qr >= a.n) continue;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (float)(acc[u][e] / l);
-        reinterpret_cast<v4f *>(a.out + (size_t)(r0 + va_v) * a.dim + h * HD)[c4] = o;
-      }
+    for (int nb = 0; nb < NB; ++nb) {
+      const int d = 16 * nb + col;
+      if (d < HD) a.out[(size_t)qr * a.dim + h * HD + d] = (float)(o[nb][r] / run_l[r]);
     }
   }
 }
@@ -425,7 +408,7 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
 }
 
 hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream) {
-  const dim3 grid((a.n + kVaQ - 1) / kVaQ, a.n_heads);
+  const dim3 grid((a.n + 63) / 64, a.n_heads);
   switch (hdim) {
     case 16: vis_attn_kernel<16><<<grid, kNT, 0, stream>>>(a); break;
     case 32: vis_attn_kernel<32><<<grid, kNT, 0, stream>>>(a); break;
