@@ -158,136 +158,177 @@ __global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
 // A[l%16][l/16], B[4][16] as lane l -> B[l/16][l%16], and leaves D[16][16]
 // as lane l, element r -> D[4r + l/16][l%16] (checked on this GPU).
 //
-// A workgroup is 4 waves x 16 patches of one head; each wave holds its 16
-// query rows as fp64 A operands in registers for the whole kernel.  Per tile
-// of 32 keys (K and V staged in LDS as fp32, biases added): two 16x16 score
-// blocks (HD/4 MFMA steps each); an online softmax in fp64 on the score
-// registers -- the 16 lanes of a DPP row hold one query row, so row maxima
-// and sums are DPP reductions; the probabilities go through LDS (16 x 32 per
-// wave) to become A operands; the output block O[16][16 * NB] is rescaled by
-// exp(m_old - m_new) and accumulates P . V (8 MFMA steps per 16 dims).  Every
-// sum is fp64; each output is rounded to fp32 once at the end.
-constexpr int kVaKeys = 32;  // keys per tile
+// The products are taken transposed, S^T = K . Q^T and O^T = V^T . P^T, so
+// that a lane (query j = l%16, g = l/16) holds the scores of query j for the
+// keys 4r + g of a 16-key block, which are exactly the P^T operand the value
+// product wants: the probabilities never leave registers.  A workgroup is
+// 4 waves x 16 queries of one head; the queries stay in registers as fp64
+// operands (lane g holds dims [g HD/4, (g+1) HD/4) of its query).  Per tile of
+// 32 keys: K and V (biases added, fp32) are staged in LDS -- V transposed,
+// its keys permuted so that the 4 a lane needs for one MFMA step are
+// adjacent -- then two 16-key score blocks, the softmax weights, and P . V
+// into the fp64 output block O^T[16 NB][16].  K and V are held in LDS as
+// fp64, converted once when staged.
+//
+// Softmax: p = exp(s - m) with m a running reference maximum per query.
+// Shifting by any m gives the same softmax; m is moved up (to the exact row
+// maximum seen so far, rescaling O and the sums by exp(m_old - m_new)) only
+// when some score of the wave exceeds it by more than kVaSlack, which keeps
+// every p <= e^kVaSlack and lets most tiles skip the row reductions.  The
+// row sums are per-lane partials, added across the 4 lanes of a query at
+// the end.  Every sum is fp64; each output is rounded to fp32 once.
+constexpr int kVaKeys = 32;          // keys per tile
+constexpr double kVaSlack = 64.0;    // e^64 * 3.4e38 * n keys stays far below DBL_MAX
 
 template <int HD>
-__global__ __launch_bounds__(kNT) void vis_attn_kernel(VisAttn a) {
-  static_assert(HD % 4 == 0 && HD <= 128, "head dim");
-  constexpr int KS = HD / 4;              // MFMA steps of the scores
-  constexpr int NB = (HD + 15) / 16;      // 16-wide output blocks
-  constexpr int RK = HD + 1;              // K row in LDS (odd: the B reads spread)
-  constexpr int RP = kVaKeys + 4;         // P row (doubles)
-  __shared__ float kt[kVaKeys * RK];
-  __shared__ float vt[kVaKeys * (16 * NB + 16)];
-  __shared__ double pw[4][16 * RP];
+__global__ __launch_bounds__(kNT, 2) void vis_attn_kernel(VisAttn a) {
+  static_assert(HD % 8 == 0 && HD <= 128, "head dim");
+  constexpr int KS = HD / 4;            // MFMA steps of a score block (dims per lane)
+  constexpr int NB = (HD + 15) / 16;    // 16-dim output blocks
+  constexpr int RK = HD + 2;            // K row in LDS (doubles)
+  constexpr int VS = kVaKeys + 2;       // V^T row in LDS (doubles)
+  constexpr int C4 = HD / 4;            // float4 per key row
+  constexpr int PF = (kVaKeys * C4 + kNT - 1) / kNT;  // float4 of K (and of V) per thread
+  __shared__ double kt[kVaKeys * RK];
+  __shared__ double vt[16 * NB * VS];
+  __shared__ double etab[128];
+  __shared__ v4f kvb[2][C4];  // the k and v biases of this head
+  typedef double v2d __attribute__((ext_vector_type(2)));
+  typedef double v4d __attribute__((ext_vector_type(4)));
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = blockIdx.y;
-  const int q0 = blockIdx.x * 64 + wave * 16;  // this wave's first query row
-  const int col = lane & 15, grp = lane >> 4;  // A/B: row/col col, k grp; D: col, rows 4r+grp
-  constexpr int VS = 16 * NB + 16;             // V row stride in LDS (floats)
+  // blocks of one head share K and V: give each XCD (blocks b, b+8, ...) a
+  // contiguous run of (head, query block) pairs so they meet in its L2
+  const int nqb = (a.n + 63) / 64, nblk = nqb * a.n_heads;
+  int blk = blockIdx.x;
+  if (nblk % 8 == 0) blk = (blk % 8) * (nblk / 8) + blk / 8;
+  const int h = blk / nqb;
+  const int q0 = (blk - h * nqb) * 64 + wave * 16;
+  const int col = lane & 15, grp = lane >> 4;
 
-  // q rows as A operands: qa[s] = Q[q0 + col][4 s + grp] + bq
   double qa[KS];
   {
-    const int qr = q0 + col;
-    const float *qrow = a.qkv + (size_t)qr * a.stride + h * HD;
-    const float *bq = a.bias + h * HD;
+    const int qr = min(q0 + col, a.n - 1);
+    const float *qrow = a.qkv + (size_t)qr * a.stride + h * HD + grp * KS;
+    const float *bq = a.bias + h * HD + grp * KS;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qa[s] = qr < a.n ? (double)(qrow[4 * s + grp] + bq[4 * s + grp]) : 0.0;
+    for (int s = 0; s < KS; ++s) qa[s] = (double)(qrow[s] + bq[s]);
   }
-  typedef double v4d __attribute__((ext_vector_type(4)));
   v4d o[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) o[nb] = v4d{0.0, 0.0, 0.0, 0.0};
-  double run_m[4], run_l[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    run_m[r] = -DBL_MAX;
-    run_l[r] = 0.0;
-  }
+  double m_ref = -DBL_MAX, l_part = 0.0;
+  const double scale = (double)a.scale;
   const float *bk = a.bias + a.dim + h * HD;
   const float *bv = a.bias + 2 * a.dim + h * HD;
+  const float *kbase = a.qkv + a.dim + h * HD;
+  const float *vbase = a.qkv + 2 * a.dim + h * HD;
 
-  for (int t0 = 0; t0 < a.n; t0 += kVaKeys) {
-    lds_barrier();  // the previous tile's K, V and P are no longer read
-    for (int i = tid; i < kVaKeys * (HD / 4); i += kNT) {
-      const int t = i / (HD / 4), c4 = i - t * (HD / 4);
-      v4f kx = {0.f, 0.f, 0.f, 0.f}, vx = kx;
-      if (t0 + t < a.n) {
-        const v4f *row = reinterpret_cast<const v4f *>(a.qkv + (size_t)(t0 + t) * a.stride);
-        kx = row[(a.dim + h * HD) / 4 + c4] + reinterpret_cast<const v4f *>(bk)[c4];
-        vx = row[(2 * a.dim + h * HD) / 4 + c4] + reinterpret_cast<const v4f *>(bv)[c4];
-      }
+  // padding dims of V^T (never overwritten by the staging below)
+  for (int i = HD * VS + tid; i < 16 * NB * VS; i += kNT) vt[i] = 0.0;
+  exp_tab_load(etab);
+  for (int i = tid; i < 2 * C4; i += kNT)
+    kvb[i / C4][i % C4] = reinterpret_cast<const v4f *>(i < C4 ? bk : bv)[i % C4];
+  const ExpConsts ec = exp_consts();
+
+  v4f kx[PF], vx[PF];
+  auto fetch = [&](int t0) {  // rows clamped into range: every load is unconditional
 #pragma unroll
-      for (int e = 0; e < 4; ++e) kt[t * RK + 4 * c4 + e] = kx[e];
-      *reinterpret_cast<v4f *>(&vt[t * VS + 4 * c4]) = vx;
+    for (int j = 0; j < PF; ++j) {
+      const int i = min(tid + j * kNT, kVaKeys * C4 - 1);
+      const int t = i / C4, c4 = i - t * C4;
+      const size_t row = (size_t)min(t0 + t, a.n - 1) * a.stride;
+      kx[j] = *reinterpret_cast<const v4f *>(kbase + row + 4 * c4);
+      vx[j] = *reinterpret_cast<const v4f *>(vbase + row + 4 * c4);
     }
-    if (16 * NB > HD)  // zero the padding columns of V (read by the last output block)
-      for (int i = tid; i < kVaKeys * (16 * NB - HD); i += kNT) {
-        const int t = i / (16 * NB - HD), c = i - t * (16 * NB - HD);
-        vt[t * VS + HD + c] = 0.0f;
-      }
+  };
+  fetch(0);
+  for (int t0 = 0; t0 < a.n; t0 += kVaKeys) {
+    lds_barrier();  // every wave is done with the previous tile
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * kNT;
+      if (i >= kVaKeys * C4) break;
+      const int t = i / C4, c4 = i - t * C4;
+      const bool ok = t0 + t < a.n;
+      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+      const v4f kv = ok ? kx[j] + kvb[0][c4] : zero;
+      const v4f vv = ok ? vx[j] + kvb[1][c4] : zero;
+      *reinterpret_cast<v2d *>(&kt[t * RK + 4 * c4]) = v2d{(double)kv[0], (double)kv[1]};
+      *reinterpret_cast<v2d *>(&kt[t * RK + 4 * c4 + 2]) = v2d{(double)kv[2], (double)kv[3]};
+      const int tp = (t & 16) | ((t & 3) << 2) | ((t >> 2) & 3);  // key 16b+4s+g -> 16b+4g+s
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + tp] = (double)vv[e];
+    }
     lds_barrier();
-    // scores: block b covers keys t0 + 16 b + col
+    if (t0 + kVaKeys < a.n) fetch(t0 + kVaKeys);
+
+    // scores: sc[b][r] = q(col) . k(t0 + 16 b + 4 r + grp)
     v4d sc[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       sc[b] = v4d{0.0, 0.0, 0.0, 0.0};
+      const double *kr = &kt[(16 * b + col) * RK + grp * KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        sc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(
-            qa[s], (double)kt[(16 * b + col) * RK + 4 * s + grp], sc[b], 0, 0, 0);
+      for (int s = 0; s < KS; s += 2) {
+        const v2d k2 = *reinterpret_cast<const v2d *>(kr + s);
+        sc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(k2[0], qa[s], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f64_16x16x4f64(k2[1], qa[s + 1], sc[b], 0, 0, 0);
+      }
     }
-    // online softmax on rows 4r + grp (the 16 lanes of this DPP row)
-    double alpha[4];
+    double tmax = -DBL_MAX;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      double s0 = t0 + col < a.n ? sc[0][r] * (double)a.scale : -DBL_MAX;
-      double s1 = t0 + 16 + col < a.n ? sc[1][r] * (double)a.scale : -DBL_MAX;
-      double m = fmax(s0, s1);
-      m = fmax(m, dpp_f64<kDppXor1>(m));
-      m = fmax(m, dpp_f64<kDppXor2>(m));
-      m = fmax(m, dpp_f64<kDppHalfMirror>(m));
-      m = fmax(m, dpp_f64<kDppMirror>(m));
-      const double m_new = fmax(run_m[r], m);
-      const double p0 = s0 == -DBL_MAX ? 0.0 : exp(s0 - m_new);
-      const double p1 = s1 == -DBL_MAX ? 0.0 : exp(s1 - m_new);
-      double l = p0 + p1;
-      l += dpp_f64<kDppXor1>(l);
-      l += dpp_f64<kDppXor2>(l);
-      l += dpp_f64<kDppHalfMirror>(l);
-      l += dpp_f64<kDppMirror>(l);
-      alpha[r] = exp(run_m[r] - m_new);
-      run_l[r] = run_l[r] * alpha[r] + l;
-      run_m[r] = m_new;
-      pw[wave][(4 * r + grp) * RP + col] = p0;
-      pw[wave][(4 * r + grp) * RP + 16 + col] = p1;
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = t0 + 16 * b + 4 * r + grp < a.n;
+        sc[b][r] = ok ? sc[b][r] * scale : -DBL_MAX;
+        tmax = fmax(tmax, sc[b][r]);
+      }
+    if (__any(tmax > m_ref + kVaSlack)) {
+      double rmax = fmax(tmax, __shfl_xor(tmax, 16, 64));
+      rmax = fmax(rmax, __shfl_xor(rmax, 32, 64));
+      const double m_new = fmax(m_ref, rmax);
+      const double alpha = exp_tab(m_ref - m_new, etab, ec);
+      m_ref = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
     }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        // a masked key (-DBL_MAX) lands on exp_tab's clamp and gives 0
+        const double pr = exp_tab(sc[b][r] - m_ref, etab, ec);
+        l_part += pr;
+        sc[b][r] = pr;
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const double *vr = &vt[(16 * nb + col) * VS + 16 * b + 4 * grp];
+        const v2d v01 = *reinterpret_cast<const v2d *>(vr);
+        const v2d v23 = *reinterpret_cast<const v2d *>(vr + 2);
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(v01[0], sc[b][0], o[nb], 0, 0, 0);
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(v01[1], sc[b][1], o[nb], 0, 0, 0);
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(v23[0], sc[b][2], o[nb], 0, 0, 0);
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(v23[1], sc[b][3], o[nb], 0, 0, 0);
+      }
+    }
+  }
+  double l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  const int qr = q0 + col;
+  if (qr < a.n) {
+    float *orow = a.out + (size_t)qr * a.dim + h * HD;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) o[nb][r] *= alpha[r];
-    lds_barrier();  // P is read back in the A layout
-#pragma unroll
-    for (int s = 0; s < kVaKeys / 4; ++s) {
-      const double pa = pw[wave][col * RP + 4 * s + grp];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(
-            pa, (double)vt[(4 * s + grp) * VS + 16 * nb + col], o[nb], 0, 0, 0);
-    }
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int qr = q0 + 4 * r + grp;
-    if (qr >= a.n) continue;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int d = 16 * nb + col;
-      if (d < HD) a.out[(size_t)qr * a.dim + h * HD + d] = (float)(o[nb][r] / run_l[r]);
-    }
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * nb + 4 * r + grp;
+        if (d < HD) orow[d] = (float)(o[nb][r] / l);
+      }
   }
 }
 
@@ -408,7 +449,7 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
 }
 
 hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream) {
-  const dim3 grid((a.n + 63) / 64, a.n_heads);
+  const dim3 grid((a.n + 63) / 64 * a.n_heads);
   switch (hdim) {
     case 16: vis_attn_kernel<16><<<grid, kNT, 0, stream>>>(a); break;
     case 32: vis_attn_kernel<32><<<grid, kNT, 0, stream>>>(a); break;
