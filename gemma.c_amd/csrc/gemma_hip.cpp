@@ -835,6 +835,7 @@ struct gemma_hip_decoder {
   float *pf_as = nullptr;
   int8_t *pf_a8 = nullptr;
   int *pf_tok = nullptr;
+  double *pf_part = nullptr;  // attention key-split partials
 };
 
 namespace {
@@ -862,7 +863,8 @@ int prefill_reserve(gemma_hip_decoder *d, int n) {
   const size_t o_x = cv.take(rows * dim * 4), o_y = cv.take(rows * dim * 4),
                o_qkv = cv.take(rows * (q_sz + 2 * kv_sz) * 4), o_xo = cv.take(rows * q_sz * 4),
                o_g = cv.take(rows * 2 * mlp * 4), o_a8 = cv.take(rows * kmax),
-               o_as = cv.take(rows * 4), o_tok = cv.take(rows * 4);
+               o_as = cv.take(rows * 4), o_tok = cv.take(rows * 4),
+               o_part = cv.take(gh::pf_attn_part_doubles(rows, c.n_heads, c.hdim) * 8);
   if (d->pf_mem != nullptr) {
     (void)hipStreamSynchronize(g.stream);
     (void)hipFree(d->pf_mem);
@@ -880,6 +882,7 @@ int prefill_reserve(gemma_hip_decoder *d, int n) {
   d->pf_a8 = (int8_t *)(m + o_a8);
   d->pf_as = (float *)(m + o_as);
   d->pf_tok = (int *)(m + o_tok);
+  d->pf_part = (double *)(m + o_part);
   d->pf_rows = n;
   return 0;
 }
@@ -921,7 +924,7 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st)
     if ((e = gh::launch_pf_qk_rope(rp, n, c.hdim, st)) != hipSuccess) return e;
     const gh::PfAttn at{d->pf_qkv, stride, kc, kc + cache, d->pf_xo, q_sz, n, pos, c.n_heads,
                         c.nkv, d->clen, sliding ? c.slide : 0,
-                        (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att};
+                        (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0};
     if ((e = gh::launch_pf_attention(at, c.hdim, st)) != hipSuccess) return e;
     // o projection
     if ((e = gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st)) !=

@@ -153,7 +153,17 @@ struct PfAttn {
   float *xo;
   int q_sz, n, pos0, n_heads, nkv, clen, slide;
   float asc, sc_att;
+  // key-range split: fp64 partials [kPfMaxSplit][n][q_sz] (unnormalized
+  // value sums) then [kPfMaxSplit][n][n_heads][2] (reference max, sum);
+  // chunk and nsplit are set by launch_pf_attention
+  double *part;
+  int chunk, nsplit;
 };
+constexpr int kPfMaxSplit = 8;
+// doubles of PfAttn::part for n rows
+inline size_t pf_attn_part_doubles(size_t n, size_t n_heads, size_t hdim) {
+  return (size_t)kPfMaxSplit * n * n_heads * (hdim + 2);
+}
 // float4 chunks per thread of the row kernels: dim <= 6144 (256 threads),
 // mlp <= 24576 (1024 threads)
 constexpr int kPfMaxNpt = 6;
@@ -161,7 +171,8 @@ hipError_t launch_pf_embed(const int *tokens, int n, const int8_t *emb_q, const 
                            float *x, int dim, float esc, hipStream_t stream);
 hipError_t launch_pf_norm_rows(const PfNorm &a, int n, hipStream_t stream);
 hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t stream);
-// hdim 128 or 256; the q heads per kv head must divide 32
+// hdim 128 or 256; the q heads per kv head must divide 32; a.part must hold
+// pf_attn_part_doubles(n, n_heads, hdim) doubles
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream);
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
                                 hipStream_t stream);

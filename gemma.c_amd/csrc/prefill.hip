@@ -26,6 +26,7 @@
 // both is the fp64 decode oracle.  The reference's own prefill evaluates its
 // attention in fp32 with a different order (blockwise gemm_fpx, softmax,
 // gemm_fpx_nn), which no fp32 bit pattern here could follow anyway.
+#include <algorithm>
 #include <type_traits>
 
 #include "dec_common.h"
@@ -113,177 +114,439 @@ __global__ __launch_bounds__(64) void pf_qk_rope_kernel(PfRope a) {
   }
 }
 
-// Causal attention of the prompt rows (gemma.c:5152-5293).  A workgroup takes
-// one kv head and QB = 32 / hn consecutive rows, i.e. the 32 query vectors of
-// its hn q heads at those rows, and walks the cached keys from the first
-// row's window start to the last row's position in tiles of kPfKeys; each
-// K/V tile is loaded once into LDS for all 32 queries.  Scores, masks, the
-// running max and sum and the value sums are fp64 (an online softmax: on a
-// new max the partial sums are rescaled by exp(m_old - m_new)); each output
-// element is rounded to fp32 once at the end.
+// Causal attention of the prompt rows (gemma.c:5152-5293) on the fp64
+// matrix cores, in the form of the vision tower's attention (vision.hip):
+// v_mfma_f64_16x16x4f64 (lane l: A[l%16][l/16], B[l/16][l%16], result r ->
+// D[4r + l/16][l%16]) on the transposed products S^T = K . Q^T and
+// O^T = V^T . P^T, so the probabilities a lane computes (query l%16, keys
+// 4r + l/16 of a 16-key block) are the operand of the value product as they
+// stand.
 //
-// Scores: thread (c, qg, kg) = (tid & 3, (tid >> 2) & 7, tid >> 5) sums
-// quarter c of the head dimension for queries 4qg..4qg+3 and keys 2kg,
-// 2kg+1 (8 products per 6 LDS vector reads), then the four quarters are
-// added across lanes.  LDS rows are padded so that the 32 (qg, c) and 8
-// (kg, c) addresses of one read fall in distinct 16-byte bank groups as far
-// as 64 banks allow.
-constexpr int kPfQ = 32;     // query vectors per workgroup
-constexpr int kPfKeys = 16;  // keys per tile
+// A workgroup is one kv head and 64 query vectors -- its hn q heads at
+// qb = 64 / hn consecutive rows -- as 4 waves x 16; each wave holds its
+// queries as fp64 operands (lane l/16 holds dims [l/16 HD/4, (l/16+1) HD/4)).
+// It walks the cached keys from the first row's window start to the last
+// row's position in tiles of 32, staged in LDS (fp32; V transposed with each
+// 16-key block's keys permuted so that one MFMA step's 4 values are
+// adjacent) with the next tile's loads in flight during the current one.  A
+// wave skips the tiles that lie wholly outside its own rows' windows;
+// per key the mask is the reference's: key <= position and, on sliding
+// layers, key > position - window.  Scores are scaled (and soft-capped) in
+// fp64; the softmax shifts by a per-query reference maximum that only moves,
+// rescaling O and the partial sums by exp(m_old - m_new), when a score
+// exceeds it by more than kPaSlack (the softmax is shift-invariant).  The
+// reference maximum starts at kPaFloor, far below any score and far above
+// -DBL_MAX, so a masked score (-DBL_MAX) gives exp = 0 even before a query
+// has seen its first key.  Every sum is fp64; each output is rounded to
+// fp32 once.
+constexpr int kPaQ = 64;              // query vectors per workgroup
+constexpr int kPfMaxMergeHeads = 64;  // q heads the merge handles
+constexpr int kPaKeys = 32;           // keys per tile (register-staged kernel)
+constexpr double kPaSlack = 64.0;     // p <= e^64: sums stay far below DBL_MAX
+constexpr double kPaFloor = -1e300;   // |score| <= 256 * FLT_MAX^2 << 1e300
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+// What a lane of a prefill attention workgroup works on: the block's
+// (kv head, row block, key chunk) and the lane's query vector.
+struct PaLane {
+  int hk, r0, rows, chunk_id, nchunks, k_lo, k_end;  // block
+  int row, head, p_abs, ws, p_top;                    // lane
+  bool valid;
+  int w_lo, w_hi;  // the keys any query of the wave can see
+  bool empty;      // no chunk for this block
+};
+
+__device__ __forceinline__ int pa_window_start(const PfAttn &a, int p_abs) {
+  return (a.slide > 0 && p_abs >= a.slide) ? p_abs + 1 - a.slide : 0;
+}
+
+// block = ((row block from the last) * nsplit + chunk) * nkv + kv head: the
+// longest rows first, and with nkv dividing 8 each XCD (blocks b, b+8, ...)
+// sees one kv head.  A chunk is chunk_id's run of a.chunk keys of the row
+// block's key range (its first row's window start, rounded down to 32, to
+// its last row's position).
+__device__ __forceinline__ PaLane pa_lane(const PfAttn &a, int wave, int col) {
+  PaLane L;
+  const int hn = a.n_heads / a.nkv, qb = kPaQ / hn;
+  const int nrb = (a.n + qb - 1) / qb;
+  L.hk = blockIdx.x % a.nkv;
+  L.chunk_id = (blockIdx.x / a.nkv) % a.nsplit;
+  L.r0 = (nrb - 1 - blockIdx.x / a.nkv / a.nsplit) * qb;
+  L.rows = min(qb, a.n - L.r0);
+  const int p_last = a.pos0 + L.r0 + L.rows - 1;
+  const int k_base = pa_window_start(a, a.pos0 + L.r0) / kPaKeys * kPaKeys;
+  L.nchunks = (p_last - k_base + a.chunk) / a.chunk;
+  L.empty = L.chunk_id >= L.nchunks;
+  L.k_lo = k_base + L.chunk_id * a.chunk;
+  L.k_end = min(L.k_lo + a.chunk - 1, p_last);
+  const int v = 16 * wave + col;
+  L.valid = v % qb < L.rows;
+  L.row = L.r0 + min(v % qb, L.rows - 1);
+  L.head = L.hk * hn + v / qb;
+  L.p_abs = L.valid ? a.pos0 + L.row : -1;  // -1: every key masked
+  L.ws = pa_window_start(a, max(L.p_abs, 0));
+  L.p_top = min(L.p_abs, L.k_end);  // the last key of this chunk the query sees
+  int hi = L.p_top, lo = L.valid ? L.ws : INT_MAX;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    hi = max(hi, __shfl_xor(hi, off, 64));
+    lo = min(lo, __shfl_xor(lo, off, 64));
+  }
+  L.w_hi = __builtin_amdgcn_readfirstlane(hi);
+  L.w_lo = __builtin_amdgcn_readfirstlane(lo);
+  return L;
+}
+
+// Scale, soft-cap and mask the scores of keys key0 + 4r + l/16 (r = 0..3),
+// move the reference maximum when the wave needs it, and turn the scores
+// into weights: p = e^(s - m).
+template <int NB, int NS>
+__device__ __forceinline__ void pa_softmax(const PfAttn &a, const PaLane &L, v4d (&sc)[NS],
+                                           int key0, int grp, double &m_ref, double &l_part,
+                                           v4d (&o)[NB], const double *etab,
+                                           const ExpConsts &ec) {
+  const double asc = (double)a.asc, cap = (double)a.sc_att;
+  double tmax = -DBL_MAX;
+#pragma unroll
+  for (int b = 0; b < NS; ++b)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = key0 + 16 * b + 4 * r + grp;
+      double x = sc[b][r] * asc;
+      if (a.sc_att != 0.0f) x = tanh(x / cap) * cap;
+      sc[b][r] = (key <= L.p_top && key >= L.ws) ? x : -DBL_MAX;
+      tmax = fmax(tmax, sc[b][r]);
+    }
+  if (__any(tmax > m_ref + kPaSlack)) {
+    double rmax = fmax(tmax, __shfl_xor(tmax, 16, 64));
+    rmax = fmax(rmax, __shfl_xor(rmax, 32, 64));
+    const double m_new = fmax(m_ref, rmax);
+    const double alpha = exp_tab(m_ref - m_new, etab, ec);
+    m_ref = m_new;
+    l_part *= alpha;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
+  }
+#pragma unroll
+  for (int b = 0; b < NS; ++b)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sc[b][r] = exp_tab(sc[b][r] - m_ref, etab, ec);
+      l_part += sc[b][r];
+    }
+}
+
+// The lane's outputs O^T[16 nb + 4 r + l/16][query]: normalized into xo when
+// the row block took one chunk, else the chunk's partial for
+// pf_attn_merge_kernel.
+template <int HD, int NB>
+__device__ __forceinline__ void pa_store(const PfAttn &a, const PaLane &L, const v4d (&o)[NB],
+                                         double m_ref, double l_part, int grp) {
+  double l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  if (!L.valid) return;
+  if (L.nchunks == 1) {
+    float *orow = a.xo + (size_t)L.row * a.q_sz + L.head * HD;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) orow[16 * nb + 4 * r + grp] = (float)(o[nb][r] / l);
+    return;
+  }
+  const size_t at = (size_t)L.chunk_id * a.n + L.row;
+  double *prow = a.part + at * a.q_sz + L.head * HD;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) prow[16 * nb + 4 * r + grp] = o[nb][r];
+  if (grp == 0) {
+    double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
+    ml[0] = m_ref;
+    ml[1] = l;
+  }
+}
+
+// HD 128.  K/V tiles of 32 keys staged through registers (the next tile's
+// loads in flight during the current one), V transposed with each 16-key
+// block's keys permuted so that one MFMA step's 4 values are adjacent; the
+// queries are fp64 registers.
+template <int HD>
+__global__ __launch_bounds__(kNT, 2) void pf_attn_kernel(PfAttn a) {
+  constexpr int KS = HD / 4;              // score MFMA steps (dims per lane)
+  constexpr int NB = HD / 16;             // 16-dim output blocks
+  constexpr int RK = HD + 4;              // K row in LDS (floats)
+  constexpr int VS = kPaKeys + 4;         // V^T row in LDS (floats)
+  constexpr int C4 = HD / 4;              // float4 per key row
+  constexpr int PF = kPaKeys * C4 / kNT;  // float4 of K (and of V) per thread
+  static_assert(PF * kNT == kPaKeys * C4, "tile staging");
+  __shared__ float kt[kPaKeys * RK];
+  __shared__ float vt[HD * VS];
+  __shared__ double etab[128];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const PaLane L = pa_lane(a, wave, col);
+  if (L.empty) return;  // the whole block: before any barrier
+  double qa[KS];
+  {
+    const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + grp * KS;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qa[s] = (double)qrow[s];
+  }
+  v4d o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4d{0.0, 0.0, 0.0, 0.0};
+  double m_ref = kPaFloor, l_part = 0.0;
+  const float *kc = a.kc + (size_t)L.hk * a.clen * HD;
+  const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
+  exp_tab_load(etab);
+  const ExpConsts ec = exp_consts();
+
+  v4f kx[PF], vx[PF];
+  auto fetch = [&](int t0) {  // rows clamped to the chunk's last key: loads are unconditional
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * kNT;
+      const int t = i / C4, c4 = i - t * C4;
+      const size_t at = (size_t)min(t0 + t, L.k_end) * HD + 4 * c4;
+      kx[j] = *reinterpret_cast<const v4f *>(kc + at);
+      vx[j] = *reinterpret_cast<const v4f *>(vc + at);
+    }
+  };
+  fetch(L.k_lo);
+  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += kPaKeys) {
+    lds_barrier();  // every wave is done with the previous tile
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * kNT;
+      const int t = i / C4, c4 = i - t * C4;
+      const bool ok = t0 + t <= L.k_end;  // later keys: another chunk's, or not in the cache yet
+      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<v4f *>(&kt[t * RK + 4 * c4]) = ok ? kx[j] : zero;
+      const v4f vv = ok ? vx[j] : zero;
+      const int tp = (t & 16) | ((t & 3) << 2) | ((t >> 2) & 3);  // key 16b+4s+g -> 16b+4g+s
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + tp] = vv[e];
+    }
+    lds_barrier();
+    if (t0 + kPaKeys <= L.k_end) fetch(t0 + kPaKeys);
+
+    if (t0 > L.w_hi || t0 + kPaKeys - 1 < L.w_lo) continue;  // wave-uniform
+    // scores of both 16-key blocks, two independent MFMA chains
+    v4d sc[2] = {v4d{0.0, 0.0, 0.0, 0.0}, v4d{0.0, 0.0, 0.0, 0.0}};
+#pragma unroll
+    for (int s = 0; s < KS; s += 4) {
+      const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
+      const v4f k1 = *reinterpret_cast<const v4f *>(&kt[(16 + col) * RK + grp * KS + s]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k0[e], qa[s + e], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k1[e], qa[s + e], sc[1], 0, 0, 0);
+      }
+    }
+    pa_softmax<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o, etab, ec);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const v4f v0 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 4 * grp]);
+      const v4f v1 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 16 + 4 * grp]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)v0[r], sc[0][r], o[nb], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)v1[r], sc[1][r], o[nb], 0, 0, 0);
+    }
+  }
+  pa_store<HD, NB>(a, L, o, m_ref, l_part, grp);
+}
+
+// HD 256.  The 64 fp64 output accumulators and the 64 fp64 query operands
+// per lane need one wave per SIMD (512 registers, no spills), so latency is
+// hidden inside the wave: K/V tiles of 32 keys go from the cache into LDS by
+// the LDS DMA loads (one key row of 1 KB is one wave's load of 64 x 16 bytes;
+// lane l's bytes land at 16 l), double-buffered -- the next tile loads
+// while the current one is computed, staging takes no registers, and there
+// is one barrier per tile.  V stays row-major: one MFMA step reads the 4
+// keys' values with 4 LDS reads whose rows sit 16 banks apart.
+// One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
+// wave-uniform).  Issued from inline asm so that the compiler does not treat
+// every later LDS read as a possible alias of the pending load (it would
+// wait for the load before each of them); the kernel waits itself (vmcnt(0)
+// and a barrier) before it reads the buffer.  m0 has no other user in the
+// kernel that calls this.
+__device__ __forceinline__ void lds_dma16(const float *g, float *lds) {
+  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)lds;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
 
 template <int HD>
-__global__ __launch_bounds__(kNT) void pf_attn_kernel(PfAttn a) {
-  constexpr int QQ = HD / 4 + 4;       // one padded quarter of a row
-  constexpr int KS = 4 * QQ;           // K row
-  constexpr int QS = 4 * QQ + 4;       // q row
-  constexpr int PS = kPfQ + 2;         // probabilities row (one key)
-  constexpr int QPT = kPfQ * HD / kNT; // query vectors per thread in the value sums
-  __shared__ __attribute__((aligned(16))) float qs[kPfQ * QS];
-  __shared__ __attribute__((aligned(16))) float kt[kPfKeys * KS];
-  __shared__ float vt[kPfKeys][HD];
-  __shared__ __attribute__((aligned(16))) double pp[kPfKeys * PS];
-  __shared__ double alpha[kPfQ], run_m[kPfQ], run_l[kPfQ];
+__global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
+  static_assert(HD == 256, "one key row is one wave's 64 x 16-byte LDS load");
+  constexpr int KS = HD / 4, NB = HD / 16;
+  constexpr int TK = kPaKeys;  // keys per tile
+  constexpr int RK = HD + 4;   // K row (floats): rows 16 bytes apart in the banks
+  constexpr int RV = HD + 16;  // V row (floats): rows 16 banks apart
+  // the K/V double buffers; after the last tile the same memory stages the
+  // outputs (16 query rows of HD + 4 doubles per wave)
+  constexpr int KB = 2 * TK * RK * 4, VB = 2 * TK * RV * 4;
+  constexpr int RO = HD + 4;
+  static_assert(kWaves * 16 * RO * 8 <= KB + VB, "output staging");
+  __shared__ __attribute__((aligned(16))) char smem[KB + VB];
+  float(*kt)[TK * RK] = reinterpret_cast<float(*)[TK * RK]>(smem);
+  float(*vt)[TK * RV] = reinterpret_cast<float(*)[TK * RV]>(smem + KB);
+  __shared__ double etab[128];
 
-  const int tid = threadIdx.x;
-  const int hn = a.n_heads / a.nkv;
-  const int qb = kPfQ / hn;                 // rows per workgroup
-  const int hk = blockIdx.y;
-  // the longest rows (most keys) first
-  const int r0 = (gridDim.x - 1 - blockIdx.x) * qb;
-  const int rows = min(qb, a.n - r0);
-  // query vector v: head h0 + v / qb, row r0 + v % qb
-  auto q_row = [&](int v) { return r0 + v % qb; };
-  auto q_head = [&](int v) { return hk * hn + v / qb; };
-  auto window_start = [&](int p_abs) {
-    return (a.slide > 0 && p_abs >= a.slide) ? p_abs + 1 - a.slide : 0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const PaLane L = pa_lane(a, wave, col);
+  if (L.empty) return;  // the whole block: before any barrier
+  double qa[KS];
+  {
+    const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + grp * KS;
+#pragma unroll
+    for (int s = 0; s < KS; s += 4) {
+      const v4f q4 = *reinterpret_cast<const v4f *>(qrow + s);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qa[s + e] = (double)q4[e];
+    }
+  }
+  v4d o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4d{0.0, 0.0, 0.0, 0.0};
+  double m_ref = kPaFloor, l_part = 0.0;
+  const float *kc = a.kc + (size_t)L.hk * a.clen * HD;
+  const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
+  exp_tab_load(etab);
+  const ExpConsts ec = exp_consts();
+
+  // wave w loads key rows w, w+4, ... of the tile at t0 (rows past the
+  // chunk's last key repeat it; their weights are 0)
+  auto issue = [&](int t0, int bi) {
+#pragma unroll
+    for (int j = 0; j < TK / kWaves; ++j) {
+      const int t = wave + kWaves * j;
+      const size_t at = (size_t)min(t0 + t, L.k_end) * HD + 4 * lane;
+      lds_dma16(kc + at, &kt[bi][t * RK]);
+      lds_dma16(vc + at, &vt[bi][t * RV]);
+    }
   };
-
-  for (int i = tid; i < kPfQ * HD / 4; i += kNT) {
-    const int v = i / (HD / 4), c4 = i - v * (HD / 4);  // 4 floats at d = 4 c4
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const v4f x = v % qb < rows ? reinterpret_cast<const v4f *>(
-                                      a.qkv + (size_t)q_row(v) * a.stride + q_head(v) * HD)[c4]
-                                : zero;
-    const int d = 4 * c4;
-    *reinterpret_cast<v4f *>(&qs[v * QS + (d / (HD / 4)) * QQ + d % (HD / 4)]) = x;
-  }
-  if (tid < kPfQ) {
-    run_m[tid] = -DBL_MAX;
-    run_l[tid] = 0.0;
-  }
-  const int p_first = a.pos0 + r0, p_last = a.pos0 + r0 + rows - 1;
-  const int k_lo = window_start(p_first) / kPfKeys * kPfKeys;
-  const float *kc = a.kc + (size_t)hk * a.clen * HD;
-  const float *vc = a.vc + (size_t)hk * a.clen * HD;
-
-  double acc[QPT];
+  issue(L.k_lo, 0);
+  int bi = 0;
+  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += TK, bi ^= 1) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's rows of the tile have landed
+    lds_barrier();  // every wave's rows have landed, and the previous tile is done
+    if (t0 + TK <= L.k_end) issue(t0 + TK, bi ^ 1);
+    if (t0 > L.w_hi || t0 + TK - 1 < L.w_lo) continue;  // wave-uniform
+    const float *kb = &kt[bi][0];
+    const float *vb = &vt[bi][0];
+    // scores of both 16-key blocks in four independent MFMA chains (even
+    // and odd steps of each block, added at the end), so that consecutive
+    // MFMAs do not wait for one another
+    v4d sc[2], sx[2];
 #pragma unroll
-  for (int u = 0; u < QPT; ++u) acc[u] = 0.0;
-  const int d_own = tid % HD;           // this thread's dimension in the value sums
-  const int v_own = (tid / HD) * QPT;   // and its first query vector
-  const int sc_c = tid & 3, sc_qg = (tid >> 2) & 7, sc_kg = tid >> 5;
-
-  for (int t0 = k_lo; t0 <= p_last; t0 += kPfKeys) {
-    lds_barrier();  // the previous tile's K, V and p are no longer read
-    for (int i = tid; i < kPfKeys * HD / 4; i += kNT) {
-      const int t = i / (HD / 4), c4 = i - t * (HD / 4);
-      const int kp = t0 + t;
-      const v4f zero = {0.f, 0.f, 0.f, 0.f};
-      const v4f kv4 = kp <= p_last ? reinterpret_cast<const v4f *>(kc + (size_t)kp * HD)[c4]
-                                   : zero;
-      const v4f vv4 = kp <= p_last ? reinterpret_cast<const v4f *>(vc + (size_t)kp * HD)[c4]
-                                   : zero;
-      const int d = 4 * c4;
-      *reinterpret_cast<v4f *>(&kt[t * KS + (d / (HD / 4)) * QQ + d % (HD / 4)]) = kv4;
-      *reinterpret_cast<v4f *>(&vt[t][d]) = vv4;
-    }
-    lds_barrier();
-    {
-      const float *qb4 = &qs[(4 * sc_qg) * QS + sc_c * QQ];
-      const float *kb2 = &kt[(2 * sc_kg) * KS + sc_c * QQ];
-      double s[4][2];
+    for (int b = 0; b < 2; ++b) sc[b] = sx[b] = v4d{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s[j][0] = s[j][1] = 0.0;
-#pragma unroll 4
-      for (int i = 0; i < HD / 4; i += 4) {
-        const v4f k0 = *reinterpret_cast<const v4f *>(kb2 + i);
-        const v4f k1 = *reinterpret_cast<const v4f *>(kb2 + KS + i);
+    for (int s = 0; s < KS; s += 4) {
+      const v4f k0 = *reinterpret_cast<const v4f *>(&kb[col * RK + grp * KS + s]);
+      const v4f k1 = *reinterpret_cast<const v4f *>(&kb[(16 + col) * RK + grp * KS + s]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v4f q = *reinterpret_cast<const v4f *>(qb4 + j * QS + i);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s[j][0] = fma((double)q[e], (double)k0[e], s[j][0]);
-            s[j][1] = fma((double)q[e], (double)k1[e], s[j][1]);
-          }
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          double part = s[j][kk];
-          part += dpp_f64<kDppXor1>(part);
-          part += dpp_f64<kDppXor2>(part);
-          const int v = 4 * sc_qg + j, t = 2 * sc_kg + kk;
-          if (sc_c == 0) {
-            const int p_abs = a.pos0 + q_row(v);
-            const int kp = t0 + t;
-            const bool live = v % qb < rows && kp <= p_abs && kp >= window_start(p_abs);
-            double sc = part * (double)a.asc;
-            if (a.sc_att != 0.0f) sc = tanh(sc / (double)a.sc_att) * (double)a.sc_att;
-            pp[t * PS + v] = live ? sc : -DBL_MAX;
-          }
-        }
-    }
-    lds_barrier();
-    // online softmax: 16 lanes (one DPP row) per query vector, lane t = key t
-    for (int v = tid / kPfKeys; v < kPfQ; v += kNT / kPfKeys) {
-      const int t = tid % kPfKeys;
-      const double sv = pp[t * PS + v];
-      double m = sv;
-      m = fmax(m, dpp_f64<kDppXor1>(m));
-      m = fmax(m, dpp_f64<kDppXor2>(m));
-      m = fmax(m, dpp_f64<kDppHalfMirror>(m));
-      m = fmax(m, dpp_f64<kDppMirror>(m));
-      const double m_old = run_m[v];
-      const double m_new = fmax(m_old, m);
-      const double e = sv == -DBL_MAX ? 0.0 : exp(sv - m_new);
-      double l = e;
-      l += dpp_f64<kDppXor1>(l);
-      l += dpp_f64<kDppXor2>(l);
-      l += dpp_f64<kDppHalfMirror>(l);
-      l += dpp_f64<kDppMirror>(l);
-      pp[t * PS + v] = e;
-      if (t == 0) {
-        const double al = exp(m_old - m_new);
-        alpha[v] = al;
-        run_l[v] = run_l[v] * al + l;
-        run_m[v] = m_new;
+      for (int e = 0; e < 4; e += 2) {
+        sc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k0[e], qa[s + e], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k1[e], qa[s + e], sc[1], 0, 0, 0);
+        sx[0] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k0[e + 1], qa[s + e + 1], sx[0], 0, 0, 0);
+        sx[1] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k1[e + 1], qa[s + e + 1], sx[1], 0, 0, 0);
       }
     }
-    lds_barrier();
-    // value sums: thread (d, queries v_own .. v_own + QPT - 1); the key's
-    // probabilities of two queries are one 16-byte broadcast read
 #pragma unroll
-    for (int u = 0; u < QPT; ++u) acc[u] *= alpha[v_own + u];
-#pragma unroll 4
-    for (int t = 0; t < kPfKeys; ++t) {
-      const double vv = (double)vt[t][d_own];
-      const double *pt = &pp[t * PS + v_own];
+    for (int b = 0; b < 2; ++b) sc[b] += sx[b];
+    pa_softmax<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o, etab, ec);
+    // value sums: consecutive MFMAs go to different output blocks
 #pragma unroll
-      for (int u = 0; u < QPT; u += 2) {
-        const double2 pr = *reinterpret_cast<const double2 *>(pt + u);
-        acc[u] = fma(pr.x, vv, acc[u]);
-        acc[u + 1] = fma(pr.y, vv, acc[u + 1]);
-      }
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+              (double)vb[(16 * b + 4 * r + grp) * RV + 16 * nb + col], sc[b][r], o[nb], 0, 0, 0);
+  }
+  // outputs through LDS, so that each query row leaves as one contiguous store
+  double l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  lds_barrier();  // every wave is done with the K/V buffers
+  double *ow = reinterpret_cast<double *>(smem) + wave * 16 * RO;
+  const bool whole = L.nchunks == 1;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      ow[col * RO + 16 * nb + 4 * r + grp] = whole ? o[nb][r] / l : o[nb][r];
+  if (!whole && grp == 0 && L.valid) {
+    const size_t at = (size_t)L.chunk_id * a.n + L.row;
+    double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
+    ml[0] = m_ref;
+    ml[1] = l;
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's rows are in LDS
+  __builtin_amdgcn_wave_barrier();
+  const int hn = a.n_heads / a.nkv, qb = kPaQ / hn;
+  for (int q = 0; q < 16; ++q) {
+    const int v = 16 * wave + q;
+    if (v % qb >= L.rows) continue;  // wave-uniform
+    const int row = L.r0 + v % qb, head = L.hk * hn + v / qb;
+    const double *src = ow + q * RO + 4 * lane;
+    if (whole) {
+      const v4f out = {(float)src[0], (float)src[1], (float)src[2], (float)src[3]};
+      *reinterpret_cast<v4f *>(a.xo + (size_t)row * a.q_sz + head * HD + 4 * lane) = out;
+    } else {
+      double *dst = a.part + ((size_t)L.chunk_id * a.n + row) * a.q_sz + head * HD + 4 * lane;
+      *reinterpret_cast<double2 *>(dst) = double2{src[0], src[1]};
+      *reinterpret_cast<double2 *>(dst + 2) = double2{src[2], src[3]};
     }
   }
-#pragma unroll
-  for (int u = 0; u < QPT; ++u) {
-    const int v = v_own + u;
-    if (v % qb < rows)
-      a.xo[(size_t)q_row(v) * a.q_sz + q_head(v) * HD + d_own] = (float)(acc[u] / run_l[v]);
+}
+
+// The chunks' partials of one row (a workgroup per row): with M the largest
+// reference maximum, out = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c in
+// fp64, rounded once.  A chunk in which a query saw no key has l = 0, O = 0
+// and m = kPaFloor, so it adds nothing.  Rows whose row block took a single
+// chunk were written by the attention kernel.
+__global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) {
+  __shared__ double wt[kPfMaxMergeHeads][kPfMaxSplit + 1];  // weights, then 1 / denominator
+  const int row = blockIdx.x;
+  const int hn = a.n_heads / a.nkv, qb = kPaQ / hn;
+  const int r0 = row / qb * qb;
+  const int p_last = a.pos0 + min(r0 + qb, a.n) - 1;
+  const int p0 = a.pos0 + r0;
+  const int k_base = ((a.slide > 0 && p0 >= a.slide) ? p0 + 1 - a.slide : 0) / kPaKeys * kPaKeys;
+  const int nchunks = (p_last - k_base + a.chunk) / a.chunk;
+  if (nchunks == 1) return;
+  const double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz;
+  for (int h = threadIdx.x; h < a.n_heads; h += kNT) {
+    double m = -DBL_MAX;
+    for (int c = 0; c < nchunks; ++c)
+      m = fmax(m, ml[(((size_t)c * a.n + row) * a.n_heads + h) * 2]);
+    double den = 0.0;
+    for (int c = 0; c < nchunks; ++c) {
+      const size_t at = ((size_t)c * a.n + row) * a.n_heads + h;
+      const double w = exp(ml[at * 2] - m);
+      wt[h][c] = w;
+      den += w * ml[at * 2 + 1];
+    }
+    wt[h][kPfMaxSplit] = den;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.q_sz; i += kNT) {
+    const int h = i / hdim;
+    double num = 0.0;
+    for (int c = 0; c < nchunks; ++c) num += wt[h][c] * a.part[((size_t)c * a.n + row) * a.q_sz + i];
+    a.xo[(size_t)row * a.q_sz + i] = (float)(num / wt[h][kPfMaxSplit]);
   }
 }
 
@@ -360,13 +623,32 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
 }
 
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
-  const int qb = kPfQ / (a.n_heads / a.nkv);
-  const dim3 grid((a.n + qb - 1) / qb, a.nkv);
+  const int hn = a.n_heads / a.nkv;
+  if (hn <= 0 || kPaQ % hn != 0 || a.n <= 0 || a.part == nullptr ||
+      a.n_heads > kPfMaxMergeHeads)
+    return hipErrorInvalidValue;
+  const int qb = kPaQ / hn, nrb = (a.n + qb - 1) / qb;
+  // the longest key range of a row block
+  int kmax = 0;
+  for (int rb = 0; rb < nrb; ++rb) {
+    const int p0 = a.pos0 + rb * qb, p_last = a.pos0 + std::min(rb * qb + qb, a.n) - 1;
+    const int k_base = ((a.slide > 0 && p0 >= a.slide) ? p0 + 1 - a.slide : 0) / kPaKeys * kPaKeys;
+    kmax = std::max(kmax, p_last - k_base + 1);
+  }
+  // split the key ranges until there are about 2048 blocks (half of them
+  // empty for causal rows), in chunks of at least one tile
+  const int want = (2048 + nrb * a.nkv - 1) / (nrb * a.nkv);
+  const int split = std::max(1, std::min({kPfMaxSplit, want, (kmax + kPaKeys - 1) / kPaKeys}));
+  PfAttn b = a;
+  b.chunk = ((kmax + split - 1) / split + kPaKeys - 1) / kPaKeys * kPaKeys;
+  b.nsplit = (kmax + b.chunk - 1) / b.chunk;
+  const dim3 grid(nrb * b.nsplit * a.nkv);
   switch (hdim) {
-    case 128: pf_attn_kernel<128><<<grid, kNT, 0, stream>>>(a); break;
-    case 256: pf_attn_kernel<256><<<grid, kNT, 0, stream>>>(a); break;
+    case 128: pf_attn_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
+    case 256: pf_attn_dma_kernel<256><<<grid, kNT, 0, stream>>>(b); break;
     default: return hipErrorInvalidValue;
   }
+  if (b.nsplit > 1) pf_attn_merge_kernel<<<a.n, kNT, 0, stream>>>(b, hdim);
   return hipGetLastError();
 }
 

@@ -36,6 +36,8 @@ CONFIGS = {
     "gemma-3-270m": dict(nl=18, n_heads=4, nkv=1, hdim=256, dim=640, mlp=2048, slide=512),
     "gemma-3-1b": dict(nl=26, n_heads=4, nkv=1, hdim=256, dim=1152, mlp=6912, slide=512),
     "gemma-3-4b": dict(nl=34, n_heads=8, nkv=4, hdim=256, dim=2560, mlp=10240, slide=1024),
+    # the head dim of the larger checkpoints (128, gemma-3-27b) at test size
+    "test-hd128": dict(nl=2, n_heads=4, nkv=2, hdim=128, dim=256, mlp=512, slide=512),
 }
 NVOCAB = 262144
 SPECIALS = ["<pad>", "<eos>", "<bos>", "<unk>", "<start_of_turn>", "<end_of_turn>"]
