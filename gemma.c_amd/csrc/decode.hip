@@ -376,19 +376,28 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
   }
 }
 
-// xo[h] = sum_b exp(m_b - M) acc_b / sum_b exp(m_b - M) l_b: grid n_heads;
-// the block weights exp(m_b - M) are computed once into LDS
+// xo[h] = sum_b exp(m_b - M) acc_b / sum_b exp(m_b - M) l_b: grid (n_heads,
+// hdim / 64).  Every workgroup of a head computes the block weights
+// exp(m_b - M) into LDS and the denominator (the same bits in each, a fixed
+// order); its 256 threads then split its 64 dimensions into 16 quads and the
+// blocks into 16 strided groups, so the partials are read 16 blocks at a
+// time rather than one after another, and the 16 group sums are added in
+// group order.
+constexpr int kCombGroups = 16;
+
 __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   extern __shared__ double wts[];
   __shared__ double red[kWaves];
+  __shared__ double2 gsum[kCombGroups][32];
   int token, pos;
   if (!step_ok(a.step, a.nvocab, a.clen, &token, &pos)) return;
   const int hd = a.hdim, h = blockIdx.x, tid = threadIdx.x;
   const int spos = (a.slide > 0 && pos >= a.slide) ? pos + 1 - a.slide : 0;
   const int nb = (pos + 1 - spos + kAttB - 1) / kAttB;
-  const double *p = a.part + (size_t)h * a.max_blocks * (hd + 2);
+  const int stride = hd + 2;
+  const double *p = a.part + (size_t)h * a.max_blocks * stride;
   double m = -DBL_MAX;
-  for (int b = tid; b < nb; b += kNT) m = fmax(m, p[(size_t)b * (hd + 2) + hd]);
+  for (int b = tid; b < nb; b += kNT) m = fmax(m, p[(size_t)b * stride + hd]);
   m = fmax(m, dpp_f64<kDppXor1>(m));
   m = fmax(m, dpp_f64<kDppXor2>(m));
   m = fmax(m, dpp_f64<kDppHalfMirror>(m));
@@ -402,16 +411,40 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   for (int w = 1; w < kWaves; ++w) m = fmax(m, red[w]);
   double den = 0.0;
   for (int b = tid; b < nb; b += kNT) {
-    const double w = exp(p[(size_t)b * (hd + 2) + hd] - m);
+    const double w = exp(p[(size_t)b * stride + hd] - m);
     wts[b] = w;
-    den += w * p[(size_t)b * (hd + 2) + hd + 1];
+    den += w * p[(size_t)b * stride + hd + 1];
   }
-  den = block_sum(den, red);
+  den = block_sum(den, red);  // ends with a barrier: wts is complete
+  // thread (group g, quad q): dims d0 + 4q .. d0 + 4q + 3 over blocks g, g + 16, ...
+  const int g = tid / 16, q = tid % 16;
+  const int d = blockIdx.y * 64 + 4 * q;
+  double2 s01 = {0.0, 0.0}, s23 = {0.0, 0.0};
+  if (d < hd)
+    for (int b = g; b < nb; b += kCombGroups) {
+      const double w = wts[b];
+      const double2 x01 = *reinterpret_cast<const double2 *>(p + (size_t)b * stride + d);
+      const double2 x23 = *reinterpret_cast<const double2 *>(p + (size_t)b * stride + d + 2);
+      s01.x += w * x01.x;
+      s01.y += w * x01.y;
+      s23.x += w * x23.x;
+      s23.y += w * x23.y;
+    }
+  gsum[g][2 * q] = s01;
+  gsum[g][2 * q + 1] = s23;
   lds_barrier();
-  for (int d = tid; d < hd; d += kNT) {
-    double num = 0.0;
-    for (int b = 0; b < nb; ++b) num += wts[b] * p[(size_t)b * (hd + 2) + d];
-    a.xo[(size_t)h * hd + d] = (float)(num / den);
+  if (tid < 32) {
+    const int dd = blockIdx.y * 64 + 2 * tid;
+    double2 t = gsum[0][tid];
+#pragma unroll
+    for (int gg = 1; gg < kCombGroups; ++gg) {
+      t.x += gsum[gg][tid].x;
+      t.y += gsum[gg][tid].y;
+    }
+    if (dd < hd) {
+      a.xo[(size_t)h * hd + dd] = (float)(t.x / den);
+      a.xo[(size_t)h * hd + dd + 1] = (float)(t.y / den);
+    }
   }
 }
 
@@ -590,7 +623,8 @@ hipError_t launch_dec_attention(const DecAttn &a, hipStream_t stream) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dec_attn_combine_kernel<<<a.n_heads, kNT, (size_t)a.max_blocks * 8, stream>>>(a);
+  dec_attn_combine_kernel<<<dim3(a.n_heads, (a.hdim + 63) / 64), kNT, (size_t)a.max_blocks * 8,
+                            stream>>>(a);
   return hipGetLastError();
 }
 
