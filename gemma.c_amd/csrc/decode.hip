@@ -151,6 +151,122 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
   }
 }
 
+// The norm prologue + int8 GEMV on the stream schedule of gemv.hip's
+// stream kernel: an all-resident grid deals groups of R = 64 / L rows to its
+// waves round robin, each wave reducing one group and then loading its next.
+// Every workgroup computes the residual + norm + quantize prologue into LDS
+// itself, with its first group's weight loads issued before it.
+//  GELU == false: rows are the flat row range of `jobs` (q, k, v); a group
+//                 lies within one job.
+//  GELU == true:  group g covers outputs r = g R/2 .. g R/2 + R/2 - 1; row
+//                 rloc of the group is gate row r (jobs.w[0]) for even rloc
+//                 and up row r (jobs.w[1]) for odd, and the gate lanes store
+//                 gelu(gate) * up to jobs.dst[0][r] (jobs.end[0] = outputs).
+// Loads are unconditional: a row past the end reads the job's last row and
+// a chunk past k reads chunk 0; neither is used.
+template <int L, int CPL, bool GELU, int NPT>
+__global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJobs jobs,
+                                                              int ngroups, int k) {
+  extern __shared__ v4i xq4[];
+  __shared__ double red[kWaves];
+  __shared__ float redf[kWaves];
+  constexpr int R = 64 / L;
+  static_assert(!GELU || R >= 2, "gate and up rows must share a wave");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane % L, rloc = lane / L;
+  const int kc = k >> 4;
+  const int nwaves = gridDim.x * kWaves;
+  const int w0 = blockIdx.x * kWaves + wave;
+
+  int gend[kMaxJobs];  // groups up to the end of each job
+  {
+    int prev = 0, g = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxJobs; ++t) {
+      if (t < jobs.njobs) g += (jobs.end[t] - prev + R - 1) / R;
+      gend[t] = g;
+      prev = jobs.end[t];
+    }
+  }
+  struct At {
+    int job, row, out;  // job, row read (clamped), row of the output
+    bool ok;
+  };
+  auto where = [&](int g) {
+    At a;
+    if (GELU) {
+      const int m = jobs.end[0];
+      a.out = g * (R / 2) + (rloc >> 1);
+      a.job = rloc & 1;
+      a.ok = g < ngroups && a.out < m;
+      a.row = a.ok ? a.out : m - 1;
+    } else {
+      int j = 0, gs = 0, rs = 0;
+#pragma unroll
+      for (int t = 0; t < kMaxJobs - 1; ++t)
+        if (t + 1 < jobs.njobs && g >= gend[t]) {
+          j = t + 1;
+          gs = gend[t];
+          rs = jobs.end[t];
+        }
+      const int m = jobs.end[j] - rs;
+      a.out = (g - gs) * R + rloc;
+      a.job = j;
+      a.ok = g < ngroups && a.out < m;
+      a.row = a.ok ? a.out : m - 1;
+    }
+    return a;
+  };
+  struct Slot {
+    v4i w[CPL];
+    float sc;  // loaded with the weights: loads complete in issue order
+  };
+  auto load = [&](int g, Slot &s) {
+    const At a = where(g);
+    const gptr<const v4i> w4 =
+        as_global(static_cast<const v4i *>(pick4(jobs.w, a.job))) + (size_t)a.row * kc;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;
+      s.w[i] = __builtin_nontemporal_load(w4 + (c < kc ? c : 0));
+    }
+    s.sc = as_global(pick4(jobs.sc, a.job))[a.row];
+  };
+
+  NormIn<NPT> in;
+  norm_load<NPT, kNT>(na, in);
+  Slot ring;
+  load(w0, ring);
+  const float act_scale =
+      norm_quant<NPT, kNT>(na, in, reinterpret_cast<int8_t *>(xq4), red, redf);
+
+  auto process = [&](int g, const Slot &s) {
+    int32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + i * L;
+      if (c < kc) acc = dot16(s.w[i], xq4[c], acc);
+    }
+    acc = group_sum_i32<L>(acc);
+    const At a = where(g);
+    const float val = rescale(acc, act_scale, s.sc);
+    if (GELU) {
+      const float up = __shfl_xor(val, L, 64);  // the up row's lanes
+      if (sub == 0 && (rloc & 1) == 0 && a.ok)
+        as_global(pick4(jobs.dst, 0))[a.out] = (float)(gelu_tanh((double)val) * (double)up);
+    } else if (sub == 0 && a.ok) {
+      as_global(pick4(jobs.dst, a.job))[a.out] = val;
+    }
+  };
+  const int mine = w0 < ngroups ? (ngroups - 1 - w0) / nwaves + 1 : 0;
+  for (int i = 0; i < mine; ++i) {
+    const int g = w0 + i * nwaves;
+    process(g, ring);
+    if (i + 1 < mine) load(g + nwaves, ring);
+  }
+}
+
 // x = dequantized embedding row of the step's token (gemma.c:5468-5493)
 __global__ __launch_bounds__(kNT) void dec_embed_kernel(DecEmbed a) {
   int token, pos;
@@ -577,12 +693,68 @@ hipError_t norm_gemv_cpl(int cpl, const DecNorm &na, const GemvJobs &jobs, int t
   return hipErrorInvalidValue;
 }
 
+// dec_norm_stream_kernel: L lanes per row (the fewest with CPL <= 10),
+// NPT covering dim = k
+constexpr int kNsMaxCpl = 10;
+typedef hipError_t (*NormStreamFn)(const DecNorm &, const GemvJobs &, int, int,
+                                   const DeviceInfo &, hipStream_t);
+
+template <int L, int CPL, bool GELU>
+hipError_t launch_norm_stream(const DecNorm &na, const GemvJobs &jobs, int ngroups, int k,
+                              const DeviceInfo &dev, hipStream_t stream) {
+  constexpr int NPT = (L * CPL * 16 + kNT * 4 - 1) / (kNT * 4);
+  const auto kern = dec_norm_stream_kernel<L, CPL, GELU, NPT>;
+  const size_t lds = (size_t)(k + 15) / 16 * 16;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kNT, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const long need = (ngroups + kWaves - 1) / kWaves;
+  const long cap = (long)dev.cus * per_cu;
+  kern<<<dim3((unsigned)(need < cap ? need : cap)), kNT, lds, stream>>>(na, jobs, ngroups, k);
+  return hipGetLastError();
+}
+
+template <int L, bool GELU, int C, int CMAX = kNsMaxCpl>
+NormStreamFn norm_stream_for(int cpl) {
+  if (cpl == C) return &launch_norm_stream<L, C, GELU>;
+  if constexpr (C < CMAX) return norm_stream_for<L, GELU, C + 1, CMAX>(cpl);
+  return nullptr;
+}
+
+// nullptr where the streamed kernel does not apply (GELU rows need L <= 32)
+NormStreamFn norm_stream_fn(int kc, bool gelu) {
+  if (kc <= 8 * kNsMaxCpl)
+    return gelu ? norm_stream_for<8, true, 1>((kc + 7) / 8) : norm_stream_for<8, false, 1>((kc + 7) / 8);
+  if (kc <= 16 * kNsMaxCpl)
+    return gelu ? norm_stream_for<16, true, 6>((kc + 15) / 16)
+                : norm_stream_for<16, false, 6>((kc + 15) / 16);
+  if (kc <= 32 * kNsMaxCpl)
+    return gelu ? norm_stream_for<32, true, 6>((kc + 31) / 32)
+                : norm_stream_for<32, false, 6>((kc + 31) / 32);
+  if (!gelu && kc <= 64 * 6) return norm_stream_for<64, false, 6, 6>((kc + 63) / 64);
+  return nullptr;
+}
+
 }  // namespace
 
 hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                                 bool gelu, const DeviceInfo &dev, hipStream_t stream) {
   if (total <= 0 || k <= 0 || k % 16 != 0 || k > 6144) return hipErrorInvalidValue;
   const int kc = k / 16;
+  if (const NormStreamFn fn = norm_stream_fn(kc, gelu)) {
+    int lanes = 8;
+    while ((kc + lanes - 1) / lanes > kNsMaxCpl) lanes *= 2;
+    const int rows = 64 / lanes;
+    int ngroups = 0;
+    if (gelu) {
+      ngroups = (total / 2 + rows / 2 - 1) / (rows / 2);
+    } else {
+      for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
+        ngroups += (jobs.end[j] - prev + rows - 1) / rows;
+    }
+    return fn(na, jobs, ngroups, k, dev, stream);
+  }
   // 32 lanes per row (two rows per wave, as the gate/up pairing needs) up to
   // 256 chunks (k = 4096); 64 lanes beyond that for plain rows
   if (kc <= 32 * 8 || gelu) {
