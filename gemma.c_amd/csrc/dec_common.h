@@ -59,12 +59,6 @@ __device__ __forceinline__ float norm_one(float x, double rms, float w) {
   return (float)((double)x * rms * ((double)w + 1.0));
 }
 
-// gelu_tanh (gemma.c:4139-4145) with the reference's fp32 constants
-__device__ __forceinline__ double gelu_tanh(double x) {
-  const double c = (double)0.79788456080287f;
-  const double k = (double)0.044715f;
-  return 0.5 * x * (1.0 + tanh(c * (x + k * x * x * x)));
-}
 
 // e^x in fp64 by Tang's table-driven method (P. T. P. Tang, "Table-driven
 // implementation of the exponential function in IEEE floating-point
@@ -72,7 +66,7 @@ __device__ __forceinline__ double gelu_tanh(double x) {
 // |r| <= ln2/256, e^x = 2^e * 2^(j/128) * e^r, e^r by its Taylor polynomial of
 // degree 5 (truncation below 6e-19 relative); ln2/128 is split so that
 // k * hi is exact for |k| < 2^21.  The result is within about 2 ulp of e^x.
-// Arguments are clamped at -800, where e^x has underflowed to 0.  kExp2Tab
+// Arguments are clamped to [-800, 800], where e^x is 0 or inf.  kExp2Tab
 // holds 2^(j/128) correctly rounded; the caller copies it into LDS
 // (exp_tab_load) and passes the constants from scalar registers
 // (exp_consts).
@@ -132,7 +126,7 @@ __device__ __forceinline__ void exp_tab_load(double *tab) {
 }
 
 __device__ __forceinline__ double exp_tab(double x, const double *tab, const ExpConsts &c) {
-  x = fmax(x, -800.0);
+  x = fmin(fmax(x, -800.0), 800.0);  // e^x is 0 below -745 and inf above 710
   const double kf = rint(x * c.inv);
   double r = fma(-kf, c.hi, x);
   r = fma(-kf, c.lo, r);
@@ -143,6 +137,18 @@ __device__ __forceinline__ double exp_tab(double x, const double *tab, const Exp
   p = fma(r, p, 1.0);
   const int k = (int)kf;
   return ldexp(tab[k & 127] * p, k >> 7);
+}
+
+// gelu_tanh (gemma.c:4139-4145) with the reference's fp32 constants, in
+// fp64: 0.5 x (1 + tanh(u)) with u = c (x + k x^3) is the same function as
+// x / (1 + e^(-2u)) (1 + tanh(u) = 2 / (1 + e^(-2u))), which costs one table
+// exponential and one division instead of tanh.  The two forms differ only
+// by fp64 rounding; at x -> -inf both give -0, at x -> +inf both give x.
+__device__ __forceinline__ double gelu(double x, const double *etab, const ExpConsts &ec) {
+  const double c = (double)0.79788456080287f;
+  const double k = (double)0.044715f;
+  const double u = c * (x + k * x * x * x);
+  return x / (1.0 + exp_tab(-2.0 * u, etab, ec));
 }
 
 // Reads the step's token and position; false when they are out of range

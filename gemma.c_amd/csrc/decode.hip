@@ -61,6 +61,9 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
   constexpr int kW = NT / 64;
   __shared__ double red[kW];
   __shared__ float redf[kW];
+  __shared__ double etab[GELU ? 128 : 1];
+  if (GELU) exp_tab_load(etab);  // visible after the prologue's barriers
+  const ExpConsts ec = exp_consts();
   constexpr int kNpt = (CPL * L * 16 + NT * 4 - 1) / (NT * 4);
   static_assert(!GELU || L <= 32, "gate and up rows must share a wave");
   constexpr int kRowsPerWave = 64 / L;
@@ -131,7 +134,7 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
     if (GELU) {
       const float up = __shfl_xor(val, L, 64);
       if (sub == 0 && (rloc & 1) == 0 && row < total)
-        as_global(pick4(jobs.dst, 0))[r] = (float)(gelu_tanh((double)val) * (double)up);
+        as_global(pick4(jobs.dst, 0))[r] = (float)(gelu((double)val, etab, ec) * (double)up);
     } else if (sub == 0 && row < total) {
       as_global(pick4(jobs.dst, j))[r] = val;
     }
@@ -170,6 +173,9 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
   extern __shared__ v4i xq4[];
   __shared__ double red[kWaves];
   __shared__ float redf[kWaves];
+  __shared__ double etab[GELU ? 128 : 1];
+  if (GELU) exp_tab_load(etab);  // visible after the prologue's barriers
+  const ExpConsts ec = exp_consts();
   constexpr int R = 64 / L;
   static_assert(!GELU || R >= 2, "gate and up rows must share a wave");
   const int lane = threadIdx.x & 63;
@@ -254,7 +260,7 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
     if (GELU) {
       const float up = __shfl_xor(val, L, 64);  // the up row's lanes
       if (sub == 0 && (rloc & 1) == 0 && a.ok)
-        as_global(pick4(jobs.dst, 0))[a.out] = (float)(gelu_tanh((double)val) * (double)up);
+        as_global(pick4(jobs.dst, 0))[a.out] = (float)(gelu((double)val, etab, ec) * (double)up);
     } else if (sub == 0 && a.ok) {
       as_global(pick4(jobs.dst, a.job))[a.out] = val;
     }

@@ -557,24 +557,31 @@ template <int NPT, int NT>
 __global__ __launch_bounds__(NT) void pf_gelu_quant_kernel(const float *g, int mlp, int8_t *xq,
                                                            float *xs) {
   __shared__ float redf[NT / 64];
+  __shared__ double etab[128];
+  exp_tab_load(etab);
+  const ExpConsts ec = exp_consts();
   const int tid = threadIdx.x;
   const int n4 = mlp >> 2;
   const float *gate = g + (size_t)blockIdx.x * 2 * mlp;
   const float *up = gate + mlp;
-  v4f out[NPT];
-  float amax = 0.0f;
+  v4f gv[NPT], uv[NPT];
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
     const int c = tid + j * NT;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const v4f gv = c < n4 ? reinterpret_cast<const v4f *>(gate)[c] : zero;
-    const v4f uv = c < n4 ? reinterpret_cast<const v4f *>(up)[c] : zero;
+    gv[j] = c < n4 ? reinterpret_cast<const v4f *>(gate)[c] : zero;
+    uv[j] = c < n4 ? reinterpret_cast<const v4f *>(up)[c] : zero;
+  }
+  lds_barrier();  // the exp table
+  v4f out[NPT];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      out[j][e] = (float)(gelu_tanh((double)gv[e]) * (double)uv[e]);
+      out[j][e] = (float)(gelu((double)gv[j][e], etab, ec) * (double)uv[j][e]);
       amax = fmaxf(amax, abs_daz(out[j][e]));
     }
-  }
   amax = block_max<NT>(amax, redf);
   const QuantParams qp = quant_params(amax);
   int8_t *row = xq + (size_t)blockIdx.x * mlp;

@@ -339,22 +339,29 @@ template <int NPT, int NT>
 __global__ __launch_bounds__(NT) void vis_gelu_quant_kernel(const float *hbuf, const float *bias,
                                                             int mlp, int8_t *xq, float *xs) {
   __shared__ float redf[NT / 64];
+  __shared__ double etab[128];
+  exp_tab_load(etab);
+  const ExpConsts ec = exp_consts();
   const int tid = threadIdx.x, n4 = mlp >> 2;
   const float *row = hbuf + (size_t)blockIdx.x * mlp;
-  v4f out[NPT];
-  float amax = 0.0f;
+  v4f hv[NPT], bv[NPT];
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
     const int c = tid + j * NT;
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    const v4f hv = c < n4 ? reinterpret_cast<const v4f *>(row)[c] : zero;
-    const v4f bv = c < n4 ? reinterpret_cast<const v4f *>(bias)[c] : zero;
+    hv[j] = c < n4 ? reinterpret_cast<const v4f *>(row)[c] : zero;
+    bv[j] = c < n4 ? reinterpret_cast<const v4f *>(bias)[c] : zero;
+  }
+  lds_barrier();  // the exp table
+  v4f out[NPT];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      out[j][e] = (float)gelu_tanh((double)(hv[e] + bv[e]));
+      out[j][e] = (float)gelu((double)(hv[j][e] + bv[j][e]), etab, ec);
       amax = fmaxf(amax, abs_daz(out[j][e]));
     }
-  }
   amax = block_max<NT>(amax, redf);
   const QuantParams qp = quant_params(amax);
   int8_t *dst = xq + (size_t)blockIdx.x * mlp;
