@@ -324,9 +324,8 @@ __device__ __forceinline__ void block_barrier() {
 
 template <int WM, int WN, int S, int BKB, bool HEADS>
 __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
-    float *__restrict__ dst, int dstr, int hdim, const int8_t *__restrict__ mat,
-    int mstr, const float *__restrict__ matsc, const int8_t *__restrict__ src,
-    int sstr, const float *__restrict__ ssc, int m, int n, int k) {
+    float *__restrict__ dst, int dstr, int hdim, GemmSegs bs, int mstr,
+    const int8_t *__restrict__ src, int sstr, const float *__restrict__ ssc, int m, int k) {
   constexpr int kBM = 64 * WM;
   constexpr int kBN = 64 * WN;
   constexpr int kC = BKB / 16;                 // 16-byte chunks per row and stage
@@ -346,17 +345,27 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int wm = wave >> 1;
   const int wn = wave & 1;
+  const int n = bs.end[bs.nseg - 1];
   int tm, tn;
   tile_of(blockIdx.x, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, &tm, &tn);
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
+  // the B matrix of this tile's columns (inner segment ends are multiples of
+  // kBN, so a tile lies in one segment); its rows are columns c0 .. of dst
+  int sj = 0;
+#pragma unroll
+  for (int t = 0; t < kMaxGemmSegs - 1; ++t)
+    if (t + 1 < bs.nseg && n0 >= bs.end[t]) sj = t + 1;
+  const int c0 = sj == 0 ? 0 : bs.end[sj - 1];
+  const int8_t *mat = bs.w[sj];
+  const int nb = bs.end[sj] - c0;
   TileScales<WM, WN> scales;
-  load_tile_scales<WM, WN>(scales, ssc, matsc, m, n, m0, n0, wm, wn, lane);
+  load_tile_scales<WM, WN>(scales, ssc, bs.s[sj] - c0, m, n, m0, n0, wm, wn, lane);
 
   const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int8_t *>(src), (short)0, (int)((uint32_t)(m - 1) * sstr + k), 0x00020000);
   const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<int8_t *>(mat), (short)0, (int)((uint32_t)(n - 1) * mstr + k), 0x00020000);
+      const_cast<int8_t *>(mat), (short)0, (int)((uint32_t)(nb - 1) * mstr + k), 0x00020000);
 
   // this lane's slot of each of its kPerWave DMA instructions
   uint32_t row_off[kPerWave];
@@ -368,8 +377,8 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
     const int slot = instr * 64 + lane - (is_a ? 0 : kBM * kC);
     const int row = slot / kC;
     const int chunk = (slot % kC) ^ swz(row);
-    const int grow = (is_a ? m0 : n0) + row;
-    const bool in = grow < (is_a ? m : n);
+    const int grow = (is_a ? m0 : n0 - c0) + row;
+    const bool in = grow < (is_a ? m : nb);
     row_off[i] = in ? (uint32_t)grow * (uint32_t)(is_a ? sstr : mstr) + chunk * 16 : kOob;
     chunk16[i] = chunk * 16;
   }
@@ -478,17 +487,31 @@ int env_tile() {
 }
 
 template <int WM, int WN, int S, int BKB = 64>
+void launch_dma_segs(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
+                     const GemmSegs &bs, int mstr, const int8_t *src, int sstr,
+                     const float *ssc, int m, int k) {
+  const int n = bs.end[bs.nseg - 1];
+  const int tiles = ((m + 64 * WM - 1) / (64 * WM)) * ((n + 64 * WN - 1) / (64 * WN));
+  if (heads)
+    gemm_i8_dma_kernel<WM, WN, S, BKB, true><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k);
+  else
+    gemm_i8_dma_kernel<WM, WN, S, BKB, false><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k);
+}
+
+template <int WM, int WN, int S, int BKB = 64>
 void launch_dma(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
                 const int8_t *mat, int mstr, const float *matsc,
                 const int8_t *src, int sstr, const float *ssc, int m, int n,
                 int k) {
-  const int tiles = ((m + 64 * WM - 1) / (64 * WM)) * ((n + 64 * WN - 1) / (64 * WN));
-  if (heads)
-    gemm_i8_dma_kernel<WM, WN, S, BKB, true><<<tiles, kThreads, 0, stream>>>(
-        dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
-  else
-    gemm_i8_dma_kernel<WM, WN, S, BKB, false><<<tiles, kThreads, 0, stream>>>(
-        dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
+  GemmSegs bs{};
+  bs.w[0] = mat;
+  bs.s[0] = matsc;
+  bs.end[0] = n;
+  bs.nseg = 1;
+  launch_dma_segs<WM, WN, S, BKB>(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m,
+                                  k);
 }
 
 template <int WM, int WN>
@@ -553,6 +576,42 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
           dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const int8_t *src,
+                               int sstr, const float *ssc, int m, int k, const DeviceInfo &dev,
+                               hipStream_t stream) {
+  if (b.nseg < 1 || b.nseg > kMaxGemmSegs || m <= 0 || k <= 0) return hipErrorInvalidValue;
+  const int n = b.end[b.nseg - 1];
+  bool fast = k % 16 == 0 && sstr % 16 == 0 && (uintptr_t)src % 16 == 0;
+  bool dma_ok = (uint64_t)(m - 1) * sstr + k < kOob && ((uint64_t)(m - 1) * dstr + n) * 4 < kOob;
+  for (int t = 0, start = 0; t < b.nseg; start = b.end[t], ++t) {
+    const int rows = b.end[t] - start;
+    if (rows <= 0) return hipErrorInvalidValue;
+    fast = fast && (uintptr_t)b.w[t] % 16 == 0;
+    dma_ok = dma_ok && (uint64_t)(rows - 1) * k + k < kOob;
+  }
+  if (fast && dma_ok && env_tile() == 0) {
+    // the tile choice of launch_gemm_i8 for the whole width
+    const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+    const bool wide = tiles128 >= dev.cus;
+    const int bn = wide ? 128 : 64;
+    bool aligned = true;
+    for (int t = 0; t + 1 < b.nseg; ++t) aligned = aligned && b.end[t] % bn == 0;
+    if (aligned) {
+      if (wide)
+        launch_dma_segs<2, 2, 2, 128>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
+      else
+        launch_dma_segs<2, 1, 4>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
+      return hipGetLastError();
+    }
+  }
+  for (int t = 0, start = 0; t < b.nseg; start = b.end[t], ++t) {
+    const hipError_t e = launch_gemm_i8(dst + start, dstr, 0, b.w[t], k, b.s[t], src, sstr, ssc,
+                                        m, b.end[t] - start, k, dev, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace gh

@@ -911,9 +911,10 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st)
                         d->pf_as, dim, c.eps};
     if ((e = gh::launch_pf_norm_rows(n1, n, st)) != hipSuccess) return e;
     // q, k, v rows (gemma.c:5045-5089)
-    if ((e = gemm(d->pf_qkv, stride, L.w[0], L.s[0], q_sz, dim)) != hipSuccess ||
-        (e = gemm(d->pf_qkv + q_sz, stride, L.w[1], L.s[1], kv_sz, dim)) != hipSuccess ||
-        (e = gemm(d->pf_qkv + q_sz + kv_sz, stride, L.w[2], L.s[2], kv_sz, dim)) != hipSuccess)
+    const gh::GemmSegs qkv{{L.w[0], L.w[1], L.w[2]}, {L.s[0], L.s[1], L.s[2]},
+                           {q_sz, q_sz + kv_sz, q_sz + 2 * kv_sz}, 3};
+    if ((e = gh::launch_gemm_i8_segs(d->pf_qkv, stride, qkv, d->pf_a8, dim, d->pf_as, n, dim,
+                                     g.info, st)) != hipSuccess)
       return e;
     // q/k norm, RoPE, KV append, attention
     const bool sliding = d->swa[l] != 0;
@@ -936,8 +937,10 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st)
                         d->pf_a8, d->pf_as, dim, c.eps};
     if ((e = gh::launch_pf_norm_rows(n3, n, st)) != hipSuccess) return e;
     // gate (w2), up (w1) (gemma.c:5365-5373), GELU(gate) * up, quantize, down
-    if ((e = gemm(d->pf_g, 2 * mlp, L.w[5], L.s[5], mlp, dim)) != hipSuccess ||
-        (e = gemm(d->pf_g + mlp, 2 * mlp, L.w[4], L.s[4], mlp, dim)) != hipSuccess ||
+    const gh::GemmSegs gu{{L.w[5], L.w[4], nullptr}, {L.s[5], L.s[4], nullptr},
+                          {mlp, 2 * mlp, 2 * mlp}, 2};
+    if ((e = gh::launch_gemm_i8_segs(d->pf_g, 2 * mlp, gu, d->pf_a8, dim, d->pf_as, n, dim,
+                                     g.info, st)) != hipSuccess ||
         (e = gh::launch_pf_gelu_quant(d->pf_g, n, mlp, d->pf_a8, d->pf_as, st)) != hipSuccess ||
         (e = gemm(d->pf_y, dim, L.w[6], L.s[6], dim, mlp)) != hipSuccess)
       return e;
@@ -1391,9 +1394,10 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
                        L.n1, L.n1b, v->a8, v->as, nullptr, dim, c.eps};
     if ((e = gh::launch_vis_ln_rows(n1, n, st)) != hipSuccess) return e;
     // q, k, v (4487-4511); their biases are added inside the attention
-    if ((e = gemm(v->qkv, 3 * dim, L.w[0], L.s[0], n, dim, dim)) != hipSuccess ||
-        (e = gemm(v->qkv + dim, 3 * dim, L.w[1], L.s[1], n, dim, dim)) != hipSuccess ||
-        (e = gemm(v->qkv + 2 * dim, 3 * dim, L.w[2], L.s[2], n, dim, dim)) != hipSuccess)
+    const gh::GemmSegs qkv{{L.w[0], L.w[1], L.w[2]}, {L.s[0], L.s[1], L.s[2]},
+                           {dim, 2 * dim, 3 * dim}, 3};
+    if ((e = gh::launch_gemm_i8_segs(v->qkv, 3 * dim, qkv, v->a8, dim, v->as, n, dim, g.info,
+                                     st)) != hipSuccess)
       return e;
     const gh::VisAttn at{v->qkv, 3 * dim, L.bqkv, v->att, n, c.n_heads, dim,
                          1.0f / sqrtf((float)v->hdim)};

@@ -51,6 +51,22 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
                           int sstr, const float *ssc, int m, int n, int k,
                           const DeviceInfo &dev, hipStream_t stream);
 
+// B as up to kMaxGemmSegs separate [rows][k] matrices (q, k, v; or gate,
+// up) whose outputs are adjacent column ranges of one dst: segment t holds
+// output columns [end[t-1], end[t]) (end[-1] = 0), scales s[t] per row.
+constexpr int kMaxGemmSegs = 3;
+struct GemmSegs {
+  const int8_t *w[kMaxGemmSegs];
+  const float *s[kMaxGemmSegs];
+  int end[kMaxGemmSegs];
+  int nseg;
+};
+// One launch over all segments when every inner segment boundary is a
+// multiple of the tile width; otherwise one launch per segment.
+hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const int8_t *src,
+                               int sstr, const float *ssc, int m, int k, const DeviceInfo &dev,
+                               hipStream_t stream);
+
 // gemm_f32.hip: dst = src . mat^T in fp32; bias (nullable) adds bias[col],
 // clamp limits every output to [-FLT_MAX, FLT_MAX] (clamp_fpx).
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
