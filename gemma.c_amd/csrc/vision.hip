@@ -178,17 +178,19 @@ __global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
 // row sums are per-lane partials, added across the 4 lanes of a query at
 // the end.  Every sum is fp64; each output is rounded to fp32 once.
 constexpr int kVaKeys = 32;          // keys per tile
+constexpr int kVaWaves = 8;          // waves (16 queries each) per workgroup
 constexpr double kVaSlack = 64.0;    // e^64 * 3.4e38 * n keys stays far below DBL_MAX
 
-template <int HD>
-__global__ __launch_bounds__(kNT, 2) void vis_attn_kernel(VisAttn a) {
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_kernel(VisAttn a) {
+  constexpr int NT = NW * 64, QB = NW * 16;  // threads, queries per workgroup
   static_assert(HD % 8 == 0 && HD <= 128, "head dim");
   constexpr int KS = HD / 4;            // MFMA steps of a score block (dims per lane)
   constexpr int NB = (HD + 15) / 16;    // 16-dim output blocks
   constexpr int RK = HD + 2;            // K row in LDS (doubles)
   constexpr int VS = kVaKeys + 2;       // V^T row in LDS (doubles)
   constexpr int C4 = HD / 4;            // float4 per key row
-  constexpr int PF = (kVaKeys * C4 + kNT - 1) / kNT;  // float4 of K (and of V) per thread
+  constexpr int PF = (kVaKeys * C4 + NT - 1) / NT;  // float4 of K (and of V) per thread
   __shared__ double kt[kVaKeys * RK];
   __shared__ double vt[16 * NB * VS];
   __shared__ double etab[128];
@@ -200,11 +202,11 @@ __global__ __launch_bounds__(kNT, 2) void vis_attn_kernel(VisAttn a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // blocks of one head share K and V: give each XCD (blocks b, b+8, ...) a
   // contiguous run of (head, query block) pairs so they meet in its L2
-  const int nqb = (a.n + 63) / 64, nblk = nqb * a.n_heads;
+  const int nqb = (a.n + QB - 1) / QB, nblk = nqb * a.n_heads;
   int blk = blockIdx.x;
   if (nblk % 8 == 0) blk = (blk % 8) * (nblk / 8) + blk / 8;
   const int h = blk / nqb;
-  const int q0 = (blk - h * nqb) * 64 + wave * 16;
+  const int q0 = (blk - h * nqb) * QB + wave * 16;
   const int col = lane & 15, grp = lane >> 4;
 
   double qa[KS];
@@ -226,9 +228,9 @@ __global__ __launch_bounds__(kNT, 2) void vis_attn_kernel(VisAttn a) {
   const float *vbase = a.qkv + 2 * a.dim + h * HD;
 
   // padding dims of V^T (never overwritten by the staging below)
-  for (int i = HD * VS + tid; i < 16 * NB * VS; i += kNT) vt[i] = 0.0;
+  for (int i = HD * VS + tid; i < 16 * NB * VS; i += NT) vt[i] = 0.0;
   exp_tab_load(etab);
-  for (int i = tid; i < 2 * C4; i += kNT)
+  for (int i = tid; i < 2 * C4; i += NT)
     kvb[i / C4][i % C4] = reinterpret_cast<const v4f *>(i < C4 ? bk : bv)[i % C4];
   const ExpConsts ec = exp_consts();
 
@@ -236,7 +238,7 @@ __global__ __launch_bounds__(kNT, 2) void vis_attn_kernel(VisAttn a) {
   auto fetch = [&](int t0) {  // rows clamped into range: every load is unconditional
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int i = min(tid + j * kNT, kVaKeys * C4 - 1);
+      const int i = min(tid + j * NT, kVaKeys * C4 - 1);
       const int t = i / C4, c4 = i - t * C4;
       const size_t row = (size_t)min(t0 + t, a.n - 1) * a.stride;
       kx[j] = *reinterpret_cast<const v4f *>(kbase + row + 4 * c4);
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(kNT, 2) void vis_attn_kernel(VisAttn a) {
     lds_barrier();  // every wave is done with the previous tile
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int i = tid + j * kNT;
+      const int i = tid + j * NT;
       if (i >= kVaKeys * C4) break;
       const int t = i / C4, c4 = i - t * C4;
       const bool ok = t0 + t < a.n;
@@ -456,13 +458,14 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
 }
 
 hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream) {
-  const dim3 grid((a.n + 63) / 64 * a.n_heads);
+  constexpr int NW = kVaWaves;
+  const dim3 grid((a.n + NW * 16 - 1) / (NW * 16) * a.n_heads);
   switch (hdim) {
-    case 16: vis_attn_kernel<16><<<grid, kNT, 0, stream>>>(a); break;
-    case 32: vis_attn_kernel<32><<<grid, kNT, 0, stream>>>(a); break;
-    case 64: vis_attn_kernel<64><<<grid, kNT, 0, stream>>>(a); break;
-    case 72: vis_attn_kernel<72><<<grid, kNT, 0, stream>>>(a); break;
-    case 128: vis_attn_kernel<128><<<grid, kNT, 0, stream>>>(a); break;
+    case 16: vis_attn_kernel<16, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+    case 32: vis_attn_kernel<32, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+    case 64: vis_attn_kernel<64, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+    case 72: vis_attn_kernel<72, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+    case 128: vis_attn_kernel<128, NW><<<grid, NW * 64, 0, stream>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -38,6 +38,9 @@ CONFIGS = {
     "gemma-3-4b": dict(nl=34, n_heads=8, nkv=4, hdim=256, dim=2560, mlp=10240, slide=1024),
     # the head dim of the larger checkpoints (128, gemma-3-27b) at test size
     "test-hd128": dict(nl=2, n_heads=4, nkv=2, hdim=128, dim=256, mlp=512, slide=512),
+    # widths that are multiples of 16 but not of the GEMM tile (64/128) or of
+    # 256-thread vectors: dim 208, mlp 1040, one q head per kv head
+    "test-odd": dict(nl=2, n_heads=2, nkv=2, hdim=128, dim=208, mlp=1040, slide=512),
 }
 NVOCAB = 262144
 SPECIALS = ["<pad>", "<eos>", "<bos>", "<unk>", "<start_of_turn>", "<end_of_turn>"]

@@ -83,6 +83,9 @@ CASES = {
     "plain": dict(name="gemma-3-270m", layers=2, slide=4096, flags=0),
     # head dim 128, two q heads per kv head, sliding window of 8 on the first layer
     "hd128": dict(name="test-hd128", layers=2, slide=8, flags=7),
+    # dim 208 and mlp 1040: no width is a multiple of the GEMM tile, so the
+    # prefill's fused q/k/v and gate/up GEMMs fall back to one launch each
+    "odd": dict(name="test-odd", layers=2, slide=8, flags=7),
 }
 
 
@@ -100,7 +103,8 @@ def models(tmp_path_factory):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("case,steps,clen", [("gemma3", 80, 96), ("softcap", 12, 32),
-                                             ("plain", 12, 32), ("hd128", 40, 48)])
+                                             ("plain", 12, 32), ("hd128", 40, 48),
+                                             ("odd", 30, 40)])
 def test_decoder_matches_oracle(gh, oracle, models, case, steps, clen):
     model = models[case]
     dec = gh.decoder(model, clen)
@@ -171,7 +175,8 @@ def _prefill_vs_oracle(gh, oracle, model, n, more, clen, chunks=None):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("case,n,more,clen", [("gemma3", 40, 8, 64), ("softcap", 20, 4, 32),
-                                              ("plain", 20, 4, 32), ("hd128", 70, 4, 96)])
+                                              ("plain", 20, 4, 32), ("hd128", 70, 4, 96),
+                                              ("odd", 45, 4, 64)])
 def test_prefill_matches_oracle(gh, oracle, models, case, n, more, clen):
     worst = _prefill_vs_oracle(gh, oracle, models[case], n, more, clen)
     print(f"prefill {case}: worst |d|/max|logit| = {worst:.3g}", flush=True)
