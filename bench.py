@@ -327,7 +327,8 @@ def bench_decode_1b(torch, gh, gen, timer, tokens):
 
 
 # decode phases of BASELINE.json configs 3 and 5: (model, context before, timed steps)
-DECODER_RUNS = (("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512))
+# BASELINE.json configs 1, 3 and 5: (model, prompt tokens, greedy decode steps)
+DECODER_RUNS = (("gemma-3-270m", 32, 64), ("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512))
 
 
 def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
@@ -475,8 +476,9 @@ def main() -> int:
     ap.add_argument("--only", choices=["sweep", "lm_head", "decoder", "vision"], default=None,
                     help="profiling aid: run just the timed sweep, the LM-head timing, "
                          "the device-resident decoder or the vision tower")
-    ap.add_argument("--decoder-models", default="gemma-3-1b,gemma-3-4b",
-                    help="models of the decoder timing (comma list of gemma-3-1b, gemma-3-4b)")
+    ap.add_argument("--decoder-models", default="gemma-3-270m,gemma-3-1b,gemma-3-4b",
+                    help="models of the decoder timing (comma list of gemma-3-270m, "
+                         "gemma-3-1b, gemma-3-4b)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="profiling aid: 3 dispatches of an elementwise kernel that reads "
                          "and writes exactly 1 GiB (calibrates FETCH_SIZE / WRITE_SIZE)")
