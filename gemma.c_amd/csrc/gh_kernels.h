@@ -174,6 +174,7 @@ struct PfAttn {
   // chunk and nsplit are set by launch_pf_attention
   double *part;
   int chunk, nsplit;
+  int qpb;  // query vectors per workgroup (set by launch_pf_attention)
 };
 constexpr int kPfMaxSplit = 8;
 // doubles of PfAttn::part for n rows

@@ -139,7 +139,9 @@ __global__ __launch_bounds__(64) void pf_qk_rope_kernel(PfRope a) {
 // -DBL_MAX, so a masked score (-DBL_MAX) gives exp = 0 even before a query
 // has seen its first key.  Every sum is fp64; each output is rounded to
 // fp32 once.
-constexpr int kPaQ = 64;              // query vectors per workgroup
+constexpr int kPaQ = 64;              // query vectors per workgroup (head dim 128)
+constexpr int kPaPairWaves = 8;       // waves per workgroup (head dim 256): 4 pairs
+constexpr int kPaQPair = kPaPairWaves * 8;  // query vectors per workgroup (16 per pair)
 constexpr int kPfMaxMergeHeads = 64;  // q heads the merge handles
 constexpr int kPaKeys = 32;           // keys per tile (register-staged kernel)
 constexpr double kPaSlack = 64.0;     // p <= e^64: sums stay far below DBL_MAX
@@ -167,7 +169,7 @@ __device__ __forceinline__ int pa_window_start(const PfAttn &a, int p_abs) {
 // its last row's position).
 __device__ __forceinline__ PaLane pa_lane(const PfAttn &a, int wave, int col) {
   PaLane L;
-  const int hn = a.n_heads / a.nkv, qb = kPaQ / hn;
+  const int hn = a.n_heads / a.nkv, qb = a.qpb / hn;
   const int nrb = (a.n + qb - 1) / qb;
   L.hk = blockIdx.x % a.nkv;
   L.chunk_id = (blockIdx.x / a.nkv) % a.nsplit;
@@ -361,14 +363,6 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_kernel(PfAttn a) {
   pa_store<HD, NB>(a, L, o, m_ref, l_part, grp);
 }
 
-// HD 256.  The 64 fp64 output accumulators and the 64 fp64 query operands
-// per lane need one wave per SIMD (512 registers, no spills), so latency is
-// hidden inside the wave: K/V tiles of 32 keys go from the cache into LDS by
-// the LDS DMA loads (one key row of 1 KB is one wave's load of 64 x 16 bytes;
-// lane l's bytes land at 16 l), double-buffered -- the next tile loads
-// while the current one is computed, staging takes no registers, and there
-// is one barrier per tile.  V stays row-major: one MFMA step reads the 4
-// keys' values with 4 LDS reads whose rows sit 16 banks apart.
 // One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
 // wave-uniform).  Issued from inline asm so that the compiler does not treat
 // every later LDS read as a possible alias of the pending load (it would
@@ -384,31 +378,45 @@ __device__ __forceinline__ void lds_dma16(const float *g, float *lds) {
 #pragma clang diagnostic pop
 }
 
-template <int HD>
-__global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
+// HD 256 on wave pairs.  A whole head dim per wave needs 64 fp64 output
+// accumulators and 64 fp64 query operands per lane, i.e. one wave per SIMD,
+// and then nothing overlaps a wave's softmax, barriers and operand reads with
+// MFMAs.  Here the two waves of a pair take the same 16 queries and one half
+// of the head dim each: a wave computes the partial scores over its half,
+// the pair exchanges them through LDS and both add them in the same order
+// (half 0 + half 1), both run the (identical) softmax, and each accumulates
+// the value sums of its half.  The MFMA count is that of one wave per query
+// group; a lane holds 32 + 32 fp64 values, so two workgroups (4 waves = 2
+// pairs = 32 query vectors each) share a CU and one's waits hide under the
+// other's MFMAs.  K/V tiles of 16 keys go from the cache into LDS by LDS DMA
+// loads (one 1 KB key row per wave instruction), double-buffered.
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void pf_attn_pair_kernel(PfAttn a) {
   static_assert(HD == 256, "one key row is one wave's 64 x 16-byte LDS load");
-  constexpr int KS = HD / 4, NB = HD / 16;
-  constexpr int TK = kPaKeys;  // keys per tile
+  constexpr int HH = HD / 2;   // dims per wave
+  constexpr int KS = HH / 4;   // score MFMA steps (dims per lane)
+  constexpr int NB = HH / 16;  // 16-dim output blocks per wave
+  constexpr int TK = 16;       // keys per tile
   constexpr int RK = HD + 4;   // K row (floats): rows 16 bytes apart in the banks
   constexpr int RV = HD + 16;  // V row (floats): rows 16 banks apart
-  // the K/V double buffers; after the last tile the same memory stages the
-  // outputs (16 query rows of HD + 4 doubles per wave)
   constexpr int KB = 2 * TK * RK * 4, VB = 2 * TK * RV * 4;
-  constexpr int RO = HD + 4;
-  static_assert(kWaves * 16 * RO * 8 <= KB + VB, "output staging");
-  __shared__ __attribute__((aligned(16))) char smem[KB + VB];
+  constexpr int RO = HH + 4;   // output staging row (doubles)
+  constexpr int OB = NW * 16 * RO * 8;
+  __shared__ __attribute__((aligned(16))) char smem[KB + VB > OB ? KB + VB : OB];
   float(*kt)[TK * RK] = reinterpret_cast<float(*)[TK * RK]>(smem);
   float(*vt)[TK * RV] = reinterpret_cast<float(*)[TK * RV]>(smem + KB);
+  __shared__ double xch[NW][4][64];  // partial scores: [wave][r][lane]
   __shared__ double etab[128];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = wave >> 1, dh = wave & 1;  // query group, dim half
   const int col = lane & 15, grp = lane >> 4;
-  const PaLane L = pa_lane(a, wave, col);
+  const PaLane L = pa_lane(a, qg, col);
   if (L.empty) return;  // the whole block: before any barrier
-  double qa[KS];
+  double qa[KS];  // dims dh * HH + grp * KS + s
   {
-    const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + grp * KS;
+    const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + dh * HH + grp * KS;
 #pragma unroll
     for (int s = 0; s < KS; s += 4) {
       const v4f q4 = *reinterpret_cast<const v4f *>(qrow + s);
@@ -425,12 +433,12 @@ __global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
   exp_tab_load(etab);
   const ExpConsts ec = exp_consts();
 
-  // wave w loads key rows w, w+4, ... of the tile at t0 (rows past the
+  // wave w loads key rows w, w + NW, ... of the tile at t0 (rows past the
   // chunk's last key repeat it; their weights are 0)
   auto issue = [&](int t0, int bi) {
 #pragma unroll
-    for (int j = 0; j < TK / kWaves; ++j) {
-      const int t = wave + kWaves * j;
+    for (int j = 0; j < TK / NW; ++j) {
+      const int t = wave + NW * j;
       const size_t at = (size_t)min(t0 + t, L.k_end) * HD + 4 * lane;
       lds_dma16(kc + at, &kt[bi][t * RK]);
       lds_dma16(vc + at, &vt[bi][t * RV]);
@@ -442,41 +450,41 @@ __global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's rows of the tile have landed
     lds_barrier();  // every wave's rows have landed, and the previous tile is done
     if (t0 + TK <= L.k_end) issue(t0 + TK, bi ^ 1);
-    if (t0 > L.w_hi || t0 + TK - 1 < L.w_lo) continue;  // wave-uniform
+    // both waves of a pair hold the same queries: the same decision
+    const bool live = !(t0 > L.w_hi || t0 + TK - 1 < L.w_lo);
     const float *kb = &kt[bi][0];
     const float *vb = &vt[bi][0];
-    // scores of both 16-key blocks in four independent MFMA chains (even
-    // and odd steps of each block, added at the end), so that consecutive
-    // MFMAs do not wait for one another
-    v4d sc[2], sx[2];
+    v4d sc[1];
+    if (live) {
+      v4d s0 = v4d{0.0, 0.0, 0.0, 0.0}, s1 = s0;  // even and odd steps: two chains
 #pragma unroll
-    for (int b = 0; b < 2; ++b) sc[b] = sx[b] = v4d{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-    for (int s = 0; s < KS; s += 4) {
-      const v4f k0 = *reinterpret_cast<const v4f *>(&kb[col * RK + grp * KS + s]);
-      const v4f k1 = *reinterpret_cast<const v4f *>(&kb[(16 + col) * RK + grp * KS + s]);
-#pragma unroll
-      for (int e = 0; e < 4; e += 2) {
-        sc[0] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k0[e], qa[s + e], sc[0], 0, 0, 0);
-        sc[1] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k1[e], qa[s + e], sc[1], 0, 0, 0);
-        sx[0] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k0[e + 1], qa[s + e + 1], sx[0], 0, 0, 0);
-        sx[1] = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k1[e + 1], qa[s + e + 1], sx[1], 0, 0, 0);
+      for (int s = 0; s < KS; s += 4) {
+        const v4f k4 = *reinterpret_cast<const v4f *>(&kb[col * RK + dh * HH + grp * KS + s]);
+        s0 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k4[0], qa[s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k4[1], qa[s + 1], s1, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k4[2], qa[s + 2], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f64_16x16x4f64((double)k4[3], qa[s + 3], s1, 0, 0, 0);
       }
+      sc[0] = s0 + s1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xch[wave][r][lane] = sc[0][r];
     }
+    lds_barrier();  // the pair's partial scores
+    if (!live) continue;
 #pragma unroll
-    for (int b = 0; b < 2; ++b) sc[b] += sx[b];
-    pa_softmax<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o, etab, ec);
-    // value sums: consecutive MFMAs go to different output blocks
+    for (int r = 0; r < 4; ++r) {
+      const double other = xch[wave ^ 1][r][lane];
+      sc[0][r] = dh == 0 ? sc[0][r] + other : other + sc[0][r];
+    }
+    pa_softmax<NB, 1>(a, L, sc, t0, grp, m_ref, l_part, o, etab, ec);
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(
-              (double)vb[(16 * b + 4 * r + grp) * RV + 16 * nb + col], sc[b][r], o[nb], 0, 0, 0);
+      for (int nb = 0; nb < NB; ++nb)
+        o[nb] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+            (double)vb[(4 * r + grp) * RV + dh * HH + 16 * nb + col], sc[0][r], o[nb], 0, 0, 0);
   }
-  // outputs through LDS, so that each query row leaves as one contiguous store
+  // outputs through LDS, so that each query row's half leaves as one contiguous store
   double l = l_part + __shfl_xor(l_part, 16, 64);
   l = l + __shfl_xor(l, 32, 64);
   lds_barrier();  // every wave is done with the K/V buffers
@@ -487,7 +495,7 @@ __global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       ow[col * RO + 16 * nb + 4 * r + grp] = whole ? o[nb][r] / l : o[nb][r];
-  if (!whole && grp == 0 && L.valid) {
+  if (!whole && dh == 0 && grp == 0 && L.valid) {
     const size_t at = (size_t)L.chunk_id * a.n + L.row;
     double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
     ml[0] = m_ref;
@@ -495,19 +503,18 @@ __global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
   }
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's rows are in LDS
   __builtin_amdgcn_wave_barrier();
-  const int hn = a.n_heads / a.nkv, qb = kPaQ / hn;
+  const int hn = a.n_heads / a.nkv, qb = a.qpb / hn;
   for (int q = 0; q < 16; ++q) {
-    const int v = 16 * wave + q;
+    const int v = 16 * qg + q;
     if (v % qb >= L.rows) continue;  // wave-uniform
     const int row = L.r0 + v % qb, head = L.hk * hn + v / qb;
-    const double *src = ow + q * RO + 4 * lane;
+    const double2 x = *reinterpret_cast<const double2 *>(ow + q * RO + 2 * lane);
+    const size_t off = (size_t)head * HD + dh * HH + 2 * lane;
     if (whole) {
-      const v4f out = {(float)src[0], (float)src[1], (float)src[2], (float)src[3]};
-      *reinterpret_cast<v4f *>(a.xo + (size_t)row * a.q_sz + head * HD + 4 * lane) = out;
+      *reinterpret_cast<float2 *>(a.xo + (size_t)row * a.q_sz + off) =
+          float2{(float)x.x, (float)x.y};
     } else {
-      double *dst = a.part + ((size_t)L.chunk_id * a.n + row) * a.q_sz + head * HD + 4 * lane;
-      *reinterpret_cast<double2 *>(dst) = double2{src[0], src[1]};
-      *reinterpret_cast<double2 *>(dst + 2) = double2{src[2], src[3]};
+      *reinterpret_cast<double2 *>(a.part + ((size_t)L.chunk_id * a.n + row) * a.q_sz + off) = x;
     }
   }
 }
@@ -520,7 +527,7 @@ __global__ __launch_bounds__(kNT, 1) void pf_attn_dma_kernel(PfAttn a) {
 __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) {
   __shared__ double wt[kPfMaxMergeHeads][kPfMaxSplit + 1];  // weights, then 1 / denominator
   const int row = blockIdx.x;
-  const int hn = a.n_heads / a.nkv, qb = kPaQ / hn;
+  const int hn = a.n_heads / a.nkv, qb = a.qpb / hn;
   const int r0 = row / qb * qb;
   const int p_last = a.pos0 + min(r0 + qb, a.n) - 1;
   const int p0 = a.pos0 + r0;
@@ -631,10 +638,11 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
 
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
   const int hn = a.n_heads / a.nkv;
-  if (hn <= 0 || kPaQ % hn != 0 || a.n <= 0 || a.part == nullptr ||
+  const int qpb = hdim == 256 ? kPaQPair : kPaQ;
+  if (hn <= 0 || qpb % hn != 0 || a.n <= 0 || a.part == nullptr ||
       a.n_heads > kPfMaxMergeHeads)
     return hipErrorInvalidValue;
-  const int qb = kPaQ / hn, nrb = (a.n + qb - 1) / qb;
+  const int qb = qpb / hn, nrb = (a.n + qb - 1) / qb;
   // the longest key range of a row block
   int kmax = 0;
   for (int rb = 0; rb < nrb; ++rb) {
@@ -647,12 +655,14 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
   const int want = (2048 + nrb * a.nkv - 1) / (nrb * a.nkv);
   const int split = std::max(1, std::min({kPfMaxSplit, want, (kmax + kPaKeys - 1) / kPaKeys}));
   PfAttn b = a;
+  b.qpb = qpb;
   b.chunk = ((kmax + split - 1) / split + kPaKeys - 1) / kPaKeys * kPaKeys;
   b.nsplit = (kmax + b.chunk - 1) / b.chunk;
   const dim3 grid(nrb * b.nsplit * a.nkv);
   switch (hdim) {
     case 128: pf_attn_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
-    case 256: pf_attn_dma_kernel<256><<<grid, kNT, 0, stream>>>(b); break;
+    case 256: pf_attn_pair_kernel<256, kPaPairWaves><<<grid, kPaPairWaves * 64, 0, stream>>>(b);
+      break;
     default: return hipErrorInvalidValue;
   }
   if (b.nsplit > 1) pf_attn_merge_kernel<<<a.n, kNT, 0, stream>>>(b, hdim);
