@@ -689,16 +689,18 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
   const bool vec = rows_aligned(jobs, k, 1, 16);
   const size_t lds = (size_t)(k + 15) / 16 * 16;
   const bool fused = xf != nullptr;
-  // Measured on MI355X (1b and 4b decode shapes): up to ~2048 rows the
+  // Measured on MI355X (1b and 4b decode shapes): up to ~4096 rows the
   // launch is latency-bound and one row per wave with every load issued up
-  // front wins (q/k/v/o, and down with its 6912-byte rows); above that the
-  // looping kernel's 8 rows per wave amortise the per-row reduction better.
+  // front wins (q/k/v/o, and down with its 6912-byte rows; the 4b o
+  // projection's 2560 rows: decoder 604 -> 607 tok/s); above that the
+  // streaming kernel's groups amortise the per-row reduction better.
   // Long rows (k >= 4096) with few of them are latency-bound on the x
   // prologue: 1024-thread workgroups pay it 4x less often (measured on the
-  // 1b/4b down projections: 8.8 -> 7.9 us and 13.9 -> 10.2 us).
+  // 1b/4b down projections: 8.8 -> 7.9 us and 13.9 -> 10.2 us; the stream
+  // kernel there: 4b decoder 604 -> 544 tok/s).
   const bool long_rows = k >= 4096 && total <= 4096;
   const bool pipelined =
-      tuning().lanes > 0 || tuning().threads > 0 || total <= 2048 || long_rows;
+      tuning().lanes > 0 || tuning().threads > 0 || total <= 4096 || long_rows;
   if (vec && pipelined && !tuning().force_loop) {
     const int kc = k / 16;
     const int lanes = tuning().lanes > 0 ? tuning().lanes : 64;
