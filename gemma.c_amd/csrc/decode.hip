@@ -320,7 +320,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
   float *q = reinterpret_cast<float *>(e + hn * kAttB);     // [hn][hd]
   float *kn = q + hn * hd;                                  // [hd]
   float *vn = kn + hd;                                      // [hd]
-  constexpr int KS = HD + 4;  // padded K rows: the score reads hit distinct banks
+  constexpr int KS = HD + 16;  // padded K rows: four rows of 16-byte score reads hit distinct banks
   float *kt = vn + hd;                                      // [kAttB][KS]
   float *vt = kt + kAttB * KS;                              // [kAttB][hd]
   const float *cs = a.rope + (size_t)pos * hd;              // cos, sin interleaved
@@ -427,20 +427,24 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
     }
   lds_barrier();
 
-  // scores: four threads per (head, key) pair, each summing every fourth
-  // element of the head dimension, then a quad reduction
+  // scores: four threads per (head, key) pair; thread c of the quad sums the
+  // 16-byte chunks c, c + 4, c + 8, ... of the head dimension, then a quad
+  // reduction
   const int npair = hn * nt;
   for (int p0 = 0; p0 < npair; p0 += kNT / 4) {
     const int pr = p0 + (tid >> 2), c = tid & 3;
     double a0 = 0.0, a1 = 0.0;
     if (pr < npair) {
       const int g = pr / nt, t = pr - g * nt;
-      const float *qg = q + g * hd + c;
-      const float *kr = kt + t * KS + c;
-#pragma unroll 8
-      for (int i = 0; i < HD / 4; i += 2) {
-        a0 += (double)qg[4 * i] * (double)kr[4 * i];
-        a1 += (double)qg[4 * i + 4] * (double)kr[4 * i + 4];
+      const v4f *qg = reinterpret_cast<const v4f *>(q + g * hd) + c;
+      const v4f *kr = reinterpret_cast<const v4f *>(kt + t * KS) + c;
+#pragma unroll 4
+      for (int i = 0; i < HD / 16; ++i) {
+        const v4f x = qg[4 * i], y = kr[4 * i];
+        a0 += (double)x[0] * (double)y[0];
+        a1 += (double)x[1] * (double)y[1];
+        a0 += (double)x[2] * (double)y[2];
+        a1 += (double)x[3] * (double)y[3];
       }
     }
     double part = a0 + a1;
@@ -473,39 +477,48 @@ __global__ __launch_bounds__(kNT) void dec_attn_kernel(DecAttn a) {
     l += dpp_f64<kDppXor2>(l);
     l += dpp_f64<kDppHalfMirror>(l);
     l += dpp_f64<kDppMirror>(l);
-    if (live) e[g * kAttB + lane] = x;
+    if (lane < kAttB) e[g * kAttB + lane] = x;  // zero past nt
     if (lane == 0) {
       out_base[g * head_stride + hd] = m;
       out_base[g * head_stride + hd + 1] = l;
     }
   }
   lds_barrier();
-  // value sums: thread d, every head of the group, four chains over the keys
+  // value sums: thread d holds the block's values of dimension d (zero past
+  // nt, where the weights are zero too) and sums them for every head of the
+  // group, four chains over the keys
   for (int d = tid; d < hd; d += kNT) {
+    double v[kAttB];
+#pragma unroll
+    for (int t = 0; t < kAttB; ++t) v[t] = t < nt ? (double)vt[t * hd + d] : 0.0;
     for (int g = 0; g < hn; ++g) {
-      const double *eg = e + g * kAttB;
+      const double2 *eg = reinterpret_cast<const double2 *>(e + g * kAttB);
       double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-      int t = 0;
-      for (; t + 4 <= nt; t += 4) {
-        a0 += eg[t] * (double)vt[t * hd + d];
-        a1 += eg[t + 1] * (double)vt[(t + 1) * hd + d];
-        a2 += eg[t + 2] * (double)vt[(t + 2) * hd + d];
-        a3 += eg[t + 3] * (double)vt[(t + 3) * hd + d];
+#pragma unroll
+      for (int t = 0; t < kAttB; t += 4) {
+        const double2 e01 = eg[t / 2], e23 = eg[t / 2 + 1];
+        a0 += e01.x * v[t];
+        a1 += e01.y * v[t + 1];
+        a2 += e23.x * v[t + 2];
+        a3 += e23.y * v[t + 3];
       }
-      for (; t < nt; ++t) a0 += eg[t] * (double)vt[t * hd + d];
       out_base[g * head_stride + d] = (a0 + a1) + (a2 + a3);
     }
   }
 }
 
 // xo[h] = sum_b exp(m_b - M) acc_b / sum_b exp(m_b - M) l_b: grid (n_heads,
-// hdim / 64).  Every workgroup of a head computes the block weights
-// exp(m_b - M) into LDS and the denominator (the same bits in each, a fixed
-// order); its 256 threads then split its 64 dimensions into 16 quads and the
-// blocks into 16 strided groups, so the partials are read 16 blocks at a
-// time rather than one after another, and the 16 group sums are added in
-// group order.
+// hdim / 64).  The 256 threads of a workgroup split its 64 dimensions into
+// 16 quads and the blocks into 16 strided groups.  At the start every thread
+// issues the loads of block tid's (m, l) and of the acc values of up to
+// kCombBatch of its group's blocks, so that (for up to 16 * kCombBatch
+// blocks) the combine waits for memory once.  Then: M = the block-wide max
+// of m; thread b computes the block weight exp(m_b - M) into LDS (the same
+// bits in every workgroup of the head) and the denominator is summed; each
+// thread sums its blocks' weighted acc values, and the 16 group sums are
+// added in group order.
 constexpr int kCombGroups = 16;
+constexpr int kCombBatch = 12;
 
 __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   extern __shared__ double wts[];
@@ -518,8 +531,29 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   const int nb = (pos + 1 - spos + kAttB - 1) / kAttB;
   const int stride = hd + 2;
   const double *p = a.part + (size_t)h * a.max_blocks * stride;
-  double m = -DBL_MAX;
-  for (int b = tid; b < nb; b += kNT) m = fmax(m, p[(size_t)b * stride + hd]);
+  const int g = tid / 16, q = tid % 16;
+  const int d = blockIdx.y * 64 + 4 * q;
+  const bool dv = d < hd;
+  // (m, l) of blocks tid and tid + 256, then this group's first kCombBatch
+  // blocks' acc values (indices clamped in range; values past nb unused)
+  constexpr int kMl = 2;
+  double mb[kMl], lb[kMl];
+#pragma unroll
+  for (int u = 0; u < kMl; ++u) {
+    const int b = tid + u * kNT;
+    const double *pb = p + (size_t)min(b, nb - 1) * stride;
+    mb[u] = b < nb ? pb[hd] : -DBL_MAX;
+    lb[u] = pb[hd + 1];
+  }
+  double2 x01[kCombBatch], x23[kCombBatch];
+#pragma unroll
+  for (int u = 0; u < kCombBatch; ++u) {
+    const double *pb = p + (size_t)min(g + u * kCombGroups, nb - 1) * stride;
+    x01[u] = dv ? *reinterpret_cast<const double2 *>(pb + d) : double2{0.0, 0.0};
+    x23[u] = dv ? *reinterpret_cast<const double2 *>(pb + d + 2) : double2{0.0, 0.0};
+  }
+  double m = fmax(mb[0], mb[1]);
+  for (int b = tid + kMl * kNT; b < nb; b += kNT) m = fmax(m, p[(size_t)b * stride + hd]);
   m = fmax(m, dpp_f64<kDppXor1>(m));
   m = fmax(m, dpp_f64<kDppXor2>(m));
   m = fmax(m, dpp_f64<kDppHalfMirror>(m));
@@ -532,25 +566,41 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
 #pragma unroll
   for (int w = 1; w < kWaves; ++w) m = fmax(m, red[w]);
   double den = 0.0;
-  for (int b = tid; b < nb; b += kNT) {
+#pragma unroll
+  for (int u = 0; u < kMl; ++u) {
+    const int b = tid + u * kNT;
+    if (b < nb) {
+      const double w = exp(mb[u] - m);
+      wts[b] = w;
+      den += w * lb[u];
+    }
+  }
+  for (int b = tid + kMl * kNT; b < nb; b += kNT) {
     const double w = exp(p[(size_t)b * stride + hd] - m);
     wts[b] = w;
     den += w * p[(size_t)b * stride + hd + 1];
   }
-  den = block_sum(den, red);  // ends with a barrier: wts is complete
-  // thread (group g, quad q): dims d0 + 4q .. d0 + 4q + 3 over blocks g, g + 16, ...
-  const int g = tid / 16, q = tid % 16;
-  const int d = blockIdx.y * 64 + 4 * q;
+  den = block_sum(den, red);  // its first barrier orders the reads of red above; ends with a barrier: wts is complete
   double2 s01 = {0.0, 0.0}, s23 = {0.0, 0.0};
-  if (d < hd)
-    for (int b = g; b < nb; b += kCombGroups) {
+#pragma unroll
+  for (int u = 0; u < kCombBatch; ++u) {
+    const int b = g + u * kCombGroups;
+    if (b >= nb) break;
+    const double w = wts[b];
+    s01.x += w * x01[u].x;
+    s01.y += w * x01[u].y;
+    s23.x += w * x23[u].x;
+    s23.y += w * x23[u].y;
+  }
+  if (dv)  // blocks past the first batch (long contexts): one more round trip each batch
+    for (int b = g + kCombBatch * kCombGroups; b < nb; b += kCombGroups) {
       const double w = wts[b];
-      const double2 x01 = *reinterpret_cast<const double2 *>(p + (size_t)b * stride + d);
-      const double2 x23 = *reinterpret_cast<const double2 *>(p + (size_t)b * stride + d + 2);
-      s01.x += w * x01.x;
-      s01.y += w * x01.y;
-      s23.x += w * x23.x;
-      s23.y += w * x23.y;
+      const double2 y01 = *reinterpret_cast<const double2 *>(p + (size_t)b * stride + d);
+      const double2 y23 = *reinterpret_cast<const double2 *>(p + (size_t)b * stride + d + 2);
+      s01.x += w * y01.x;
+      s01.y += w * y01.y;
+      s23.x += w * y23.x;
+      s23.y += w * y23.y;
     }
   gsum[g][2 * q] = s01;
   gsum[g][2 * q + 1] = s23;

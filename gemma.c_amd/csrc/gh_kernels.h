@@ -109,7 +109,7 @@ struct DecEmbed {
 constexpr int kDecAttnBlock = 16;
 inline size_t dec_attn_lds(int hn, int hdim) {
   return (size_t)hn * kDecAttnBlock * 8 +
-         ((size_t)hn * hdim + 2 * (size_t)hdim + (size_t)kDecAttnBlock * (2 * hdim + 4)) * 4;
+         ((size_t)hn * hdim + 2 * (size_t)hdim + (size_t)kDecAttnBlock * (2 * hdim + 16)) * 4;
 }
 
 // One layer's attention: q/k/v rows in, xo out; kc/vc are the layer's cache
