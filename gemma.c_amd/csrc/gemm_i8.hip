@@ -323,7 +323,7 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 template <int WM, int WN, int S, int BKB, bool HEADS>
-__global__ __launch_bounds__(kThreads, 2) void gemm_i8_dma_kernel(
+__global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
     float *__restrict__ dst, int dstr, int hdim, GemmSegs bs, int mstr,
     const int8_t *__restrict__ src, int sstr, const float *__restrict__ ssc, int m, int k) {
   constexpr int kBM = 64 * WM;
@@ -359,12 +359,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_i8_dma_kernel(
   const int c0 = sj == 0 ? 0 : bs.end[sj - 1];
   const int8_t *mat = bs.w[sj];
   const int nb = bs.end[sj] - c0;
-  // 4x2 wave tiles need their registers for the K loop: their scales are
-  // loaded after it
-  constexpr bool kLateScales = WM * WN >= 8;
-  const float *wsc = bs.s[sj] - c0;
   TileScales<WM, WN> scales;
-  if (!kLateScales) load_tile_scales<WM, WN>(scales, ssc, wsc, m, n, m0, n0, wm, wn, lane);
+  load_tile_scales<WM, WN>(scales, ssc, bs.s[sj] - c0, m, n, m0, n0, wm, wn, lane);
 
   const __amdgpu_buffer_rsrc_t rs_a = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int8_t *>(src), (short)0, (int)((uint32_t)(m - 1) * sstr + k), 0x00020000);
@@ -448,7 +444,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_i8_dma_kernel(
   }
 
   // epilogue: rescale and store (gemma.c:3854-3865)
-  if (kLateScales) load_tile_scales<WM, WN>(scales, ssc, wsc, m, n, m0, n0, wm, wn, lane);
   store_tile<WM, WN, HEADS>(acc, scales, dst, dstr, hdim, m, n, m0, n0, wm, wn, lane);
 }
 
@@ -560,8 +555,6 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
       case 224: launch_dma<2, 2, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
       case 223: launch_dma<2, 2, 3>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
       case 226: launch_dma<2, 2, 6>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
-      case 423: launch_dma<4, 2, 3>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
-      case 243: launch_dma<2, 4, 3>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
       case 424: launch_dma<4, 2, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
       case 244: launch_dma<2, 4, 4>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
       case 2221: launch_dma<2, 2, 2, 128>(heads, stream, dst, dstr, hdim, mat, mstr, matsc, src, sstr, ssc, m, n, k); break;
