@@ -25,8 +25,12 @@
 //    used when an operand is too large for 32-bit buffer offsets.
 //  - gemm_i8_generic_kernel: one thread per output, any shape/alignment.
 // Tile choice and the measurements behind it are in launch_gemm_i8.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "gh_arith.h"
 #include "gh_kernels.h"
@@ -322,10 +326,25 @@ __device__ __forceinline__ void block_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int WM, int WN, int S, int BKB, bool HEADS>
+// Split-K (SK): workgroup b computes the K stages [s nk / splits, (s + 1) nk /
+// splits) of tile b % tiles, s = b / tiles.  Each writes its int32 partial
+// tile to the workspace, waits for the writes to complete, and (after a
+// barrier) counts itself in with one atomic add on the tile's counter; the
+// workgroup that arrives last adds the other partials to its own, runs the
+// epilogue and resets the counter for the next launch on the stream.  Integer sums
+// are exact, so the result is bit-identical to the unsplit kernel.  No
+// workgroup ever waits for another.
+struct SplitK {
+  int splits;
+  int *ws;   // [tiles][splits][kThreads * WM * WN * 16] int32
+  int *cnt;  // [tiles], zero between launches
+};
+
+template <int WM, int WN, int S, int BKB, bool HEADS, bool SK>
 __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
     float *__restrict__ dst, int dstr, int hdim, GemmSegs bs, int mstr,
-    const int8_t *__restrict__ src, int sstr, const float *__restrict__ ssc, int m, int k) {
+    const int8_t *__restrict__ src, int sstr, const float *__restrict__ ssc, int m, int k,
+    SplitK sk) {
   constexpr int kBM = 64 * WM;
   constexpr int kBN = 64 * WN;
   constexpr int kC = BKB / 16;                 // 16-byte chunks per row and stage
@@ -346,8 +365,11 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
   const int wm = wave >> 1;
   const int wn = wave & 1;
   const int n = bs.end[bs.nseg - 1];
+  const int tiles_m = (m + kBM - 1) / kBM, tiles_n = (n + kBN - 1) / kBN;
+  const int tile = SK ? (int)(blockIdx.x % (unsigned)(tiles_m * tiles_n)) : (int)blockIdx.x;
+  const int sidx = SK ? (int)(blockIdx.x / (unsigned)(tiles_m * tiles_n)) : 0;
   int tm, tn;
-  tile_of(blockIdx.x, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, &tm, &tn);
+  tile_of(tile, tiles_m, tiles_n, &tm, &tn);
   const int m0 = tm * kBM;
   const int n0 = tn * kBN;
   // the B matrix of this tile's columns (inner segment ends are multiples of
@@ -402,10 +424,12 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v16i{};
 
-  const int nk = (k + BKB - 1) / BKB;
+  const int nk_all = (k + BKB - 1) / BKB;
+  const int kbeg = SK ? (int)((long)sidx * nk_all / sk.splits) : 0;
+  const int nk = (SK ? (int)((long)(sidx + 1) * nk_all / sk.splits) : nk_all) - kbeg;
 #pragma unroll
   for (int st = 0; st < S - 1; ++st)
-    if (st < nk) issue(st, st);
+    if (st < nk) issue(kbeg + st, st);
 
   const int frag_row = lane & 31;
   const int frag_chunk = lane >> 5;
@@ -426,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
     const int ahead = min(S - 2, nk - 1 - kt);
     wait_ahead<kPerWave, S - 2>(ahead);
     block_barrier();
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    if (kt + S - 1 < nk) issue(kbeg + kt + S - 1, (kt + S - 1) % S);
     const v4i *stage = lds[kt % S];
     // fragments of sub-step ks+1 are read while the MFMAs of ks run
     v4i a[2][WM], b[2][WN];
@@ -443,6 +467,43 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
     }
   }
 
+  if constexpr (SK) {
+    if (sk.splits > 1) {
+      // Partials go out and come back in with device-coherent (agent-scope)
+      // accesses, which write through and read past this XCD's L2; no cache
+      // maintenance is needed, which matters: invalidating the L2 here would
+      // also evict the operands of every other workgroup on the XCD.
+      constexpr int kTileInts = kThreads * WM * WN * 16;
+      int *mine = sk.ws + ((size_t)tile * sk.splits + sidx) * kTileInts;
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            __hip_atomic_store(mine + ((i * WN + j) * 16 + r) * kThreads + tid, acc[i][j][r],
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __shared__ int last;
+      wait_vmcnt<0>();  // this thread's partial has reached the coherence point
+      __syncthreads();
+      if (tid == 0) last = atomicAdd(sk.cnt + tile, 1) == sk.splits - 1;
+      __syncthreads();
+      if (!last) return;
+      for (int o = 0; o < sk.splits; ++o) {
+        if (o == sidx) continue;
+        const int *other = sk.ws + ((size_t)tile * sk.splits + o) * kTileInts;
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              acc[i][j][r] += __hip_atomic_load(other + ((i * WN + j) * 16 + r) * kThreads + tid,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (tid == 0) sk.cnt[tile] = 0;
+    }
+  }
   // epilogue: rescale and store (gemma.c:3854-3865)
   store_tile<WM, WN, HEADS>(acc, scales, dst, dstr, hdim, m, n, m0, n0, wm, wn, lane);
 }
@@ -492,12 +553,99 @@ void launch_dma_segs(bool heads, hipStream_t stream, float *dst, int dstr, int h
                      const float *ssc, int m, int k) {
   const int n = bs.end[bs.nseg - 1];
   const int tiles = ((m + 64 * WM - 1) / (64 * WM)) * ((n + 64 * WN - 1) / (64 * WN));
+  const SplitK none{1, nullptr, nullptr};
   if (heads)
-    gemm_i8_dma_kernel<WM, WN, S, BKB, true><<<tiles, kThreads, 0, stream>>>(
-        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k);
+    gemm_i8_dma_kernel<WM, WN, S, BKB, true, false><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, none);
   else
-    gemm_i8_dma_kernel<WM, WN, S, BKB, false><<<tiles, kThreads, 0, stream>>>(
-        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k);
+    gemm_i8_dma_kernel<WM, WN, S, BKB, false, false><<<tiles, kThreads, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, none);
+}
+
+// Split-K workspace and tile counters, one set per (device, stream): launches
+// on one stream run in order, so they can share it.  Grown (never shrunk) on
+// demand; the counters start at zero and every launch leaves them at zero.
+struct SplitWs {
+  int *ws = nullptr, *cnt = nullptr;
+  size_t ws_ints = 0;
+  int ncnt = 0;
+};
+std::mutex g_split_mu;
+std::map<std::pair<int, hipStream_t>, SplitWs> g_split;
+
+hipError_t split_ws(hipStream_t stream, size_t ws_ints, int ncnt, SplitK *sk) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  SplitWs &w = g_split[{dev, stream}];
+  if (w.ws_ints < ws_ints || w.ncnt < ncnt) {
+    // launches already queued on the stream may still use the old buffers
+    if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+    if (w.ws_ints < ws_ints) {
+      if (w.ws != nullptr && (e = hipFree(w.ws)) != hipSuccess) return e;
+      w.ws = nullptr;
+      w.ws_ints = 0;
+      if ((e = hipMalloc(&w.ws, ws_ints * sizeof(int))) != hipSuccess) return e;
+      w.ws_ints = ws_ints;
+    }
+    if (w.ncnt < ncnt) {
+      if (w.cnt != nullptr && (e = hipFree(w.cnt)) != hipSuccess) return e;
+      w.cnt = nullptr;
+      w.ncnt = 0;
+      if ((e = hipMalloc(&w.cnt, ncnt * sizeof(int))) != hipSuccess) return e;
+      if ((e = hipMemsetAsync(w.cnt, 0, ncnt * sizeof(int), stream)) != hipSuccess) return e;
+      w.ncnt = ncnt;
+    }
+  }
+  sk->ws = w.ws;
+  sk->cnt = w.cnt;
+  return hipSuccess;
+}
+
+// GEMMA_HIP_GEMM_SPLIT=s forces s-way split-K on the 128x128 kernel (a
+// launch-shape knob like GEMMA_HIP_GEMM_TILE; read at every launch, so a
+// process can change it); 0 or unset = the cost model.
+int env_split() {
+  const char *e = getenv("GEMMA_HIP_GEMM_SPLIT");
+  return e == nullptr ? 0 : atoi(e);
+}
+
+// 128x128 tiles, two 128-byte stages, split-K over `splits` workgroups per
+// tile (splits >= 2, at most the number of K stages).
+hipError_t launch_dma_split(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
+                            const GemmSegs &bs, int mstr, const int8_t *src, int sstr,
+                            const float *ssc, int m, int k, int splits) {
+  const int n = bs.end[bs.nseg - 1];
+  const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  SplitK sk{splits, nullptr, nullptr};
+  hipError_t e = split_ws(stream, (size_t)tiles * splits * kThreads * 4 * 16, tiles, &sk);
+  if (e != hipSuccess) return e;
+  if (heads)
+    gemm_i8_dma_kernel<2, 2, 2, 128, true, true><<<tiles * splits, kThreads, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, sk);
+  else
+    gemm_i8_dma_kernel<2, 2, 2, 128, false, true><<<tiles * splits, kThreads, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, sk);
+  return hipGetLastError();
+}
+
+// Splits for the 128x128 kernel (1 = none).  Measured on MI355X, the partial
+// tiles' round trip through memory costs about as much as 15 K stages, so a
+// split pays only when the grid leaves most CUs idle and K is long: gemma-3-1b
+// down at 512 tokens (36 tiles, 54 stages) goes from 253 to 348 TOPS with 6
+// splits, while every gemma-3-4b and SigLIP shape (>= 128 tiles) lost 15-60%.
+int choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t stream) {
+  const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  const int nk = (k + 127) / 128;
+  const int forced = env_split();
+  if (forced > 0) return forced > nk ? nk : forced;
+  if (tiles * 4 > dev.cus || nk < 32) return 1;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+    return 1;  // the workspace may have to be allocated: not under capture
+  const int s = std::min(std::min(8, dev.cus / tiles), nk / 8);
+  return s >= 2 ? s : 1;
 }
 
 template <int WM, int WN, int S, int BKB = 64>
@@ -543,6 +691,18 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
                       ((uint64_t)(m - 1) * dstr + n) * 4 < kOob;
   if (fast) {
     int tile = env_tile();
+    if (tile == 0 && dma_ok) {
+      const int sp = choose_split(m, n, k, dev, stream);
+      if (sp > 1) {
+        GemmSegs bs{};
+        bs.w[0] = mat;
+        bs.s[0] = matsc;
+        bs.end[0] = n;
+        bs.nseg = 1;
+        return launch_dma_split(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k,
+                                sp);
+      }
+    }
     if (tile == 0) {
       // measured on MI355X at the 1b/4b prefill and SigLIP shapes: 128x128
       // tiles with two 128-byte K stages are fastest once there is a tile
@@ -594,11 +754,14 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
   if (fast && dma_ok && env_tile() == 0) {
     // the tile choice of launch_gemm_i8 for the whole width
     const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
-    const bool wide = tiles128 >= dev.cus;
+    const int sp = choose_split(m, n, k, dev, stream);
+    const bool wide = sp > 1 || tiles128 >= dev.cus;
     const int bn = wide ? 128 : 64;
     bool aligned = true;
     for (int t = 0; t + 1 < b.nseg; ++t) aligned = aligned && b.end[t] % bn == 0;
     if (aligned) {
+      if (sp > 1)
+        return launch_dma_split(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k, sp);
       if (wide)
         launch_dma_segs<2, 2, 2, 128>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
       else

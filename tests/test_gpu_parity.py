@@ -273,6 +273,36 @@ def test_gemm_heads_vs_oracle(gh, oracle):
     assert np.array_equal(bits(host(dst)), bits(np.ascontiguousarray(ref)))
 
 
+@pytest.mark.parametrize("splits", [2, 3, 7])
+def test_gemm_split_k(gh, oracle, monkeypatch, splits):
+    """Split-K (int32 partials summed by the last workgroup of a tile) forced
+    on ragged shapes: M, N and K (9 stages of 128 bytes, the last partial)
+    off the tile grid, uneven stage ranges, row-major and head-major outputs;
+    two launches in a row reuse the tile counters."""
+    monkeypatch.setenv("GEMMA_HIP_GEMM_SPLIT", str(splits))
+    rng = np.random.default_rng(40 + splits)
+    m, n, k = 300, 200, 1040
+    A = outlier_acts(rng, (m, k))
+    qo, so = oracle.quantize_acts(A)
+    for rep in range(2):
+        B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+        bs = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+        dst = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        gh.matmul(dst, n, dev(B), k, dev(bs), dev(qo), k, dev(so), m, n, k, stream())
+        ref, _ = oracle.gemm_int8(B, bs, qo, so)
+        assert np.array_equal(bits(host(dst)), bits(ref)), f"launch {rep}"
+    heads, hdim, kh = 4, 256, 1152
+    Ah = outlier_acts(rng, (m, kh))
+    qh, sh = oracle.quantize_acts(Ah)
+    B = rng.integers(-127, 128, (heads * hdim, kh), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, heads * hdim).astype(np.float32)
+    dst = torch.empty((heads, m, hdim), dtype=torch.float32, device="cuda")
+    gh.matmul_heads(dst, dev(B), dev(bs), dev(qh), dev(sh), m, heads, hdim, kh, stream())
+    ref, _ = oracle.gemm_int8(B, bs, qh, sh)
+    ref = ref.reshape(m, heads, hdim).transpose(1, 0, 2)
+    assert np.array_equal(bits(host(dst)), bits(np.ascontiguousarray(ref)))
+
+
 # --------------------------------------------------------------- fp32
 def check_f32(got, mat, src, oracle):
     exact, mag = oracle.gemm_f64(mat, src)
