@@ -452,6 +452,11 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
     block_barrier();
     if (kt + S - 1 < nk) issue(kbeg + kt + S - 1, (kt + S - 1) % S);
     const v4i *stage = lds[kt % S];
+    // interleave the fragment reads with the MFMAs (the compiler's default
+    // order issues the reads of sub-step ks+1 after the MFMAs of ks and
+    // waits on them): 128x128 tiles measured +7% at gemma-3-4b down, +5% at
+    // o, -2% at gate/up
+    __builtin_amdgcn_iglp_opt(0);
     // fragments of sub-step ks+1 are read while the MFMAs of ks run
     v4i a[2][WM], b[2][WN];
     load_frags(stage, 0, a[0], b[0]);
