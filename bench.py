@@ -473,9 +473,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=2.0,
                     help="CPU-baseline sample time per sweep shape")
-    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder", "vision"], default=None,
+    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder", "vision", "gemm"],
+                    default=None,
                     help="profiling aid: run just the timed sweep, the LM-head timing, "
-                         "the device-resident decoder or the vision tower")
+                         "the device-resident decoder, the vision tower or the GEMM shapes")
     ap.add_argument("--decoder-models", default="gemma-3-270m,gemma-3-1b,gemma-3-4b",
                     help="models of the decoder timing (comma list of gemma-3-270m, "
                          "gemma-3-1b, gemma-3-4b)")
@@ -517,6 +518,10 @@ def main() -> int:
     gen = torch.Generator(device="cuda")
     gen.manual_seed(1234)
     timer = Timer(torch)
+    if args.only == "gemm":
+        print(json.dumps(bench_gemm(torch, gh, gen, timer, reps=10)), flush=True)
+        gh.close()
+        return 0
     shapes = build_sweep(torch, gh, gen)
     step_bytes = sum(sh["bytes"] for sh in shapes)
     lm = shapes[-1]
