@@ -608,6 +608,19 @@ hipError_t split_ws(hipStream_t stream, size_t ws_ints, int ncnt, SplitK *sk) {
   return hipSuccess;
 }
 
+}  // namespace
+
+void release_gemm_workspaces() {
+  std::lock_guard<std::mutex> lock(g_split_mu);
+  for (auto &kv : g_split) {  // hipFree waits for the device's queued work
+    if (kv.second.ws != nullptr) (void)hipFree(kv.second.ws);
+    if (kv.second.cnt != nullptr) (void)hipFree(kv.second.cnt);
+  }
+  g_split.clear();
+}
+
+namespace {
+
 // GEMMA_HIP_GEMM_SPLIT=s forces s-way split-K on the 128x128 kernel (a
 // launch-shape knob like GEMMA_HIP_GEMM_TILE; read at every launch, so a
 // process can change it); 0 or unset = the cost model.

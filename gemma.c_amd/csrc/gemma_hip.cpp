@@ -285,6 +285,7 @@ int gemma_hip_init(int device) {
 void gemma_hip_shutdown(void) {
   if (!g.ready) return;
   (void)hipStreamSynchronize(g.stream);
+  gh::release_gemm_workspaces();
   {
     std::lock_guard<std::mutex> guard(g.lock);
     for (auto &kv : g.regions) (void)hipFree(kv.second.device);

@@ -63,6 +63,9 @@ struct GemmSegs {
 };
 // One launch over all segments when every inner segment boundary is a
 // multiple of the tile width; otherwise one launch per segment.
+// Frees the split-K workspaces of every (device, stream) (library shutdown).
+void release_gemm_workspaces();
+
 hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const int8_t *src,
                                int sstr, const float *ssc, int m, int k, const DeviceInfo &dev,
                                hipStream_t stream);
