@@ -676,12 +676,19 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
 
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
                                 hipStream_t stream) {
-  constexpr int NT = 1024;
-  const int npt = (mlp / 4 + NT - 1) / NT;
-  return by_npt<1, kPfMaxNpt>(npt, [&](auto c) {
-    pf_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(g, mlp, xq, xs);
-    return hipGetLastError();
-  });
+  // the fewest threads per row that cover it in kPfMaxNpt chunks (fewer idle
+  // slots: gemma-3-4b's 10240 columns take 512 threads x 5 chunks exactly)
+  const int n4 = mlp / 4;
+  auto go = [&](auto nt) {
+    constexpr int NT = decltype(nt)::value;
+    return by_npt<1, kPfMaxNpt>((n4 + NT - 1) / NT, [&](auto c) {
+      pf_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(g, mlp, xq, xs);
+      return hipGetLastError();
+    });
+  };
+  if ((n4 + 255) / 256 <= kPfMaxNpt) return go(std::integral_constant<int, 256>{});
+  if ((n4 + 511) / 512 <= kPfMaxNpt) return go(std::integral_constant<int, 512>{});
+  return go(std::integral_constant<int, 1024>{});
 }
 
 }  // namespace gh

@@ -473,11 +473,20 @@ hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream) 
 
 hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int mlp, int8_t *xq,
                                  float *xs, hipStream_t stream) {
-  constexpr int NT = 1024;
-  return by_npt<1, kPfMaxNpt>((mlp / 4 + NT - 1) / NT, [&](auto c) {
-    vis_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(h, bias, mlp, xq, xs);
-    return hipGetLastError();
-  });
+  // the fewest threads per row that cover it in kPfMaxNpt chunks: at SigLIP's
+  // 4304 columns, 256 threads leave 16% of the slots empty, 1024 threads 47%
+  // (54.7 -> 36.7 us per layer measured)
+  const int n4 = mlp / 4;
+  auto go = [&](auto nt) {
+    constexpr int NT = decltype(nt)::value;
+    return by_npt<1, kPfMaxNpt>((n4 + NT - 1) / NT, [&](auto c) {
+      vis_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(h, bias, mlp, xq, xs);
+      return hipGetLastError();
+    });
+  };
+  if ((n4 + 255) / 256 <= kPfMaxNpt) return go(std::integral_constant<int, 256>{});
+  if ((n4 + 511) / 512 <= kPfMaxNpt) return go(std::integral_constant<int, 512>{});
+  return go(std::integral_constant<int, 1024>{});
 }
 
 hipError_t launch_vis_pool(const VisPool &a, int ntok, hipStream_t stream) {
