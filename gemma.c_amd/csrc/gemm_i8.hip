@@ -658,7 +658,7 @@ int choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t stream)
   const int nk = (k + 127) / 128;
   const int forced = env_split();
   if (forced > 0) return forced > nk ? nk : forced;
-  if (tiles * 4 > dev.cus || nk < 32) return 1;
+  if (tiles <= 0 || tiles * 4 > dev.cus || nk < 32) return 1;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
     return 1;  // the workspace may have to be allocated: not under capture
