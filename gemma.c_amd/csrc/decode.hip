@@ -580,7 +580,9 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
     wts[b] = w;
     den += w * p[(size_t)b * stride + hd + 1];
   }
-  den = block_sum(den, red);  // its first barrier orders the reads of red above; ends with a barrier: wts is complete
+  // block_sum's first barrier orders the reads of red above before red is
+  // reused; its last one makes wts complete
+  den = block_sum(den, red);
   double2 s01 = {0.0, 0.0}, s23 = {0.0, 0.0};
 #pragma unroll
   for (int u = 0; u < kCombBatch; ++u) {

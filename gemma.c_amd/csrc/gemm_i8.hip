@@ -331,9 +331,9 @@ __device__ __forceinline__ void block_barrier() {
 // tile to the workspace, waits for the writes to complete, and (after a
 // barrier) counts itself in with one atomic add on the tile's counter; the
 // workgroup that arrives last adds the other partials to its own, runs the
-// epilogue and resets the counter for the next launch on the stream.  Integer sums
-// are exact, so the result is bit-identical to the unsplit kernel.  No
-// workgroup ever waits for another.
+// epilogue and resets the counter for the next launch on the stream.
+// Integer sums are exact, so the result is bit-identical to the unsplit
+// kernel.  No workgroup ever waits for another.
 struct SplitK {
   int splits;
   int *ws;   // [tiles][splits][kThreads * WM * WN * 16] int32
