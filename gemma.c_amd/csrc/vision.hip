@@ -77,10 +77,10 @@ __global__ __launch_bounds__(kNT) void vis_patch_kernel(VisPatch a) {
 // fp64: mean, variance about it, (x - mean) / sqrt(var + eps) * w + b,
 // rounded once; the row is quantized into xq[r] / xs[r] (quantize_acts)
 // when xq is given, else stored to h[r].
-template <int NPT>
-__global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
-  __shared__ double red[kWaves];
-  __shared__ float redf[kWaves];
+template <int NPT, int NT>
+__global__ __launch_bounds__(NT) void vis_ln_rows_kernel(VisLn a) {
+  __shared__ double red[NT / 64];
+  __shared__ float redf[NT / 64];
   const int tid = threadIdx.x, n4 = a.dim >> 2;
   const size_t r = blockIdx.x;
   float *xr = a.x + r * a.dim;
@@ -88,7 +88,7 @@ __global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
   const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
-    const int c = tid + j * kNT;
+    const int c = tid + j * NT;
     xv[j] = c < n4 ? reinterpret_cast<const v4f *>(xr)[c] : zero;
     if (a.y != nullptr && c < n4) {
       const v4f yv = reinterpret_cast<const v4f *>(a.y + r * a.dim)[c];
@@ -103,21 +103,21 @@ __global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
   for (int j = 0; j < NPT; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) s += (double)xv[j][e];
-  const double mean = block_sum<kNT>(s, red) / (double)a.dim;
+  const double mean = block_sum<NT>(s, red) / (double)a.dim;
   double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < NPT; ++j)
-    if (tid + j * kNT < n4)
+    if (tid + j * NT < n4)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const double d = (double)xv[j][e] - mean;
         ss += d * d;
       }
-  const double inv = 1.0 / sqrt(block_sum<kNT>(ss, red) / (double)a.dim + (double)a.eps);
+  const double inv = 1.0 / sqrt(block_sum<NT>(ss, red) / (double)a.dim + (double)a.eps);
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
-    const int c = tid + j * kNT;
+    const int c = tid + j * NT;
     if (c >= n4) {
       xv[j] = zero;
       continue;
@@ -133,15 +133,15 @@ __global__ __launch_bounds__(kNT) void vis_ln_rows_kernel(VisLn a) {
   if (a.xq == nullptr) {
 #pragma unroll
     for (int j = 0; j < NPT; ++j)
-      if (tid + j * kNT < n4) reinterpret_cast<v4f *>(a.h + r * a.dim)[tid + j * kNT] = xv[j];
+      if (tid + j * NT < n4) reinterpret_cast<v4f *>(a.h + r * a.dim)[tid + j * NT] = xv[j];
     return;
   }
-  amax = block_max<kNT>(amax, redf);
+  amax = block_max<NT>(amax, redf);
   const QuantParams qp = quant_params(amax);
   int8_t *row = a.xq + r * a.dim;
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
-    const int c = tid + j * kNT;
+    const int c = tid + j * NT;
     if (c < n4)
       reinterpret_cast<uint32_t *>(row)[c] =
           pack4(quant_one(xv[j].x, qp.inv), quant_one(xv[j].y, qp.inv),
@@ -451,10 +451,19 @@ hipError_t launch_vis_patch(const VisPatch &a, hipStream_t stream) {
 }
 
 hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
-  return by_npt<1, kPfMaxNpt>((a.dim / 4 + kNT - 1) / kNT, [&](auto c) {
-    vis_ln_rows_kernel<decltype(c)::value><<<n, kNT, 0, stream>>>(a);
-    return hipGetLastError();
-  });
+  // the fewest threads per row that cover it in kPfMaxNpt chunks: more rows
+  // in flight per CU (SigLIP's 1152 columns: one wave, 5 chunks)
+  const int n4 = a.dim / 4;
+  auto go = [&](auto nt) {
+    constexpr int NT = decltype(nt)::value;
+    return by_npt<1, kPfMaxNpt>((n4 + NT - 1) / NT, [&](auto c) {
+      vis_ln_rows_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(a);
+      return hipGetLastError();
+    });
+  };
+  if ((n4 + 63) / 64 <= kPfMaxNpt) return go(std::integral_constant<int, 64>{});
+  if ((n4 + 127) / 128 <= kPfMaxNpt) return go(std::integral_constant<int, 128>{});
+  return go(std::integral_constant<int, 256>{});
 }
 
 hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream) {
