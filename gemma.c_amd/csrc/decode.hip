@@ -799,6 +799,12 @@ NormStreamFn norm_stream_fn(int kc, bool gelu) {
 hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                                 bool gelu, const DeviceInfo &dev, hipStream_t stream) {
   if (total <= 0 || k <= 0 || k % 16 != 0 || k > 6144) return hipErrorInvalidValue;
+  // every plain job must have rows: the kernels clamp a group's row to its
+  // job's last row, which an empty job does not have (the GELU form pairs
+  // gate and up rows of one range, given as end[0] = end[1] = 2 * mlp)
+  if (!gelu)
+    for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
+      if (jobs.end[j] <= prev) return hipErrorInvalidValue;
   const int kc = k / 16;
   if (const NormStreamFn fn = norm_stream_fn(kc, gelu)) {
     int lanes = 8;

@@ -74,11 +74,12 @@ def _pascal(s: str) -> bytes:
 def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
               layers: int | None = None, slide: int | None = None, sc_att: float = 0.0,
               sc_log: float = 0.0, flags: int = 4 | 2 | 1, norm_std: float = 0.0,
-              vision: dict | None = None) -> str:
+              vision: dict | None = None, swa: list | None = None) -> str:
     """Write a random-init W8A8 (f32 build) text model of shape `name`;
     `nvocab` and `layers` shrink it for quick tests, `slide`, the softcaps
     and the flags byte (4 qk-norm, 2 pre-FFN norm, 1 post-FFN norm) select
-    the other code paths of the reference's decoder; norm_std > 0 draws the
+    the other code paths of the reference's decoder (`swa`, one flag per
+    layer, overrides gemma 3's five sliding layers per global one); norm_std > 0 draws the
     norm weights from N(0, norm_std) instead of zeros.  `vision`, a
     synth_vision() dict whose text_dim is this model's dim, makes the file
     multimodal (flag 8): its VisionConfig follows the flags byte (gemma.c:
@@ -106,7 +107,8 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
         nbytes = (nl + 7) // 8
         bits = bytearray(nbytes)
         for i in range(nl):
-            if (i + 1) % 6 != 0:  # gemma 3: five sliding-window layers per global one
+            sliding = swa[i] if swa is not None else (i + 1) % 6 != 0
+            if sliding:  # gemma 3: five sliding-window layers per global one
                 bits[i // 8] |= 1 << (7 - i % 8)
         f.write(bytes([nbytes]) + bytes(bits))
         f.write(bytes([(flags & 7) | (8 if vc is not None else 0)]))

@@ -28,10 +28,20 @@ F32 = np.float32
 F64 = np.float64
 
 
+def int_dot(a, b):
+    """Exact int32 sums a @ b.T of int8 operands a [m][k], b [n][k] (or
+    vectors), computed as a float64 product: every partial sum is an integer
+    of magnitude <= k * 127^2 < 2^53 for k < 5e11, so float64 represents it
+    exactly and the summation order cannot matter."""
+    assert np.shape(a)[-1] * 127 * 127 < 2 ** 53
+    r = np.asarray(a, F64) @ np.asarray(b, F64).T
+    return r.astype(np.int64).astype(np.int32)
+
+
 def rmsnorm(x, w, eps):
-    """gemma.c:2508-2521: x * rsqrt(mean(x^2) + eps) * (w + 1)."""
+    """gemma.c:2508-2521: x * rsqrt(mean(x^2) + eps) * (w + 1), per row of x."""
     x = np.asarray(x, F64)
-    rms = 1.0 / np.sqrt(np.mean(x * x) + F64(F32(eps)))
+    rms = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + F64(F32(eps)))
     return (x * rms * (np.asarray(w, F64) + 1.0)).astype(F32)
 
 
@@ -49,20 +59,21 @@ def gelu_tanh(x):
 
 def rope_table(theta, hdim, pos):
     """rope_freqs_pos (gemma.c:4178-4196): freq = theta^(-2d/hdim) and the
-    angle freq*pos rounded to float32 as the reference computes them."""
+    angle freq*pos rounded to float32 as the reference computes them; pos
+    may be an array of positions (one table row each)."""
     d = np.arange(hdim // 2)
     ex = (F32(-2) * d.astype(F32)) / F32(hdim)
     freq = np.power(F64(F32(theta)), ex.astype(F64)).astype(F32)
-    ang = (freq * F32(pos)).astype(F32)
+    ang = (freq * np.asarray(pos, F32)[..., None]).astype(F32)
     return np.cos(ang.astype(F64)).astype(F32), np.sin(ang.astype(F64)).astype(F32)
 
 
 def rope(x, cos, sin):
-    """rope_apply (gemma.c:4223-4246) on one head vector."""
-    h = len(x) // 2
-    a, b = np.asarray(x[:h], F64), np.asarray(x[h:], F64)
+    """rope_apply (gemma.c:4223-4246) on head vectors (the last axis)."""
+    h = np.shape(x)[-1] // 2
+    a, b = np.asarray(x[..., :h], F64), np.asarray(x[..., h:], F64)
     c, s = cos.astype(F64), sin.astype(F64)
-    return np.concatenate([a * c - b * s, a * s + b * c]).astype(F32)
+    return np.concatenate([a * c - b * s, a * s + b * c], axis=-1).astype(F32)
 
 
 def attend(q, keys, vals, asc, sc_att):
@@ -91,8 +102,15 @@ class DecodeOracle:
     def gemv(self, w, x_f32):
         """quantize_act + gemv_int8 (gemma.c:2590-2788): exact."""
         q, xs = self.o.quantize_act(np.ascontiguousarray(x_f32, F32))
-        acc = np.asarray(w[0], np.int64) @ q.astype(np.int64)
-        return acc.astype(np.int32).astype(F32) * (F32(xs) * np.asarray(w[1], F32))
+        acc = int_dot(q, w[0])
+        return acc.astype(F32) * (F32(xs) * np.asarray(w[1], F32))
+
+    def gemm(self, w, x_f32):
+        """quantize_acts + gemm_int8 (gemma.c:2652-2674, 3937-4054) over the
+        rows of x_f32, exact; row i equals gemv(w, x_f32[i])."""
+        q, xs = self.o.quantize_acts(np.ascontiguousarray(x_f32, F32))
+        acc = int_dot(q, w[0])
+        return acc.astype(F32) * (xs[:, None] * np.asarray(w[1], F32)[None, :])
 
     def step(self, token: int, pos: int) -> np.ndarray:
         c, m = self.c, self.m
@@ -138,6 +156,78 @@ class DecodeOracle:
                 y = rmsnorm(y, ly["n4"], eps)
             x = clamp_f32(y.astype(F64) + resid.astype(F64))
         h = rmsnorm(x, m["fnorm"], eps)
+        logits = self.gemv(m["emb"], h)
+        if c["sc_log"] != 0.0:
+            logits = (np.tanh(logits.astype(F64) / c["sc_log"]) * c["sc_log"]).astype(F32)
+        return logits
+
+    def prefill(self, tokens, pos0: int) -> np.ndarray:
+        """The prompt chunk of forward_gemma_prefill (gemma.c:5501) and
+        forward_text_chunk (4985-5453): the tokens at positions pos0, pos0+1,
+        ... go through each layer together, row i with step()'s formulas at
+        position pos0 + i (causal, sliding-window attention over the cache).
+        Fills the KV cache and returns the last row's logits.  Row for row it
+        is step() vectorized; tests/test_decoder.py checks the two agree."""
+        c, m = self.c, self.m
+        toks = np.asarray(tokens, np.int64)
+        n = len(toks)
+        dim, hd, nh, nkv = c["dim"], c["hdim"], c["n_heads"], c["nkv"]
+        eps = c["eps"]
+        esc0 = F32(1.0) if c["mlp_pre"] else F32(np.sqrt(F32(dim)))
+        esc = (esc0 * np.asarray(m["emb"][1], F32)[toks]).astype(F32)
+        x = (np.asarray(m["emb"][0])[toks].astype(F32) * esc[:, None]).astype(F32)
+        asc = F32(1.0) / F32(np.sqrt(F32(c["q_scale"])))
+        pos = pos0 + np.arange(n)
+        hn = nh // nkv
+        for li, ly in enumerate(m["layers"]):
+            resid = x
+            h = rmsnorm(x, ly["n1"], eps)
+            q = self.gemm(ly["wq"], h).reshape(n, nh, hd)
+            k = self.gemm(ly["wk"], h).reshape(n, nkv, hd)
+            v = self.gemm(ly["wv"], h).reshape(n, nkv, hd)
+            if c["qk_norm"]:
+                q = rmsnorm(q, ly["nq"], eps)
+                k = rmsnorm(k, ly["nk"], eps)
+            sliding = bool(c["swa"][li])
+            cos, sin = rope_table(c["theta_l"] if sliding else c["theta_g"], hd, pos)
+            q = rope(q, cos[:, None, :], sin[:, None, :])
+            k = rope(k, cos[:, None, :], sin[:, None, :])
+            self.kc[li, :, pos0:pos0 + n] = k.transpose(1, 0, 2)
+            self.vc[li, :, pos0:pos0 + n] = v.transpose(1, 0, 2)
+            if sliding:
+                spos = np.where(pos >= c["slide"], pos + 1 - c["slide"], 0)
+            else:
+                spos = np.zeros(n, np.int64)
+            ctx = pos0 + n
+            xo = np.empty((n, nh, hd), F32)
+            for hh in range(nh):
+                keys = np.asarray(self.kc[li, hh // hn, :ctx], F64)
+                vals = np.asarray(self.vc[li, hh // hn, :ctx], F64)
+                for r0 in range(0, n, 512):
+                    r1 = min(n, r0 + 512)
+                    s = np.asarray(q[r0:r1, hh], F64) @ keys.T * F64(asc)
+                    if c["sc_att"] != 0.0:
+                        s = np.tanh(s / F64(c["sc_att"])) * F64(c["sc_att"])
+                    j = np.arange(ctx)[None, :]
+                    live = (j <= pos[r0:r1, None]) & (j >= spos[r0:r1, None])
+                    s = np.where(live, s, -np.inf)
+                    p = np.exp(s - s.max(axis=1, keepdims=True))
+                    p /= p.sum(axis=1, keepdims=True)
+                    xo[r0:r1, hh] = (p @ vals).astype(F32)
+            y = self.gemm(ly["wo"], xo.reshape(n, -1))
+            if c["mlp_pre"]:
+                y = rmsnorm(y, ly["n2"], eps)
+            x = clamp_f32(y.astype(F64) + resid.astype(F64))
+            resid = x
+            h = rmsnorm(x, ly["n3"] if c["mlp_pre"] else ly["n2"], eps)
+            gate = self.gemm(ly["w2"], h)
+            up = self.gemm(ly["w1"], h)
+            g = (gelu_tanh(gate) * up.astype(F64)).astype(F32)
+            y = self.gemm(ly["w3"], g)
+            if c["mlp_pst"]:
+                y = rmsnorm(y, ly["n4"], eps)
+            x = clamp_f32(y.astype(F64) + resid.astype(F64))
+        h = rmsnorm(x[-1], m["fnorm"], eps)
         logits = self.gemv(m["emb"], h)
         if c["sc_log"] != 0.0:
             logits = (np.tanh(logits.astype(F64) / c["sc_log"]) * c["sc_log"]).astype(F32)

@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle.decode_oracle import clamp_f32, gelu_tanh, rmsnorm
+from oracle.decode_oracle import clamp_f32, gelu_tanh, int_dot, rmsnorm
 
 F32 = np.float32
 F64 = np.float64
@@ -64,8 +64,8 @@ class VisionOracle:
     def gemm(self, w, x_f32):
         """quantize_acts + gemm_int8 (gemma.c:2652-2674, 3937-4054): exact."""
         q, xs = self.o.quantize_acts(np.ascontiguousarray(x_f32, F32))
-        acc = q.astype(np.int64) @ np.asarray(w[0], np.int64).T
-        return acc.astype(np.int32).astype(F32) * (xs[:, None] * np.asarray(w[1], F32)[None, :])
+        acc = int_dot(q, w[0])
+        return acc.astype(F32) * (xs[:, None] * np.asarray(w[1], F32)[None, :])
 
     def forward(self, img):
         c, v = self.c, self.v

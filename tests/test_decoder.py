@@ -144,17 +144,22 @@ def gqa_model(tmp_path_factory):
                                                   norm_std=0.1))
 
 
-def _prefill_vs_oracle(gh, oracle, model, n, more, clen, chunks=None):
+def _prefill_vs_oracle(gh, oracle, model, n, more, clen, chunks=None, batched=False):
     """The batched prompt pass (in `chunks`, default one) against the oracle fed
-    the same tokens one at a time: the last prompt token's logits, then `more`
-    decode steps on the KV cache the prefill filled."""
+    the same tokens one at a time (or, `batched`, through its own vectorized
+    prefill, which test_oracle_prefill_equals_steps ties to the steps): the
+    last prompt token's logits, then `more` decode steps on the KV cache the
+    prefill filled."""
     nv = model["config"]["nvocab"]
     prompt = np.random.default_rng(n * 31 + clen).integers(0, nv, n).astype(np.int32)
     dec = gh.decoder(model, clen)
     try:
         ref = dorc.DecodeOracle(model, oracle, clen)
-        for pos, t in enumerate(prompt):
-            want = ref.step(int(t), pos)
+        if batched:
+            want = ref.prefill(prompt, 0)
+        else:
+            for pos, t in enumerate(prompt):
+                want = ref.step(int(t), pos)
         logits = np.empty(nv, np.float32)
         cuts = [0] + list(chunks or []) + [n]
         for a, b in zip(cuts[:-1], cuts[1:]):
@@ -171,6 +176,27 @@ def _prefill_vs_oracle(gh, oracle, model, n, more, clen, chunks=None):
         return worst
     finally:
         dec.close()
+
+
+def test_oracle_prefill_equals_steps(oracle, models):
+    """The oracle's vectorized prefill against its own step() fed the same
+    tokens one at a time: logits and KV cache agree to float64 rounding on
+    every code path the cases select (sliding and global layers, softcaps,
+    no qk norm, head dim 128, odd widths), also when a second chunk continues
+    the first."""
+    for key in ("gemma3", "softcap", "plain", "hd128", "odd"):
+        model = models[key]
+        nv = model["config"]["nvocab"]
+        prompt = np.random.default_rng(4).integers(0, nv, 21).astype(np.int32)
+        a = dorc.DecodeOracle(model, oracle, 24)
+        b = dorc.DecodeOracle(model, oracle, 24)
+        for pos, t in enumerate(prompt):
+            want = a.step(int(t), pos)
+        b.prefill(prompt[:13], 0)
+        got = b.prefill(prompt[13:], 13)
+        assert np.allclose(got, want, rtol=0, atol=1e-6 * float(np.abs(want).max())), key
+        assert np.allclose(b.kc, a.kc, rtol=1e-6, atol=1e-6), key
+        assert np.allclose(b.vc, a.vc, rtol=1e-6, atol=1e-6), key
 
 
 @pytest.mark.gpu
@@ -190,6 +216,65 @@ def test_prefill_gqa_matches_oracle(gh, oracle, gqa_model, n, clen):
     blocks, so the chunk order is rotated per row block (nkv * nsplit = 16)."""
     worst = _prefill_vs_oracle(gh, oracle, gqa_model, n, 3, clen)
     print(f"prefill gqa {n}: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def wide_1b(tmp_path_factory):
+    """gemma-3-1b widths (dim 1152, mlp 6912, 4 q heads over 1 kv head of
+    256): the norm-GEMV launches at K = 1152 and the prefill row kernels at
+    the width config 3 runs.  Two layers, a sliding window of 512 then a
+    global layer, small vocabulary."""
+    d = tmp_path_factory.mktemp("w1b")
+    return model_bin.read_bin(model_bin.write_bin(str(d / "w1b.bin"), "gemma-3-1b", seed=9,
+                                                  nvocab=1024, layers=2, swa=[1, 0],
+                                                  norm_std=0.1))
+
+
+@pytest.mark.gpu
+def test_prefill_1b_width_matches_oracle(gh, oracle, wide_1b):
+    """Config 3's prompt length (512) at gemma-3-1b widths plus 8 decode
+    steps, the last of them past the sliding window."""
+    worst = _prefill_vs_oracle(gh, oracle, wide_1b, 512, 8, 528, batched=True)
+    print(f"prefill 1b width: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
+@pytest.mark.gpu
+def test_decoder_1b_width_steps(gh, oracle, wide_1b):
+    """The decode step alone at gemma-3-1b widths (every position through
+    the step graph, no prefill)."""
+    model = wide_1b
+    dec = gh.decoder(model, 24)
+    try:
+        ref = dorc.DecodeOracle(model, oracle, 24)
+        logits = np.empty(model["config"]["nvocab"], np.float32)
+        token = 3
+        for pos in range(20):
+            nxt = dec.step(token, pos, logits)
+            want = ref.step(token, pos)
+            _check_logits(logits, want, f"1b-width step at {pos}")
+            assert nxt == int(np.argmax(want))
+            token = nxt
+    finally:
+        dec.close()
+
+
+@pytest.fixture(scope="module")
+def long_ctx(tmp_path_factory):
+    """One global layer at gemma-3-270m widths, for contexts past 8192."""
+    d = tmp_path_factory.mktemp("long")
+    return model_bin.read_bin(model_bin.write_bin(str(d / "long.bin"), "gemma-3-270m", seed=3,
+                                                  nvocab=512, layers=1, swa=[0],
+                                                  norm_std=0.1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [3100, 8200])
+def test_decoder_long_context(gh, oracle, long_ctx, n):
+    """Decode steps over more than 192 (n = 3100) and more than 512 (n =
+    8200) attention blocks of 16 keys: the combine's second load batch and
+    its loops past 2 x 256 blocks."""
+    worst = _prefill_vs_oracle(gh, oracle, long_ctx, n, 3, n + 8, batched=True)
+    print(f"long context {n}: worst |d|/max|logit| = {worst:.3g}", flush=True)
 
 
 @pytest.mark.gpu

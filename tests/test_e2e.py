@@ -127,7 +127,7 @@ def model_dir(tmp_path_factory):
 @pytest.mark.parametrize("name,prompt_len,steps,chunk", [
     ("gemma-3-270m", 32, 64, None),   # config 1
     ("gemma-3-270m", 40, 8, 16),      # chunked prefill: M = 16, 16, 8
-    ("gemma-3-1b", 512, 16, None),    # config 3's prefill (M = 512)
+    ("gemma-3-1b", 512, 256, None),   # config 3: prefill M = 512, 256 decode steps
 ])
 def test_e2e_hip_build_matches_reference(model_dir, name, prompt_len, steps, chunk):
     path = model_bin.ensure_bin(model_dir, name)

@@ -152,10 +152,16 @@ def test_gemv_sweep_1b_vs_oracle(gh, oracle, name, n, k):
     assert np.array_equal(bits(host(y)), bits(yo))
 
 
+# The gemma-3-4b decode launches (config 5) as the decode call sites issue
+# them: q/k/v and gate/up fused, o, down and the tied LM head.
 @pytest.mark.parametrize("rows,k", [((1024, 256, 256), 1152), ((6912, 6912), 1152),
-                                    ((2048, 1024, 1024), 2560), ((40, 3, 17, 64), 656)])
+                                    ((2048, 1024, 1024), 2560), ((10240, 10240), 2560),
+                                    ((2560,), 2048), ((2560,), 10240), ((262144,), 2560),
+                                    ((40, 3, 17, 64), 656)])
 def test_fused_multi_vs_oracle(gh, oracle, rows, k):
-    """q/k/v and gate/up as one launch (gemma.c:4768-4773, 4911-4915)."""
+    """q/k/v and gate/up as one launch (gemma.c:4768-4773, 4911-4915), and
+    the single-job launches at the 4b widths (4858-4859, 4929-4930,
+    4964-4965)."""
     note(f"fused multi rows={rows} k={k}")
     rng = np.random.default_rng(sum(rows) + k)
     x = outlier_acts(rng, (k,))

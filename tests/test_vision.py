@@ -65,6 +65,11 @@ SHAPES = {
     "hd72": dict(nl=2, n_heads=2, img_px=56, psize=14, dim=144, mlp_dim=288, img_tok=4),
     # 64 patches (two query tiles, four key tiles), 16 tokens, head dim 16
     "hd16": dict(nl=3, n_heads=4, img_px=112, psize=14, dim=64, mlp_dim=128, img_tok=16),
+    # SigLIP's own widths (dim 1152, 16 heads of 72, mlp 4304) at 224 px: 256
+    # patches, two query blocks per head (32 blocks, so the XCD renumbering
+    # runs), the 1152-wide layer-norm rows and multi-chunk GELU rows of
+    # config 4, pooled 4x4 to 16 tokens
+    "siglip": dict(nl=2, n_heads=16, img_px=224, psize=14, dim=1152, mlp_dim=4304, img_tok=16),
 }
 
 
