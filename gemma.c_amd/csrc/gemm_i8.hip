@@ -35,8 +35,20 @@
 #include "gh_arith.h"
 #include "gh_kernels.h"
 
+// Caller-free workspace of gemma_hip_matmul_noalloc: the int32 partial tiles
+// and tile counters of split-K launches, one copy per GPU that loads the
+// library, held until the process ends.  Host code never passes `scratch`
+// itself to a kernel (in host code the name is a host-side stand-in, not a
+// device address): it uses the address hipGetSymbolAddress returned for the
+// device, kept in g_scratch_dev.
+static __device__ __align__(256) int scratch[gh::kGemmScratchBytes / sizeof(int)];
+
 namespace gh {
 namespace {
+
+constexpr int kMaxDevices = 64;
+int *g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
 
 constexpr int kThreads = 256;
 constexpr int kBK = 64;                   // bytes of K per step
@@ -610,6 +622,23 @@ hipError_t split_ws(hipStream_t stream, size_t ws_ints, int ncnt, SplitK *sk) {
 
 }  // namespace
 
+hipError_t gemm_scratch_init(int device) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[device] != nullptr) return hipSuccess;
+  void *p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  g_scratch_dev[device] = static_cast<int *>(p);
+  return hipSuccess;
+}
+
+GemmWs gemm_scratch(int device) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device < 0 || device >= kMaxDevices) return GemmWs{nullptr, 0};
+  return GemmWs{g_scratch_dev[device], g_scratch_dev[device] ? kGemmScratchBytes : 0};
+}
+
 void release_gemm_workspaces() {
   std::lock_guard<std::mutex> lock(g_split_mu);
   for (auto &kv : g_split) {  // hipFree waits for the device's queued work
@@ -629,16 +658,38 @@ int env_split() {
   return e == nullptr ? 0 : atoi(e);
 }
 
+// Counters of a caller-free workspace are cleared by a kernel (not
+// hipMemsetAsync) on every call, so the call may be captured into a graph.
+__global__ __launch_bounds__(kThreads) void gemm_zero_kernel(int *p, int n) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// Bytes of workspace a split-K launch over `tiles` 128x128 tiles in `splits`
+// pieces needs: the partial tiles, then the counters on a 256-byte boundary.
+size_t split_bytes(int tiles, int splits) {
+  const size_t part = (size_t)tiles * splits * kThreads * 4 * 16 * sizeof(int);
+  return part + (((size_t)tiles * sizeof(int) + 255) & ~(size_t)255);
+}
+
 // 128x128 tiles, two 128-byte stages, split-K over `splits` workgroups per
 // tile (splits >= 2, at most the number of K stages).
 hipError_t launch_dma_split(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
                             const GemmSegs &bs, int mstr, const int8_t *src, int sstr,
-                            const float *ssc, int m, int k, int splits) {
+                            const float *ssc, int m, int k, int splits, const GemmWs *fixed) {
   const int n = bs.end[bs.nseg - 1];
   const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
   SplitK sk{splits, nullptr, nullptr};
-  hipError_t e = split_ws(stream, (size_t)tiles * splits * kThreads * 4 * 16, tiles, &sk);
-  if (e != hipSuccess) return e;
+  if (fixed != nullptr) {
+    const size_t part = (size_t)tiles * splits * kThreads * 4 * 16;
+    if (split_bytes(tiles, splits) > fixed->bytes) return hipErrorOutOfMemory;
+    sk.ws = fixed->base;
+    sk.cnt = fixed->base + ((part * sizeof(int) + 255) & ~(size_t)255) / sizeof(int);
+    gemm_zero_kernel<<<(tiles + kThreads - 1) / kThreads, kThreads, 0, stream>>>(sk.cnt, tiles);
+  } else {
+    hipError_t e = split_ws(stream, (size_t)tiles * splits * kThreads * 4 * 16, tiles, &sk);
+    if (e != hipSuccess) return e;
+  }
   if (heads)
     gemm_i8_dma_kernel<2, 2, 2, 128, true, true><<<tiles * splits, kThreads, 0, stream>>>(
         dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, sk);
@@ -653,14 +704,16 @@ hipError_t launch_dma_split(bool heads, hipStream_t stream, float *dst, int dstr
 // split pays only when the grid leaves most CUs idle and K is long: gemma-3-1b
 // down at 512 tokens (36 tiles, 54 stages) goes from 253 to 348 TOPS with 6
 // splits, while every gemma-3-4b and SigLIP shape (>= 128 tiles) lost 15-60%.
-int choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t stream) {
+int choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t stream,
+                 bool fixed_ws) {
   const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
   const int nk = (k + 127) / 128;
   const int forced = env_split();
   if (forced > 0) return forced > nk ? nk : forced;
   if (tiles <= 0 || tiles * 4 > dev.cus || nk < 32) return 1;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+  if (!fixed_ws &&
+      (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone))
     return 1;  // the workspace may have to be allocated: not under capture
   const int s = std::min(std::min(8, dev.cus / tiles), nk / 8);
   return s >= 2 ? s : 1;
@@ -696,10 +749,23 @@ void launch_tiled(bool heads, hipStream_t stream, float *dst, int dstr, int hdim
 
 }  // namespace
 
+size_t gemm_i8_scratch_bytes(int m, int n, int k, bool heads, const int8_t *mat, int mstr,
+                             const int8_t *src, int sstr, int dstr, const DeviceInfo &dev) {
+  const bool fast = k % 16 == 0 && mstr % 16 == 0 && sstr % 16 == 0 &&
+                    (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
+  const bool dma_ok = (uint64_t)(m - 1) * sstr + k < kOob &&
+                      (uint64_t)(n - 1) * mstr + k < kOob &&
+                      ((uint64_t)(m - 1) * dstr + n) * 4 < kOob;
+  (void)heads;
+  if (!fast || !dma_ok || env_tile() != 0) return 0;
+  const int sp = choose_split(m, n, k, dev, nullptr, true);
+  return sp > 1 ? split_bytes(((m + 127) / 128) * ((n + 127) / 128), sp) : 0;
+}
+
 hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
                           int mstr, const float *matsc, const int8_t *src,
                           int sstr, const float *ssc, int m, int n, int k,
-                          const DeviceInfo &dev, hipStream_t stream) {
+                          const DeviceInfo &dev, hipStream_t stream, const GemmWs *fixed) {
   const bool fast = k % 16 == 0 && mstr % 16 == 0 && sstr % 16 == 0 &&
                     (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
   const bool heads = hdim > 0;
@@ -710,15 +776,16 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
   if (fast) {
     int tile = env_tile();
     if (tile == 0 && dma_ok) {
-      const int sp = choose_split(m, n, k, dev, stream);
+      const int sp = choose_split(m, n, k, dev, stream, fixed != nullptr);
       if (sp > 1) {
         GemmSegs bs{};
         bs.w[0] = mat;
         bs.s[0] = matsc;
         bs.end[0] = n;
         bs.nseg = 1;
-        return launch_dma_split(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k,
-                                sp);
+        const hipError_t e = launch_dma_split(heads, stream, dst, dstr, hdim, bs, mstr, src,
+                                              sstr, ssc, m, k, sp, fixed);
+        return e != hipSuccess ? e : hipGetLastError();
       }
     }
     if (tile == 0) {
@@ -772,14 +839,17 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
   if (fast && dma_ok && env_tile() == 0) {
     // the tile choice of launch_gemm_i8 for the whole width
     const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
-    const int sp = choose_split(m, n, k, dev, stream);
+    const int sp = choose_split(m, n, k, dev, stream, false);
     const bool wide = sp > 1 || tiles128 >= dev.cus;
     const int bn = wide ? 128 : 64;
     bool aligned = true;
     for (int t = 0; t + 1 < b.nseg; ++t) aligned = aligned && b.end[t] % bn == 0;
     if (aligned) {
-      if (sp > 1)
-        return launch_dma_split(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k, sp);
+      if (sp > 1) {
+        const hipError_t e =
+            launch_dma_split(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k, sp, nullptr);
+        return e != hipSuccess ? e : hipGetLastError();
+      }
       if (wide)
         launch_dma_segs<2, 2, 2, 128>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
       else
@@ -789,7 +859,7 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
   }
   for (int t = 0, start = 0; t < b.nseg; start = b.end[t], ++t) {
     const hipError_t e = launch_gemm_i8(dst + start, dstr, 0, b.w[t], k, b.s[t], src, sstr, ssc,
-                                        m, b.end[t] - start, k, dev, stream);
+                                        m, b.end[t] - start, k, dev, stream, nullptr);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -273,6 +273,7 @@ int gemma_hip_init(int device) {
     return fail("gemma_hip_init: device %d is %s; this library is built for gfx950",
                 device, prop.gcnArchName);
   GH_CHECK("gemma_hip_init: hipSetDevice", hipSetDevice(device));
+  GH_CHECK("gemma_hip_init: scratch address", gh::gemm_scratch_init(device));
   GH_CHECK("gemma_hip_init: hipStreamCreate",
            hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
   g.info.cus = prop.multiProcessorCount;
@@ -383,17 +384,22 @@ int gemma_hip_quantize(int8_t *dst, float *dsc, const float *src, int sstr,
   return 0;
 }
 
-int gemma_hip_matmul(float *dst, int dstr, const int8_t *mat, int mstr,
-                     const float *matsc, const int8_t *src, int sstr,
-                     const float *ssc, int m, int n, int k, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// gemma_hip_matmul and gemma_hip_matmul_noalloc: `noalloc` takes the GEMM's
+// workspace from the library's static scratch instead of memory it allocates.
+int matmul_impl(const char *name, float *dst, int dstr, const int8_t *mat, int mstr,
+                const float *matsc, const int8_t *src, int sstr, const float *ssc, int m,
+                int n, int k, void *stream, bool noalloc) {
   if (need_init()) return 1;
   if (dstr == 0) dstr = n;
   if (mstr == 0) mstr = k;
   if (sstr == 0) sstr = k;
-  if (check_matmul_shape("gemma_hip_matmul", m, n, k, dstr, mstr, sstr)) return 1;
+  if (check_matmul_shape(name, m, n, k, dstr, mstr, sstr)) return 1;
   if (m == 0) return 0;
-  if (!dst || !mat || !matsc || !src || !ssc)
-    return fail("gemma_hip_matmul: null pointer");
+  if (!dst || !mat || !matsc || !src || !ssc) return fail("%s: null pointer", name);
   hipStream_t s = pick_stream(stream);
   if (m == 1 && mstr == k && k <= kMaxGemvK8) {
     gh::GemvJobs jobs{};
@@ -402,15 +408,43 @@ int gemma_hip_matmul(float *dst, int dstr, const int8_t *mat, int mstr,
     jobs.dst[0] = dst;
     for (int j = 0; j < gh::kMaxJobs; ++j) jobs.end[j] = n;
     jobs.njobs = 1;
-    GH_CHECK("gemma_hip_matmul: gemv launch",
-             gh::launch_gemv_i8(jobs, k, src, ssc, nullptr, nullptr, nullptr,
-                                g.info, s));
+    const hipError_t e =
+        gh::launch_gemv_i8(jobs, k, src, ssc, nullptr, nullptr, nullptr, g.info, s);
+    if (e != hipSuccess) return fail("%s: gemv launch: %s", name, hipGetErrorString(e));
     return 0;
   }
-  GH_CHECK("gemma_hip_matmul: gemm launch",
-           gh::launch_gemm_i8(dst, dstr, 0, mat, mstr, matsc, src, sstr, ssc, m,
-                              n, k, g.info, s));
+  gh::GemmWs ws{};
+  if (noalloc) {
+    ws = gh::gemm_scratch(g.device);
+    if (ws.base == nullptr) return fail("%s: scratch not resolved on device %d", name, g.device);
+    const size_t need =
+        gh::gemm_i8_scratch_bytes(m, n, k, false, mat, mstr, src, sstr, dstr, g.info);
+    if (need > ws.bytes)
+      return fail("%s: m=%d n=%d k=%d needs %zu bytes of scratch, more than the %zu it has",
+                  name, m, n, k, need, ws.bytes);
+  }
+  const hipError_t e = gh::launch_gemm_i8(dst, dstr, 0, mat, mstr, matsc, src, sstr, ssc, m,
+                                          n, k, g.info, s, noalloc ? &ws : nullptr);
+  if (e != hipSuccess) return fail("%s: gemm launch: %s", name, hipGetErrorString(e));
   return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gemma_hip_matmul(float *dst, int dstr, const int8_t *mat, int mstr,
+                     const float *matsc, const int8_t *src, int sstr,
+                     const float *ssc, int m, int n, int k, void *stream) {
+  return matmul_impl("gemma_hip_matmul", dst, dstr, mat, mstr, matsc, src, sstr, ssc, m, n, k,
+                     stream, false);
+}
+
+int gemma_hip_matmul_noalloc(float *dst, int dstr, const int8_t *mat, int mstr,
+                             const float *matsc, const int8_t *src, int sstr,
+                             const float *ssc, int m, int n, int k, void *stream) {
+  return matmul_impl("gemma_hip_matmul_noalloc", dst, dstr, mat, mstr, matsc, src, sstr, ssc, m,
+                     n, k, stream, true);
 }
 
 int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,

@@ -44,12 +44,32 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
 hipError_t launch_gemv_f32(const GemvJobs &jobs, int k, const float *x,
                            const DeviceInfo &dev, hipStream_t stream);
 
+// Workspace of split-K GEMM launches (int32 partial tiles + tile counters).
+struct GemmWs {
+  int *base;
+  size_t bytes;
+};
+// Size of the caller-free workspace (gemm_i8.hip's static `scratch`).
+constexpr size_t kGemmScratchBytes = (size_t)32 << 20;
+// Resolves the device address of `scratch` on `device`, which must be the
+// current device (once per device; later calls return at once).
+hipError_t gemm_scratch_init(int device);
+// The caller-free workspace of `device` ({nullptr, 0} before init).
+GemmWs gemm_scratch(int device);
+
 // gemm_i8.hip: dst = rescale(src . mat^T).  hdim > 0 selects the head-major
-// output layout dst[((j/hdim)*m + i)*hdim + j%hdim] (dstr ignored).
+// output layout dst[((j/hdim)*m + i)*hdim + j%hdim] (dstr ignored).  With
+// `fixed` the launch takes its workspace from there (and returns
+// hipErrorOutOfMemory if it needs more), else from a per-stream one the
+// library allocates on first need.
 hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
                           int mstr, const float *matsc, const int8_t *src,
                           int sstr, const float *ssc, int m, int n, int k,
-                          const DeviceInfo &dev, hipStream_t stream);
+                          const DeviceInfo &dev, hipStream_t stream,
+                          const GemmWs *fixed = nullptr);
+// Workspace bytes launch_gemm_i8 needs for this shape (0: none).
+size_t gemm_i8_scratch_bytes(int m, int n, int k, bool heads, const int8_t *mat, int mstr,
+                             const int8_t *src, int sstr, int dstr, const DeviceInfo &dev);
 
 // B as up to kMaxGemmSegs separate [rows][k] matrices (q, k, v; or gate,
 // up) whose outputs are adjacent column ranges of one dst: segment t holds

@@ -83,6 +83,7 @@ _SIGS = {
     "gemma_hip_device_ptr": (_P, [_P]),
     "gemma_hip_quantize": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "gemma_hip_matmul": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
+    "gemma_hip_matmul_noalloc": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
     "gemma_hip_matmul_heads": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "gemma_hip_matmul_multi": (_I, [ctypes.POINTER(Job), _I, _P, _P, _I, _P]),
     "gemma_hip_quantize_matmul": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P, _P, _P]),
@@ -177,6 +178,12 @@ class GemmaHip:
     def matmul(self, dst, dstr, mat, mstr, matsc, src, sstr, ssc, m, n, k, stream=None):
         self._check(self.lib.gemma_hip_matmul(_addr(dst), dstr, _addr(mat), mstr, _addr(matsc),
                                               _addr(src), sstr, _addr(ssc), m, n, k, stream))
+
+    def matmul_noalloc(self, dst, dstr, mat, mstr, matsc, src, sstr, ssc, m, n, k,
+                       stream=None):
+        self._check(self.lib.gemma_hip_matmul_noalloc(_addr(dst), dstr, _addr(mat), mstr,
+                                                      _addr(matsc), _addr(src), sstr, _addr(ssc),
+                                                      m, n, k, stream))
 
     def matmul_heads(self, dst, mat, matsc, src, ssc, m, heads, hdim, k, stream=None):
         self._check(self.lib.gemma_hip_matmul_heads(_addr(dst), _addr(mat), _addr(matsc),

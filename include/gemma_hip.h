@@ -111,6 +111,20 @@ int gemma_hip_matmul(float *dst, int dstr, const int8_t *mat, int mstr,
                      const float *matsc, const int8_t *src, int sstr,
                      const float *ssc, int m, int n, int k, void *stream);
 
+/* gemma_hip_matmul without any allocation, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops): no
+ * counterpart in the reference.  Same arguments, result bit-identical to
+ * gemma_hip_matmul.  The split-K partial tiles and tile counters that some
+ * shapes use live in a static device array of 32 MiB that each GPU the
+ * library runs on holds until the process ends; a shape whose launch plan
+ * needs more fails with an error naming both sizes.  The counters are
+ * cleared by a kernel on every call (no memset, so the call may be captured).
+ * All calls on one GPU share that array: calls that overlap in time on one
+ * GPU (several streams, or several host threads) race. */
+int gemma_hip_matmul_noalloc(float *dst, int dstr, const int8_t *mat, int mstr,
+                             const float *matsc, const int8_t *src, int sstr,
+                             const float *ssc, int m, int n, int k, void *stream);
+
 /* The prefill QKV site (gemma.c:5045-5089) as one launch: the same product
  * as gemma_hip_matmul with n = heads*hdim and dense operands, written
  * head-major, dst[(h*m + i)*hdim + j] for output column h*hdim + j. */
