@@ -47,6 +47,9 @@ import argparse
 import json
 import math
 import os
+import platform
+import statistics
+import subprocess
 import sys
 
 REPO = os.path.dirname(os.path.abspath(__file__))
@@ -62,6 +65,8 @@ INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 ROTATE_BYTES = 512 << 20   # > 2x the 256 MB Infinity Cache
 ROT_STEPS = 8              # steps per captured graph
+TIMING_RUNS = 5            # per-launch and GEMM timings: median of this many runs
+MIN_TIMED_MS = 100.0       # the headline's K-step region is repeated to at least this
 
 METRIC = ("int8 GEMV HBM GB/s + GEMM TOPS (% roofline); decode tok/s at "
           "gemma-3-1b shape")
@@ -186,12 +191,31 @@ def launch_gemv(gh, sh, copy, stream):
         raise RuntimeError(gh.lib.gemma_hip_last_error().decode())
 
 
-def sweep_graph(torch, gh, shapes):
+def sweep_graph(torch, gh, shapes, nsteps=ROT_STEPS):
     def steps(stream):
-        for step in range(ROT_STEPS):
+        for step in range(nsteps):
             for sh in shapes:
                 launch_gemv(gh, sh, step, stream)
     return capture(torch, steps)
+
+
+class StepRunner:
+    """Replays exactly k sweep steps: k // ROT_STEPS replays of the
+    ROT_STEPS-step graph, then one graph of the remaining steps (captured on
+    first use)."""
+
+    def __init__(self, torch, gh, shapes):
+        self.torch, self.gh, self.shapes = torch, gh, shapes
+        self.graphs = {ROT_STEPS: sweep_graph(torch, gh, shapes)}
+
+    def run(self, k):
+        for _ in range(k // ROT_STEPS):
+            self.graphs[ROT_STEPS].replay()
+        r = k % ROT_STEPS
+        if r:
+            if r not in self.graphs:
+                self.graphs[r] = sweep_graph(self.torch, self.gh, self.shapes, r)
+            self.graphs[r].replay()
 
 
 def per_gemv(torch, gh, shapes, timer, busy, reps):
@@ -208,9 +232,9 @@ def per_gemv(torch, gh, shapes, timer, busy, reps):
                 launch_gemv(gh, sh, i, stream)
 
         run()
-        best = min(timer.elapsed_ms(run, busy) for _ in range(3)) / launches
-        out[sh["name"]] = dict(n=sh["n"], k=sh["k"], us=round(best * 1e3, 3),
-                               gbs=round(sh["bytes"] / (best * 1e-3) / 1e9, 1),
+        med = statistics.median(timer.elapsed_ms(run, busy) for _ in range(TIMING_RUNS)) / launches
+        out[sh["name"]] = dict(n=sh["n"], k=sh["k"], us=round(med * 1e3, 3),
+                               gbs=round(sh["bytes"] / (med * 1e-3) / 1e9, 1),
                                copies=sh["copies"])
     return out
 
@@ -230,7 +254,7 @@ def bench_gemm(torch, gh, gen, timer, reps):
                 gh.matmul(d, n, b, k, bsc, a, k, asc, m, n, k, stream)
 
         run()
-        ms = min(timer.elapsed_ms(run) for _ in range(3)) / reps
+        ms = statistics.median(timer.elapsed_ms(run) for _ in range(TIMING_RUNS)) / reps
         tops = gemm_ops(m, n, k) / (ms * 1e-3) / 1e12
         out[name] = dict(m=m, n=n, k=k, us=round(ms * 1e3, 2), tops=round(tops, 1),
                          frac=round(tops / INT8_PEAK_TOPS, 4))
@@ -248,7 +272,7 @@ def bench_gemm(torch, gh, gen, timer, reps):
             gh.patch_embed(emb, img, pe, pe_b, img_px, psize, dim, None, stream)
 
     run_pe()
-    ms = min(timer.elapsed_ms(run_pe) for _ in range(3)) / reps
+    ms = statistics.median(timer.elapsed_ms(run_pe) for _ in range(TIMING_RUNS)) / reps
     tflops = 2 * npatch * dim * kdim / (ms * 1e-3) / 1e12
     patch = dict(img_px=img_px, psize=psize, dim=dim, us=round(ms * 1e3, 2),
                  tflops=round(tflops, 1), frac_fp32=round(tflops / FP32_PEAK_TFLOPS, 4))
@@ -433,6 +457,30 @@ def measured_traffic(kernel: str) -> dict | None:
     return d if d.get("kernel") == kernel else None
 
 
+def host_description() -> dict:
+    """The host the CPU baseline ran on: lscpu's model, sockets and cores,
+    and the compilers' versions."""
+    def first_line(cmd):
+        try:
+            return subprocess.run(cmd, capture_output=True, text=True,
+                                  timeout=20).stdout.splitlines()[0].strip()
+        except (OSError, IndexError, subprocess.SubprocessError):
+            return None
+    info = {"nproc": os.cpu_count(), "machine": platform.machine()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "Socket(s)", "Core(s) per socket",
+                               "Thread(s) per core", "CPU(s)"):
+                info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info["gcc"] = first_line(["gcc", "--version"])
+    info["clang"] = first_line(["/opt/rocm/llvm/bin/clang", "--version"])
+    return info
+
+
 def cpu_baseline(threads: int, seconds_per_shape: float) -> dict | None:
     """The reference's own quantize_act + gemv_int8 (compiled from
     /root/reference/gemma.c by oracle/Makefile; AVX2 clang build) over the
@@ -457,7 +505,12 @@ def cpu_baseline(threads: int, seconds_per_shape: float) -> dict | None:
         total_bytes += gemv_bytes(n, k)
         total_s += per_call
     return dict(value=round(total_bytes / total_s / 1e9, 2), unit="GB/s", cores=threads,
-                kind="reference",
+                kind="reference", host=host_description(),
+                compiler_note=("clang -O3 -ffast-math -march=x86-64-v3 -fopenmp builds the "
+                               "reference's AVX2 path unmodified; the reference Makefile's gcc "
+                               "-O3 -ffast-math -march=native needs _mm256_dpbssd_epi32 "
+                               "(gemma.c:3741-3800, gcc >= 13), which this image's gcc lacks, "
+                               "and no stand-in for it is written"),
                 sample=(f"reference quantize_act + gemv_int8 / gemv_int8_multi (gemma.c:2590, "
                         f"2770, 2808) built by clang -O3 -ffast-math -march=x86-64-v3 -fopenmp, "
                         f"{threads} OpenMP threads, the same {len(SWEEP_1B)} launches, >=512 MB "
@@ -536,30 +589,33 @@ def main() -> int:
         print(json.dumps(per), flush=True)
         return 0
 
-    graph = sweep_graph(torch, gh, shapes)
-    replays_w = max(1, math.ceil(args.warmup / ROT_STEPS))
-    replays = max(1, math.ceil(args.steps / ROT_STEPS))
-    steps = replays * ROT_STEPS
-    for _ in range(replays_w):
-        graph.replay()
+    # exactly --warmup untimed steps, then regions of exactly --steps steps,
+    # each bracketed by synchronisations and timed with HIP events, repeated
+    # until MIN_TIMED_MS have been timed (at least 5); the median region counts
+    steps = max(1, args.steps)
+    runner = StepRunner(torch, gh, shapes)
+    runner.run(max(0, args.warmup))
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end)
+    regions = []
+    while len(regions) < 5 or (sum(regions) < MIN_TIMED_MS and len(regions) < 100000):
+        torch.cuda.synchronize()
+        start.record()
+        runner.run(steps)
+        end.record()
+        torch.cuda.synchronize()
+        regions.append(start.elapsed_time(end))
+    ms = statistics.median(regions)
     value = step_bytes * steps / (ms * 1e-3) / 1e9
-    print(f"# sweep: {steps} steps in {ms:.2f} ms -> {value:.1f} GB/s", file=sys.stderr,
-          flush=True)
+    print(f"# sweep: {len(regions)} regions of {steps} steps, median {ms:.3f} ms -> "
+          f"{value:.1f} GB/s", file=sys.stderr, flush=True)
     if args.only == "sweep":
         return 0
 
     per = per_gemv(torch, gh, shapes, timer, busy, reps=64)
     print(f"# per-gemv: {json.dumps(per)}", file=sys.stderr, flush=True)
-    del graph, shapes
+    del runner, shapes
     torch.cuda.empty_cache()
     shapes_4b = build_sweep(torch, gh, gen, SWEEP_4B)
     per_4b = per_gemv(torch, gh, shapes_4b, timer, busy, reps=16)
@@ -597,8 +653,13 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": replays_w * ROT_STEPS,
+        "warmup": max(0, args.warmup),
         "ms_per_step": round(ms / steps, 5),
+        "timing": {"regions": len(regions), "timed_ms_total": round(sum(regions), 3),
+                   "region_ms_median": round(ms, 4), "region_ms_min": round(min(regions), 4),
+                   "region_ms_max": round(max(regions), 4),
+                   "what": "value from the median of the timed regions, each exactly "
+                           "`steps` steps between synchronisations"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -638,6 +699,7 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    torch.cuda.synchronize()
     gh.close()
     return 0
 
