@@ -93,6 +93,102 @@ struct State {
 
 State g;
 
+// ---- per-op GPU timing (the reference's PerfBench, gemma.c:2402-2431) ----
+// When enabled, every device entry point records a HIP event before and
+// after its launches on its stream; the pairs are resolved into totals per
+// (phase, op) lazily (when many are pending, and on read).  Launches on a
+// stream that is being captured into a graph are not timed.
+enum PerfOp { kOpQuantizeAct, kOpGemvInt8, kOpGemmInt8, kOpGemvFpx, kOpGemmFpx, kOpCount };
+const char *const kOpName[kOpCount] = {"quantize_act", "gemv_int8", "gemm_int8", "gemv_fpx",
+                                       "gemm_fpx"};
+constexpr int kPhases = 3;  // PerfPhase: prefill, decode, vision (gemma.c:2402-2407)
+
+struct Perf {
+  std::mutex mu;
+  bool on = false;
+  int phase = 0;
+  struct Pending {
+    int op, phase;
+    hipEvent_t a, b;
+  };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> pool;
+  double sec[kPhases][kOpCount] = {};
+  long calls[kPhases][kOpCount] = {};
+
+  hipEvent_t take() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+  }
+  // resolves every pending pair (waits for its end event)
+  hipError_t drain() {
+    hipError_t err = hipSuccess;
+    for (const Pending &p : pending) {
+      float ms = 0.0f;
+      hipError_t e = hipEventSynchronize(p.b);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, p.a, p.b);
+      if (e == hipSuccess) {
+        sec[p.phase][p.op] += ms * 1e-3;
+        calls[p.phase][p.op] += 1;
+      } else if (err == hipSuccess) {
+        err = e;
+      }
+      pool.push_back(p.a);
+      pool.push_back(p.b);
+    }
+    pending.clear();
+    return err;
+  }
+  void release() {
+    (void)drain();
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+    pool.clear();
+  }
+};
+Perf g_perf;
+
+// Times the launches made during its lifetime on `stream` as one call of op.
+class PerfScope {
+ public:
+  PerfScope(int op, hipStream_t stream) : op_(op), stream_(stream) {
+    if (!g_perf.on) return;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+      return;
+    std::lock_guard<std::mutex> lock(g_perf.mu);
+    a_ = g_perf.take();
+    b_ = g_perf.take();
+    if (a_ == nullptr || b_ == nullptr || hipEventRecord(a_, stream) != hipSuccess) {
+      if (a_ != nullptr) g_perf.pool.push_back(a_);
+      if (b_ != nullptr) g_perf.pool.push_back(b_);
+      a_ = b_ = nullptr;
+    }
+  }
+  ~PerfScope() {
+    if (a_ == nullptr) return;
+    std::lock_guard<std::mutex> lock(g_perf.mu);
+    if (hipEventRecord(b_, stream_) != hipSuccess) {
+      g_perf.pool.push_back(a_);
+      g_perf.pool.push_back(b_);
+      return;
+    }
+    g_perf.pending.push_back(Perf::Pending{op_, g_perf.phase, a_, b_});
+    if (g_perf.pending.size() >= 512) (void)g_perf.drain();
+  }
+  PerfScope(const PerfScope &) = delete;
+  PerfScope &operator=(const PerfScope &) = delete;
+
+ private:
+  int op_;
+  hipStream_t stream_;
+  hipEvent_t a_ = nullptr, b_ = nullptr;
+};
+
 // NULL is HIP's default (null) stream, so work on it is ordered with the
 // caller's own default-stream copies.
 hipStream_t pick_stream(void *stream) { return static_cast<hipStream_t>(stream); }
@@ -286,6 +382,11 @@ int gemma_hip_init(int device) {
 void gemma_hip_shutdown(void) {
   if (!g.ready) return;
   (void)hipStreamSynchronize(g.stream);
+  {
+    std::lock_guard<std::mutex> lock(g_perf.mu);
+    g_perf.release();
+    g_perf.on = false;
+  }
   gh::release_gemm_workspaces();
   {
     std::lock_guard<std::mutex> guard(g.lock);
@@ -316,6 +417,45 @@ const char *gemma_hip_last_error(void) { return g_err; }
 int gemma_hip_sync(void *stream) {
   if (need_init()) return 1;
   GH_CHECK("gemma_hip_sync", hipStreamSynchronize(pick_stream(stream)));
+  return 0;
+}
+
+int gemma_hip_perf_enable(int on) {
+  if (need_init()) return 1;
+  std::lock_guard<std::mutex> lock(g_perf.mu);
+  if (on && !g_perf.on) {
+    (void)g_perf.drain();
+    memset(g_perf.sec, 0, sizeof(g_perf.sec));
+    memset(g_perf.calls, 0, sizeof(g_perf.calls));
+  }
+  g_perf.on = on != 0;
+  return 0;
+}
+
+int gemma_hip_perf_phase(int phase) {
+  if (phase < 0 || phase >= kPhases)
+    return fail("gemma_hip_perf_phase: phase %d outside 0..%d", phase, kPhases - 1);
+  std::lock_guard<std::mutex> lock(g_perf.mu);
+  g_perf.phase = phase;
+  return 0;
+}
+
+int gemma_hip_perf_read(gemma_hip_perf_entry *out, int max, int *count) {
+  if (need_init()) return 1;
+  if (count == nullptr || max < 0 || (max > 0 && out == nullptr))
+    return fail("gemma_hip_perf_read: bad arguments");
+  std::lock_guard<std::mutex> lock(g_perf.mu);
+  const hipError_t e = g_perf.drain();
+  if (e != hipSuccess) return hip_fail("gemma_hip_perf_read", e);
+  int n = 0;
+  for (int ph = 0; ph < kPhases; ++ph)
+    for (int op = 0; op < kOpCount; ++op) {
+      if (g_perf.calls[ph][op] == 0) continue;
+      if (n < max) out[n] = gemma_hip_perf_entry{kOpName[op], ph, g_perf.sec[ph][op],
+                                                 g_perf.calls[ph][op]};
+      ++n;
+    }
+  *count = n;
   return 0;
 }
 
@@ -379,6 +519,7 @@ int gemma_hip_quantize(int8_t *dst, float *dsc, const float *src, int sstr,
   if (m == 0) return 0;
   if (dst == nullptr || dsc == nullptr || src == nullptr)
     return fail("gemma_hip_quantize: null pointer");
+  PerfScope perf(kOpQuantizeAct, pick_stream(stream));
   GH_CHECK("gemma_hip_quantize: launch",
            gh::launch_quantize(dst, dsc, src, sstr, m, n, pick_stream(stream)));
   return 0;
@@ -392,7 +533,7 @@ namespace {
 // workspace from the library's static scratch instead of memory it allocates.
 int matmul_impl(const char *name, float *dst, int dstr, const int8_t *mat, int mstr,
                 const float *matsc, const int8_t *src, int sstr, const float *ssc, int m,
-                int n, int k, void *stream, bool noalloc) {
+                int n, int k, void *stream, bool noalloc, int op = -1) {
   if (need_init()) return 1;
   if (dstr == 0) dstr = n;
   if (mstr == 0) mstr = k;
@@ -401,6 +542,7 @@ int matmul_impl(const char *name, float *dst, int dstr, const int8_t *mat, int m
   if (m == 0) return 0;
   if (!dst || !mat || !matsc || !src || !ssc) return fail("%s: null pointer", name);
   hipStream_t s = pick_stream(stream);
+  PerfScope perf(op >= 0 ? op : m == 1 ? kOpGemvInt8 : kOpGemmInt8, s);
   if (m == 1 && mstr == k && k <= kMaxGemvK8) {
     gh::GemvJobs jobs{};
     jobs.w[0] = mat;
@@ -457,6 +599,7 @@ int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,
   if (m == 0) return 0;
   if (!dst || !mat || !matsc || !src || !ssc)
     return fail("gemma_hip_matmul_heads: null pointer");
+  PerfScope perf(kOpGemmInt8, pick_stream(stream));
   GH_CHECK("gemma_hip_matmul_heads: launch",
            gh::launch_gemm_i8(dst, hdim, hdim, mat, k, matsc, src, k, ssc, m,
                               heads * hdim, k, g.info, pick_stream(stream)));
@@ -477,6 +620,7 @@ int gemma_hip_matmul_multi(const gemma_hip_job *jobs, int njobs,
     if (jobs[j].m > 0 && jobs[j].sc == nullptr)
       return fail("gemma_hip_matmul_multi: job %d has no scales", j);
   if (gj.end[njobs - 1] == 0) return 0;
+  PerfScope perf(kOpGemvInt8, pick_stream(stream));
   GH_CHECK("gemma_hip_matmul_multi: launch",
            gh::launch_gemv_i8(gj, k, x, xs, nullptr, nullptr, nullptr, g.info,
                               pick_stream(stream)));
@@ -496,6 +640,8 @@ int gemma_hip_quantize_matmul(const gemma_hip_job *jobs, int njobs,
     if (jobs[j].m > 0 && jobs[j].sc == nullptr)
       return fail("gemma_hip_quantize_matmul: job %d has no scales", j);
   hipStream_t s = pick_stream(stream);
+  // the quantize is fused into the GEMV kernel: one launch, timed as gemv_int8
+  PerfScope perf(gj.end[njobs - 1] == 0 ? kOpQuantizeAct : kOpGemvInt8, s);
   if (gj.end[njobs - 1] == 0) {
     // no rows: still produce the quantized vector when asked for
     if (xq != nullptr && xs != nullptr)
@@ -508,9 +654,28 @@ int gemma_hip_quantize_matmul(const gemma_hip_job *jobs, int njobs,
   return 0;
 }
 
+}  // extern "C"
+
+namespace {
+int matmul_f32_impl(float *dst, int dstr, const float *mat, int mstr, const float *src,
+                    int sstr, int m, int n, int k, void *stream, int op);
+}  // namespace
+
+extern "C" {
+
 int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
                          const float *src, int sstr, int m, int n, int k,
                          void *stream) {
+  return matmul_f32_impl(dst, dstr, mat, mstr, src, sstr, m, n, k, stream, -1);
+}
+
+}  // extern "C"
+
+namespace {
+// gemma_hip_matmul_f32; op >= 0 names the timed op (the _host gemm_fpx
+// drop-in counts m == 1 calls as gemm_fpx, as the reference does)
+int matmul_f32_impl(float *dst, int dstr, const float *mat, int mstr, const float *src,
+                    int sstr, int m, int n, int k, void *stream, int op) {
   if (need_init()) return 1;
   if (dstr == 0) dstr = n;
   if (mstr == 0) mstr = k;
@@ -519,6 +684,7 @@ int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
   if (m == 0) return 0;
   if (!dst || !mat || !src) return fail("gemma_hip_matmul_f32: null pointer");
   hipStream_t s = pick_stream(stream);
+  PerfScope perf(op >= 0 ? op : m == 1 ? kOpGemvFpx : kOpGemmFpx, s);
   if (m == 1 && mstr == k && k <= kMaxGemvK32) {
     gh::GemvJobs jobs{};
     jobs.w[0] = mat;
@@ -534,6 +700,9 @@ int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
                                g.info, s));
   return 0;
 }
+}  // namespace
+
+extern "C" {
 
 int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
                                const float *x, int k, void *stream) {
@@ -544,6 +713,7 @@ int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
     return fail("gemma_hip_matmul_f32_multi: k=%d outside 1..%d", k, kMaxGemvK32);
   if (x == nullptr) return fail("gemma_hip_matmul_f32_multi: null activation pointer");
   if (gj.end[njobs - 1] == 0) return 0;
+  PerfScope perf(kOpGemvFpx, pick_stream(stream));
   GH_CHECK("gemma_hip_matmul_f32_multi: launch",
            gh::launch_gemv_f32(gj, k, x, g.info, pick_stream(stream)));
   return 0;
@@ -619,6 +789,7 @@ int gemma_hip_quantize_acts_host(int8_t *dst, float *dsc, const float *src,
              hipMemcpyAsync(g.staging, g.pinned, in_bytes, hipMemcpyHostToDevice, g.stream));
     in = (const float *)g.staging;
   }
+  PerfScope perf(kOpQuantizeAct, g.stream);
   GH_CHECK("quantize_acts_host: launch",
            gh::launch_quantize(g.act.dev_q, g.act.dev_s, in, sstr, m, n, g.stream,
                                g.act.mir_q_dev, g.act.mir_s_dev));
@@ -724,8 +895,9 @@ int gemma_hip_gemm_int8_host(float *dst, int dstr, const int8_t *mat, int mstr,
     GH_CHECK("gemm_int8_host: H2D",
              hipMemcpyAsync(base + o_as, ssc, (size_t)m * 4, hipMemcpyHostToDevice, g.stream));
   }
-  if (gemma_hip_matmul((float *)(base + o_y), dstr, (const int8_t *)dmat, mstr,
-                       (const float *)dsc, a, sstr, as, m, n, k, g.stream))
+  if (matmul_impl("gemma_hip_gemm_int8_host", (float *)(base + o_y), dstr,
+                  (const int8_t *)dmat, mstr, (const float *)dsc, a, sstr, as, m, n, k,
+                  g.stream, false, kOpGemmInt8))
     return 1;
   GH_CHECK("gemm_int8_host: D2H",
            hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,
@@ -795,8 +967,8 @@ int gemma_hip_gemm_fpx_host(float *dst, int dstr, const float *mat, int mstr,
   char *base = g.staging;
   GH_CHECK("gemm_fpx_host: H2D",
            hipMemcpyAsync(base + o_a, src, src_floats * 4, hipMemcpyHostToDevice, g.stream));
-  if (gemma_hip_matmul_f32((float *)(base + o_y), dstr, (const float *)dmat, mstr,
-                           (const float *)(base + o_a), sstr, m, n, k, g.stream))
+  if (matmul_f32_impl((float *)(base + o_y), dstr, (const float *)dmat, mstr,
+                      (const float *)(base + o_a), sstr, m, n, k, g.stream, kOpGemmFpx))
     return 1;
   GH_CHECK("gemm_fpx_host: D2H",
            hipMemcpy2DAsync(dst, (size_t)dstr * 4, base + o_y, (size_t)dstr * 4,

@@ -27,6 +27,16 @@ class GemmaHipError(RuntimeError):
     pass
 
 
+class PerfEntry(ctypes.Structure):
+    """gemma_hip_perf_entry: one (phase, op) total of GPU time."""
+
+    _fields_ = [("op", ctypes.c_char_p), ("phase", ctypes.c_int), ("sec", ctypes.c_double),
+                ("calls", ctypes.c_long)]
+
+
+PERF_PHASES = ("prefill", "decode", "vision")  # the reference's PerfPhase order
+
+
 class Job(ctypes.Structure):
     """gemma_hip_job: mirrors the reference's GemvJob (gemma.c:2790-2800)."""
 
@@ -84,6 +94,9 @@ _SIGS = {
     "gemma_hip_quantize": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "gemma_hip_matmul": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
     "gemma_hip_matmul_noalloc": (_I, [_P, _I, _P, _I, _P, _P, _I, _P, _I, _I, _I, _P]),
+    "gemma_hip_perf_enable": (_I, [_I]),
+    "gemma_hip_perf_phase": (_I, [_I]),
+    "gemma_hip_perf_read": (_I, [ctypes.POINTER(PerfEntry), _I, ctypes.POINTER(_I)]),
     "gemma_hip_matmul_heads": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "gemma_hip_matmul_multi": (_I, [ctypes.POINTER(Job), _I, _P, _P, _I, _P]),
     "gemma_hip_quantize_matmul": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P, _P, _P]),
@@ -178,6 +191,22 @@ class GemmaHip:
     def matmul(self, dst, dstr, mat, mstr, matsc, src, sstr, ssc, m, n, k, stream=None):
         self._check(self.lib.gemma_hip_matmul(_addr(dst), dstr, _addr(mat), mstr, _addr(matsc),
                                               _addr(src), sstr, _addr(ssc), m, n, k, stream))
+
+    def perf_enable(self, on=True):
+        self._check(self.lib.gemma_hip_perf_enable(1 if on else 0))
+
+    def perf_phase(self, phase):
+        self._check(self.lib.gemma_hip_perf_phase(PERF_PHASES.index(phase)))
+
+    def perf_read(self):
+        """{phase: {op: (seconds, calls)}} of the timed entry points."""
+        out = (PerfEntry * 64)()
+        n = ctypes.c_int(0)
+        self._check(self.lib.gemma_hip_perf_read(out, 64, ctypes.byref(n)))
+        res = {}
+        for e in out[:min(n.value, 64)]:
+            res.setdefault(PERF_PHASES[e.phase], {})[e.op.decode()] = (e.sec, e.calls)
+        return res
 
     def matmul_noalloc(self, dst, dstr, mat, mstr, matsc, src, sstr, ssc, m, n, k,
                        stream=None):

@@ -80,6 +80,37 @@ const char *gemma_hip_last_error(void);
  * has finished. */
 int gemma_hip_sync(void *stream);
 
+/* ---- per-op GPU timing ------------------------------------------------- */
+/* The reference's PerfBench (gemma.c:2402-2431, accumulated by PERF_TOC,
+ * 2468-2476) on the device: while enabled, the GPU time of every device
+ * entry point's launches (HIP events on its stream, so PCIe copies of the
+ * _host calls are not included) is summed per phase and op, under the
+ * reference's op names: "quantize_act" (gemma_hip_quantize and the _host
+ * quantizes), "gemv_int8" (matmul with m == 1, matmul_multi, and
+ * quantize_matmul, whose quantize is fused into the GEMV launch), "gemm_int8"
+ * (matmul with m > 1, matmul_heads), "gemv_fpx" and "gemm_fpx" (the fp32
+ * entry points).  Launches on a stream under graph capture are not timed;
+ * the device-resident decoder and vision tower are not broken down. */
+
+/* One (phase, op) total: seconds of GPU time over `calls` calls. */
+typedef struct {
+  const char *op; /* static string: one of the names above */
+  int phase;      /* the reference's PerfPhase: 0 prefill, 1 decode, 2 vision */
+  double sec;
+  long calls;
+} gemma_hip_perf_entry;
+
+/* Start (on != 0, clearing the totals) or stop timing. */
+int gemma_hip_perf_enable(int on);
+
+/* Attribute the calls that follow to `phase` (PERF_PHASE, gemma.c:2479-2485). */
+int gemma_hip_perf_phase(int phase);
+
+/* Waits for the timed launches, then writes up to `max` non-empty totals to
+ * out (phase-major, ops in the reference's report order) and their number to
+ * *count. */
+int gemma_hip_perf_read(gemma_hip_perf_entry *out, int max, int *count);
+
 /* ---- weights: uploaded once, addressed by their host pointers ---------- */
 
 /* Copy [host, host+bytes) to a new device allocation.  Registered ranges are

@@ -302,6 +302,13 @@ int main(int argc, char **argv) {
   hip_or_die(gemma_hip_init(0), "init");
   weight_bytes = register_decoder(model->decoder);
   setup_sec = now_sec() - setup_tic;
+  hip_or_die(gemma_hip_perf_enable(1), "perf");
+#endif
+/* device-side per-op timing follows the reference's phases (PERF_PHASE) */
+#ifdef GEMMA_E2E_HIP
+#define E2E_PHASE(ph) hip_or_die(gemma_hip_perf_phase(ph), "perf phase")
+#else
+#define E2E_PHASE(ph) ((void)0)
 #endif
 
   int *prompt = malloc((size_t)prompt_len * sizeof(int));
@@ -330,6 +337,7 @@ int main(int argc, char **argv) {
 
   if (decode_only) {
     /* every position through the decode path, <bos> first */
+    E2E_PHASE(PERF_PHASE_DECODE);
     double tic = now_sec();
     for (int idx = 0; idx <= prompt_len; idx++) {
       int tok = idx == 0 ? bos_tok : prompt[idx - 1];
@@ -349,6 +357,7 @@ int main(int argc, char **argv) {
     }
     prefill_sec = now_sec() - tic;
   } else {
+    E2E_PHASE(PERF_PHASE_PREFILL);
     double tic = now_sec();
     if (forward_gemma_prefill(model, buf, &bos_tok, 1, &pos, chunk, NULL, false,
                               threads, &perf) != 0) {
@@ -371,6 +380,7 @@ int main(int argc, char **argv) {
   int token = argmax(buf->logits, nvocab, threads);
   generated[0] = token;
 
+  E2E_PHASE(PERF_PHASE_DECODE);
   double tic = now_sec();
   for (int step = 0; step < decode_steps; step++) {
     if (forward_gemma_decode(model, buf, token, pos, threads, &perf) != 0) {
@@ -414,7 +424,29 @@ int main(int argc, char **argv) {
     }
     printf("}");
   }
-  printf("}, \"bos\": %d, \"logits_fnv\": \"%016" PRIx64 "\", \"prompt\": [",
+  printf("}, ");
+#ifdef GEMMA_E2E_HIP
+  /* the library's GPU time of the same ops (HIP events, no PCIe copies) */
+  gemma_hip_perf_entry dev_ops[32];
+  int ndev = 0;
+  hip_or_die(gemma_hip_perf_read(dev_ops, 32, &ndev), "perf read");
+  printf("\"device_ops\": {");
+  for (int phase = 0; phase < 2; phase++) {
+    printf("%s\"%s\": {", phase ? ", " : "", phase ? "decode" : "prefill");
+    int first = 1;
+    for (int i = 0; i < ndev && i < 32; i++) {
+      if (dev_ops[i].phase != phase) {
+        continue;
+      }
+      printf("%s\"%s\": [%.6f, %ld]", first ? "" : ", ", dev_ops[i].op, dev_ops[i].sec,
+             dev_ops[i].calls);
+      first = 0;
+    }
+    printf("}");
+  }
+  printf("}, ");
+#endif
+  printf("\"bos\": %d, \"logits_fnv\": \"%016" PRIx64 "\", \"prompt\": [",
          bos_tok, hash);
   for (int idx = 0; idx < prompt_len; idx++) {
     printf("%s%d", idx ? ", " : "", prompt[idx]);

@@ -139,6 +139,12 @@ def test_e2e_hip_build_matches_reference(model_dir, name, prompt_len, steps, chu
     # the library really ran: every int8 op of the HIP build went through it
     assert hip["weight_bytes"] > 0
     assert "gemm_int8" in hip["ops"]["prefill"] and "gemv_int8" in hip["ops"]["decode"]
+    # the library's own GPU timing counts the same calls under the same names
+    for phase in ("prefill", "decode"):
+        for op, (sec, calls) in hip["device_ops"][phase].items():
+            assert op in hip["ops"][phase], (phase, op)
+            assert calls == hip["ops"][phase][op][1], (phase, op)
+            assert 0 < sec <= hip["ops"][phase][op][0] * 1.01 + 1e-3, (phase, op)
 
 
 # ------------------------------------------- decode glue vs the reference program

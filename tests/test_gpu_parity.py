@@ -556,3 +556,37 @@ def test_patch_embed_host(gh, oracle):
     finally:
         gh.release_weights(pe)
         gh.release_weights(pe_b)
+
+
+# ------------------------------------------------------------- per-op timing
+def test_perf_counts_ops_under_reference_names(gh):
+    """gemma_hip_perf_*: GPU time per (phase, op) under the reference's
+    PerfBench names (gemma.c:2426-2431)."""
+    rng = np.random.default_rng(5)
+    k, n, m = 640, 512, 96
+    W = dev(rng.integers(-127, 128, (n, k), dtype=np.int8))
+    ws = dev(rng.uniform(1e-3, 1e-2, n).astype(np.float32))
+    x = dev(rng.standard_normal((m, k)).astype(np.float32))
+    xq = torch.empty((m, k), dtype=torch.int8, device="cuda")
+    xs = torch.empty(m, dtype=torch.float32, device="cuda")
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.perf_enable(True)
+    try:
+        gh.perf_phase("prefill")
+        gh.quantize(xq, xs, x, k, m, k, stream())
+        gh.matmul(y, n, W, k, ws, xq, k, xs, m, n, k, stream())
+        gh.matmul(y, n, W, k, ws, xq, k, xs, m, n, k, stream())
+        gh.perf_phase("decode")
+        for _ in range(3):
+            gh.quantize_matmul([(W, ws, y, n)], x, k, None, None, stream())
+        got = gh.perf_read()
+    finally:
+        gh.perf_enable(False)
+    assert set(got) == {"prefill", "decode"}
+    assert got["prefill"]["quantize_act"][1] == 1
+    assert got["prefill"]["gemm_int8"][1] == 2
+    assert got["decode"] == {"gemv_int8": got["decode"]["gemv_int8"]}
+    assert got["decode"]["gemv_int8"][1] == 3
+    for ph in got.values():
+        for sec, calls in ph.values():
+            assert 0 < sec < 1.0
