@@ -25,6 +25,10 @@ The JSON line also carries, measured in the same run:
                 their sum ("all": bytes of the five launches / summed time)
   gemm          int8 MFMA GEMM TOPS at the gemma-3-4b prefill shapes (M=2048)
                 and the SigLIP tower shapes (M=4096), % of the 5.0 POPS peak
+  per_gemv_f32  the fp32 fallback ('U' files, gemv_fpx): the sweep's launches
+                with fp32 weights, GB/s per launch
+  gemm_f32      the fp32 GEMM (gemm_fpx) at the gemma-3-4b prefill shapes,
+                TFLOP/s against the 157.3 TFLOP/s fp32 matrix peak
   decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
                 decode token (26 layers x {qkv, o, gate/up, down} + LM head)
   decoder       configs 3 (gemma-3-1b: 512 prompt tokens, then 256 decode
@@ -103,6 +107,11 @@ def gemv_bytes(n: int, k: int) -> int:
     one or several jobs sharing x): int8 W [n][k], fp32 row scales [n], fp32
     x [k], fp32 y [n]."""
     return n * k + 4 * n + 4 * k + 4 * n
+
+
+def gemv_f32_bytes(n: int, k: int) -> int:
+    """Algorithmic HBM bytes of one fp32 GEMV: fp32 W [n][k], x [k], y [n]."""
+    return 4 * n * k + 4 * k + 4 * n
 
 
 def gemm_ops(m: int, n: int, k: int) -> int:
@@ -185,10 +194,30 @@ def build_sweep(torch, gh, gen, sweep=SWEEP_1B):
 
 def launch_gemv(gh, sh, copy, stream):
     arr, nj = sh["jobs"][copy % sh["copies"]]
-    rc = gh.lib.gemma_hip_quantize_matmul(arr, nj, sh["x"].data_ptr(), sh["k"], None, None,
-                                          stream)
+    if sh.get("f32"):
+        rc = gh.lib.gemma_hip_matmul_f32_multi(arr, nj, sh["x"].data_ptr(), sh["k"], stream)
+    else:
+        rc = gh.lib.gemma_hip_quantize_matmul(arr, nj, sh["x"].data_ptr(), sh["k"], None, None,
+                                              stream)
     if rc != 0:
         raise RuntimeError(gh.lib.gemma_hip_last_error().decode())
+
+
+def build_sweep_f32(torch, gh, gen, sweep=SWEEP_1B):
+    """The sweep's launches on the fp32 path (gemv_fpx / gemv_fpx_multi,
+    gemma.c:2730-2752, 2839-2858): fp32 weights N(0, 0.02), fp32 x."""
+    shapes = []
+    for name, ns, k in sweep:
+        n = sum(ns)
+        copies = max(1, min(ROT_STEPS, math.ceil(ROTATE_BYTES / (4 * n * k))))
+        ws = [[torch.randn((r, k), generator=gen, device="cuda") * 0.02 for r in ns]
+              for _ in range(copies)]
+        x = outlier_acts(torch, (k,), gen)
+        ys = [torch.empty(r, device="cuda", dtype=torch.float32) for r in ns]
+        jobs = [gh.jobs([(w, None, y, r) for w, y, r in zip(wc, ys, ns)]) for wc in ws]
+        shapes.append(dict(name=name, n=list(ns), k=k, copies=copies, w=ws, x=x, y=ys,
+                           jobs=jobs, f32=True, bytes=gemv_f32_bytes(n, k)))
+    return shapes
 
 
 def sweep_graph(torch, gh, shapes, nsteps=ROT_STEPS):
@@ -284,6 +313,30 @@ def bench_gemm(torch, gh, gen, timer, reps):
         tops = ops / (us * 1e-6) / 1e12
         groups[prefix + "_layer"] = dict(tops=round(tops, 1), frac=round(tops / INT8_PEAK_TOPS, 4))
     return dict(peak_tops=INT8_PEAK_TOPS, shapes=out, **groups)
+
+
+def bench_gemm_f32(torch, gh, gen, timer, reps):
+    """The fp32 GEMM (gemm_fpx, gemma.c:3304-3399; 'U' model files) at the
+    gemma-3-4b prefill shapes, TFLOP/s against the 157.3 TFLOP/s fp32 matrix
+    peak."""
+    out = {}
+    stream = torch.cuda.current_stream().cuda_stream
+    for name, m, n, k in GEMM_SHAPES[:5]:
+        a = torch.randn((m, k), generator=gen, device="cuda")
+        b = torch.randn((n, k), generator=gen, device="cuda") * 0.02
+        d = torch.empty((m, n), device="cuda", dtype=torch.float32)
+
+        def run():
+            for _ in range(reps):
+                gh.matmul_f32(d, n, b, k, a, k, m, n, k, stream)
+
+        run()
+        ms = statistics.median(timer.elapsed_ms(run) for _ in range(TIMING_RUNS)) / reps
+        tf = gemm_ops(m, n, k) / (ms * 1e-3) / 1e12
+        out[name] = dict(m=m, n=n, k=k, us=round(ms * 1e3, 2), tflops=round(tf, 1),
+                         frac=round(tf / FP32_PEAK_TFLOPS, 4))
+        del a, b, d
+    return {"peak_tflops": FP32_PEAK_TFLOPS, "shapes": out}
 
 
 def bench_decode_1b(torch, gh, gen, timer, tokens):
@@ -526,7 +579,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=2.0,
                     help="CPU-baseline sample time per sweep shape")
-    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder", "vision", "gemm"],
+    ap.add_argument("--only", choices=["sweep", "lm_head", "decoder", "vision", "gemm", "f32"],
                     default=None,
                     help="profiling aid: run just the timed sweep, the LM-head timing, "
                          "the device-resident decoder, the vision tower or the GEMM shapes")
@@ -573,6 +626,21 @@ def main() -> int:
     timer = Timer(torch)
     if args.only == "gemm":
         print(json.dumps(bench_gemm(torch, gh, gen, timer, reps=10)), flush=True)
+        gh.close()
+        return 0
+    if args.only == "f32":
+        stream = torch.cuda.current_stream().cuda_stream
+        shapes_f32 = build_sweep_f32(torch, gh, gen)
+        lm_f32 = shapes_f32[-1]
+
+        def busy_f32():
+            for i in range(2):
+                launch_gemv(gh, lm_f32, i, stream)
+
+        print(json.dumps({"per_gemv_f32": per_gemv(torch, gh, shapes_f32, timer, busy_f32,
+                                                    reps=16),
+                          "gemm_f32": bench_gemm_f32(torch, gh, gen, timer, reps=5)}),
+              flush=True)
         gh.close()
         return 0
     shapes = build_sweep(torch, gh, gen)
@@ -628,6 +696,13 @@ def main() -> int:
     torch.cuda.empty_cache()
     gemm = bench_gemm(torch, gh, gen, timer, reps=10)
     print(f"# gemm: {json.dumps(gemm)}", file=sys.stderr, flush=True)
+    shapes_f32 = build_sweep_f32(torch, gh, gen)
+    per_f32 = per_gemv(torch, gh, shapes_f32, timer, busy, reps=16)
+    print(f"# per-gemv fp32: {json.dumps(per_f32)}", file=sys.stderr, flush=True)
+    del shapes_f32
+    torch.cuda.empty_cache()
+    gemm_f32 = bench_gemm_f32(torch, gh, gen, timer, reps=5)
+    print(f"# gemm fp32: {json.dumps(gemm_f32)}", file=sys.stderr, flush=True)
     dec = bench_decode_1b(torch, gh, gen, timer, tokens=50)
     print(f"# decode_1b: {json.dumps(dec)}", file=sys.stderr, flush=True)
     decoder = {}
@@ -693,6 +768,8 @@ def main() -> int:
         "per_gemv": per,
         "per_gemv_4b": per_4b,
         "gemm": gemm,
+        "per_gemv_f32": per_f32,
+        "gemm_f32": gemm_f32,
         "decode_1b": dec,
         "decoder": decoder,
         "vision": vision,

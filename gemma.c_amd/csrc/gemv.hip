@@ -472,6 +472,133 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(
   }
 }
 
+// fp32 GEMV on the streaming schedule of gemv_i8_stream_kernel (gemv_fpx,
+// gemma.c:2730-2752, and gemv_fpx_multi, 2839-2858): groups of R = 64 / L
+// consecutive rows of one job dealt round robin to an all-resident grid, raw
+// buffer loads whose out-of-range offsets return zeros (rows past a job's
+// end, chunks past k, groups past the last), nontemporal weight loads.  A
+// row of k floats is kc = k / 4 chunks of 16 bytes; lane `sub` of a row
+// takes chunks sub, sub + L, ... in PASSES passes of CPL chunks.  x is
+// staged in LDS as fp32.  The sum is fp32 FMAs in two chains per lane, then
+// a fixed tree over the L lanes (the reference's order is its compiler's;
+// the bound is the fp32 tolerance).  Requires every job's m * k * 4 < 2^31.
+template <int L>
+__device__ __forceinline__ float group_sum_f32(float v) {
+  static_assert(L == 8 || L == 16 || L == 32 || L == 64, "L is 8, 16, 32 or 64");
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppHalfMirror>(v);
+  if (L >= 16) v += dpp_f32<kDppMirror>(v);
+  if (L >= 32) v += __shfl_xor(v, 16, 64);
+  if (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int L, int CPL, int NT>
+__global__ __launch_bounds__(NT) void gemv_f32_stream_kernel(GemvJobs jobs, int ngroups, int k,
+                                                             int passes,
+                                                             const float *__restrict__ x) {
+  extern __shared__ v4f lds_f4[];
+  constexpr int R = 64 / L;
+  constexpr int kBlockWaves = NT / 64;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane % L;
+  const int rloc = lane / L;
+  const int kc = k >> 2;
+  const int nwaves = gridDim.x * kBlockWaves;
+  const int w0 = blockIdx.x * kBlockWaves + wave;
+
+  int gend[kMaxJobs];
+  {
+    int prev = 0, g = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxJobs; ++t) {
+      if (t < jobs.njobs) g += (jobs.end[t] - prev + R - 1) / R;
+      gend[t] = g;
+      prev = jobs.end[t];
+    }
+  }
+  struct Where {
+    int job, row, m;
+  };
+  auto where = [&](int g) {
+    int j = 0, gs = 0, rs = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxJobs - 1; ++t)
+      if (t + 1 < jobs.njobs && g >= gend[t]) {
+        j = t + 1;
+        gs = gend[t];
+        rs = jobs.end[t];
+      }
+    return Where{j, (g - gs) * R + rloc, jobs.end[j] - rs};
+  };
+  auto pick_s = [&](auto const (&a)[kMaxJobs], int j) {  // j is wave-uniform
+    auto v = a[0];
+#pragma unroll
+    for (int t = 1; t < kMaxJobs; ++t)
+      if (j == t) v = a[t];
+    return v;
+  };
+  struct Slot {
+    v4f w[CPL];
+  };
+  auto load = [&](int g, int pass, Slot &s) {
+    const Where at = where(g);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void *>(pick_s(jobs.w, at.job)), (short)0, at.m * k * 4, 0x00020000);
+    const bool ok = g < ngroups && at.row < at.m;
+    const uint32_t row_off = ok ? (uint32_t)at.row * (uint32_t)k * 4u : kOutOfRange;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + (pass * CPL + i) * L;
+      s.w[i] = __builtin_bit_cast(
+          v4f, __builtin_amdgcn_raw_buffer_load_b128(
+                   rw, c < kc ? row_off + (uint32_t)c * 16u : kOutOfRange, 0, kStreamPolicy));
+    }
+  };
+
+  // work items t = (group i = t / passes of this wave, pass t % passes); the
+  // loads of item t+1 are in flight while item t is summed
+  const int mine = w0 < ngroups ? (ngroups - 1 - w0) / nwaves + 1 : 0;
+  const int items = mine * passes;
+  auto item_load = [&](int t, Slot &s) { load(w0 + (t / passes) * nwaves, t % passes, s); };
+  Slot buf0, buf1;
+  item_load(0, buf0);
+  for (int c = threadIdx.x; c < kc; c += NT) lds_f4[c] = reinterpret_cast<const v4f *>(x)[c];
+  lds_barrier();
+
+  float a0 = 0.0f, a1 = 0.0f;
+  auto item_sum = [&](int t, const Slot &s) {
+    const int pass = t % passes;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int c = sub + (pass * CPL + u) * L;  // chunks past k hold zeros
+      const v4f xv = lds_f4[c < kc ? c : 0];
+      a0 = __builtin_fmaf(s.w[u].x, xv.x, a0);
+      a1 = __builtin_fmaf(s.w[u].y, xv.y, a1);
+      a0 = __builtin_fmaf(s.w[u].z, xv.z, a0);
+      a1 = __builtin_fmaf(s.w[u].w, xv.w, a1);
+    }
+    if (pass == passes - 1) {
+      const int g = w0 + (t / passes) * nwaves;
+      const float acc = group_sum_f32<L>(a0 + a1);
+      const Where at = where(g);
+      if (sub == 0 && g < ngroups && at.row < at.m) pick_s(jobs.dst, at.job)[at.row] = acc;
+      a0 = 0.0f;
+      a1 = 0.0f;
+    }
+  };
+  for (int t = 0; t < items; t += 2) {
+    item_load(t + 1, buf1);
+    item_sum(t, buf0);
+    if (t + 1 < items) {
+      item_load(t + 2, buf0);
+      item_sum(t + 1, buf1);
+    }
+  }
+}
+
 // Lanes per row: the widest L whose chunks divide evenly with >= 4 chunks per
 // lane, else 8.
 int lanes_for(int chunks) {
@@ -747,10 +874,81 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
                                               xs_out);
 }
 
+namespace {
+
+constexpr int kF32Cpl = 8;  // 16-byte chunks per lane and pass of the fp32 stream kernel
+
+template <int L>
+hipError_t launch_f32_stream(const DeviceInfo &dev, hipStream_t stream, const GemvJobs &jobs,
+                             int ngroups, int k, int passes, const float *x) {
+  auto kern = gemv_f32_stream_kernel<L, kF32Cpl, kStreamNT>;
+  const size_t lds = (size_t)(k / 4) * 16;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStreamNT, lds) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const long need = (ngroups + kStreamNT / 64 - 1) / (kStreamNT / 64);
+  const long cap = (long)dev.cus * per_cu;
+  kern<<<dim3((unsigned)(need < cap ? need : cap)), kStreamNT, lds, stream>>>(jobs, ngroups, k,
+                                                                              passes, x);
+  return hipGetLastError();
+}
+
+// jobs with rows split so that every job's m * k * 4 < 2^31 (the stream
+// kernel's buffer offsets), or false when that needs more than kMaxJobs jobs
+bool split_f32_jobs(const GemvJobs &in, int k, GemvJobs *out) {
+  const long max_rows = ((long)kOutOfRange - 1) / ((long)k * 4);
+  if (max_rows < 1) return false;
+  GemvJobs o{};
+  int n = 0;
+  for (int j = 0, prev = 0; j < in.njobs; prev = in.end[j], ++j) {
+    for (int r0 = prev; r0 < in.end[j]; r0 += (int)max_rows) {
+      if (n == kMaxJobs) return false;
+      const int r1 = (int)std::min<long>(in.end[j], (long)r0 + max_rows);
+      o.w[n] = static_cast<const float *>(in.w[j]) + (size_t)(r0 - prev) * k;
+      o.sc[n] = nullptr;
+      o.dst[n] = in.dst[j] + (r0 - prev);
+      o.end[n] = r1;
+      ++n;
+    }
+  }
+  if (n == 0) return false;
+  for (int t = n; t < kMaxJobs; ++t) o.end[t] = o.end[n - 1];
+  o.njobs = n;
+  *out = o;
+  return true;
+}
+
+}  // namespace
+
 hipError_t launch_gemv_f32(const GemvJobs &jobs, int k, const float *x,
                            const DeviceInfo &dev, hipStream_t stream) {
   const int total = jobs.end[jobs.njobs - 1];
   const bool vec = rows_aligned(jobs, k, 4, 16);
+  GemvJobs sj;
+  if (vec && ((uintptr_t)x & 15) == 0 && !tuning().force_loop && split_f32_jobs(jobs, k, &sj)) {
+    // lanes per row: the fewest (8 .. 64) that cover a row in at most two
+    // passes of kF32Cpl chunks, else 64 lanes and as many passes as needed
+    const int kc = k / 4;
+    int lanes = 64;
+    for (int l = 8; l <= 64; l *= 2)
+      if ((kc + l * kF32Cpl - 1) / (l * kF32Cpl) <= 2) {
+        lanes = l;
+        break;
+      }
+    const int passes = (kc + lanes * kF32Cpl - 1) / (lanes * kF32Cpl);
+    const int rows = 64 / lanes;
+    int ngroups = 0;
+    for (int j = 0, prev = 0; j < sj.njobs; prev = sj.end[j], ++j)
+      ngroups += (sj.end[j] - prev + rows - 1) / rows;
+    switch (lanes) {
+      case 8: return launch_f32_stream<8>(dev, stream, sj, ngroups, k, passes, x);
+      case 16: return launch_f32_stream<16>(dev, stream, sj, ngroups, k, passes, x);
+      case 32: return launch_f32_stream<32>(dev, stream, sj, ngroups, k, passes, x);
+      default: return launch_f32_stream<64>(dev, stream, sj, ngroups, k, passes, x);
+    }
+  }
   const int lanes = vec ? lanes_for(k / 4) : 64;
   const dim3 grid(grid_for(total, lanes, dev));
   const size_t lds = (size_t)(k + 3) / 4 * 16;

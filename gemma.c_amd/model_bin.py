@@ -65,6 +65,14 @@ def _write_qtensor(f, rng, rows: int, cols: int, chunk_rows: int = 32768) -> Non
     f.write(scales.tobytes())
 
 
+def _write_ftensor(f, rng, rows: int, cols: int, chunk_rows: int = 32768) -> None:
+    """An unquantized linear layer ('U' files): fp32 [rows][cols], N(0, 0.02)."""
+    for r0 in range(0, rows, chunk_rows):
+        r1 = min(rows, r0 + chunk_rows)
+        f.write((rng.standard_normal((r1 - r0, cols), dtype=np.float32)
+                 * np.float32(0.02)).tobytes())
+
+
 def _pascal(s: str) -> bytes:
     b = s.encode()
     assert len(b) <= 255
@@ -74,7 +82,7 @@ def _pascal(s: str) -> bytes:
 def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
               layers: int | None = None, slide: int | None = None, sc_att: float = 0.0,
               sc_log: float = 0.0, flags: int = 4 | 2 | 1, norm_std: float = 0.0,
-              vision: dict | None = None, swa: list | None = None) -> str:
+              vision: dict | None = None, swa: list | None = None, quant: bool = True) -> str:
     """Write a random-init W8A8 (f32 build) text model of shape `name`;
     `nvocab` and `layers` shrink it for quick tests, `slide`, the softcaps
     and the flags byte (4 qk-norm, 2 pre-FFN norm, 1 post-FFN norm) select
@@ -85,7 +93,9 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
     multimodal (flag 8): its VisionConfig follows the flags byte (gemma.c:
     723-733), the vocabulary gains the image soft token (905-913) and the
     tower's tensors follow the text decoder's in read_vision_encoder's order
-    (1688-1762)."""
+    (1688-1762).  quant=False writes an unquantized ('U') file: every linear
+    layer fp32 [out][in] with no scales (qtensor_size, gemma.c:1125-1131),
+    the path the reference's gemv_fpx / gemm_fpx call sites take."""
     c = dict(CONFIGS[name])
     nl, dim, hdim, mlp = c["nl"], c["dim"], c["hdim"], c["mlp"]
     if layers is not None:
@@ -94,9 +104,12 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
         c["slide"] = slide
     q_sz, kv_sz = c["n_heads"] * hdim, c["nkv"] * hdim
     rng = np.random.default_rng(seed)
+    if not quant and vision is not None:
+        raise ValueError("the writer's vision tower is W8A8 only")
+    linear = _write_qtensor if quant else _write_ftensor
     tmp = path + ".tmp"
     with open(tmp, "wb") as f:
-        f.write(b"GEMA" + b"f32" + b"Q")
+        f.write(b"GEMA" + b"f32" + (b"Q" if quant else b"U"))
         vc = vision["config"] if vision is not None else None
         if vc is not None and vc["text_dim"] != dim:
             raise ValueError("the vision tower's text_dim must be the model's dim")
@@ -126,17 +139,17 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
                 return np.zeros(n, np.float32).tobytes()
             return (rng.standard_normal(n, dtype=np.float32) * np.float32(norm_std)).tobytes()
 
-        _write_qtensor(f, rng, nvocab, dim)  # emb, also the tied LM head
+        linear(f, rng, nvocab, dim)  # emb, also the tied LM head
         for _ in range(nl):
-            _write_qtensor(f, rng, q_sz, dim)    # wq
-            _write_qtensor(f, rng, kv_sz, dim)   # wk
-            _write_qtensor(f, rng, kv_sz, dim)   # wv
-            _write_qtensor(f, rng, dim, q_sz)    # wo
+            linear(f, rng, q_sz, dim)    # wq
+            linear(f, rng, kv_sz, dim)   # wk
+            linear(f, rng, kv_sz, dim)   # wv
+            linear(f, rng, dim, q_sz)    # wo
             if flags & 4:
                 f.write(norm(hdim) + norm(hdim))  # nq, nk
-            _write_qtensor(f, rng, mlp, dim)     # w1 (up)
-            _write_qtensor(f, rng, mlp, dim)     # w2 (gate)
-            _write_qtensor(f, rng, dim, mlp)     # w3 (down)
+            linear(f, rng, mlp, dim)     # w1 (up)
+            linear(f, rng, mlp, dim)     # w2 (gate)
+            linear(f, rng, dim, mlp)     # w3 (down)
             for _ in range(2 + ((flags & 2) != 0) + ((flags & 1) != 0)):
                 f.write(norm(dim))               # n1 n2 [n3] [n4]
         f.write(norm(dim))                       # fnorm
@@ -173,15 +186,18 @@ def _write_vision(f, v: dict) -> None:
 
 
 def read_bin(path: str) -> dict:
-    """Map a W8A8 f32 .bin (text decoder) into numpy views, as the reference's
+    """Map an f32 .bin (text decoder) into numpy views, as the reference's
     mmap loader does (gemma.c:1942-2055, tensor order 1386-1469).  Returns
     {"config": {...}, "emb": (q, s), "layers": [{"wq": (q, s), ..., "n1": ...}],
-    "fnorm": ...}; int8 tensors are read-only views of the file."""
+    "fnorm": ...}; tensors are read-only views of the file.  In an fp32 ('U')
+    file (config["quant"] False) each linear layer is one fp32 [out][in]
+    array instead of the (int8, scales) pair."""
     data = np.memmap(path, dtype=np.uint8, mode="r")
     if bytes(data[:4]) != b"GEMA" or bytes(data[4:7]) != b"f32":
         raise ValueError(f"{path}: not an f32 Gemma.c model")
-    if bytes(data[7:8]) != b"Q":
-        raise ValueError(f"{path}: not a W8A8 ('Q') model")
+    if bytes(data[7:8]) not in (b"Q", b"U"):
+        raise ValueError(f"{path}: neither a W8A8 ('Q') nor an fp32 ('U') model")
+    quant = bytes(data[7:8]) == b"Q"
     at = 8
     (nl, n_heads, nkv, hdim, dim, mlp, q_scale, slide, img_tok, max_seq, nvocab, theta_l,
      theta_g, eps, sc_att, sc_log) = struct.unpack(">BBBHHHHHHIIfffff", bytes(data[at:at + 43]))
@@ -215,6 +231,8 @@ def read_bin(path: str) -> dict:
 
     def qt(rows, cols):
         nonlocal at
+        if not quant:  # 'U': fp32 [rows][cols]
+            return f32(rows * cols).reshape(rows, cols)
         q = np.frombuffer(data, np.int8, rows * cols, at).reshape(rows, cols)
         at += rows * cols
         return q, f32(rows)
@@ -222,7 +240,8 @@ def read_bin(path: str) -> dict:
     cfg = dict(nl=nl, n_heads=n_heads, nkv=nkv, hdim=hdim, dim=dim, mlp_dim=mlp,
                q_scale=q_scale, slide=slide, nvocab=nvocab, theta_l=theta_l, theta_g=theta_g,
                eps=eps, sc_att=sc_att, sc_log=sc_log, qk_norm=bool(flags & 4),
-               mlp_pre=bool(flags & 2), mlp_pst=bool(flags & 1), swa=swa, max_seq=max_seq)
+               mlp_pre=bool(flags & 2), mlp_pst=bool(flags & 1), swa=swa, max_seq=max_seq,
+               quant=quant)
     q_sz, kv_sz = n_heads * hdim, nkv * hdim
     emb = qt(nvocab, dim)
     layers = []

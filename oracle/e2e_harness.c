@@ -8,7 +8,9 @@
  *                  matmul runs on the CPU (the reference's own kernels).
  *   gemma_e2e_hip  the same source with the forward passes' calls to
  *                  quantize_act, quantize_acts, gemv_int8, gemv_int8_multi
- *                  and gemm_int8 renamed to the GH_ shims below (the rename
+ *                  and gemm_int8, and to the fp32 twins gemv_fpx,
+ *                  gemv_fpx_multi and gemm_fpx (unquantized 'U' model
+ *                  files), renamed to the GH_ shims below (the rename
  *                  is a sed script applied while the source is piped into
  *                  the compiler, e2e_retarget.sed), which call the library's
  *                  host entry points.  Everything else -- embedding, norms,
@@ -18,7 +20,9 @@
  *
  * Because the library's quantize and int8 matmul results are bit-identical
  * to the reference's, both builds must produce the same logits, bit for bit,
- * at every step, and so the same greedy token stream.
+ * at every step, and so the same greedy token stream, on a W8A8 ('Q')
+ * file.  On an fp32 ('U') file the sums' order differs (the reference's is
+ * its compiler's), so the logits agree to fp32 rounding, not bit for bit.
  *
  * The run follows sample() (gemma.c:5978-6075) with temperature 0: prefill
  * <bos> without logits (6010-6014), prefill the prompt with logits, then
@@ -152,13 +156,70 @@ static int GH_gemm_int8(float *dst, int dstr, const int8_t *mat, int mstr,
   return 0;
 }
 
+/* gemv_fpx (gemma.c:2734): every call site passes a weight matrix */
+static void GH_gemv_fpx(float *dst, const float *mat, const float *vec, int rows,
+                        int cols, bool omp, int threads, void *perf_any) {
+  (void)omp;
+  (void)threads;
+  PerfBench *perf = perf_any;
+  double tic = PERF_TIC(perf);
+  hip_or_die(gemma_hip_gemv_fpx_host(dst, mat, vec, rows, cols), "gemv_fpx");
+  PERF_TOC(perf, PERF_OP_GEMV_FPX, tic);
+}
+
+/* gemv_fpx_multi (gemma.c:2840) */
+static void GH_gemv_fpx_multi(const void *jobs_any, int njobs, const float *vec,
+                              int cols, int threads, void *perf_any) {
+  (void)threads;
+  const GemvJob *jobs = jobs_any;
+  PerfBench *perf = perf_any;
+  double tic = PERF_TIC(perf);
+  gemma_hip_job hjobs[GEMMA_HIP_MAX_JOBS];
+  if (njobs < 1 || njobs > GEMMA_HIP_MAX_JOBS) {
+    die_with("gemv_fpx_multi", "too many jobs");
+  }
+  for (int idx = 0; idx < njobs; idx++) {
+    hjobs[idx].w = jobs[idx].w;
+    hjobs[idx].sc = NULL;
+    hjobs[idx].dst = jobs[idx].dst;
+    hjobs[idx].m = jobs[idx].m;
+  }
+  hip_or_die(gemma_hip_gemv_fpx_multi_host(hjobs, njobs, vec, cols), "gemv_fpx_multi");
+  PERF_TOC(perf, PERF_OP_GEMV_FPX, tic);
+}
+
+/* gemm_fpx (gemma.c:3308).  The forward passes also use it for products of
+ * two activations (the attention scores of the vision tower and of the
+ * prefill, gemma.c:4538, 5222, 5271), which are outside the library's scope:
+ * a `mat` that is not a registered weight goes to the reference's own
+ * gemm_fpx (which times itself). */
+static int GH_gemm_fpx(float *dst, int dstr, const float *mat, int mstr,
+                       const float *src, int sstr, int rows, int cols,
+                       int depth, bool omp, int threads, void *perf_any) {
+  PerfBench *perf = perf_any;
+  if (gemma_hip_device_ptr(mat) == NULL) {
+    return gemm_fpx(dst, dstr, mat, mstr, src, sstr, rows, cols, depth, omp,
+                    threads, perf);
+  }
+  double tic = PERF_TIC(perf);
+  if (gemma_hip_gemm_fpx_host(dst, dstr, mat, mstr, src, sstr, rows, cols,
+                              depth) != 0) {
+    log_error("gemm_fpx (hip): %s", gemma_hip_last_error());
+    return 1;
+  }
+  PERF_TOC(perf, PERF_OP_GEMM_FPX, tic);
+  return 0;
+}
+
 /* one device copy per tensor: the int8 rows and the scales are separate
  * ranges, so each lands 256-byte aligned on the device even though the
  * mmapped file places them at arbitrary byte offsets */
 static size_t register_qtensor(const QTensor *tensor, size_t rows,
                                size_t cols) {
-  if (!tensor->quant) {
-    die_with("register", "the e2e harness expects a W8A8 ('Q') model");
+  if (!tensor->quant) {  /* an fp32 ('U') model file */
+    hip_or_die(gemma_hip_register_weights(tensor->fpx, rows * cols * sizeof(float)),
+               "register fp32 weights");
+    return rows * cols * sizeof(float);
   }
   hip_or_die(gemma_hip_register_weights(tensor->i8.q, rows * cols),
              "register int8 weights");

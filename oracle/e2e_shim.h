@@ -5,7 +5,7 @@
  * The HIP build compiles the reference's gemma.c with the call sites of its
  * forward passes (the "forward passes" section, gemma.c:4386-5595) renamed
  * from quantize_act / quantize_acts / gemv_int8 / gemv_int8_multi / gemm_int8
- * to the GH_ names below; e2e_harness.c defines them on top of the
+ * and gemv_fpx / gemv_fpx_multi / gemm_fpx to the GH_ names below; e2e_harness.c defines them on top of the
  * libgemma_hip host entry points.  They are declared here, before any of the
  * reference's types exist, so PerfBench* and GemvJob* travel as void*; the
  * argument order and meaning are the reference's own (gemma.c:2590, 2656,
@@ -33,5 +33,13 @@ static int GH_gemm_int8(float *dst, int dstr, const int8_t *mat, int mstr,
                         const float *matsc, const int8_t *src, int sstr,
                         const float *ssc, int m, int n, int k, bool omp,
                         int threads, void *perf);
+/* the fp32 twins (gemma.c:2734, 2840, 3308) */
+static void GH_gemv_fpx(float *dst, const float *mat, const float *vec, int m,
+                        int n, bool omp, int threads, void *perf);
+static void GH_gemv_fpx_multi(const void *jobs, int njobs, const float *vec,
+                              int n, int threads, void *perf);
+static int GH_gemm_fpx(float *dst, int dstr, const float *mat, int mstr,
+                       const float *src, int sstr, int m, int n, int k,
+                       bool omp, int threads, void *perf);
 
 #endif

@@ -37,12 +37,16 @@ needs_e2e = pytest.mark.skipif(
     reason="oracle/_ref e2e harnesses not built (they need /root/reference)")
 
 
-def run_e2e(binary, model, prompt_len, steps, threads=THREADS, chunk=None, seed=1234):
+def run_e2e(binary, model, prompt_len, steps, threads=THREADS, chunk=None, seed=1234,
+            logits=None):
     cmd = [binary, model, str(prompt_len), str(steps), str(seed), str(threads)]
     if chunk is not None:
         cmd.append(str(chunk))
     print("run:", " ".join(cmd), flush=True)
-    out = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    env = dict(os.environ)
+    if logits is not None:
+        env["GEMMA_E2E_LOGITS"] = str(logits)
+    out = subprocess.run(cmd, capture_output=True, text=True, timeout=600, env=env)
     assert out.returncode == 0, f"{binary} exited {out.returncode}: {out.stderr[-2000:]}"
     res = json.loads(out.stdout.strip().splitlines()[-1])
     summary = {k: res[k] for k in ("build", "prefill_tok_s", "decode_tok_s", "setup_s",
@@ -115,6 +119,22 @@ def test_reference_runs_written_model_deterministically(tmp_path):
     assert len(a["tokens"]) == 7 and all(0 <= t < 2048 for t in a["tokens"])
 
 
+@needs_e2e
+def test_reference_runs_written_fp32_model(tmp_path):
+    """An unquantized ('U') file from the writer: the reference's loader
+    accepts it (check_head, gemma.c:1915-1939), runs its fp32 path, and its
+    greedy tokens do not depend on the thread count."""
+    path = model_bin.write_bin(str(tmp_path / "u.bin"), "gemma-3-270m", seed=5,
+                               nvocab=2048, layers=3, quant=False)
+    with open(path, "rb") as f:
+        assert f.read(8) == b"GEMAf32U"
+    a = run_e2e(E2E_CPU, path, 9, 6, threads=2, chunk=4)
+    b = run_e2e(E2E_CPU, path, 9, 6, threads=5, chunk=4)
+    assert a["tokens"] == b["tokens"]
+    assert "gemv_fpx" in a["ops"]["decode"] and "gemm_fpx" in a["ops"]["prefill"]
+    assert "gemv_int8" not in a["ops"]["decode"]
+
+
 # ------------------------------------------------------------------ GPU
 @pytest.fixture(scope="module")
 def model_dir(tmp_path_factory):
@@ -145,6 +165,47 @@ def test_e2e_hip_build_matches_reference(model_dir, name, prompt_len, steps, chu
             assert op in hip["ops"][phase], (phase, op)
             assert calls == hip["ops"][phase][op][1], (phase, op)
             assert 0 < sec <= hip["ops"][phase][op][0] * 1.01 + 1e-3, (phase, op)
+
+
+# The fp32 ('U') path: the reference's gemv_fpx / gemv_fpx_multi / gemm_fpx call
+# sites (gemma.c:4766-5432) on the library.  There is no bit target (the
+# reference's fp32 sums are in its compiler's order), and no int8 requantization
+# amplifies rounding differences, so the HIP build's logits must stay within
+# FP32_E2E_TOL of the reference's (relative to the step's largest logit) at
+# every step both runs have reached with the same tokens; greedy streams may
+# part where two logits are closer than that, and the agreement is reported.
+FP32_E2E_TOL = 1e-4
+
+
+@pytest.mark.gpu
+@needs_e2e
+@pytest.mark.timeout(600)
+def test_e2e_hip_build_follows_reference_fp32(tmp_path):
+    """Config 1's shape (gemma-3-270m: 18 layers, vocab 262144) as an fp32
+    file: 32 prompt ids, 64 greedy steps."""
+    path = model_bin.write_bin(str(tmp_path / "u270m.bin"), "gemma-3-270m", seed=1234,
+                               quant=False)
+    nv = model_bin.read_bin(path)["config"]["nvocab"]
+    ref = run_e2e(E2E_CPU, path, 32, 64, logits=tmp_path / "ref.f32")
+    hip = run_e2e(E2E_HIP, path, 32, 64, logits=tmp_path / "hip.f32")
+    assert hip["prompt"] == ref["prompt"]
+    a = np.fromfile(tmp_path / "ref.f32", np.float32).reshape(-1, nv)
+    b = np.fromfile(tmp_path / "hip.f32", np.float32).reshape(-1, nv)
+    assert a.shape == b.shape == (65, nv)
+    same = 0  # steps whose input token both runs share
+    while same < 64 and hip["tokens"][same] == ref["tokens"][same]:
+        same += 1
+    worst = 0.0
+    for i in range(same + 1):  # logits row i comes from the token of step i - 1
+        rel = float(np.abs(a[i] - b[i]).max() / np.abs(a[i]).max())
+        worst = max(worst, rel)
+        assert rel <= FP32_E2E_TOL, f"step {i}: {rel:.3g}"
+    print(f"fp32 e2e: tokens agree for {same} of 65, worst |d|/max|logit| {worst:.3g}",
+          flush=True)
+    assert same >= 16
+    assert "gemv_fpx" in hip["device_ops"]["decode"]
+    assert "gemm_fpx" in hip["device_ops"]["prefill"]
+    assert hip["weight_bytes"] > 0
 
 
 # ------------------------------------------- decode glue vs the reference program

@@ -359,6 +359,49 @@ def test_f32_multi(gh, oracle):
         check_f32(host(o)[None, :], w, x[None, :], oracle)
 
 
+# The fp32 GEMV on the streaming schedule: the config-2 launches with fp32
+# weights (gemv_fpx / gemv_fpx_multi), rows of 2 and 4 passes (k = 2560, 6912,
+# 10240), ragged jobs with an empty one, and the gemma-3-4b LM head, whose
+# 2.7 GB of fp32 rows the launcher splits into jobs below 2 GB.
+@pytest.mark.parametrize("rows,k", [((1024, 256, 256), 1152), ((1152,), 1024),
+                                    ((6912, 6912), 1152), ((1152,), 6912),
+                                    ((262144,), 1152), ((2560,), 10240),
+                                    ((3001, 5, 0, 2999), 2560), ((17,), 16)])
+def test_f32_stream_gemv_vs_oracle(gh, oracle, rows, k):
+    note(f"f32 stream rows={rows} k={k}")
+    rng = np.random.default_rng(sum(rows) + k)
+    x = outlier_acts(rng, (k,))
+    mats, outs, specs = [], [], []
+    for r in rows:
+        w = (rng.standard_normal((max(r, 1), k), dtype=np.float32) * np.float32(0.02))
+        mats.append(w)
+        outs.append(torch.full((max(r, 1),), 7.0, dtype=torch.float32, device="cuda"))
+        specs.append((dev(w), None, outs[-1], r))
+    gh.matmul_f32_multi(specs, dev(x), k, stream())
+    for w, o, r in zip(mats, outs, rows):
+        got = host(o)
+        if r:
+            check_f32(got[None, :r], w[:r], x[None, :], oracle)
+        assert np.all(got[r:] == 7.0)
+
+
+def test_f32_stream_gemv_split_lm_head(gh, oracle):
+    """262144 x 2560 fp32 (the gemma-3-4b tied LM head, 2.7 GB): rows a tiled
+    random block, so that every split part reads distinct rows."""
+    n, k = 262144, 2560
+    rng = np.random.default_rng(9)
+    block = (rng.standard_normal((4096, k), dtype=np.float32) * np.float32(0.02))
+    W = torch.from_numpy(block).to("cuda").repeat(n // 4096, 1)
+    W += torch.arange(n, device="cuda", dtype=torch.float32)[:, None] * 1e-6
+    x = outlier_acts(rng, (k,))
+    y = torch.empty(n, dtype=torch.float32, device="cuda")
+    gh.matmul_f32(y, 0, W, 0, dev(x), 0, 1, n, k, stream())
+    rows = np.concatenate([np.arange(0, 8), rng.integers(0, n, 56), np.arange(n - 8, n)])
+    Wr = W[torch.from_numpy(rows).cuda()].cpu().numpy()
+    check_f32(host(y)[rows][None, :], Wr, x[None, :], oracle)
+    del W
+
+
 # --------------------------------------------------------------- host drop-ins
 def test_host_entry_points(gh, oracle):
     """The reference-shaped entry points on host buffers, with weights
