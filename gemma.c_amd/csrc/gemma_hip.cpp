@@ -1097,7 +1097,11 @@ int prefill_reserve(gemma_hip_decoder *d, int n) {
 // Enqueues the prompt pass of rows pos .. pos+n-1 (forward_text_chunk,
 // gemma.c:4985-5453) and the decode step's tail on the last row.  The step
 // record must hold {last token, pos + n - 1, 0} (the argmax advances it).
-hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st) {
+// embed: the rows are the tokens in pf_tok, embedded here; else pf_x holds
+// them already.  dense: mask=false, every row attends to every key up to the
+// last row, with no sliding window (gemma.c:5258-5290).
+hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, bool dense,
+                           hipStream_t st) {
   const gemma_hip_text_config &c = d->cfg;
   const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim, dim = c.dim, mlp = c.mlp_dim;
   const int stride = q_sz + 2 * kv_sz;
@@ -1107,8 +1111,8 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st)
     return gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, d->pf_a8, k, d->pf_as, n, nout, k, g.info,
                               st);
   };
-  if ((e = gh::launch_pf_embed(d->pf_tok, n, d->emb, d->emb_s, d->pf_x, dim,
-                               c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
+  if (embed && (e = gh::launch_pf_embed(d->pf_tok, n, d->emb, d->emb_s, d->pf_x, dim,
+                                        c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
     return e;
   for (int l = 0; l < c.nl; ++l) {
     const auto &L = d->layers[l];
@@ -1132,7 +1136,8 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st)
     if ((e = gh::launch_pf_qk_rope(rp, n, c.hdim, st)) != hipSuccess) return e;
     const gh::PfAttn at{d->pf_qkv, stride, kc, kc + cache, d->pf_xo, q_sz, n, pos, c.n_heads,
                         c.nkv, d->clen, sliding ? c.slide : 0,
-                        (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0};
+                        (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
+                        0, dense ? 1 : 0};
     if ((e = gh::launch_pf_attention(at, c.hdim, st)) != hipSuccess) return e;
     // o projection
     if ((e = gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st)) !=
@@ -1170,6 +1175,52 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, hipStream_t st)
     return e;
   return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
                                d->tokens, d->clen, st);
+}
+
+// The checks every prefill entry point makes of n rows at pos.
+int prefill_check(const gemma_hip_decoder *dec, const char *name, int n, int pos) {
+  const gemma_hip_text_config &c = dec->cfg;
+  if (n < 1 || pos < 0 || pos > dec->clen - n)
+    return fail("%s: %d rows at pos %d out of range (clen %d)", name, n, pos, dec->clen);
+  const int hn = c.n_heads / c.nkv;
+  if ((c.hdim != 128 && c.hdim != 256) || 32 % hn != 0 || c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt)
+    return fail("%s: unsupported shape (head dim %d must be 128 or 256, "
+                "%d q heads per kv head must divide 32, mlp %d at most %d)",
+                name, c.hdim, hn, c.mlp_dim, 4 * 1024 * gh::kPfMaxNpt);
+  return 0;
+}
+
+#define PF_CHECK(what, expr)                                                           \
+  do {                                                                                 \
+    hipError_t gh_e_ = (expr);                                                         \
+    if (gh_e_ != hipSuccess) return fail("%s: %s: %s", kName, what, hipGetErrorString(gh_e_)); \
+  } while (0)
+
+// Waits for earlier work on the stream and makes room for n rows.
+int prefill_stage(gemma_hip_decoder *dec, const char *kName, int n) {
+  PF_CHECK("sync", hipStreamSynchronize(g.stream));
+  return prefill_reserve(dec, n);
+}
+
+// With the rows staged (tokens in pf_tok when embed, else the rows in pf_x):
+// sets the step record to {last token, pos + n - 1}, runs the pass and
+// returns the last row's logits and argmax (both nullable).
+int prefill_run(gemma_hip_decoder *dec, const char *kName, int n, int pos, int last_token,
+                bool embed, bool dense, float *logits, int *next) {
+  dec->pin[0] = last_token;
+  dec->pin[1] = pos + n - 1;
+  dec->pin[2] = 0;
+  dec->pin[3] = 0;
+  PF_CHECK("step H2D", hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
+  PF_CHECK("launch", prefill_enqueue(dec, n, pos, embed, dense, g.stream));
+  if (logits != nullptr)
+    PF_CHECK("logits D2H", hipMemcpyAsync(logits, dec->logits, (size_t)dec->cfg.nvocab * 4,
+                                          hipMemcpyDeviceToHost, g.stream));
+  if (next != nullptr)
+    PF_CHECK("D2H", hipMemcpyAsync(dec->pin + 4, dec->tokens, 4, hipMemcpyDeviceToHost, g.stream));
+  PF_CHECK("sync", hipStreamSynchronize(g.stream));
+  if (next != nullptr) *next = dec->pin[4];
+  return 0;
 }
 
 // Enqueues one decode step on `st` (captured into the decoder's graph).
@@ -1505,44 +1556,29 @@ int gemma_hip_decoder_generate(gemma_hip_decoder *dec, int token, int pos, int n
 
 int gemma_hip_decoder_prefill(gemma_hip_decoder *dec, const int *tokens, int n, int pos,
                               float *logits, int *next) {
+  static const char *kName = "gemma_hip_decoder_prefill";
   if (need_init()) return 1;
-  if (dec == nullptr || tokens == nullptr)
-    return fail("gemma_hip_decoder_prefill: null argument");
-  const gemma_hip_text_config &c = dec->cfg;
-  if (n < 1 || pos < 0 || pos > dec->clen - n)
-    return fail("gemma_hip_decoder_prefill: %d tokens at pos %d out of range (clen %d)", n, pos,
-                dec->clen);
+  if (dec == nullptr || tokens == nullptr) return fail("%s: null argument", kName);
+  if (prefill_check(dec, kName, n, pos)) return 1;
   for (int i = 0; i < n; ++i)
-    if (tokens[i] < 0 || tokens[i] >= c.nvocab)
-      return fail("gemma_hip_decoder_prefill: token %d at %d out of range (vocab %d)", tokens[i],
-                  i, c.nvocab);
-  const int hn = c.n_heads / c.nkv;
-  if ((c.hdim != 128 && c.hdim != 256) || 32 % hn != 0 ||
-      c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt)
-    return fail("gemma_hip_decoder_prefill: unsupported shape (head dim %d must be 128 or 256, "
-                "%d q heads per kv head must divide 32, mlp %d at most %d)",
-                c.hdim, hn, c.mlp_dim, 4 * 1024 * gh::kPfMaxNpt);
-  GH_CHECK("gemma_hip_decoder_prefill: sync", hipStreamSynchronize(g.stream));
-  if (prefill_reserve(dec, n)) return 1;
-  GH_CHECK("gemma_hip_decoder_prefill: tokens H2D",
+    if (tokens[i] < 0 || tokens[i] >= dec->cfg.nvocab)
+      return fail("%s: token %d at %d out of range (vocab %d)", kName, tokens[i], i,
+                  dec->cfg.nvocab);
+  if (prefill_stage(dec, kName, n)) return 1;
+  PF_CHECK("tokens H2D",
            hipMemcpyAsync(dec->pf_tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, g.stream));
-  dec->pin[0] = tokens[n - 1];
-  dec->pin[1] = pos + n - 1;
-  dec->pin[2] = 0;
-  dec->pin[3] = 0;
-  GH_CHECK("gemma_hip_decoder_prefill: step H2D",
-           hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
-  GH_CHECK("gemma_hip_decoder_prefill: launch", prefill_enqueue(dec, n, pos, g.stream));
-  if (logits != nullptr)
-    GH_CHECK("gemma_hip_decoder_prefill: logits D2H",
-             hipMemcpyAsync(logits, dec->logits, (size_t)c.nvocab * 4, hipMemcpyDeviceToHost,
-                            g.stream));
-  if (next != nullptr)
-    GH_CHECK("gemma_hip_decoder_prefill: D2H",
-             hipMemcpyAsync(dec->pin + 4, dec->tokens, 4, hipMemcpyDeviceToHost, g.stream));
-  GH_CHECK("gemma_hip_decoder_prefill: sync", hipStreamSynchronize(g.stream));
-  if (next != nullptr) *next = dec->pin[4];
-  return 0;
+  return prefill_run(dec, kName, n, pos, tokens[n - 1], true, false, logits, next);
+}
+
+int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n, int pos,
+                                   int mask, float *logits, int *next) {
+  static const char *kName = "gemma_hip_decoder_prefill_rows";
+  if (need_init()) return 1;
+  if (dec == nullptr || x == nullptr) return fail("%s: null argument", kName);
+  if (prefill_check(dec, kName, n, pos) || prefill_stage(dec, kName, n)) return 1;
+  PF_CHECK("rows copy", hipMemcpyAsync(dec->pf_x, x, (size_t)n * dec->cfg.dim * 4,
+                                       hipMemcpyDefault, g.stream));
+  return prefill_run(dec, kName, n, pos, 0, false, mask == 0, logits, next);
 }
 
 const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec) {
@@ -1797,6 +1833,28 @@ int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out
            hipMemcpyAsync(out, vis->out, (size_t)c.img_tok * c.text_dim * 4,
                           hipMemcpyDeviceToHost, g.stream));
   GH_CHECK("gemma_hip_vision_forward: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_gemma_image(gemma_hip_decoder *dec, gemma_hip_vision *vis, const float *img,
+                          int *pos, float *logits, int *next) {
+  static const char *kName = "gemma_hip_gemma_image";
+  if (need_init()) return 1;
+  if (dec == nullptr || vis == nullptr || img == nullptr || pos == nullptr)
+    return fail("%s: null argument", kName);
+  const gemma_hip_vision_config &c = vis->cfg;
+  if (c.text_dim != dec->cfg.dim)
+    return fail("%s: the tower projects to %d, the decoder is %d wide", kName, c.text_dim,
+                dec->cfg.dim);
+  if (prefill_check(dec, kName, c.img_tok, *pos) || prefill_stage(dec, kName, c.img_tok))
+    return 1;
+  PF_CHECK("image H2D", hipMemcpyAsync(vis->img, img, (size_t)c.img_px * c.img_px * 3 * 4,
+                                       hipMemcpyHostToDevice, g.stream));
+  PF_CHECK("vision", vision_enqueue(vis, g.stream));
+  PF_CHECK("soft tokens", hipMemcpyAsync(dec->pf_x, vis->out, (size_t)c.img_tok * c.text_dim * 4,
+                                         hipMemcpyDeviceToDevice, g.stream));
+  if (prefill_run(dec, kName, c.img_tok, *pos, 0, false, true, logits, next)) return 1;
+  *pos += c.img_tok;
   return 0;
 }
 

@@ -198,6 +198,10 @@ struct PfAttn {
   double *part;
   int chunk, nsplit;
   int qpb;  // query vectors per workgroup (set by launch_pf_attention)
+  // 0: causal, sliding-window rows (forward_text_chunk with mask=true);
+  // 1: every row sees keys 0 .. pos0+n-1, no window (mask=false, the image
+  // tokens' bidirectional attention, gemma.c:5258-5290)
+  int dense;
 };
 constexpr int kPfMaxSplit = 8;
 // doubles of PfAttn::part for n rows

@@ -10,7 +10,9 @@
 //   q/k rows         q/k norm, RoPE at each row's position, k and v rows
 //                    appended to the KV cache
 //   attention        causal (and sliding-window) attention of every row over
-//                    the cache, query rows in tiles that share K/V tiles
+//                    the cache, query rows in tiles that share K/V tiles; or
+//                    dense: every row over the whole cache up to the last row
+//                    (the image tokens' bidirectional attention)
 //   quantize + GEMM o
 //   norm rows        residual add of the attention output (post-attention
 //                    norm n2), pre-FFN norm n3, quantize
@@ -158,8 +160,19 @@ struct PaLane {
   bool empty;      // no chunk for this block
 };
 
-__device__ __forceinline__ int pa_window_start(const PfAttn &a, int p_abs) {
-  return (a.slide > 0 && p_abs >= a.slide) ? p_abs + 1 - a.slide : 0;
+__host__ __device__ __forceinline__ int pa_window_start(const PfAttn &a, int p_abs) {
+  return (!a.dense && a.slide > 0 && p_abs >= a.slide) ? p_abs + 1 - a.slide : 0;
+}
+
+// The keys rows r0 .. r0+rows-1 read: from the first row's window start,
+// rounded down to a key tile, to the last row's position -- or, dense, every
+// key 0 .. pos0+n-1 for every row.
+struct PaRange {
+  int k_base, p_last;
+};
+__host__ __device__ __forceinline__ PaRange pa_range(const PfAttn &a, int r0, int rows) {
+  const int p_last = a.dense ? a.pos0 + a.n - 1 : a.pos0 + r0 + rows - 1;
+  return {pa_window_start(a, a.pos0 + r0) / kPaKeys * kPaKeys, p_last};
 }
 
 // block = ((row block from the last) * nsplit + c) * nkv + kv head: the
@@ -180,8 +193,7 @@ __device__ __forceinline__ PaLane pa_lane(const PfAttn &a, int wave, int col) {
   L.chunk_id = ((blockIdx.x / a.nkv) % a.nsplit + rot) % a.nsplit;
   L.r0 = (nrb - 1 - blockIdx.x / a.nkv / a.nsplit) * qb;
   L.rows = min(qb, a.n - L.r0);
-  const int p_last = a.pos0 + L.r0 + L.rows - 1;
-  const int k_base = pa_window_start(a, a.pos0 + L.r0) / kPaKeys * kPaKeys;
+  const auto [k_base, p_last] = pa_range(a, L.r0, L.rows);
   L.nchunks = (p_last - k_base + a.chunk) / a.chunk;
   L.empty = L.chunk_id >= L.nchunks;
   L.k_lo = k_base + L.chunk_id * a.chunk;
@@ -190,7 +202,8 @@ __device__ __forceinline__ PaLane pa_lane(const PfAttn &a, int wave, int col) {
   L.valid = v % qb < L.rows;
   L.row = L.r0 + min(v % qb, L.rows - 1);
   L.head = L.hk * hn + v / qb;
-  L.p_abs = L.valid ? a.pos0 + L.row : -1;  // -1: every key masked
+  // the last key the query sees; -1: every key masked
+  L.p_abs = !L.valid ? -1 : a.dense ? p_last : a.pos0 + L.row;
   L.ws = pa_window_start(a, max(L.p_abs, 0));
   L.p_top = min(L.p_abs, L.k_end);  // the last key of this chunk the query sees
   int hi = L.p_top, lo = L.valid ? L.ws : INT_MAX;
@@ -534,9 +547,7 @@ __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) 
   const int row = blockIdx.x;
   const int hn = a.n_heads / a.nkv, qb = a.qpb / hn;
   const int r0 = row / qb * qb;
-  const int p_last = a.pos0 + min(r0 + qb, a.n) - 1;
-  const int p0 = a.pos0 + r0;
-  const int k_base = ((a.slide > 0 && p0 >= a.slide) ? p0 + 1 - a.slide : 0) / kPaKeys * kPaKeys;
+  const auto [k_base, p_last] = pa_range(a, r0, min(qb, a.n - r0));
   const int nchunks = (p_last - k_base + a.chunk) / a.chunk;
   if (nchunks == 1) return;
   const double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz;
@@ -651,9 +662,8 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
   // the longest key range of a row block
   int kmax = 0;
   for (int rb = 0; rb < nrb; ++rb) {
-    const int p0 = a.pos0 + rb * qb, p_last = a.pos0 + std::min(rb * qb + qb, a.n) - 1;
-    const int k_base = ((a.slide > 0 && p0 >= a.slide) ? p0 + 1 - a.slide : 0) / kPaKeys * kPaKeys;
-    kmax = std::max(kmax, p_last - k_base + 1);
+    const PaRange r = pa_range(a, rb * qb, std::min(qb, a.n - rb * qb));
+    kmax = std::max(kmax, r.p_last - r.k_base + 1);
   }
   // split the key ranges until there are about 2048 blocks (half of them
   // empty for causal rows), in chunks of at least one tile

@@ -118,6 +118,8 @@ _SIGS = {
     "gemma_hip_decoder_step": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_generate": (_I, [_P, _I, _I, _I, _P]),
     "gemma_hip_decoder_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I)]),
+    "gemma_hip_decoder_prefill_rows": (_I, [_P, _P, _I, _I, _I, _P, ctypes.POINTER(_I)]),
+    "gemma_hip_gemma_image": (_I, [_P, _P, _P, ctypes.POINTER(_I), _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_logits": (_P, [_P]),
     "gemma_hip_vision_create": (_P, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "gemma_hip_vision_destroy": (None, [_P]),
@@ -334,6 +336,34 @@ class Decoder:
                                                           int(toks.size), pos, _addr(logits),
                                                           ctypes.byref(nxt)))
         return nxt.value
+
+    def prefill_rows(self, x, pos: int, mask: bool = True, logits=None) -> int:
+        """The prompt pass over embedding rows x [n][dim] (forward_text_chunk,
+        gemma.c:4985, on rows a caller placed in tb->x) at positions
+        pos .. pos+n-1; mask=False is the dense attention of image tokens
+        (gemma.c:5258-5290).  Returns the argmax after the last row."""
+        import numpy as np
+
+        x = np.ascontiguousarray(x, np.float32)
+        nxt = ctypes.c_int(-1)
+        self.gh._check(self.lib.gemma_hip_decoder_prefill_rows(
+            self.handle, x.ctypes.data, int(x.shape[0]), pos, int(bool(mask)), _addr(logits),
+            ctypes.byref(nxt)))
+        return nxt.value
+
+    def image(self, vision: "Vision", img, pos: int, logits=None):
+        """forward_gemma_image (gemma.c:5561): the vision tower on img and the
+        dense prompt pass of its soft tokens at pos, device to device.
+        Returns (next position, argmax after the last soft token)."""
+        import numpy as np
+
+        img = np.ascontiguousarray(img, np.float32)
+        assert img.shape == vision.img_shape
+        p, nxt = ctypes.c_int(pos), ctypes.c_int(-1)
+        self.gh._check(self.lib.gemma_hip_gemma_image(self.handle, vision.handle, img.ctypes.data,
+                                                      ctypes.byref(p), _addr(logits),
+                                                      ctypes.byref(nxt)))
+        return p.value, nxt.value
 
     def generate(self, token: int, pos: int, n: int):
         import numpy as np

@@ -302,6 +302,18 @@ int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos,
 int gemma_hip_decoder_prefill(gemma_hip_decoder *dec, const int *tokens, int n, int pos,
                               float *logits, int *next);
 
+/* The prompt pass over n rows given as embeddings (n x dim fp32, a host or
+ * a device pointer) instead of token ids: forward_text_chunk (gemma.c:4985)
+ * on what its callers place in tb->x.  mask != 0 is the causal
+ * (sliding-window) attention of text tokens; mask == 0 the dense path
+ * (gemma.c:5258-5290) forward_gemma_image (5561-5595) takes for image soft
+ * tokens: every row attends to every cached key up to pos + n - 1, with no
+ * window.  Rows are used as given (no embedding scale).  Otherwise as
+ * gemma_hip_decoder_prefill; the step record's token is 0 (next, when
+ * given, is the argmax of the last row). */
+int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n, int pos,
+                                   int mask, float *logits, int *next);
+
 /* n greedy steps without host round trips: step i consumes the token step
  * i-1 produced (the first consumes `token` at `pos`); tokens[i] receives the
  * argmax of step i (host, n ints).  pos + n <= clen. */
@@ -361,6 +373,14 @@ void gemma_hip_vision_destroy(gemma_hip_vision *vis);
  * 4271-4273 leaves it) in, out (host, [img_tok][text_dim] fp32: the image's
  * soft tokens, what forward_vision leaves in tb->x) out. */
 int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out);
+
+/* forward_gemma_image (gemma.c:5561-5595) on the device: the vision tower on
+ * img, its img_tok soft tokens handed to the decoder in HBM, and the dense
+ * (mask=false) prompt pass at *pos, which advances by img_tok on success.
+ * logits / next (nullable) as gemma_hip_decoder_prefill.  The tower's
+ * text_dim must be the decoder's dim. */
+int gemma_hip_gemma_image(gemma_hip_decoder *dec, gemma_hip_vision *vis, const float *img,
+                          int *pos, float *logits, int *next);
 
 #ifdef __cplusplus
 }

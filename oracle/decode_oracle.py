@@ -161,21 +161,29 @@ class DecodeOracle:
             logits = (np.tanh(logits.astype(F64) / c["sc_log"]) * c["sc_log"]).astype(F32)
         return logits
 
-    def prefill(self, tokens, pos0: int) -> np.ndarray:
+    def prefill(self, tokens, pos0: int, rows=None, mask: bool = True) -> np.ndarray:
         """The prompt chunk of forward_gemma_prefill (gemma.c:5501) and
         forward_text_chunk (4985-5453): the tokens at positions pos0, pos0+1,
         ... go through each layer together, row i with step()'s formulas at
         position pos0 + i (causal, sliding-window attention over the cache).
         Fills the KV cache and returns the last row's logits.  Row for row it
-        is step() vectorized; tests/test_decoder.py checks the two agree."""
+        is step() vectorized; tests/test_decoder.py checks the two agree.
+
+        rows (n x dim fp32) replaces the embedded tokens (tokens is then
+        ignored): what forward_gemma_image (5561-5595) places in tb->x.
+        mask=False is forward_text_chunk's dense path (5258-5290): every row
+        attends to every key 0 .. pos0+n-1, with no sliding window."""
         c, m = self.c, self.m
-        toks = np.asarray(tokens, np.int64)
-        n = len(toks)
         dim, hd, nh, nkv = c["dim"], c["hdim"], c["n_heads"], c["nkv"]
         eps = c["eps"]
-        esc0 = F32(1.0) if c["mlp_pre"] else F32(np.sqrt(F32(dim)))
-        esc = (esc0 * np.asarray(m["emb"][1], F32)[toks]).astype(F32)
-        x = (np.asarray(m["emb"][0])[toks].astype(F32) * esc[:, None]).astype(F32)
+        if rows is not None:
+            x = np.array(rows, F32).reshape(-1, dim)
+        else:
+            toks = np.asarray(tokens, np.int64)
+            esc0 = F32(1.0) if c["mlp_pre"] else F32(np.sqrt(F32(dim)))
+            esc = (esc0 * np.asarray(m["emb"][1], F32)[toks]).astype(F32)
+            x = (np.asarray(m["emb"][0])[toks].astype(F32) * esc[:, None]).astype(F32)
+        n = len(x)
         asc = F32(1.0) / F32(np.sqrt(F32(c["q_scale"])))
         pos = pos0 + np.arange(n)
         hn = nh // nkv
@@ -209,7 +217,10 @@ class DecodeOracle:
                     if c["sc_att"] != 0.0:
                         s = np.tanh(s / F64(c["sc_att"])) * F64(c["sc_att"])
                     j = np.arange(ctx)[None, :]
-                    live = (j <= pos[r0:r1, None]) & (j >= spos[r0:r1, None])
+                    if mask:
+                        live = (j <= pos[r0:r1, None]) & (j >= spos[r0:r1, None])
+                    else:
+                        live = np.ones((r1 - r0, ctx), bool)
                     s = np.where(live, s, -np.inf)
                     p = np.exp(s - s.max(axis=1, keepdims=True))
                     p /= p.sum(axis=1, keepdims=True)

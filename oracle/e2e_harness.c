@@ -50,6 +50,14 @@
  *                            first file, run forward_vision (4394-4725) and
  *                            write the image's soft tokens (float32 [img_tok]
  *                            [dim], tb->x) to the second
+ *   GEMMA_E2E_IMAGE=<path>   (CPU build, multimodal model) an image prompt, as
+ *                            sample() (5978-6075) takes one: prefill <bos>,
+ *                            then forward_gemma_image (5561-5595: the vision
+ *                            tower, then its soft tokens through the decoder
+ *                            with mask=false), then the text prompt (chunked
+ *                            prefill), then the decode steps.  The logits
+ *                            after the image, after the prompt and after each
+ *                            step go to GEMMA_E2E_LOGITS (required here)
  *
  * Everything below the include uses identifiers of three characters or more
  * (the stb blob at the end of gemma.c defines one- and two-letter macros,
@@ -319,7 +327,103 @@ static int run_vision(const char *model_path, const char *img_path,
   return 0;
 }
 
+/* sample() with an image prompt (see GEMMA_E2E_IMAGE); prints one JSON line
+ * with the greedy tokens. */
+static int run_image(const char *model_path, const char *img_path,
+                     const char *logits_path, int prompt_len, int decode_steps,
+                     uint64_t seed, int threads) {
+  GemmaModel *model = mmap_gemma_model(model_path, true);
+  if (model == NULL || model->encoder == NULL) {
+    die_with("load (multimodal)", model == NULL ? get_error() : "no vision tower");
+  }
+  TextConfig *cfg = model->decoder->config;
+  VisionConfig *vcfg = model->encoder->config;
+  int img_tok = (int)cfg->img_tok;
+  int nvocab = (int)cfg->nvocab;
+  int chunk = img_tok > prompt_len ? img_tok : prompt_len;
+  TextBuffer *buf = malloc_text_buffer(cfg, vcfg, 1 + img_tok + prompt_len + decode_steps,
+                                       chunk, true, model->quant);
+  VisionBuffer *vbuf = malloc_vision_buffer(vcfg, model->quant);
+  if (buf == NULL || vbuf == NULL) {
+    die_with("buffers", get_error());
+  }
+  size_t npix = (size_t)vcfg->img_px * vcfg->img_px * 3;
+  float *img = malloc(npix * sizeof(float));
+  int *prompt = malloc((size_t)(prompt_len + 1) * sizeof(int));
+  FILE *fin = fopen(img_path, "rb");
+  if (img == NULL || prompt == NULL || fin == NULL ||
+      fread(img, sizeof(float), npix, fin) != npix) {
+    die_with("image", img_path);
+  }
+  fclose(fin);
+  FILE *dump = fopen(logits_path, "wb");
+  if (dump == NULL) {
+    die_with("logits file", logits_path);
+  }
+  mix_state = seed;
+  for (int idx = 0; idx < prompt_len; idx++) {
+    prompt[idx] = (int)(splitmix_next() % (uint64_t)nvocab);
+  }
+  PerfBench perf;
+  memset(&perf, 0, sizeof(perf));
+  int pos = 0;
+  int bos_tok = model->tok->bos;
+  if (forward_gemma_prefill(model, buf, &bos_tok, 1, &pos, chunk, NULL, false, threads,
+                            &perf) != 0) {
+    die_with("prefill <bos>", get_error());
+  }
+  if (forward_gemma_image(model, buf, vbuf, img, &pos, true, threads, &perf) != 0) {
+    die_with("forward_gemma_image", get_error());
+  }
+  fwrite(buf->logits, sizeof(float), (size_t)nvocab, dump);
+  if (prompt_len > 0) {
+    if (forward_gemma_prefill(model, buf, prompt, prompt_len, &pos, chunk, NULL, true,
+                              threads, &perf) != 0) {
+      die_with("prefill", get_error());
+    }
+    fwrite(buf->logits, sizeof(float), (size_t)nvocab, dump);
+  }
+  printf("{\"build\": \"cpu\", \"model\": \"%s\", \"img_tok\": %d, \"bos\": %d, "
+         "\"prompt\": [", model_path, img_tok, bos_tok);
+  for (int idx = 0; idx < prompt_len; idx++) {
+    printf("%s%d", idx ? ", " : "", prompt[idx]);
+  }
+  printf("], \"tokens\": [");
+  int token = argmax(buf->logits, nvocab, threads);
+  for (int step = 0; step <= decode_steps; step++) {
+    printf("%s%d", step ? ", " : "", token);
+    if (step == decode_steps) {
+      break;
+    }
+    if (forward_gemma_decode(model, buf, token, pos, threads, &perf) != 0) {
+      die_with("decode", get_error());
+    }
+    pos++;
+    fwrite(buf->logits, sizeof(float), (size_t)nvocab, dump);
+    token = argmax(buf->logits, nvocab, threads);
+  }
+  printf("]}\n");
+  fclose(dump);
+  free(prompt);
+  free(img);
+  free_vision_buffer(vbuf, model->quant);
+  free_text_buffer(buf, model->quant);
+  munmap_gemma_model(model);
+  return 0;
+}
+
 int main(int argc, char **argv) {
+  const char *image_prompt = getenv("GEMMA_E2E_IMAGE");
+  if (image_prompt != NULL) {
+    const char *dump_to = getenv("GEMMA_E2E_LOGITS");
+    if (dump_to == NULL || argc < 6) {
+      fprintf(stderr, "gemma_e2e: GEMMA_E2E_IMAGE needs GEMMA_E2E_LOGITS and "
+                      "<model.bin> <prompt_len> <decode_steps> <seed> <threads>\n");
+      return 2;
+    }
+    return run_image(argv[1], image_prompt, dump_to, atoi(argv[2]), atoi(argv[3]),
+                     strtoull(argv[4], NULL, 10), atoi(argv[5]));
+  }
   const char *vis_img = getenv("GEMMA_E2E_VISION_IMAGE");
   const char *vis_out = getenv("GEMMA_E2E_VISION_OUT");
   if (vis_img != NULL && vis_out != NULL && argc >= 2) {

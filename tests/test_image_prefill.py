@@ -1,0 +1,339 @@
+"""Image prompts: the vision tower's soft tokens through the decoder with the
+dense (mask=false) attention of forward_gemma_image (gemma.c:5561-5595,
+forward_text_chunk's dense path 5258-5290), on the device
+(gemma_hip_decoder_prefill_rows, gemma_hip_gemma_image) against the decode
+oracle (oracle/decode_oracle.py, DecodeOracle.prefill(rows=..., mask=False))
+and against the reference program itself (oracle/e2e_harness.c,
+GEMMA_E2E_IMAGE).
+
+Bars: device against oracle as in tests/test_decoder.py (both evaluate the
+glue in fp64 and round once: logits to LOGIT_TOL of their largest entry, the
+same argmax).  Oracle or device against the reference program: the reference
+evaluates the glue in fp32, so the two agree to fp32 rounding (measured
+6e-8 .. 3.2e-7 of the largest logit) until an fp32 difference straddles an
+int8 requantization boundary, which moves this random model's logits by 1%
+to 4% from there on; the comparison runs on seeds measured flip-free, with
+the bound REL_PRE_FLIP.  It is sharp: causal attention over the image block
+moves the logits by 13% to 20%, and a sliding window kept in the dense path
+(16 image tokens under a window of 8) by 48%.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import model_bin
+from oracle import decode_oracle as dorc
+from oracle import vision_oracle as vorc
+
+LOGIT_TOL = 1e-5
+REL_PRE_FLIP = 1e-5
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+E2E_CPU = os.path.join(REPO, "oracle", "_ref", "gemma_e2e_cpu")
+needs_e2e = pytest.mark.skipif(not os.path.exists(E2E_CPU),
+                               reason="oracle/_ref/gemma_e2e_cpu not built (needs /root/reference)")
+
+VISION = {
+    # SigLIP's head dim (72), 16 patches pooled to 4 tokens
+    "hd72": dict(nl=2, n_heads=2, img_px=56, psize=14, dim=144, mlp_dim=288, img_tok=4),
+    # 64 patches pooled to 16 tokens: the image block is longer than the window of 8
+    "hd16": dict(nl=3, n_heads=4, img_px=112, psize=14, dim=64, mlp_dim=128, img_tok=16),
+    # SigLIP's own widths at 224 px, pooled to 16 tokens
+    "siglip": dict(nl=2, n_heads=16, img_px=224, psize=14, dim=1152, mlp_dim=4304, img_tok=16),
+}
+# shape, vision weight seed, image seed (measured flip-free against the reference)
+REF_CASES = {"hd72": ("hd72", 1, 101), "hd16": ("hd16", 4, 104)}
+
+
+def mm_model(path, shape, seed, text="gemma-3-270m"):
+    """A multimodal file: two text layers (sliding window 8, then global) of
+    `text`'s widths under the tower `shape`."""
+    dim = model_bin.CONFIGS[text]["dim"]
+    vis = model_bin.synth_vision(seed=seed, text_dim=dim, **VISION[shape])
+    return model_bin.read_bin(model_bin.write_bin(str(path), text, seed=5, nvocab=512, layers=2,
+                                                  vision=vis, norm_std=0.1, slide=8,
+                                                  swa=[1, 0]))
+
+
+def oracle_chain(model, oracle, img, bos, prompt, tokens, steps, clen):
+    """The oracle through sample()'s image prompt: <bos>, the image's soft
+    tokens (dense), the text prompt, then `steps` teacher-forced decode steps
+    on `tokens`; the logits after each stage."""
+    soft = vorc.VisionOracle(model["vision"], oracle).forward(img)
+    d = dorc.DecodeOracle(model, oracle, clen)
+    d.prefill([bos], 0)
+    out = [d.prefill(None, 1, rows=soft, mask=False)]
+    pos = 1 + len(soft)
+    if len(prompt):
+        out.append(d.prefill(prompt, pos))
+        pos += len(prompt)
+    for i in range(steps):
+        out.append(d.step(int(tokens[i]), pos))
+        pos += 1
+    return np.array(out), soft
+
+
+def device_chain(gh, model, img, bos, prompt, tokens, steps, clen):
+    """The device through the same stages (gemma_hip_gemma_image for the image)."""
+    nv = model["config"]["nvocab"]
+    dec = gh.decoder(model, clen)
+    tower = gh.vision(model["vision"])
+    try:
+        out, nxt = [], []
+        lg = np.empty(nv, np.float32)
+        dec.prefill(np.array([bos], np.int32), 0)
+        pos, first = dec.image(tower, img, 1, lg)
+        out.append(lg.copy())
+        nxt.append(first)
+        if len(prompt):
+            nxt.append(dec.prefill(np.asarray(prompt, np.int32), pos, lg))
+            out.append(lg.copy())
+            pos += len(prompt)
+        for i in range(steps):
+            nxt.append(dec.step(int(tokens[i]), pos, lg))
+            out.append(lg.copy())
+            pos += 1
+        return np.array(out), nxt, pos
+    finally:
+        tower.close()
+        dec.close()
+
+
+def rel_rows(got, ref):
+    return np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
+
+
+def run_reference_image(tmp_path, case, prompt_len=5, steps=3):
+    shape, seed, img_seed = REF_CASES[case]
+    path = tmp_path / f"mm_{case}.bin"
+    model = mm_model(path, shape, seed)
+    img = model_bin.synth_image(VISION[shape]["img_px"], seed=img_seed)
+    img_path, lg_path = tmp_path / "img.f32", tmp_path / "logits.f32"
+    img.tofile(img_path)
+    env = dict(os.environ, GEMMA_E2E_IMAGE=str(img_path), GEMMA_E2E_LOGITS=str(lg_path))
+    out = subprocess.run([E2E_CPU, str(path), str(prompt_len), str(steps), "77", "4"], env=env,
+                         capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    res = json.loads(out.stdout.strip().splitlines()[-1])
+    ref = np.fromfile(lg_path, np.float32).reshape(-1, model["config"]["nvocab"])
+    assert len(ref) == 2 + steps and res["img_tok"] == VISION[shape]["img_tok"]
+    return model, img, res, ref
+
+
+# ------------------------------------------------------------ oracle pins (CPU)
+@pytest.fixture(scope="module")
+def text_models(tmp_path_factory):
+    d = tmp_path_factory.mktemp("img_text")
+    out = {}
+    for key, layers in (("one", 1), ("two", 2)):
+        out[key] = model_bin.read_bin(model_bin.write_bin(
+            str(d / f"{key}.bin"), "gemma-3-270m", seed=13, nvocab=512, layers=layers,
+            swa=[0] * layers, norm_std=0.1))
+    return out
+
+
+def _embed(model, toks):
+    emb_q, emb_s = model["emb"]
+    return (emb_q[toks].astype(np.float32) * emb_s[toks][:, None]).astype(np.float32)
+
+
+def test_oracle_rows_equal_tokens(oracle, text_models):
+    """Rows that are the tokens' own embeddings (gemma 3: esc = 1, times the
+    row scale, gemma.c:5468-5493) give the token prefill's logits and cache."""
+    model = text_models["two"]
+    toks = np.random.default_rng(1).integers(0, 512, 11)
+    a = dorc.DecodeOracle(model, oracle, 16)
+    b = dorc.DecodeOracle(model, oracle, 16)
+    want = a.prefill(toks, 2)
+    got = b.prefill(None, 2, rows=_embed(model, toks))
+    assert np.array_equal(got, want)
+    assert np.array_equal(a.kc, b.kc) and np.array_equal(a.vc, b.vc)
+
+
+def test_oracle_dense_closed_forms(oracle, text_models):
+    """The last row of a chunk sees every key 0 .. pos0+n-1 with or without the
+    causal mask, so in a single global layer its logits are the same both ways
+    (and k/v, written before attention, are too); with a second layer the
+    earlier rows' dense outputs reach it through that layer's keys and values,
+    so the logits must move."""
+    toks = np.random.default_rng(2).integers(0, 512, 9)
+    for key, same in (("one", True), ("two", False)):
+        model = text_models[key]
+        rows = _embed(model, toks)
+        a = dorc.DecodeOracle(model, oracle, 16)
+        b = dorc.DecodeOracle(model, oracle, 16)
+        a.prefill([2], 0)
+        b.prefill([2], 0)
+        causal = a.prefill(None, 1, rows=rows, mask=True)
+        dense = b.prefill(None, 1, rows=rows, mask=False)
+        rel = float(np.abs(dense - causal).max() / np.abs(causal).max())
+        if same:
+            assert rel <= 1e-12, rel
+            assert np.array_equal(a.kc, b.kc) and np.array_equal(a.vc, b.vc)
+        else:
+            assert rel > 1e-3, rel
+
+
+@needs_e2e
+@pytest.mark.parametrize("case", sorted(REF_CASES))
+def test_oracle_image_follows_reference_program(tmp_path, oracle, case):
+    """forward_gemma_image and the text after it, compiled from the
+    reference's source, against the oracle's chain, stage by stage."""
+    model, img, res, ref = run_reference_image(tmp_path, case)
+    clen = 1 + res["img_tok"] + len(res["prompt"]) + len(res["tokens"])
+    got, _ = oracle_chain(model, oracle, img, res["bos"], res["prompt"], res["tokens"],
+                          len(ref) - 2, clen)
+    rel = rel_rows(got, ref)
+    print(f"oracle vs reference image prompt ({case}): {np.array2string(rel, precision=2)}",
+          flush=True)
+    assert rel.max() <= REL_PRE_FLIP
+    assert res["tokens"][0] == int(np.argmax(got[1]))
+
+
+@needs_e2e
+def test_image_comparison_catches_causal_mask(tmp_path, oracle, monkeypatch):
+    """The same comparison with the image block under the causal mask (the
+    text path's attention) fails by far."""
+    model, img, res, ref = run_reference_image(tmp_path, "hd16")
+    prefill = dorc.DecodeOracle.prefill
+    monkeypatch.setattr(dorc.DecodeOracle, "prefill",
+                        lambda self, t, p, rows=None, mask=True: prefill(self, t, p, rows, True))
+    clen = 1 + res["img_tok"] + len(res["prompt"]) + len(res["tokens"])
+    got, _ = oracle_chain(model, oracle, img, res["bos"], res["prompt"], res["tokens"],
+                          len(ref) - 2, clen)
+    assert rel_rows(got, ref)[0] > 100 * REL_PRE_FLIP
+
+
+# ------------------------------------------------------------------ GPU
+@pytest.fixture(scope="module")
+def gqa_model(tmp_path_factory):
+    """gemma-3-4b widths (8 q heads over 4 kv heads of 256), a sliding layer
+    (window 8) then a global one: the shape config 2's 256 image tokens take."""
+    d = tmp_path_factory.mktemp("img_gqa")
+    return model_bin.read_bin(model_bin.write_bin(str(d / "gqa.bin"), "gemma-3-4b", seed=5,
+                                                  nvocab=1024, layers=2, slide=8, swa=[1, 0],
+                                                  norm_std=0.1))
+
+
+def _check(got, want, what):
+    scale = float(np.abs(want).max())
+    diff = float(np.abs(got - want).max())
+    assert diff <= LOGIT_TOL * scale, f"{what}: |d| {diff:.3g} vs {scale:.3g}"
+    return diff / scale
+
+
+@pytest.mark.gpu
+def test_prefill_rows_equal_token_prefill(gh, text_models):
+    """Rows holding the tokens' embeddings through the causal path give the
+    token prefill's logits bit for bit (the device embeds in the same fp32
+    product), and the same next token."""
+    model = text_models["two"]
+    toks = np.random.default_rng(3).integers(0, 512, 40).astype(np.int32)
+    lg_a, lg_b = np.empty(512, np.float32), np.empty(512, np.float32)
+    dec = gh.decoder(model, 48)
+    try:
+        na = dec.prefill(toks, 3, lg_a)
+        nb = dec.prefill_rows(_embed(model, toks), 3, True, lg_b)
+    finally:
+        dec.close()
+    assert na == nb and np.array_equal(lg_a, lg_b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,pos0", [(256, 1), (77, 30), (1, 5)])
+def test_prefill_rows_dense_matches_oracle(gh, oracle, gqa_model, n, pos0):
+    """Dense rows at gemma-3-4b widths: 256 rows (one image of config 2) after
+    <bos>, a ragged block that starts past the window and ends inside an
+    attention tile, and a single row; then decode steps over the cache."""
+    model = gqa_model
+    nv, dim = model["config"]["nvocab"], model["config"]["dim"]
+    rng = np.random.default_rng(n)
+    rows = (rng.standard_normal((n, dim)) * 0.5).astype(np.float32)
+    prefix = rng.integers(0, nv, pos0).astype(np.int32)
+    clen = pos0 + n + 4
+    dec = gh.decoder(model, clen)
+    try:
+        ref = dorc.DecodeOracle(model, oracle, clen)
+        ref.prefill(prefix, 0)
+        want = ref.prefill(None, pos0, rows=rows, mask=False)
+        lg = np.empty(nv, np.float32)
+        dec.prefill(prefix, 0)
+        nxt = dec.prefill_rows(rows, pos0, False, lg)
+        worst = _check(lg, want, f"dense rows {n} at {pos0}")
+        assert nxt == int(np.argmax(want))
+        token, pos = nxt, pos0 + n
+        for _ in range(3):
+            nxt = dec.step(token, pos, lg)
+            want = ref.step(token, pos)
+            worst = max(worst, _check(lg, want, f"step at {pos} after dense rows"))
+            assert nxt == int(np.argmax(want))
+            token, pos = nxt, pos + 1
+    finally:
+        dec.close()
+    print(f"dense rows {n} at {pos0}: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape", sorted(VISION))
+def test_gemma_image_matches_oracle(gh, oracle, tmp_path, shape):
+    """gemma_hip_gemma_image (tower -> soft tokens in HBM -> dense prefill)
+    and the text after it against the oracle's chain, stage by stage."""
+    model = mm_model(tmp_path / f"{shape}.bin", shape, 2)
+    img = model_bin.synth_image(VISION[shape]["img_px"], seed=9)
+    prompt = np.random.default_rng(5).integers(0, 512, 6)
+    tokens = np.random.default_rng(6).integers(0, 512, 3)
+    clen = 1 + VISION[shape]["img_tok"] + 6 + 3
+    got, nxt, pos = device_chain(gh, model, img, 2, prompt, tokens, 3, clen)
+    want, _ = oracle_chain(model, oracle, img, 2, prompt, tokens, 3, clen)
+    assert pos == clen
+    worst = max(_check(g, w, f"{shape} stage {i}") for i, (g, w) in enumerate(zip(got, want)))
+    assert nxt == [int(np.argmax(w)) for w in want]
+    print(f"image {shape}: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
+@pytest.mark.gpu
+@needs_e2e
+@pytest.mark.parametrize("case", sorted(REF_CASES))
+def test_device_image_follows_reference_program(gh, tmp_path, case):
+    """The device chain against forward_gemma_image compiled from the
+    reference's source (flip-free seeds, as above)."""
+    model, img, res, ref = run_reference_image(tmp_path, case)
+    clen = 1 + res["img_tok"] + len(res["prompt"]) + len(res["tokens"])
+    got, nxt, _ = device_chain(gh, model, img, res["bos"], res["prompt"], res["tokens"],
+                               len(ref) - 2, clen)
+    rel = rel_rows(got, ref)
+    print(f"device vs reference image prompt ({case}): {np.array2string(rel, precision=2)}",
+          flush=True)
+    assert rel.max() <= REL_PRE_FLIP
+    assert nxt[1:] == res["tokens"]
+
+
+@pytest.mark.gpu
+def test_image_argument_errors(gh, tmp_path, text_models):
+    from gemma_hip import GemmaHipError
+
+    model = mm_model(tmp_path / "mm.bin", "hd72", 1)
+    img = model_bin.synth_image(VISION["hd72"]["img_px"], seed=1)
+    dec = gh.decoder(model, 8)
+    tower = gh.vision(model["vision"])
+    other = gh.decoder(text_models["two"], 8)
+    narrow = gh.vision(model_bin.synth_vision(seed=1, text_dim=64, **VISION["hd72"]))
+    try:
+        with pytest.raises(GemmaHipError, match="out of range"):
+            dec.image(tower, img, 5)  # 4 soft tokens at 5 .. 8 do not fit a cache of 8
+        with pytest.raises(GemmaHipError, match="projects to 64"):
+            other.image(narrow, img, 0)
+        with pytest.raises(GemmaHipError, match="out of range"):
+            dec.prefill_rows(np.zeros((0, 640), np.float32), 0, False)
+        assert dec.image(tower, img, 4)[0] == 8  # and the last fitting position works
+    finally:
+        narrow.close()
+        other.close()
+        tower.close()
+        dec.close()
