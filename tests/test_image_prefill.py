@@ -13,9 +13,10 @@ evaluates the glue in fp32, so the two agree to fp32 rounding (measured
 6e-8 .. 3.2e-7 of the largest logit) until an fp32 difference straddles an
 int8 requantization boundary, which moves this random model's logits by 1%
 to 4% from there on; the comparison runs on seeds measured flip-free, with
-the bound REL_PRE_FLIP.  It is sharp: causal attention over the image block
-moves the logits by 13% to 20%, and a sliding window kept in the dense path
-(16 image tokens under a window of 8) by 48%.
+the bound REL_PRE_FLIP (among them a 256-token image, as gemma 3 feeds one).
+It is sharp: causal attention over the image block moves the logits by 13% to
+20%, and a sliding window kept in the dense path (16 image tokens under a
+window of 8) by 48%.
 """
 
 from __future__ import annotations
@@ -46,19 +47,24 @@ VISION = {
     "hd16": dict(nl=3, n_heads=4, img_px=112, psize=14, dim=64, mlp_dim=128, img_tok=16),
     # SigLIP's own widths at 224 px, pooled to 16 tokens
     "siglip": dict(nl=2, n_heads=16, img_px=224, psize=14, dim=1152, mlp_dim=4304, img_tok=16),
+    # 256 patches, unpooled: a gemma-3 image's 256 soft tokens
+    "tok256": dict(nl=1, n_heads=2, img_px=224, psize=14, dim=64, mlp_dim=128, img_tok=256),
 }
-# shape, vision weight seed, image seed (measured flip-free against the reference)
-REF_CASES = {"hd72": ("hd72", 1, 101), "hd16": ("hd16", 4, 104)}
+# shape, vision weight seed, image seed, text layers (measured flip-free against
+# the reference; with 256 image tokens only a single text layer stays clear of
+# requantization flips on some seeds)
+REF_CASES = {"hd72": ("hd72", 1, 101, 2), "hd16": ("hd16", 4, 104, 2),
+             "tok256": ("tok256", 2, 102, 1)}
 
 
-def mm_model(path, shape, seed, text="gemma-3-270m"):
-    """A multimodal file: two text layers (sliding window 8, then global) of
-    `text`'s widths under the tower `shape`."""
+def mm_model(path, shape, seed, layers=2, text="gemma-3-270m"):
+    """A multimodal file: text layers of `text`'s widths (a sliding window of
+    8, then a global layer) under the tower `shape`."""
     dim = model_bin.CONFIGS[text]["dim"]
     vis = model_bin.synth_vision(seed=seed, text_dim=dim, **VISION[shape])
-    return model_bin.read_bin(model_bin.write_bin(str(path), text, seed=5, nvocab=512, layers=2,
-                                                  vision=vis, norm_std=0.1, slide=8,
-                                                  swa=[1, 0]))
+    return model_bin.read_bin(model_bin.write_bin(str(path), text, seed=5, nvocab=512,
+                                                  layers=layers, vision=vis, norm_std=0.1,
+                                                  slide=8, swa=[1, 0][:layers]))
 
 
 def oracle_chain(model, oracle, img, bos, prompt, tokens, steps, clen):
@@ -110,9 +116,9 @@ def rel_rows(got, ref):
 
 
 def run_reference_image(tmp_path, case, prompt_len=5, steps=3):
-    shape, seed, img_seed = REF_CASES[case]
+    shape, seed, img_seed, layers = REF_CASES[case]
     path = tmp_path / f"mm_{case}.bin"
-    model = mm_model(path, shape, seed)
+    model = mm_model(path, shape, seed, layers)
     img = model_bin.synth_image(VISION[shape]["img_px"], seed=img_seed)
     img_path, lg_path = tmp_path / "img.f32", tmp_path / "logits.f32"
     img.tofile(img_path)
