@@ -56,14 +56,20 @@ __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
 // loads between the two phases does not delay the activation behind them.
 constexpr int kXRegs = 4;
 
+// Every load is issued (a chunk past k reloads chunk 0) and zeroed after it
+// returns: a conditional load would make the compiler's wait counts wait
+// for it, and for everything issued before it, at its first use.
 template <int NT>
 __device__ __forceinline__ void x_load(int k, const float *__restrict__ xf, v4f (&xr)[kXRegs]) {
   const int tid = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < kXRegs; ++j) {
     const int c = tid + j * NT;
-    xr[j] = c < k / 4 ? reinterpret_cast<const v4f *>(xf)[c] : v4f{0.f, 0.f, 0.f, 0.f};
+    xr[j] = reinterpret_cast<const v4f *>(xf)[c < k / 4 ? c : 0];
   }
+#pragma unroll
+  for (int j = 0; j < kXRegs; ++j)
+    if (tid + j * NT >= k / 4) xr[j] = v4f{0.f, 0.f, 0.f, 0.f};
 }
 
 template <int NT>
