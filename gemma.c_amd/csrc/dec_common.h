@@ -171,20 +171,57 @@ struct NormIn {
   v4f y[NPT], xr[NPT], wp[NPT], wq[NPT];
 };
 
+// Every load is issued (a chunk past dim reloads chunk 0, an absent vector
+// reads x_res) and the unused values are zeroed after they return: a
+// conditional load makes the compiler's wait counts wait for it, and for
+// everything issued before it, at its first use.
 template <int NPT, int NT>
 __device__ __forceinline__ void norm_load(const DecNorm &a, NormIn<NPT> &in) {
   const int tid = threadIdx.x;
   const int n4 = a.dim >> 2;
+  const v4f *y = reinterpret_cast<const v4f *>(a.y != nullptr ? a.y : a.x_res);
+  const v4f *wp = reinterpret_cast<const v4f *>(a.w_post != nullptr ? a.w_post : a.x_res);
 #pragma unroll
   for (int j = 0; j < NPT; ++j) {
-    const int c = tid + j * NT;
-    const bool ok = c < n4;
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-    in.xr[j] = ok ? reinterpret_cast<const v4f *>(a.x_res)[c] : zero;
-    in.wq[j] = ok ? reinterpret_cast<const v4f *>(a.w_pre)[c] : zero;
-    in.y[j] = (ok && a.y != nullptr) ? reinterpret_cast<const v4f *>(a.y)[c] : zero;
-    in.wp[j] = (ok && a.w_post != nullptr) ? reinterpret_cast<const v4f *>(a.w_post)[c] : zero;
+    const int c = tid + j * NT < n4 ? tid + j * NT : 0;
+    in.xr[j] = reinterpret_cast<const v4f *>(a.x_res)[c];
+    in.wq[j] = reinterpret_cast<const v4f *>(a.w_pre)[c];
+    in.y[j] = y[c];
+    in.wp[j] = wp[c];
   }
+}
+
+// Zeroes what norm_load read past dim or from an absent vector (call once
+// the values are needed).
+template <int NPT, int NT>
+__device__ __forceinline__ void norm_fix(const DecNorm &a, NormIn<NPT> &in) {
+  const int tid = threadIdx.x;
+  const int n4 = a.dim >> 2;
+  const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const bool ok = tid + j * NT < n4;
+    if (!ok) in.xr[j] = in.wq[j] = zero;
+    if (!ok || a.y == nullptr) in.y[j] = zero;
+    if (!ok || a.w_post == nullptr) in.wp[j] = zero;
+  }
+}
+
+// Kernel arguments into scalar registers at once.  The compiler otherwise
+// loads each argument where it is first used, and an argument read behind a
+// branch (a job's end, a nullable vector) costs a dependent scalar-memory
+// round trip before the loads that follow it can issue.
+__device__ __forceinline__ void hold_args(const DecNorm &n) {
+  asm volatile("" ::"s"(n.x_res), "s"(n.y), "s"(n.w_post), "s"(n.w_pre), "s"(n.x_out),
+               "s"(n.h_out), "s"(n.dim), "s"(n.eps));
+}
+__device__ __forceinline__ void hold_args(const GemvJobs &j) { hold_jobs(j); }
+__device__ __forceinline__ void hold_args(const DecAttn &a) {
+  asm volatile("" ::"s"(a.xq), "s"(a.xk), "s"(a.xv), "s"(a.nq), "s"(a.nk), "s"(a.rope),
+               "s"(a.kc), "s"(a.vc), "s"(a.step), "s"(a.part));
+  asm volatile("" ::"s"(a.xo), "s"(a.n_heads), "s"(a.nkv), "s"(a.hdim), "s"(a.clen),
+               "s"(a.slide), "s"(a.max_blocks), "s"(a.nvocab), "s"(a.asc), "s"(a.sc_att),
+               "s"(a.eps));
 }
 
 // The arithmetic of the prologue; returns the activation scale.  Workgroup 0
@@ -196,6 +233,7 @@ __device__ float norm_quant(const DecNorm &a, NormIn<NPT> &in, int8_t *xq, doubl
                             float *redf) {
   const int tid = threadIdx.x;
   const int n4 = a.dim >> 2;
+  norm_fix<NPT, NT>(a, in);
   if (a.y != nullptr) {
     double rms = 1.0;
     if (a.w_post != nullptr) {

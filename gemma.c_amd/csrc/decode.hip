@@ -62,6 +62,8 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
   __shared__ double red[kW];
   __shared__ float redf[kW];
   __shared__ double etab[GELU ? 128 : 1];
+  hold_args(na);
+  hold_args(jobs);
   if (GELU) exp_tab_load(etab);  // visible after the prologue's barriers
   const ExpConsts ec = exp_consts();
   constexpr int kNpt = (CPL * L * 16 + NT * 4 - 1) / (NT * 4);
@@ -174,7 +176,12 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
   __shared__ double red[kWaves];
   __shared__ float redf[kWaves];
   __shared__ double etab[GELU ? 128 : 1];
-  if (GELU) exp_tab_load(etab);  // visible after the prologue's barriers
+  hold_args(na);
+  hold_args(jobs);
+  asm volatile("" ::"s"(ngroups), "s"(k));
+  // the exp table is loaded first and stored to LDS after the other loads
+  // are issued (visible after the prologue's barriers)
+  const double etv = GELU ? kExp2Tab[threadIdx.x & 127] : 0.0;
   const ExpConsts ec = exp_consts();
   constexpr int R = 64 / L;
   static_assert(!GELU || R >= 2, "gate and up rows must share a wave");
@@ -216,7 +223,7 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
           gs = gend[t];
           rs = jobs.end[t];
         }
-      const int m = jobs.end[j] - rs;
+      const int m = pick4(jobs.end, j) - rs;  // a register select, not a memory read
       a.out = (g - gs) * R + rloc;
       a.job = j;
       a.ok = g < ngroups && a.out < m;
@@ -244,6 +251,7 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
   norm_load<NPT, kNT>(na, in);
   Slot ring;
   load(w0, ring);
+  if (GELU && threadIdx.x < 128) etab[threadIdx.x] = etv;
   const float act_scale =
       norm_quant<NPT, kNT>(na, in, reinterpret_cast<int8_t *>(xq4), red, redf);
 
@@ -287,6 +295,7 @@ template <int NPT>
 __global__ __launch_bounds__(kNT) void dec_final_norm_kernel(DecNorm na) {
   __shared__ double red[kWaves];
   __shared__ float redf[kWaves];
+  hold_args(na);
   NormIn<NPT> in;
   norm_load<NPT, kNT>(na, in);
   norm_quant<NPT, kNT>(na, in, nullptr, red, redf);
@@ -548,6 +557,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   extern __shared__ double wts[];
   __shared__ double red[kWaves];
   __shared__ double2 gsum[kCombGroups][32];
+  hold_args(a);
   int token, pos;
   if (!step_ok(a.step, a.nvocab, a.clen, &token, &pos)) return;
   const int hd = a.hdim, h = blockIdx.x, tid = threadIdx.x;

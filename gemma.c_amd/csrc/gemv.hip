@@ -236,6 +236,8 @@ __global__ __launch_bounds__(NT) void gemv_i8_pipelined_kernel(
     const float *__restrict__ xs, const float *__restrict__ xf,
     int8_t *__restrict__ xq_out, float *__restrict__ xs_out) {
   extern __shared__ v4i lds_x4[];
+  hold_jobs(jobs);
+  asm volatile("" ::"s"(k), "s"(xq), "s"(xs), "s"(xf), "s"(xq_out), "s"(xs_out));
   constexpr int kRowsPerWave = 64 / L;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -326,6 +328,8 @@ __global__ __launch_bounds__(NT) void gemv_i8_stream_kernel(
     const float *__restrict__ xs, const float *__restrict__ xf,
     int8_t *__restrict__ xq_out, float *__restrict__ xs_out) {
   extern __shared__ v4i lds_x4[];
+  hold_jobs(jobs);
+  asm volatile("" ::"s"(ngroups), "s"(k), "s"(xq), "s"(xs), "s"(xf), "s"(xq_out), "s"(xs_out));
   constexpr int R = 64 / L;
   constexpr int kBlockWaves = NT / 64;
   const int lane = threadIdx.x & 63;
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(NT) void gemv_i8_stream_kernel(
         gs = gend[t];
         rs = jobs.end[t];
       }
-    return Where{j, (g - gs) * R + rloc, jobs.end[j] - rs};
+    return Where{j, (g - gs) * R + rloc, pick4(jobs.end, j) - rs};
   };
   auto pick_s = [&](auto const (&a)[kMaxJobs], int j) {  // j is wave-uniform
     auto v = a[0];
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(NT) void gemv_f32_stream_kernel(GemvJobs jobs, int 
         gs = gend[t];
         rs = jobs.end[t];
       }
-    return Where{j, (g - gs) * R + rloc, jobs.end[j] - rs};
+    return Where{j, (g - gs) * R + rloc, pick4(jobs.end, j) - rs};
   };
   auto pick_s = [&](auto const (&a)[kMaxJobs], int j) {  // j is wave-uniform
     auto v = a[0];

@@ -156,6 +156,18 @@ __device__ __forceinline__ T pick4(T const (&a)[4], int j) {
   return j == 3 ? v3 : j == 2 ? v2 : j == 1 ? v1 : v0;
 }
 
+// A GemvJobs argument in scalar registers at once: the compiler otherwise
+// loads each field where it is first used, and a field read behind a branch
+// (a job's end) costs a dependent scalar-memory round trip before the loads
+// that follow it can issue.
+template <class Jobs>
+__device__ __forceinline__ void hold_jobs(const Jobs &j) {
+  asm volatile("" ::"s"(j.w[0]), "s"(j.w[1]), "s"(j.w[2]), "s"(j.w[3]), "s"(j.sc[0]),
+               "s"(j.sc[1]), "s"(j.sc[2]), "s"(j.sc[3]));
+  asm volatile("" ::"s"(j.dst[0]), "s"(j.dst[1]), "s"(j.dst[2]), "s"(j.dst[3]), "s"(j.end[0]),
+               "s"(j.end[1]), "s"(j.end[2]), "s"(j.end[3]), "s"(j.njobs));
+}
+
 // The global-memory view of a pointer.  After in_sgpr the compiler no longer
 // knows a pointer is global, and flat accesses through it count against both
 // vmcnt and lgkmcnt, so waits for them cannot be partial.
