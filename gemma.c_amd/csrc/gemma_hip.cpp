@@ -756,6 +756,23 @@ int gemma_hip_patch_embed(float *dst, const float *img, const float *pe,
   return 0;
 }
 
+int gemma_hip_vision_attention(float *out, const float *qkv, const float *bias, int n,
+                               int n_heads, int dim, int mode, void *stream) {
+  if (need_init()) return 1;
+  if (!out || !qkv || !bias) return fail("gemma_hip_vision_attention: null pointer");
+  const int hdim = n_heads > 0 && dim % n_heads == 0 ? dim / n_heads : 0;
+  if (n < 1 || (hdim != 16 && hdim != 32 && hdim != 64 && hdim != 72 && hdim != 128) ||
+      (long)n * 3 * dim > (1l << 30))
+    return fail("gemma_hip_vision_attention: unsupported shape n=%d heads=%d dim=%d "
+                "(head dim 16, 32, 64, 72 or 128)", n, n_heads, dim);
+  if (mode != GEMMA_HIP_ATTN_F64 && mode != GEMMA_HIP_ATTN_F32)
+    return fail("gemma_hip_vision_attention: unknown mode %d", mode);
+  const gh::VisAttn at{qkv, 3 * dim, bias, out, n, n_heads, dim, 1.0f / sqrtf((float)hdim)};
+  GH_CHECK("gemma_hip_vision_attention: launch",
+           gh::launch_vis_attention(at, hdim, mode == GEMMA_HIP_ATTN_F32, pick_stream(stream)));
+  return 0;
+}
+
 /* ---- host drop-ins ------------------------------------------------------ */
 
 // Inputs up to this size are read by the kernels straight from pinned host
@@ -1592,6 +1609,7 @@ const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec) {
 struct gemma_hip_vision {
   gemma_hip_vision_config cfg{};
   int npatch = 0, ppi = 0, ksize = 0, hdim = 0;
+  bool attn_f32 = false;  // attention on the fp32 matrix cores (gemma_hip_vision_set_attention)
   struct Layer {
     const int8_t *w[6];  // wq wk wv wo w1 w2, device
     const float *s[6];
@@ -1644,7 +1662,7 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
       return e;
     const gh::VisAttn at{v->qkv, 3 * dim, L.bqkv, v->att, n, c.n_heads, dim,
                          1.0f / sqrtf((float)v->hdim)};
-    if ((e = gh::launch_vis_attention(at, v->hdim, st)) != hipSuccess) return e;
+    if ((e = gh::launch_vis_attention(at, v->hdim, v->attn_f32, st)) != hipSuccess) return e;
     // o (4563-4573), then its bias, the residual and the second layer norm
     if ((e = gh::launch_quantize(v->a8, v->as, v->att, dim, n, dim, st)) != hipSuccess ||
         (e = gemm(v->y, dim, L.w[3], L.s[3], n, dim, dim)) != hipSuccess)
@@ -1833,6 +1851,14 @@ int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out
            hipMemcpyAsync(out, vis->out, (size_t)c.img_tok * c.text_dim * 4,
                           hipMemcpyDeviceToHost, g.stream));
   GH_CHECK("gemma_hip_vision_forward: sync", hipStreamSynchronize(g.stream));
+  return 0;
+}
+
+int gemma_hip_vision_set_attention(gemma_hip_vision *vis, int mode) {
+  if (vis == nullptr) return fail("gemma_hip_vision_set_attention: null argument");
+  if (mode != GEMMA_HIP_ATTN_F64 && mode != GEMMA_HIP_ATTN_F32)
+    return fail("gemma_hip_vision_set_attention: unknown mode %d", mode);
+  vis->attn_f32 = mode == GEMMA_HIP_ATTN_F32;
   return 0;
 }
 

@@ -334,6 +334,159 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_kernel(VisAttn a) {
   }
 }
 
+// The same attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32, twice
+// the fp64 rate): q, k, v, scores, weights and value sums in fp32, as the
+// reference computes them (gemm_fpx, softmax, gemm_fpx_nn), in a different
+// order, so the result agrees with the fp64 form to fp32 rounding rather
+// than bit for bit.  The fp32 MFMA takes A and B as the fp64 one does but
+// leaves D as lane l, element r -> D[4 (l/16) + r][l%16] (checked on this
+// GPU), so a lane (query col, g = l/16) holds the scores of keys 4g + r of a
+// 16-key block, and the value product's MFMA step r takes keys 4g + r from
+// lane group g: V^T stays in natural key order and a lane reads its four
+// keys as one float4.  The reference maximum moves when a score exceeds it
+// by more than 16 (e^16 * n keys * |v| stays far below FLT_MAX).
+constexpr float kVaSlackF = 16.0f;
+
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a) {
+  constexpr int NT = NW * 64, QB = NW * 16;
+  static_assert(HD % 8 == 0 && HD <= 128, "head dim");
+  constexpr int KS = HD / 4;          // MFMA steps of a score block (dims per lane)
+  constexpr int NB = (HD + 15) / 16;  // 16-dim output blocks
+  constexpr int RK = HD + 2;          // K row in LDS (floats)
+  constexpr int VS = kVaKeys + 4;     // V^T row in LDS (floats)
+  constexpr int C4 = HD / 4;
+  constexpr int PF = (kVaKeys * C4 + NT - 1) / NT;
+  __shared__ float kt[kVaKeys * RK];
+  __shared__ float vt[16 * NB * VS];
+  __shared__ v4f kvb[2][C4];
+  typedef float v2f __attribute__((ext_vector_type(2)));
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nqb = (a.n + QB - 1) / QB, nblk = nqb * a.n_heads;
+  int blk = blockIdx.x;
+  if (nblk % 8 == 0) blk = (blk % 8) * (nblk / 8) + blk / 8;
+  const int h = blk / nqb;
+  const int q0 = (blk - h * nqb) * QB + wave * 16;
+  const int col = lane & 15, grp = lane >> 4;
+
+  float qa[KS];
+  {
+    const int qr = min(q0 + col, a.n - 1);
+    const float *qrow = a.qkv + (size_t)qr * a.stride + h * HD + grp * KS;
+    const float *bq = a.bias + h * HD + grp * KS;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qa[s] = qrow[s] + bq[s];
+  }
+  v4f o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -FLT_MAX, l_part = 0.0f;
+  const float *bk = a.bias + a.dim + h * HD;
+  const float *bv = a.bias + 2 * a.dim + h * HD;
+  const float *kbase = a.qkv + a.dim + h * HD;
+  const float *vbase = a.qkv + 2 * a.dim + h * HD;
+
+  for (int i = HD * VS + tid; i < 16 * NB * VS; i += NT) vt[i] = 0.0f;  // padding dims
+  for (int i = tid; i < 2 * C4; i += NT)
+    kvb[i / C4][i % C4] = reinterpret_cast<const v4f *>(i < C4 ? bk : bv)[i % C4];
+
+  v4f kx[PF], vx[PF];
+  auto fetch = [&](int t0) {  // rows clamped into range: every load is unconditional
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = min(tid + j * NT, kVaKeys * C4 - 1);
+      const int t = i / C4, c4 = i - t * C4;
+      const size_t row = (size_t)min(t0 + t, a.n - 1) * a.stride;
+      kx[j] = *reinterpret_cast<const v4f *>(kbase + row + 4 * c4);
+      vx[j] = *reinterpret_cast<const v4f *>(vbase + row + 4 * c4);
+    }
+  };
+  fetch(0);
+  for (int t0 = 0; t0 < a.n; t0 += kVaKeys) {
+    lds_barrier();  // every wave is done with the previous tile
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * NT;
+      if (i >= kVaKeys * C4) break;
+      const int t = i / C4, c4 = i - t * C4;
+      const bool ok = t0 + t < a.n;
+      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+      const v4f kv = ok ? kx[j] + kvb[0][c4] : zero;
+      const v4f vv = ok ? vx[j] + kvb[1][c4] : zero;
+      *reinterpret_cast<v2f *>(&kt[t * RK + 4 * c4]) = v2f{kv[0], kv[1]};
+      *reinterpret_cast<v2f *>(&kt[t * RK + 4 * c4 + 2]) = v2f{kv[2], kv[3]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + t] = vv[e];
+    }
+    lds_barrier();
+    if (t0 + kVaKeys < a.n) fetch(t0 + kVaKeys);
+
+    // scores: sc[b][r] = q(col) . k(t0 + 16 b + 4 grp + r)
+    v4f sc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+      const float *kr = &kt[(16 * b + col) * RK + grp * KS];
+#pragma unroll
+      for (int s = 0; s < KS; s += 2) {
+        const v2f k2 = *reinterpret_cast<const v2f *>(kr + s);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(k2[0], qa[s], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(k2[1], qa[s + 1], sc[b], 0, 0, 0);
+      }
+    }
+    float tmax = -FLT_MAX;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = t0 + 16 * b + 4 * grp + r < a.n;
+        sc[b][r] = ok ? sc[b][r] * a.scale : -FLT_MAX;
+        tmax = fmaxf(tmax, sc[b][r]);
+      }
+    if (__any(tmax > m_ref + kVaSlackF)) {
+      float rmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+      const float m_new = fmaxf(m_ref, rmax);
+      const float alpha = expf(m_ref - m_new);
+      m_ref = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = sc[b][r] > -FLT_MAX ? expf(sc[b][r] - m_ref) : 0.0f;
+        l_part += pr;
+        sc[b][r] = pr;
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const v4f v4 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 16 * b + 4 * grp]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[r], sc[b][r], o[nb], 0, 0, 0);
+      }
+    }
+  }
+  float l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  const int qr = q0 + col;
+  if (qr < a.n) {
+    float *orow = a.out + (size_t)qr * a.dim + h * HD;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * nb + 4 * grp + r;
+        if (d < HD) orow[d] = o[nb][r] / l;
+      }
+  }
+}
+
 // One workgroup per row: (float)gelu_tanh(h + b1) (gemma.c:4600-4604 with
 // gelu 4150-4172: the bias added in fp32, the GELU in fp64 rounded once),
 // quantized into xq[r] / xs[r].
@@ -466,9 +619,20 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
   return go(std::integral_constant<int, 256>{});
 }
 
-hipError_t launch_vis_attention(const VisAttn &a, int hdim, hipStream_t stream) {
+hipError_t launch_vis_attention(const VisAttn &a, int hdim, bool f32, hipStream_t stream) {
   constexpr int NW = kVaWaves;
   const dim3 grid((a.n + NW * 16 - 1) / (NW * 16) * a.n_heads);
+  if (f32) {
+    switch (hdim) {
+      case 16: vis_attn_f32_kernel<16, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 32: vis_attn_f32_kernel<32, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 64: vis_attn_f32_kernel<64, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 72: vis_attn_f32_kernel<72, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 128: vis_attn_f32_kernel<128, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   switch (hdim) {
     case 16: vis_attn_kernel<16, NW><<<grid, NW * 64, 0, stream>>>(a); break;
     case 32: vis_attn_kernel<32, NW><<<grid, NW * 64, 0, stream>>>(a); break;

@@ -124,6 +124,8 @@ _SIGS = {
     "gemma_hip_vision_create": (_P, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "gemma_hip_vision_destroy": (None, [_P]),
     "gemma_hip_vision_forward": (_I, [_P, _P, _P]),
+    "gemma_hip_vision_set_attention": (_I, [_P, _I]),
+    "gemma_hip_vision_attention": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
 }
 
 
@@ -244,6 +246,12 @@ class GemmaHip:
                                                    _addr(work), stream))
 
     # weights ---------------------------------------------------------------
+    def vision_attention(self, out, qkv, bias, n, n_heads, dim, mode=0, stream=None):
+        """gemma_hip_vision_attention on device pointers."""
+        self._check(self.lib.gemma_hip_vision_attention(_addr(out), _addr(qkv), _addr(bias), n,
+                                                        n_heads, dim, mode,
+                                                        stream))
+
     def register_weights(self, host, nbytes: int):
         self._check(self.lib.gemma_hip_register_weights(_addr(host), nbytes))
 
@@ -434,6 +442,13 @@ class Vision:
         for arr in self._registered:
             self.gh.release_weights(arr)
         self._registered = []
+
+    ATTN_F64, ATTN_F32 = 0, 1
+
+    def set_attention(self, mode: int):
+        """GEMMA_HIP_ATTN_F64 (0, the default) or GEMMA_HIP_ATTN_F32 (1): the
+        attention's arithmetic, fp64 or fp32 matrix cores."""
+        self.gh._check(self.lib.gemma_hip_vision_set_attention(self.handle, int(mode)))
 
     def forward(self, img):
         """img [img_px][img_px][3] float32 -> soft tokens [img_tok][text_dim]."""

@@ -374,6 +374,28 @@ void gemma_hip_vision_destroy(gemma_hip_vision *vis);
  * soft tokens, what forward_vision leaves in tb->x) out. */
 int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out);
 
+/* The arithmetic of the tower's attention (gemma.c:4533-4561; set before
+ * forward, kept until changed):
+ *   GEMMA_HIP_ATTN_F64 (the default) -- fp64 matrix cores, every output
+ *     rounded once: equal to the fp64 vision oracle;
+ *   GEMMA_HIP_ATTN_F32 -- fp32 matrix cores at twice the rate, fp32
+ *     throughout as the reference computes it (its summation order differs),
+ *     so results agree with the fp64 form to fp32 rounding, amplified where a
+ *     later int8 quantization flips.
+ * The rest of the tower is unchanged.  0 or 1 on an unknown mode. */
+#define GEMMA_HIP_ATTN_F64 0
+#define GEMMA_HIP_ATTN_F32 1
+int gemma_hip_vision_set_attention(gemma_hip_vision *vis, int mode);
+
+/* The tower's attention block alone (gemma.c:4527-4561) on device buffers:
+ * qkv [n][3*dim] holds the q, k and v GEMM outputs of each patch, bias
+ * [3*dim] their biases (added in fp32, 4517-4526); out [n][dim] receives, per
+ * head of dim/n_heads (16, 32, 64, 72 or 128), softmax(q.k * scale) v over all
+ * n patches with scale = 1/sqrtf(head dim).  mode as above.  On `stream`
+ * (NULL: the library's). */
+int gemma_hip_vision_attention(float *out, const float *qkv, const float *bias, int n,
+                               int n_heads, int dim, int mode, void *stream);
+
 /* forward_gemma_image (gemma.c:5561-5595) on the device: the vision tower on
  * img, its img_tok soft tokens handed to the decoder in HBM, and the dense
  * (mask=false) prompt pass at *pos, which advances by img_tok on success.

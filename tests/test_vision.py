@@ -92,6 +92,107 @@ def test_vision_matches_oracle(gh, oracle, shape):
     assert np.array_equal(got, again)  # deterministic
 
 
+# The fp32-matrix-core attention (GEMMA_HIP_ATTN_F32) in the whole tower: on
+# seeds measured free of int8 requantization flips it agrees with the fp64
+# oracle to fp32 rounding (measured 5e-8 .. 1.5e-7 of the largest output); at
+# SigLIP's widths a flip is certain somewhere, and one moves the pooled soft
+# tokens by ~1% (measured 1.0% .. 1.4% max, 0.2% median), so there the bar is
+# the flip level.  The attention kernel itself is pinned directly below.
+F32_TOWER_CASES = [("hd16", 7, 8), ("hd16", 8, 9), ("hd72", 8, 9), ("hd72", 9, 10)]
+F32_PRE_FLIP = 1e-6
+F32_FLIP_LEVEL = 5e-2
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("shape,seed,img_seed", F32_TOWER_CASES)
+def test_vision_f32_attention_matches_oracle(gh, oracle, shape, seed, img_seed):
+    vis = model_bin.synth_vision(seed=seed, text_dim=64, **SHAPES[shape])
+    img = model_bin.synth_image(SHAPES[shape]["img_px"], seed=img_seed)
+    want = vorc.VisionOracle(vis, oracle).forward(img)
+    tower = gh.vision(vis)
+    try:
+        tower.set_attention(tower.ATTN_F32)
+        got = tower.forward(img)
+        again = tower.forward(img)
+        tower.set_attention(tower.ATTN_F64)
+        exact = tower.forward(img)
+    finally:
+        tower.close()
+    rel = float(np.abs(got - want).max() / np.abs(want).max())
+    print(f"vision f32 attention {shape} seed {seed}: {rel:.3g}", flush=True)
+    assert rel <= F32_PRE_FLIP
+    assert np.array_equal(got, again)
+    assert np.array_equal(exact, want) or float(np.abs(exact - want).max()) <= TOL * float(
+        np.abs(want).max())  # switching back restores the fp64 path
+
+
+@pytest.mark.gpu
+def test_vision_f32_attention_siglip_width_flip_level(gh, oracle):
+    vis = model_bin.synth_vision(seed=7, text_dim=64, **SHAPES["siglip"])
+    img = model_bin.synth_image(SHAPES["siglip"]["img_px"], seed=8)
+    want = vorc.VisionOracle(vis, oracle).forward(img)
+    tower = gh.vision(vis)
+    try:
+        tower.set_attention(tower.ATTN_F32)
+        got = tower.forward(img)
+    finally:
+        tower.close()
+    rel = float(np.abs(got - want).max() / np.abs(want).max())
+    print(f"vision f32 attention siglip width: {rel:.3g}", flush=True)
+    assert rel <= F32_FLIP_LEVEL
+
+
+# The attention block alone (gemma_hip_vision_attention) against the fp64
+# oracle's attention, before any quantization: the fp64 kernel to one fp32
+# rounding, the fp32 kernel to the fp32 accumulation error over n keys.
+ATT_CASES = {
+    # n, heads, dim: SigLIP at 896 px; ragged query and key tiles at head
+    # dims 16, 32, 128; SigLIP's head dim at an odd patch count
+    "siglip896": (4096, 16, 1152),
+    "hd16": (200, 4, 64),
+    "hd32": (77, 3, 96),
+    "hd128": (300, 2, 256),
+    "hd72": (1000, 4, 288),
+}
+ATT_F64_TOL = 2.4e-7  # two fp32 ulps of the largest output
+ATT_F32_TOL = 2e-5
+
+
+def _attention_inputs(n, heads, dim, seed):
+    rng = np.random.default_rng(seed)
+    qkv = rng.standard_normal((n, 3 * dim)).astype(np.float32)
+    bias = (0.5 * rng.standard_normal(3 * dim)).astype(np.float32)
+    hd = dim // heads
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    q = qkv[:, :dim] + bias[:dim]
+    k = qkv[:, dim:2 * dim] + bias[dim:2 * dim]
+    v = qkv[:, 2 * dim:] + bias[2 * dim:]
+    want = np.concatenate([vorc.attention(q[:, h * hd:(h + 1) * hd], k[:, h * hd:(h + 1) * hd],
+                                          v[:, h * hd:(h + 1) * hd], scale)
+                           for h in range(heads)], axis=1)
+    return qkv, bias, want
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", sorted(ATT_CASES))
+def test_vision_attention_kernels_match_oracle(gh, case):
+    import torch
+
+    n, heads, dim = ATT_CASES[case]
+    qkv, bias, want = _attention_inputs(n, heads, dim, seed=n + heads)
+    dq, db = torch.from_numpy(qkv).cuda(), torch.from_numpy(bias).cuda()
+    scale = float(np.abs(want).max())
+    for mode, tol in ((0, ATT_F64_TOL), (1, ATT_F32_TOL)):
+        out = torch.full((n, dim), float("nan"), device="cuda")
+        gh.vision_attention(out, dq, db, n, heads, dim, mode,
+                            stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        rel = float(np.abs(got - want).max()) / scale
+        print(f"vision attention {case} mode {mode}: |d|/max = {rel:.3g}", flush=True)
+        assert rel <= tol, (case, mode, rel)
+
+
 @pytest.mark.gpu
 def test_vision_argument_errors(gh):
     import ctypes
