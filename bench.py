@@ -410,10 +410,13 @@ DECODER_RUNS = (("gemma-3-270m", 32, 64), ("gemma-3-1b", 512, 256), ("gemma-3-4b
 
 def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     """The prompt and the greedy decode fully on the GPU: `prompt` random token
-    ids go through the batched prefill (gemma_hip_decoder_prefill; timed once
-    after a warm-up call that allocates its row buffers), then `steps` decode
-    steps from the KV cache it filled are timed (one HIP graph launch each,
-    tokens fed back on the device, one readback at the end)."""
+    ids go through the batched prefill (gemma_hip_decoder_prefill; the median
+    of TIMING_RUNS calls after a warm-up call that allocates its row buffers,
+    with the attention on the fp64 matrix cores, the default, and on the fp32
+    ones), then `steps` decode steps from the KV cache the fp64 prefill filled
+    are timed (one HIP graph launch each, tokens fed back on the device, one
+    readback at the end)."""
+    import statistics
     import time
 
     import numpy as np
@@ -427,9 +430,16 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     try:
         dec.prefill(ids, 0)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        first = dec.prefill(ids, 0)
-        t_pf = time.perf_counter() - t0
+        t_mode = {}
+        for mode in (dec.ATTN_F32, dec.ATTN_F64):  # the fp64 prefill last: its cache is decoded
+            dec.set_attention(mode)
+            ts = []
+            for _ in range(TIMING_RUNS):
+                t0 = time.perf_counter()
+                first = dec.prefill(ids, 0)
+                ts.append(time.perf_counter() - t0)
+            t_mode[mode] = statistics.median(ts)
+        t_pf, t_pf32 = t_mode[dec.ATTN_F64], t_mode[dec.ATTN_F32]
         best = None
         for _ in range(2):
             t0 = time.perf_counter()
@@ -445,7 +455,8 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
                         + gemm_ops(prompt, c["dim"], c["mlp_dim"]))
     prefill = dict(tokens=prompt, ms=round(1e3 * t_pf, 3), tok_s=round(prompt / t_pf, 1),
                    int8_tops=round(pf_ops / t_pf / 1e12, 1),
-                   int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4))
+                   int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4),
+                   ms_attn_f32=round(1e3 * t_pf32, 3), tok_s_attn_f32=round(prompt / t_pf32, 1))
     per_layer = (gemv_bytes(q_sz + 2 * kv_sz, c["dim"]) + gemv_bytes(c["dim"], q_sz)
                  + gemv_bytes(2 * c["mlp_dim"], c["dim"]) + gemv_bytes(c["dim"], c["mlp_dim"]))
     weights = c["nl"] * per_layer + gemv_bytes(c["nvocab"], c["dim"])

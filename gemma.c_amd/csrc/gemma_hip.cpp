@@ -1033,6 +1033,7 @@ struct gemma_hip_decoder {
   gemma_hip_text_config cfg{};
   std::vector<unsigned char> swa;
   int clen = 0, max_blocks = 0, nparts = 256;
+  bool attn_f32 = false;  // prefill attention on the fp32 matrix cores
   struct Layer {
     const int8_t *w[7];  // wq wk wv wo w1(up) w2(gate) w3(down), device
     const float *s[7];
@@ -1155,7 +1156,7 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
                         c.nkv, d->clen, sliding ? c.slide : 0,
                         (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
                         0, dense ? 1 : 0};
-    if ((e = gh::launch_pf_attention(at, c.hdim, st)) != hipSuccess) return e;
+    if ((e = gh::launch_pf_attention(at, c.hdim, d->attn_f32, st)) != hipSuccess) return e;
     // o projection
     if ((e = gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st)) !=
             hipSuccess ||
@@ -1596,6 +1597,14 @@ int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n
   PF_CHECK("rows copy", hipMemcpyAsync(dec->pf_x, x, (size_t)n * dec->cfg.dim * 4,
                                        hipMemcpyDefault, g.stream));
   return prefill_run(dec, kName, n, pos, 0, false, mask == 0, logits, next);
+}
+
+int gemma_hip_decoder_set_attention(gemma_hip_decoder *dec, int mode) {
+  if (dec == nullptr) return fail("gemma_hip_decoder_set_attention: null argument");
+  if (mode != GEMMA_HIP_ATTN_F64 && mode != GEMMA_HIP_ATTN_F32)
+    return fail("gemma_hip_decoder_set_attention: unknown mode %d", mode);
+  dec->attn_f32 = mode == GEMMA_HIP_ATTN_F32;
+  return 0;
 }
 
 const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec) {

@@ -381,6 +381,166 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_kernel(PfAttn a) {
   pa_store<HD, NB>(a, L, o, m_ref, l_part, grp);
 }
 
+// The same attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32, twice
+// the fp64 rate), head dims 128 and 256: queries, scores, weights and value
+// sums in fp32, as the reference computes them (gemm_fpx, softmax,
+// gemm_fpx_nn, gemma.c:5198-5255), in a different order, so the result
+// agrees with the fp64 form to fp32 rounding rather than bit for bit.  One
+// wave per 16 query vectors holds a whole head dim (64 + 64 registers at
+// 256); K/V tiles of 32 keys are staged through registers as in
+// pf_attn_kernel.  The fp32 MFMA leaves D as lane l, element r ->
+// D[4 (l/16) + r][l%16], so a lane (query col, g) holds keys 4g + r of a
+// 16-key block and V^T stays in natural key order.  Partials of a key-split
+// row block go to the fp64 merge as for the fp64 kernels.
+constexpr float kPaSlackF = 16.0f;    // p <= e^16
+constexpr float kPaFloorF = -1e30f;   // far below any score, far above -FLT_MAX
+
+template <int NB, int NS>
+__device__ __forceinline__ void pa_softmax_f32(const PfAttn &a, const PaLane &L, v4f (&sc)[NS],
+                                               int key0, int grp, float &m_ref, float &l_part,
+                                               v4f (&o)[NB]) {
+  float tmax = -FLT_MAX;
+#pragma unroll
+  for (int b = 0; b < NS; ++b)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = key0 + 16 * b + 4 * grp + r;
+      float x = sc[b][r] * a.asc;
+      if (a.sc_att != 0.0f) x = tanhf(x / a.sc_att) * a.sc_att;
+      sc[b][r] = (key <= L.p_top && key >= L.ws) ? x : -FLT_MAX;
+      tmax = fmaxf(tmax, sc[b][r]);
+    }
+  if (__any(tmax > m_ref + kPaSlackF)) {
+    float rmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+    const float m_new = fmaxf(m_ref, rmax);
+    const float alpha = expf(m_ref - m_new);
+    m_ref = m_new;
+    l_part *= alpha;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
+  }
+#pragma unroll
+  for (int b = 0; b < NS; ++b)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sc[b][r] = sc[b][r] > -FLT_MAX ? expf(sc[b][r] - m_ref) : 0.0f;
+      l_part += sc[b][r];
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
+  constexpr int KS = HD / 4;              // score MFMA steps (dims per lane)
+  constexpr int NB = HD / 16;             // 16-dim output blocks
+  constexpr int RK = HD + 4;              // K row in LDS (floats)
+  constexpr int VS = kPaKeys + 4;         // V^T row in LDS (floats)
+  constexpr int C4 = HD / 4;              // float4 per key row
+  constexpr int PF = kPaKeys * C4 / kNT;  // float4 of K (and of V) per thread
+  static_assert(PF * kNT == kPaKeys * C4, "tile staging");
+  __shared__ float kt[kPaKeys * RK];
+  __shared__ float vt[HD * VS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const PaLane L = pa_lane(a, wave, col);
+  if (L.empty) return;  // the whole block: before any barrier
+  float qa[KS];
+  {
+    const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + grp * KS;
+#pragma unroll
+    for (int s = 0; s < KS; s += 4) {
+      const v4f q4 = *reinterpret_cast<const v4f *>(qrow + s);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qa[s + e] = q4[e];
+    }
+  }
+  v4f o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_ref = kPaFloorF, l_part = 0.0f;
+  const float *kc = a.kc + (size_t)L.hk * a.clen * HD;
+  const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
+
+  v4f kx[PF], vx[PF];
+  auto fetch = [&](int t0) {  // rows clamped to the chunk's last key: loads are unconditional
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * kNT;
+      const int t = i / C4, c4 = i - t * C4;
+      const size_t at = (size_t)min(t0 + t, L.k_end) * HD + 4 * c4;
+      kx[j] = *reinterpret_cast<const v4f *>(kc + at);
+      vx[j] = *reinterpret_cast<const v4f *>(vc + at);
+    }
+  };
+  fetch(L.k_lo);
+  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += kPaKeys) {
+    lds_barrier();  // every wave is done with the previous tile
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * kNT;
+      const int t = i / C4, c4 = i - t * C4;
+      const bool ok = t0 + t <= L.k_end;  // later keys: another chunk's, or not in the cache yet
+      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<v4f *>(&kt[t * RK + 4 * c4]) = ok ? kx[j] : zero;
+      const v4f vv = ok ? vx[j] : zero;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + t] = vv[e];
+    }
+    lds_barrier();
+    if (t0 + kPaKeys <= L.k_end) fetch(t0 + kPaKeys);
+
+    if (t0 > L.w_hi || t0 + kPaKeys - 1 < L.w_lo) continue;  // wave-uniform
+    // scores of both 16-key blocks, two independent MFMA chains
+    v4f sc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int s = 0; s < KS; s += 4) {
+      const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
+      const v4f k1 = *reinterpret_cast<const v4f *>(&kt[(16 + col) * RK + grp * KS + s]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[e], qa[s + e], sc[0], 0, 0, 0);
+        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[e], qa[s + e], sc[1], 0, 0, 0);
+      }
+    }
+    pa_softmax_f32<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const v4f v0 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 4 * grp]);
+      const v4f v1 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 16 + 4 * grp]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[r], sc[0][r], o[nb], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1[r], sc[1][r], o[nb], 0, 0, 0);
+    }
+  }
+  // outputs: lane (col, grp) holds dims 16 nb + 4 grp + r of its query
+  float l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  if (!L.valid) return;
+  if (L.nchunks == 1) {
+    float *orow = a.xo + (size_t)L.row * a.q_sz + L.head * HD;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      *reinterpret_cast<v4f *>(orow + 16 * nb + 4 * grp) = o[nb] / l;
+    return;
+  }
+  const size_t at = (size_t)L.chunk_id * a.n + L.row;
+  double *prow = a.part + at * a.q_sz + L.head * HD;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) prow[16 * nb + 4 * grp + r] = (double)o[nb][r];
+  if (grp == 0) {
+    double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
+    ml[0] = (double)m_ref;
+    ml[1] = (double)l;
+  }
+}
+
 // One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
 // wave-uniform).  Issued from inline asm so that the compiler does not treat
 // every later LDS read as a possible alias of the pending load (it would
@@ -652,9 +812,9 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
   return hipGetLastError();
 }
 
-hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
+hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t stream) {
   const int hn = a.n_heads / a.nkv;
-  const int qpb = hdim == 256 ? kPaQPair : kPaQ;
+  const int qpb = f32 ? kPaQ : hdim == 256 ? kPaQPair : kPaQ;
   if (hn <= 0 || qpb % hn != 0 || a.n <= 0 || a.part == nullptr ||
       a.n_heads > kPfMaxMergeHeads)
     return hipErrorInvalidValue;
@@ -674,11 +834,19 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, hipStream_t stream) {
   b.chunk = ((kmax + split - 1) / split + kPaKeys - 1) / kPaKeys * kPaKeys;
   b.nsplit = (kmax + b.chunk - 1) / b.chunk;
   const dim3 grid(nrb * b.nsplit * a.nkv);
-  switch (hdim) {
-    case 128: pf_attn_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
-    case 256: pf_attn_pair_kernel<256, kPaPairWaves><<<grid, kPaPairWaves * 64, 0, stream>>>(b);
-      break;
-    default: return hipErrorInvalidValue;
+  if (f32) {
+    switch (hdim) {
+      case 128: pf_attn_f32_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
+      case 256: pf_attn_f32_kernel<256><<<grid, kNT, 0, stream>>>(b); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    switch (hdim) {
+      case 128: pf_attn_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
+      case 256: pf_attn_pair_kernel<256, kPaPairWaves><<<grid, kPaPairWaves * 64, 0, stream>>>(b);
+        break;
+      default: return hipErrorInvalidValue;
+    }
   }
   if (b.nsplit > 1) pf_attn_merge_kernel<<<a.n, kNT, 0, stream>>>(b, hdim);
   return hipGetLastError();

@@ -121,6 +121,7 @@ _SIGS = {
     "gemma_hip_decoder_prefill_rows": (_I, [_P, _P, _I, _I, _I, _P, ctypes.POINTER(_I)]),
     "gemma_hip_gemma_image": (_I, [_P, _P, _P, ctypes.POINTER(_I), _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_logits": (_P, [_P]),
+    "gemma_hip_decoder_set_attention": (_I, [_P, _I]),
     "gemma_hip_vision_create": (_P, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "gemma_hip_vision_destroy": (None, [_P]),
     "gemma_hip_vision_forward": (_I, [_P, _P, _P]),
@@ -380,6 +381,13 @@ class Decoder:
         self.gh._check(self.lib.gemma_hip_decoder_generate(self.handle, token, pos, n,
                                                            out.ctypes.data))
         return out[:n]
+
+    ATTN_F64, ATTN_F32 = 0, 1
+
+    def set_attention(self, mode: int):
+        """GEMMA_HIP_ATTN_F64 (0, the default) or GEMMA_HIP_ATTN_F32 (1): the
+        prompt passes' attention on the fp64 or the fp32 matrix cores."""
+        self.gh._check(self.lib.gemma_hip_decoder_set_attention(self.handle, int(mode)))
 
     def logits_ptr(self) -> int:
         return self.lib.gemma_hip_decoder_logits(self.handle)

@@ -314,6 +314,17 @@ int gemma_hip_decoder_prefill(gemma_hip_decoder *dec, const int *tokens, int n, 
 int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n, int pos,
                                    int mask, float *logits, int *next);
 
+/* The arithmetic of the prompt passes' attention (prefill, prefill_rows,
+ * image): GEMMA_HIP_ATTN_F64 (the default; fp64 matrix cores, each output
+ * rounded once, equal to the decode oracle) or GEMMA_HIP_ATTN_F32 (fp32
+ * matrix cores at twice the rate, fp32 throughout as the reference's
+ * gemm_fpx/softmax/gemm_fpx_nn, gemma.c:5198-5255: agrees to fp32 rounding,
+ * amplified where a later int8 quantization flips).  The decode step's
+ * attention is fp64 either way.  0 or 1 on an unknown mode. */
+#define GEMMA_HIP_ATTN_F64 0
+#define GEMMA_HIP_ATTN_F32 1
+int gemma_hip_decoder_set_attention(gemma_hip_decoder *dec, int mode);
+
 /* n greedy steps without host round trips: step i consumes the token step
  * i-1 produced (the first consumes `token` at `pos`); tokens[i] receives the
  * argmax of step i (host, n ints).  pos + n <= clen. */
@@ -383,8 +394,6 @@ int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out
  *     so results agree with the fp64 form to fp32 rounding, amplified where a
  *     later int8 quantization flips.
  * The rest of the tower is unchanged.  0 or 1 on an unknown mode. */
-#define GEMMA_HIP_ATTN_F64 0
-#define GEMMA_HIP_ATTN_F32 1
 int gemma_hip_vision_set_attention(gemma_hip_vision *vis, int mode);
 
 /* The tower's attention block alone (gemma.c:4527-4561) on device buffers:
