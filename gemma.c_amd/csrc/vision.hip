@@ -344,20 +344,26 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_kernel(VisAttn a) {
 // 16-key block, and the value product's MFMA step r takes keys 4g + r from
 // lane group g: V^T stays in natural key order and a lane reads its four
 // keys as one float4.  The reference maximum moves when a score exceeds it
-// by more than 16 (e^16 * n keys * |v| stays far below FLT_MAX).
+// by more than 16 (e^16 * n keys * |v| stays far below FLT_MAX).  The
+// exponential is __expf (v_exp_f32 on x log2 e: a relative error near
+// |x| 2^-24 for the arguments here, |x| <= 16 past the masked keys), and two
+// workgroups share a CU (113 registers at head dim 72): 880 -> 785 us per
+// SigLIP layer against expf at one workgroup per CU.
 constexpr float kVaSlackF = 16.0f;
+constexpr int kVaKeysF = 32;  // keys per tile (fp32 kernel; 64 measured 2% slower)
 
-template <int HD, int NW>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a) {
+template <int HD, int NW, int TK>
+__global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_f32_kernel(VisAttn a) {
+  constexpr int NS = TK / 16;         // 16-key score blocks per tile
   constexpr int NT = NW * 64, QB = NW * 16;
   static_assert(HD % 8 == 0 && HD <= 128, "head dim");
   constexpr int KS = HD / 4;          // MFMA steps of a score block (dims per lane)
   constexpr int NB = (HD + 15) / 16;  // 16-dim output blocks
   constexpr int RK = HD + 2;          // K row in LDS (floats)
-  constexpr int VS = kVaKeys + 4;     // V^T row in LDS (floats)
+  constexpr int VS = TK + 4;     // V^T row in LDS (floats)
   constexpr int C4 = HD / 4;
-  constexpr int PF = (kVaKeys * C4 + NT - 1) / NT;
-  __shared__ float kt[kVaKeys * RK];
+  constexpr int PF = (TK * C4 + NT - 1) / NT;
+  __shared__ float kt[TK * RK];
   __shared__ float vt[16 * NB * VS];
   __shared__ v4f kvb[2][C4];
   typedef float v2f __attribute__((ext_vector_type(2)));
@@ -396,7 +402,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a
   auto fetch = [&](int t0) {  // rows clamped into range: every load is unconditional
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
-      const int i = min(tid + j * NT, kVaKeys * C4 - 1);
+      const int i = min(tid + j * NT, TK * C4 - 1);
       const int t = i / C4, c4 = i - t * C4;
       const size_t row = (size_t)min(t0 + t, a.n - 1) * a.stride;
       kx[j] = *reinterpret_cast<const v4f *>(kbase + row + 4 * c4);
@@ -404,12 +410,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a
     }
   };
   fetch(0);
-  for (int t0 = 0; t0 < a.n; t0 += kVaKeys) {
+  for (int t0 = 0; t0 < a.n; t0 += TK) {
     lds_barrier();  // every wave is done with the previous tile
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int i = tid + j * NT;
-      if (i >= kVaKeys * C4) break;
+      if (i >= TK * C4) break;
       const int t = i / C4, c4 = i - t * C4;
       const bool ok = t0 + t < a.n;
       const v4f zero = {0.f, 0.f, 0.f, 0.f};
@@ -421,12 +427,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a
       for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + t] = vv[e];
     }
     lds_barrier();
-    if (t0 + kVaKeys < a.n) fetch(t0 + kVaKeys);
+    if (t0 + TK < a.n) fetch(t0 + TK);
 
     // scores: sc[b][r] = q(col) . k(t0 + 16 b + 4 grp + r)
-    v4f sc[2];
+    v4f sc[NS];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < NS; ++b) {
       sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
       const float *kr = &kt[(16 * b + col) * RK + grp * KS];
 #pragma unroll
@@ -438,7 +444,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a
     }
     float tmax = -FLT_MAX;
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < NS; ++b)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const bool ok = t0 + 16 * b + 4 * grp + r < a.n;
@@ -449,17 +455,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void vis_attn_f32_kernel(VisAttn a
       float rmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
       const float m_new = fmaxf(m_ref, rmax);
-      const float alpha = expf(m_ref - m_new);
+      const float alpha = __expf(m_ref - m_new);
       m_ref = m_new;
       l_part *= alpha;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
     }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < NS; ++b) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pr = sc[b][r] > -FLT_MAX ? expf(sc[b][r] - m_ref) : 0.0f;
+        const float pr = sc[b][r] > -FLT_MAX ? __expf(sc[b][r] - m_ref) : 0.0f;
         l_part += pr;
         sc[b][r] = pr;
       }
@@ -624,11 +630,11 @@ hipError_t launch_vis_attention(const VisAttn &a, int hdim, bool f32, hipStream_
   const dim3 grid((a.n + NW * 16 - 1) / (NW * 16) * a.n_heads);
   if (f32) {
     switch (hdim) {
-      case 16: vis_attn_f32_kernel<16, NW><<<grid, NW * 64, 0, stream>>>(a); break;
-      case 32: vis_attn_f32_kernel<32, NW><<<grid, NW * 64, 0, stream>>>(a); break;
-      case 64: vis_attn_f32_kernel<64, NW><<<grid, NW * 64, 0, stream>>>(a); break;
-      case 72: vis_attn_f32_kernel<72, NW><<<grid, NW * 64, 0, stream>>>(a); break;
-      case 128: vis_attn_f32_kernel<128, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 16: vis_attn_f32_kernel<16, NW, kVaKeysF><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 32: vis_attn_f32_kernel<32, NW, kVaKeysF><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 64: vis_attn_f32_kernel<64, NW, kVaKeysF><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 72: vis_attn_f32_kernel<72, NW, kVaKeysF><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 128: vis_attn_f32_kernel<128, NW, kVaKeysF><<<grid, NW * 64, 0, stream>>>(a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
