@@ -166,7 +166,8 @@ __global__ __launch_bounds__(NT) void dec_norm_gemv_kernel(DecNorm na, GemvJobs 
 //  GELU == true:  group g covers outputs r = g R/2 .. g R/2 + R/2 - 1; row
 //                 rloc of the group is gate row r (jobs.w[0]) for even rloc
 //                 and up row r (jobs.w[1]) for odd, and the gate lanes store
-//                 gelu(gate) * up to jobs.dst[0][r] (jobs.end[0] = outputs).
+//                 gelu(gate) * up to jobs.dst[0][r] (jobs.end[0] = 2 x outputs,
+//                 the gate and up rows together; the launcher checks it).
 // Loads are unconditional: a row past the end reads the job's last row and
 // a chunk past k reads chunk 0; neither is used.
 template <int L, int CPL, bool GELU, int NPT>
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
   auto where = [&](int g) {
     At a;
     if (GELU) {
-      const int m = jobs.end[0];
+      const int m = jobs.end[0] >> 1;  // outputs: end[0] counts gate and up rows
       a.out = g * (R / 2) + (rloc >> 1);
       a.job = rloc & 1;
       a.ok = g < ngroups && a.out < m;
@@ -836,9 +837,12 @@ hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int tot
   // every plain job must have rows: the kernels clamp a group's row to its
   // job's last row, which an empty job does not have (the GELU form pairs
   // gate and up rows of one range, given as end[0] = end[1] = 2 * mlp)
-  if (!gelu)
+  if (!gelu) {
     for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
       if (jobs.end[j] <= prev) return hipErrorInvalidValue;
+  } else if (total % 2 != 0 || jobs.end[0] != total) {
+    return hipErrorInvalidValue;
+  }
   const int kc = k / 16;
   if (const NormStreamFn fn = norm_stream_fn(kc, gelu)) {
     int lanes = 8;
