@@ -528,16 +528,17 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
       *reinterpret_cast<v4f *>(orow + 16 * nb + 4 * grp) = o[nb] / l;
     return;
   }
+  // fp32 partials (the fp64 kernels' layout in floats: half the bytes; the
+  // merge still combines them in fp64)
+  float *pf = reinterpret_cast<float *>(a.part);
   const size_t at = (size_t)L.chunk_id * a.n + L.row;
-  double *prow = a.part + at * a.q_sz + L.head * HD;
+  float *prow = pf + at * a.q_sz + L.head * HD;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) prow[16 * nb + 4 * grp + r] = (double)o[nb][r];
+  for (int nb = 0; nb < NB; ++nb) *reinterpret_cast<v4f *>(prow + 16 * nb + 4 * grp) = o[nb];
   if (grp == 0) {
-    double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
-    ml[0] = (double)m_ref;
-    ml[1] = (double)l;
+    float *ml = pf + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
+    ml[0] = m_ref;
+    ml[1] = l;
   }
 }
 
@@ -700,8 +701,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void pf_attn_pair_kernel(PfAttn a)
 // The chunks' partials of one row (a workgroup per row): with M the largest
 // reference maximum, out = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c in
 // fp64, rounded once.  A chunk in which a query saw no key has l = 0, O = 0
-// and m = kPaFloor, so it adds nothing.  Rows whose row block took a single
-// chunk were written by the attention kernel.
+// and m = kPaFloor (kPaFloorF), so it adds nothing.  Rows whose row block
+// took a single chunk were written by the attention kernel.  P: the
+// partials' type (double from the fp64 kernels, float from the fp32 one).
+template <class P>
 __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) {
   __shared__ double wt[kPfMaxMergeHeads][kPfMaxSplit + 1];  // weights, then 1 / denominator
   const int row = blockIdx.x;
@@ -710,17 +713,18 @@ __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) 
   const auto [k_base, p_last] = pa_range(a, r0, min(qb, a.n - r0));
   const int nchunks = (p_last - k_base + a.chunk) / a.chunk;
   if (nchunks == 1) return;
-  const double *ml = a.part + (size_t)kPfMaxSplit * a.n * a.q_sz;
+  const P *part = reinterpret_cast<const P *>(a.part);
+  const P *ml = part + (size_t)kPfMaxSplit * a.n * a.q_sz;
   for (int h = threadIdx.x; h < a.n_heads; h += kNT) {
     double m = -DBL_MAX;
     for (int c = 0; c < nchunks; ++c)
-      m = fmax(m, ml[(((size_t)c * a.n + row) * a.n_heads + h) * 2]);
+      m = fmax(m, (double)ml[(((size_t)c * a.n + row) * a.n_heads + h) * 2]);
     double den = 0.0;
     for (int c = 0; c < nchunks; ++c) {
       const size_t at = ((size_t)c * a.n + row) * a.n_heads + h;
-      const double w = exp(ml[at * 2] - m);
+      const double w = exp((double)ml[at * 2] - m);
       wt[h][c] = w;
-      den += w * ml[at * 2 + 1];
+      den += w * (double)ml[at * 2 + 1];
     }
     wt[h][kPfMaxSplit] = den;
   }
@@ -728,7 +732,8 @@ __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) 
   for (int i = threadIdx.x; i < a.q_sz; i += kNT) {
     const int h = i / hdim;
     double num = 0.0;
-    for (int c = 0; c < nchunks; ++c) num += wt[h][c] * a.part[((size_t)c * a.n + row) * a.q_sz + i];
+    for (int c = 0; c < nchunks; ++c)
+      num += wt[h][c] * (double)part[((size_t)c * a.n + row) * a.q_sz + i];
     a.xo[(size_t)row * a.q_sz + i] = (float)(num / wt[h][kPfMaxSplit]);
   }
 }
@@ -848,7 +853,12 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
       default: return hipErrorInvalidValue;
     }
   }
-  if (b.nsplit > 1) pf_attn_merge_kernel<<<a.n, kNT, 0, stream>>>(b, hdim);
+  if (b.nsplit > 1) {
+    if (f32)
+      pf_attn_merge_kernel<float><<<a.n, kNT, 0, stream>>>(b, hdim);
+    else
+      pf_attn_merge_kernel<double><<<a.n, kNT, 0, stream>>>(b, hdim);
+  }
   return hipGetLastError();
 }
 
