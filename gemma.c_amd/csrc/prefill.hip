@@ -437,7 +437,7 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   constexpr int VS = kPaKeys + 4;         // V^T row in LDS (floats)
   constexpr int C4 = HD / 4;              // float4 per key row
   constexpr int PF = kPaKeys * C4 / kNT;  // float4 of K (and of V) per thread
-  static_assert(PF * kNT == kPaKeys * C4, "tile staging");
+  static_assert(PF * kNT == kPaKeys * C4 && PF % 4 == 0 && kPaKeys == 32, "tile staging");
   __shared__ float kt[kPaKeys * RK];
   __shared__ float vt[HD * VS];
 
@@ -463,30 +463,55 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   const float *kc = a.kc + (size_t)L.hk * a.clen * HD;
   const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
 
-  v4f kx[PF], vx[PF];
+  // K: float4 j of the tile is row i / C4, dims 4 (i % C4) .. +3 (i = tid +
+  // j kNT).  V goes to LDS transposed, in blocks of 4 keys x 4 dims: thread
+  // block (tq, c4) = (b % 8, b / 8) loads keys 4 tq .. 4 tq + 3 of dims
+  // 4 c4 .. 4 c4 + 3 (every load instruction reads whole 128-byte rows) and
+  // writes them as 4 float4 of V^T; eight consecutive lanes differ in tq, so
+  // with the V^T row pitch VS = kPaKeys + 4 their 16-byte writes fall in
+  // eight different bank groups.
+  constexpr int PB = PF / 4;  // V blocks per thread
+  v4f kx[PF], vx[PB][4];
   auto fetch = [&](int t0) {  // rows clamped to the chunk's last key: loads are unconditional
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int i = tid + j * kNT;
       const int t = i / C4, c4 = i - t * C4;
-      const size_t at = (size_t)min(t0 + t, L.k_end) * HD + 4 * c4;
-      kx[j] = *reinterpret_cast<const v4f *>(kc + at);
-      vx[j] = *reinterpret_cast<const v4f *>(vc + at);
+      kx[j] = *reinterpret_cast<const v4f *>(kc + (size_t)min(t0 + t, L.k_end) * HD + 4 * c4);
+    }
+#pragma unroll
+    for (int j = 0; j < PB; ++j) {
+      const int b = tid + j * kNT;
+      const int tq = b % 8, c4 = b / 8;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        vx[j][u] = *reinterpret_cast<const v4f *>(
+            vc + (size_t)min(t0 + 4 * tq + u, L.k_end) * HD + 4 * c4);
     }
   };
   fetch(L.k_lo);
   for (int t0 = L.k_lo; t0 <= L.k_end; t0 += kPaKeys) {
     lds_barrier();  // every wave is done with the previous tile
+    // keys past the chunk's last (another chunk's, or not in the cache yet)
+    // are staged as zeros
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int i = tid + j * kNT;
       const int t = i / C4, c4 = i - t * C4;
-      const bool ok = t0 + t <= L.k_end;  // later keys: another chunk's, or not in the cache yet
-      const v4f zero = {0.f, 0.f, 0.f, 0.f};
-      *reinterpret_cast<v4f *>(&kt[t * RK + 4 * c4]) = ok ? kx[j] : zero;
-      const v4f vv = ok ? vx[j] : zero;
+      *reinterpret_cast<v4f *>(&kt[t * RK + 4 * c4]) = t0 + t <= L.k_end ? kx[j] : zero;
+    }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + t] = vv[e];
+    for (int j = 0; j < PB; ++j) {
+      const int b = tid + j * kNT;
+      const int tq = b % 8, c4 = b / 8;
+      v4f r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = t0 + 4 * tq + u <= L.k_end ? vx[j][u] : zero;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<v4f *>(&vt[(4 * c4 + e) * VS + 4 * tq]) =
+            v4f{r[0][e], r[1][e], r[2][e], r[3][e]};
     }
     lds_barrier();
     if (t0 + kPaKeys <= L.k_end) fetch(t0 + kPaKeys);
