@@ -398,33 +398,60 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_f32_kernel(VisAttn 
   for (int i = tid; i < 2 * C4; i += NT)
     kvb[i / C4][i % C4] = reinterpret_cast<const v4f *>(i < C4 ? bk : bv)[i % C4];
 
-  v4f kx[PF], vx[PF];
+  // K: float4 i of the tile is key i / C4, dims 4 (i % C4) .. +3.  V goes
+  // to LDS transposed in blocks of 4 keys x 4 dims: block b = (tq, c4) =
+  // (b % 8, b / 8) holds keys 4 tq .. 4 tq + 3 of dims 4 c4 .. 4 c4 + 3 and
+  // is written as 4 float4 of V^T; eight consecutive lanes differ in tq, so
+  // with the row pitch VS = TK + 4 their 16-byte writes fall in eight
+  // different bank groups (scattering single floats instead put a
+  // half-wave's writes on two banks).
+  static_assert(TK % 4 == 0 && TK / 4 == 8, "V blocks: 8 key quads per tile");
+  constexpr int VB = 8 * C4;               // V blocks per tile
+  constexpr int PV = (VB + NT - 1) / NT;   // V blocks per thread
+  v4f kx[PF], vx[PV][4];
   auto fetch = [&](int t0) {  // rows clamped into range: every load is unconditional
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int i = min(tid + j * NT, TK * C4 - 1);
       const int t = i / C4, c4 = i - t * C4;
-      const size_t row = (size_t)min(t0 + t, a.n - 1) * a.stride;
-      kx[j] = *reinterpret_cast<const v4f *>(kbase + row + 4 * c4);
-      vx[j] = *reinterpret_cast<const v4f *>(vbase + row + 4 * c4);
+      kx[j] = *reinterpret_cast<const v4f *>(kbase + (size_t)min(t0 + t, a.n - 1) * a.stride +
+                                             4 * c4);
+    }
+#pragma unroll
+    for (int j = 0; j < PV; ++j) {
+      const int b = min(tid + j * NT, VB - 1);
+      const int tq = b % 8, c4 = b / 8;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        vx[j][u] = *reinterpret_cast<const v4f *>(
+            vbase + (size_t)min(t0 + 4 * tq + u, a.n - 1) * a.stride + 4 * c4);
     }
   };
   fetch(0);
   for (int t0 = 0; t0 < a.n; t0 += TK) {
     lds_barrier();  // every wave is done with the previous tile
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < PF; ++j) {
       const int i = tid + j * NT;
       if (i >= TK * C4) break;
       const int t = i / C4, c4 = i - t * C4;
-      const bool ok = t0 + t < a.n;
-      const v4f zero = {0.f, 0.f, 0.f, 0.f};
-      const v4f kv = ok ? kx[j] + kvb[0][c4] : zero;
-      const v4f vv = ok ? vx[j] + kvb[1][c4] : zero;
+      const v4f kv = t0 + t < a.n ? kx[j] + kvb[0][c4] : zero;
       *reinterpret_cast<v2f *>(&kt[t * RK + 4 * c4]) = v2f{kv[0], kv[1]};
       *reinterpret_cast<v2f *>(&kt[t * RK + 4 * c4 + 2]) = v2f{kv[2], kv[3]};
+    }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vt[(4 * c4 + e) * VS + t] = vv[e];
+    for (int j = 0; j < PV; ++j) {
+      const int b = tid + j * NT;
+      if (b >= VB) break;
+      const int tq = b % 8, c4 = b / 8;
+      v4f r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = t0 + 4 * tq + u < a.n ? vx[j][u] + kvb[1][c4] : zero;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        *reinterpret_cast<v4f *>(&vt[(4 * c4 + e) * VS + 4 * tq]) =
+            v4f{r[0][e], r[1][e], r[2][e], r[3][e]};
     }
     lds_barrier();
     if (t0 + TK < a.n) fetch(t0 + TK);
