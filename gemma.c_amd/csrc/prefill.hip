@@ -429,16 +429,21 @@ __device__ __forceinline__ void pa_softmax_f32(const PfAttn &a, const PaLane &L,
     }
 }
 
-template <int HD>
+template <int HD, int TK>
 __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   constexpr int KS = HD / 4;              // score MFMA steps (dims per lane)
   constexpr int NB = HD / 16;             // 16-dim output blocks
+  constexpr int NS = TK / 16;             // 16-key score blocks per tile
   constexpr int RK = HD + 4;              // K row in LDS (floats)
-  constexpr int VS = kPaKeys + 4;         // V^T row in LDS (floats)
+  constexpr int VS = TK + 4;              // V^T row in LDS (floats)
   constexpr int C4 = HD / 4;              // float4 per key row
-  constexpr int PF = kPaKeys * C4 / kNT;  // float4 of K (and of V) per thread
-  static_assert(PF * kNT == kPaKeys * C4 && PF % 4 == 0 && kPaKeys == 32, "tile staging");
-  __shared__ float kt[kPaKeys * RK];
+  constexpr int PF = TK * C4 / kNT;       // float4 of K per thread
+  constexpr int KQ = TK / 4;              // key quads per tile
+  constexpr int VB = KQ * C4;             // V blocks (4 keys x 4 dims) per tile
+  constexpr int PB = (VB + kNT - 1) / kNT;  // V blocks per thread
+  static_assert(PF * kNT == TK * C4 && (TK == 16 || TK == 32) && kPaKeys % TK == 0,
+                "tile staging");
+  __shared__ float kt[TK * RK];
   __shared__ float vt[HD * VS];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -464,13 +469,14 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
 
   // K: float4 j of the tile is row i / C4, dims 4 (i % C4) .. +3 (i = tid +
-  // j kNT).  V goes to LDS transposed, in blocks of 4 keys x 4 dims: thread
-  // block (tq, c4) = (b % 8, b / 8) loads keys 4 tq .. 4 tq + 3 of dims
-  // 4 c4 .. 4 c4 + 3 (every load instruction reads whole 128-byte rows) and
-  // writes them as 4 float4 of V^T; eight consecutive lanes differ in tq, so
-  // with the V^T row pitch VS = kPaKeys + 4 their 16-byte writes fall in
-  // eight different bank groups.
-  constexpr int PB = PF / 4;  // V blocks per thread
+  // j kNT).  V goes to LDS transposed, in blocks of 4 keys x 4 dims: block
+  // b = (tq, c4) = (b % KQ, b / KQ) holds keys 4 tq .. 4 tq + 3 of dims
+  // 4 c4 .. 4 c4 + 3 (every load instruction reads whole 128-byte row
+  // pieces) and is written as 4 float4 of V^T; with the row pitch VS = TK + 4
+  // the 16-byte writes of eight consecutive lanes fall in eight different
+  // bank groups.  The next tile waits in registers (kx, vx) while the
+  // current one is computed: 16-key tiles at head dim 256 keep that within
+  // the register budget (32-key ones spilled it).
   v4f kx[PF], vx[PB][4];
   auto fetch = [&](int t0) {  // rows clamped to the chunk's last key: loads are unconditional
 #pragma unroll
@@ -481,8 +487,8 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
     }
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
-      const int b = tid + j * kNT;
-      const int tq = b % 8, c4 = b / 8;
+      const int b = min(tid + j * kNT, VB - 1);
+      const int tq = b % KQ, c4 = b / KQ;
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         vx[j][u] = *reinterpret_cast<const v4f *>(
@@ -490,7 +496,7 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
     }
   };
   fetch(L.k_lo);
-  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += kPaKeys) {
+  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += TK) {
     lds_barrier();  // every wave is done with the previous tile
     // keys past the chunk's last (another chunk's, or not in the cache yet)
     // are staged as zeros
@@ -504,7 +510,8 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
 #pragma unroll
     for (int j = 0; j < PB; ++j) {
       const int b = tid + j * kNT;
-      const int tq = b % 8, c4 = b / 8;
+      if (b >= VB) break;
+      const int tq = b % KQ, c4 = b / KQ;
       v4f r[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) r[u] = t0 + 4 * tq + u <= L.k_end ? vx[j][u] : zero;
@@ -514,33 +521,46 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
             v4f{r[0][e], r[1][e], r[2][e], r[3][e]};
     }
     lds_barrier();
-    if (t0 + kPaKeys <= L.k_end) fetch(t0 + kPaKeys);
+    if (t0 + TK <= L.k_end) fetch(t0 + TK);
 
-    if (t0 > L.w_hi || t0 + kPaKeys - 1 < L.w_lo) continue;  // wave-uniform
-    // scores of both 16-key blocks, two independent MFMA chains
-    v4f sc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
+    if (t0 > L.w_hi || t0 + TK - 1 < L.w_lo) continue;  // wave-uniform
+    // scores, two independent MFMA chains: the two 16-key blocks, or (one
+    // block) alternate dims of the one block
+    v4f sc[NS];
+    if constexpr (NS == 2) {
+      sc[0] = sc[1] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS; s += 4) {
-      const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
-      const v4f k1 = *reinterpret_cast<const v4f *>(&kt[(16 + col) * RK + grp * KS + s]);
+      for (int s = 0; s < KS; s += 4) {
+        const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
+        const v4f k1 = *reinterpret_cast<const v4f *>(&kt[(16 + col) * RK + grp * KS + s]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[e], qa[s + e], sc[0], 0, 0, 0);
-        sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[e], qa[s + e], sc[1], 0, 0, 0);
+        for (int e = 0; e < 4; ++e) {
+          sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[e], qa[s + e], sc[0], 0, 0, 0);
+          sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[e], qa[s + e], sc[1], 0, 0, 0);
+        }
       }
+    } else {
+      v4f s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; s += 4) {
+        const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[0], qa[s], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[1], qa[s + 1], s1, 0, 0, 0);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[2], qa[s + 2], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[3], qa[s + 3], s1, 0, 0, 0);
+      }
+      sc[0] = s0 + s1;
     }
-    pa_softmax_f32<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o);
+    pa_softmax_f32<NB, NS>(a, L, sc, t0, grp, m_ref, l_part, o);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const v4f v0 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 4 * grp]);
-      const v4f v1 = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 16 + 4 * grp]);
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[r], sc[0][r], o[nb], 0, 0, 0);
+      for (int b = 0; b < NS; ++b) {
+        const v4f v = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 16 * b + 4 * grp]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v1[r], sc[1][r], o[nb], 0, 0, 0);
-    }
+        for (int r = 0; r < 4; ++r)
+          o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[r], sc[b][r], o[nb], 0, 0, 0);
+      }
   }
   // outputs: lane (col, grp) holds dims 16 nb + 4 grp + r of its query
   float l = l_part + __shfl_xor(l_part, 16, 64);
@@ -866,8 +886,8 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
   const dim3 grid(nrb * b.nsplit * a.nkv);
   if (f32) {
     switch (hdim) {
-      case 128: pf_attn_f32_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
-      case 256: pf_attn_f32_kernel<256><<<grid, kNT, 0, stream>>>(b); break;
+      case 128: pf_attn_f32_kernel<128, 32><<<grid, kNT, 0, stream>>>(b); break;
+      case 256: pf_attn_f32_kernel<256, 16><<<grid, kNT, 0, stream>>>(b); break;
       default: return hipErrorInvalidValue;
     }
   } else {
