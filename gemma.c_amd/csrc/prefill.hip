@@ -429,22 +429,44 @@ __device__ __forceinline__ void pa_softmax_f32(const PfAttn &a, const PaLane &L,
     }
 }
 
-template <int HD, int TK>
+// One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
+// wave-uniform).  Issued from inline asm so that the compiler does not treat
+// every later LDS read as a possible alias of the pending load (it would
+// wait for the load before each of them); the kernel waits itself (vmcnt(0)
+// and a barrier) before it reads the buffer.  m0 has no other user in the
+// kernel that calls this.
+__device__ __forceinline__ void lds_dma16(const float *g, float *lds) {
+  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)lds;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// K and V tiles of 16 keys go from the cache straight into a two-slot LDS
+// ring by DMA (no registers held, one barrier per tile), each row of HD
+// floats as HD/4 16-byte chunks with chunk c of tile row t at position
+// c ^ (t & 7): the K reads (16 lanes = 16 rows, one chunk) then hit 8
+// different bank groups per 8 lanes.  Scores: lane (key col, group g)
+// feeds K[col][g KS + s + e] against qa[s + e], two MFMA chains over
+// alternate dims.  Values: V stays in key-major order; one 16-byte read of
+// V[4 g + r][64 q + 4 col .. + 3] feeds four MFMAs, one for each of the
+// output blocks 4 q + e, whose row col is dim 64 q + 4 col + e.  The lane
+// (query col, g) then holds dims 64 q + 16 g + 4 r + e in o[4 q + e][r].
+template <int HD>
 __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
-  constexpr int KS = HD / 4;              // score MFMA steps (dims per lane)
-  constexpr int NB = HD / 16;             // 16-dim output blocks
-  constexpr int NS = TK / 16;             // 16-key score blocks per tile
-  constexpr int RK = HD + 4;              // K row in LDS (floats)
-  constexpr int VS = TK + 4;              // V^T row in LDS (floats)
-  constexpr int C4 = HD / 4;              // float4 per key row
-  constexpr int PF = TK * C4 / kNT;       // float4 of K per thread
-  constexpr int KQ = TK / 4;              // key quads per tile
-  constexpr int VB = KQ * C4;             // V blocks (4 keys x 4 dims) per tile
-  constexpr int PB = (VB + kNT - 1) / kNT;  // V blocks per thread
-  static_assert(PF * kNT == TK * C4 && (TK == 16 || TK == 32) && kPaKeys % TK == 0,
+  constexpr int TK = 16;                   // keys per tile
+  constexpr int KS = HD / 4;               // score MFMA steps (dims per lane)
+  constexpr int NB = HD / 16;              // 16-dim output blocks
+  constexpr int CR = HD / 4;               // 16-byte chunks per key row
+  constexpr int TC = TK * CR;              // chunks per K (or V) tile
+  constexpr int NI = 2 * TC / 64;          // DMA instructions per tile (K, then V)
+  constexpr int NIW = NI / kWaves;         // per wave
+  constexpr int RPI = 64 / CR;             // tile rows per DMA instruction
+  static_assert(HD % 64 == 0 && CR >= 8 && NIW * kWaves == NI && kPaKeys % TK == 0,
                 "tile staging");
-  __shared__ float kt[TK * RK];
-  __shared__ float vt[HD * VS];
+  __shared__ v4f ring[2][2][TC];           // [slot][K, V][chunk]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -468,109 +490,73 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   const float *kc = a.kc + (size_t)L.hk * a.clen * HD;
   const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
 
-  // K: float4 j of the tile is row i / C4, dims 4 (i % C4) .. +3 (i = tid +
-  // j kNT).  V goes to LDS transposed, in blocks of 4 keys x 4 dims: block
-  // b = (tq, c4) = (b % KQ, b / KQ) holds keys 4 tq .. 4 tq + 3 of dims
-  // 4 c4 .. 4 c4 + 3 (every load instruction reads whole 128-byte row
-  // pieces) and is written as 4 float4 of V^T; with the row pitch VS = TK + 4
-  // the 16-byte writes of eight consecutive lanes fall in eight different
-  // bank groups.  The next tile waits in registers (kx, vx) while the
-  // current one is computed: 16-key tiles at head dim 256 keep that within
-  // the register budget (32-key ones spilled it).
-  v4f kx[PF], vx[PB][4];
-  auto fetch = [&](int t0) {  // rows clamped to the chunk's last key: loads are unconditional
+  // this lane's share of each of the wave's DMA instructions: tile row and
+  // the source chunk that lands at the lane's position (rows past the
+  // chunk's last key repeat it: their weights are exactly 0)
+  int trow[NIW], tsrc[NIW];
 #pragma unroll
-    for (int j = 0; j < PF; ++j) {
-      const int i = tid + j * kNT;
-      const int t = i / C4, c4 = i - t * C4;
-      kx[j] = *reinterpret_cast<const v4f *>(kc + (size_t)min(t0 + t, L.k_end) * HD + 4 * c4);
-    }
+  for (int j = 0; j < NIW; ++j) {
+    const int ri = (wave * NIW + j) % (NI / 2);
+    const int t = ri * RPI + lane / CR, pos = lane % CR;
+    trow[j] = t;
+    tsrc[j] = 4 * (pos ^ (t & 7));
+  }
+  auto issue = [&](int t0, int slot) {
 #pragma unroll
-    for (int j = 0; j < PB; ++j) {
-      const int b = min(tid + j * kNT, VB - 1);
-      const int tq = b % KQ, c4 = b / KQ;
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        vx[j][u] = *reinterpret_cast<const v4f *>(
-            vc + (size_t)min(t0 + 4 * tq + u, L.k_end) * HD + 4 * c4);
+    for (int j = 0; j < NIW; ++j) {
+      const int i = wave * NIW + j;  // wave-uniform
+      const int kv = i / (NI / 2), ri = i % (NI / 2);
+      const size_t at = (size_t)min(t0 + trow[j], L.k_end) * HD + tsrc[j];
+      lds_dma16((kv == 0 ? kc : vc) + at,
+                reinterpret_cast<float *>(&ring[slot][kv][ri * 64]));
     }
   };
-  fetch(L.k_lo);
-  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += TK) {
-    lds_barrier();  // every wave is done with the previous tile
-    // keys past the chunk's last (another chunk's, or not in the cache yet)
-    // are staged as zeros
-    const v4f zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < PF; ++j) {
-      const int i = tid + j * kNT;
-      const int t = i / C4, c4 = i - t * C4;
-      *reinterpret_cast<v4f *>(&kt[t * RK + 4 * c4]) = t0 + t <= L.k_end ? kx[j] : zero;
-    }
-#pragma unroll
-    for (int j = 0; j < PB; ++j) {
-      const int b = tid + j * kNT;
-      if (b >= VB) break;
-      const int tq = b % KQ, c4 = b / KQ;
-      v4f r[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) r[u] = t0 + 4 * tq + u <= L.k_end ? vx[j][u] : zero;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        *reinterpret_cast<v4f *>(&vt[(4 * c4 + e) * VS + 4 * tq]) =
-            v4f{r[0][e], r[1][e], r[2][e], r[3][e]};
-    }
-    lds_barrier();
-    if (t0 + TK <= L.k_end) fetch(t0 + TK);
+  issue(L.k_lo, 0);
+  int slot = 0;
+  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += TK, slot ^= 1) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's part of the tile has landed
+    lds_barrier();  // every wave's part has landed, and every wave is done with the other slot
+    if (t0 + TK <= L.k_end) issue(t0 + TK, slot ^ 1);
 
     if (t0 > L.w_hi || t0 + TK - 1 < L.w_lo) continue;  // wave-uniform
-    // scores, two independent MFMA chains: the two 16-key blocks, or (one
-    // block) alternate dims of the one block
-    v4f sc[NS];
-    if constexpr (NS == 2) {
-      sc[0] = sc[1] = v4f{0.f, 0.f, 0.f, 0.f};
+    const v4f *kt = ring[slot][0];
+    const v4f *vt = ring[slot][1];
+    v4f s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KS; s += 4) {
-        const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
-        const v4f k1 = *reinterpret_cast<const v4f *>(&kt[(16 + col) * RK + grp * KS + s]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          sc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[e], qa[s + e], sc[0], 0, 0, 0);
-          sc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(k1[e], qa[s + e], sc[1], 0, 0, 0);
-        }
-      }
-    } else {
-      v4f s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; s += 4) {
-        const v4f k0 = *reinterpret_cast<const v4f *>(&kt[col * RK + grp * KS + s]);
-        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[0], qa[s], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[1], qa[s + 1], s1, 0, 0, 0);
-        s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[2], qa[s + 2], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k0[3], qa[s + 3], s1, 0, 0, 0);
-      }
-      sc[0] = s0 + s1;
+    for (int s = 0; s < KS; s += 4) {
+      const v4f k4 = kt[col * CR + (((grp * KS + s) >> 2) ^ (col & 7))];
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[0], qa[s], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[1], qa[s + 1], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[2], qa[s + 2], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k4[3], qa[s + 3], s1, 0, 0, 0);
     }
-    pa_softmax_f32<NB, NS>(a, L, sc, t0, grp, m_ref, l_part, o);
+    v4f sc[1] = {s0 + s1};
+    pa_softmax_f32<NB, 1>(a, L, sc, t0, grp, m_ref, l_part, o);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int q = 0; q < NB / 4; ++q)
 #pragma unroll
-      for (int b = 0; b < NS; ++b) {
-        const v4f v = *reinterpret_cast<const v4f *>(&vt[(16 * nb + col) * VS + 16 * b + 4 * grp]);
+      for (int r = 0; r < 4; ++r) {
+        const int t = 4 * grp + r;
+        const v4f v4 = vt[t * CR + ((16 * q + col) ^ (t & 7))];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          o[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[r], sc[b][r], o[nb], 0, 0, 0);
+        for (int e = 0; e < 4; ++e)
+          o[4 * q + e] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4[e], sc[0][r], o[4 * q + e], 0, 0, 0);
       }
   }
-  // outputs: lane (col, grp) holds dims 16 nb + 4 grp + r of its query
   float l = l_part + __shfl_xor(l_part, 16, 64);
   l = l + __shfl_xor(l, 32, 64);
   if (!L.valid) return;
+  // dims 64 q + 16 grp + 4 r .. + 3 are o[4 q .. 4 q + 3][r]
+  auto out4 = [&](int q, int r) {
+    return v4f{o[4 * q][r], o[4 * q + 1][r], o[4 * q + 2][r], o[4 * q + 3][r]};
+  };
   if (L.nchunks == 1) {
     float *orow = a.xo + (size_t)L.row * a.q_sz + L.head * HD;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      *reinterpret_cast<v4f *>(orow + 16 * nb + 4 * grp) = o[nb] / l;
+    for (int q = 0; q < NB / 4; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *reinterpret_cast<v4f *>(orow + 64 * q + 16 * grp + 4 * r) = out4(q, r) / l;
     return;
   }
   // fp32 partials (the fp64 kernels' layout in floats: half the bytes; the
@@ -579,27 +565,15 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   const size_t at = (size_t)L.chunk_id * a.n + L.row;
   float *prow = pf + at * a.q_sz + L.head * HD;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) *reinterpret_cast<v4f *>(prow + 16 * nb + 4 * grp) = o[nb];
+  for (int q = 0; q < NB / 4; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<v4f *>(prow + 64 * q + 16 * grp + 4 * r) = out4(q, r);
   if (grp == 0) {
     float *ml = pf + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
     ml[0] = m_ref;
     ml[1] = l;
   }
-}
-
-// One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
-// wave-uniform).  Issued from inline asm so that the compiler does not treat
-// every later LDS read as a possible alias of the pending load (it would
-// wait for the load before each of them); the kernel waits itself (vmcnt(0)
-// and a barrier) before it reads the buffer.  m0 has no other user in the
-// kernel that calls this.
-__device__ __forceinline__ void lds_dma16(const float *g, float *lds) {
-  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float *)lds;
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g)
-               : "memory", "m0");
-#pragma clang diagnostic pop
 }
 
 // HD 256 on wave pairs.  A whole head dim per wave needs 64 fp64 output
@@ -886,8 +860,8 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
   const dim3 grid(nrb * b.nsplit * a.nkv);
   if (f32) {
     switch (hdim) {
-      case 128: pf_attn_f32_kernel<128, 32><<<grid, kNT, 0, stream>>>(b); break;
-      case 256: pf_attn_f32_kernel<256, 16><<<grid, kNT, 0, stream>>>(b); break;
+      case 128: pf_attn_f32_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
+      case 256: pf_attn_f32_kernel<256><<<grid, kNT, 0, stream>>>(b); break;
       default: return hipErrorInvalidValue;
     }
   } else {
