@@ -285,6 +285,59 @@ def test_prefill_rows_dense_matches_oracle(gh, oracle, gqa_model, n, pos0):
     print(f"dense rows {n} at {pos0}: worst |d|/max|logit| = {worst:.3g}", flush=True)
 
 
+# The dense rows with the prompt pass's attention on the fp32 matrix cores
+# (GEMMA_HIP_ATTN_F32: the fp32 kernel's bidirectional form, head dims 256
+# and 128).  Where no int8 requantization flips, the logits agree with the
+# fp64 oracle to fp32 rounding (the flip-free cases measured 0: the last
+# row's logits come out bit-identical); the cases measured with a flip (the
+# 256 rows at gemma-3-270m widths, 1.2% of the largest logit, and the
+# multi-row ones at gemma-3-4b widths, 1.7% and 1.8%: in the dense form every
+# row's flips reach the last row through its keys and values in the next
+# layer) are held to the flip level and the argmax, as the causal fp32 cases
+# of test_decoder.py.
+F32_PRE_FLIP = 1e-6
+F32_FLIP_LEVEL = 5e-2
+F32_DENSE_CASES = [  # model, rows, first position, measured with a flip
+    ("two", 77, 30, False), ("two", 256, 1, True), ("hd128", 77, 30, False),
+    ("hd128", 200, 3, False), ("gqa", 1, 5, False), ("gqa", 77, 30, True),
+    ("gqa", 256, 1, True)]
+
+
+@pytest.fixture(scope="module")
+def hd128_model(tmp_path_factory):
+    d = tmp_path_factory.mktemp("hd128")
+    return model_bin.read_bin(model_bin.write_bin(str(d / "hd128.bin"), "test-hd128", seed=7,
+                                                  nvocab=512, layers=2, slide=16, flags=7,
+                                                  norm_std=0.1))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("key,n,pos0,flip", F32_DENSE_CASES)
+def test_prefill_rows_dense_f32_attention(gh, oracle, text_models, hd128_model, gqa_model, key,
+                                          n, pos0, flip):
+    model = {"two": text_models.get("two"), "hd128": hd128_model, "gqa": gqa_model}[key]
+    nv, dim = model["config"]["nvocab"], model["config"]["dim"]
+    rng = np.random.default_rng(n)
+    rows = (rng.standard_normal((n, dim)) * 0.5).astype(np.float32)
+    prefix = rng.integers(0, nv, pos0).astype(np.int32)
+    clen = pos0 + n + 4
+    dec = gh.decoder(model, clen)
+    try:
+        dec.set_attention(dec.ATTN_F32)
+        ref = dorc.DecodeOracle(model, oracle, clen)
+        ref.prefill(prefix, 0)
+        want = ref.prefill(None, pos0, rows=rows, mask=False)
+        lg = np.empty(nv, np.float32)
+        dec.prefill(prefix, 0)
+        nxt = dec.prefill_rows(rows, pos0, False, lg)
+    finally:
+        dec.close()
+    rel = float(np.abs(lg - want).max() / np.abs(want).max())
+    print(f"dense rows {key} {n} at {pos0}, fp32 attention: {rel:.3g}", flush=True)
+    assert rel <= (F32_FLIP_LEVEL if flip else F32_PRE_FLIP)
+    assert nxt == int(np.argmax(want))
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape", sorted(VISION))
 def test_gemma_image_matches_oracle(gh, oracle, tmp_path, shape):
