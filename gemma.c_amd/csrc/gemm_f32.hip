@@ -3,12 +3,14 @@
 //
 //   dst[i][j] = sum_l src[i][l]*mat[j][l]
 //
-// Same tiling as the int8 GEMM: 256 threads, 2x2 waves, 128x128 block tile,
-// a K step of 16 floats (64 bytes per row) double-buffered in LDS.  A lane
+// 256 threads, 2x2 waves, 128x128 or 64x64 block tiles, a K step of 16
+// floats (64 bytes per row) double-buffered in LDS.  A lane
 // owns 8 consecutive k of each step (lane / 32 picks the half) for A and B
 // alike, so each of the 8 MFMA sub-steps pairs matching k.  The reference's
 // fp32 sum has no fixed order (vectorised, KC-chunked, gemma.c:3287-3299), so
 // parity for this path is a tolerance on |y - y_exact| / sum|a*b|.
+#include <cstdlib>
+
 #include "gh_arith.h"
 #include "gh_kernels.h"
 
@@ -16,15 +18,17 @@ namespace gh {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBM = 128;
-constexpr int kBN = 128;
 constexpr int kBK = 16;                   // floats of K per step
 constexpr int kRowChunks = kBK / 4 + 1;   // float4 chunks per LDS row (+1 pad)
 
+// WM x WN: each wave's sub-tile in 32x32 MFMA tiles; the 2x2 waves make a
+// (64 WM) x (64 WN) block tile.
+template <int WM, int WN>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
     const float *__restrict__ src, int sstr, int m, int n, int k,
     const float *__restrict__ bias, bool clamp) {
+  constexpr int kBM = 64 * WM, kBN = 64 * WN;
   __shared__ v4f lds_a[2][kBM][kRowChunks];
   __shared__ v4f lds_b[2][kBN][kRowChunks];
 
@@ -38,17 +42,19 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
   const int ld_row = tid >> 2;
   const int ld_chunk = tid & 3;
 
-  v4f ra[2], rb[2];
+  v4f ra[WM], rb[WN];
   auto load_tiles = [&](int kt) {
     const int kb = kt * kBK + ld_chunk * 4;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = ld_row + 64 * h;
-      const int gm = m0 + r;
-      const int gn = n0 + r;
+    for (int h = 0; h < WM; ++h) {
+      const int gm = m0 + ld_row + 64 * h;
       ra[h] = (gm < m && kb < k)
                   ? *reinterpret_cast<const v4f *>(src + (size_t)gm * sstr + kb)
                   : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int h = 0; h < WN; ++h) {
+      const int gn = n0 + ld_row + 64 * h;
       rb[h] = (gn < n && kb < k)
                   ? *reinterpret_cast<const v4f *>(mat + (size_t)gn * mstr + kb)
                   : v4f{0.f, 0.f, 0.f, 0.f};
@@ -56,17 +62,16 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
   };
   auto store_tiles = [&](int buf) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      lds_a[buf][ld_row + 64 * h][ld_chunk] = ra[h];
-      lds_b[buf][ld_row + 64 * h][ld_chunk] = rb[h];
-    }
+    for (int h = 0; h < WM; ++h) lds_a[buf][ld_row + 64 * h][ld_chunk] = ra[h];
+#pragma unroll
+    for (int h = 0; h < WN; ++h) lds_b[buf][ld_row + 64 * h][ld_chunk] = rb[h];
   };
 
-  v16f acc[2][2];
+  v16f acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+    for (int j = 0; j < WN; ++j) acc[i][j] = v16f{};
 
   const int nk = (k + kBK - 1) / kBK;
   load_tiles(0);
@@ -78,20 +83,23 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < nk) load_tiles(kt + 1);
-    v4f a[2][2], b[2][2];
+    v4f a[WM][2], b[WN][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      a[i][0] = lds_a[cur][wm * 64 + i * 32 + frag_row][half * 2];
-      a[i][1] = lds_a[cur][wm * 64 + i * 32 + frag_row][half * 2 + 1];
-      b[i][0] = lds_b[cur][wn * 64 + i * 32 + frag_row][half * 2];
-      b[i][1] = lds_b[cur][wn * 64 + i * 32 + frag_row][half * 2 + 1];
+    for (int i = 0; i < WM; ++i) {
+      a[i][0] = lds_a[cur][wm * 32 * WM + i * 32 + frag_row][half * 2];
+      a[i][1] = lds_a[cur][wm * 32 * WM + i * 32 + frag_row][half * 2 + 1];
+    }
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      b[j][0] = lds_b[cur][wn * 32 * WN + j * 32 + frag_row][half * 2];
+      b[j][1] = lds_b[cur][wn * 32 * WN + j * 32 + frag_row][half * 2 + 1];
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < WN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
               a[i][s >> 2][s & 3], b[j][s >> 2][s & 3], acc[i][j], 0, 0, 0);
     if (kt + 1 < nk) store_tiles(cur ^ 1);
@@ -99,16 +107,16 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
   }
 
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+  for (int j = 0; j < WN; ++j) {
+    const int col = n0 + wn * 32 * WN + j * 32 + (lane & 31);
     if (col >= n) continue;
     const float b = bias != nullptr ? bias[col] : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row =
-            m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            m0 + wm * 32 * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         float y = bias != nullptr ? acc[i][j][r] + b : acc[i][j][r];
         if (clamp) y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y));
         if (row < m) dst[(size_t)row * dstr + col] = y;
@@ -135,17 +143,31 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
 
 }  // namespace
 
+// Block tile: 128x128 when that gives every CU at least two workgroups,
+// else 64x64 (k/v, o and down at the gemma-3-4b prefill shapes leave most of
+// the GPU idle at 128x128).  GEMMA_HIP_GEMM_F32_TILE=128 or 64 forces one.
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const float *src, int sstr, int m, int n, int k,
                            const float *bias, bool clamp,
                            const DeviceInfo &dev, hipStream_t stream) {
-  (void)dev;
   const bool fast = k % 4 == 0 && mstr % 4 == 0 && sstr % 4 == 0 &&
                     (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
   if (fast) {
-    const dim3 grid((n + kBN - 1) / kBN, (m + kBM - 1) / kBM);
-    gemm_f32_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src,
-                                                   sstr, m, n, k, bias, clamp);
+    static const int forced = [] {
+      const char *e = getenv("GEMMA_HIP_GEMM_F32_TILE");
+      return e != nullptr ? atoi(e) : 0;
+    }();
+    const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+    const bool big = forced == 128 || (forced != 64 && tiles128 >= 2L * dev.cus);
+    if (big) {
+      const dim3 grid((n + 127) / 128, (m + 127) / 128);
+      gemm_f32_kernel<2, 2><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
+                                                          n, k, bias, clamp);
+    } else {
+      const dim3 grid((n + 63) / 64, (m + 63) / 64);
+      gemm_f32_kernel<1, 1><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
+                                                          n, k, bias, clamp);
+    }
   } else {
     const dim3 grid((n + 63) / 64, (m + 3) / 4);
     gemm_f32_generic_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr,

@@ -333,9 +333,12 @@ def test_f32_golden(gh, golden, oracle):
     assert np.all(np.abs(host(d) - g["gemm_dst"]) <= 2 * TOL_F32 * mag)
 
 
+# (2048, 8192, 64) and (1000, 9000, 100) give at least two 128x128 tiles per
+# CU, so they take the 128x128 kernel (the others the 64x64 one), the second
+# with tails in every dimension
 @pytest.mark.parametrize("m,n,k", [(1, 6912, 1152), (1, 1152, 6912), (1, 32768, 2560),
                                    (64, 1152, 588), (300, 640, 2048), (4096, 1152, 588),
-                                   (5, 7, 9)])
+                                   (5, 7, 9), (2048, 8192, 64), (1000, 9000, 100)])
 def test_f32_vs_oracle(gh, oracle, m, n, k):
     note(f"f32 m={m} n={n} k={k}")
     rng = np.random.default_rng(m + n + k)
