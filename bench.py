@@ -412,9 +412,9 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     """The prompt and the greedy decode fully on the GPU: `prompt` random token
     ids go through the batched prefill (gemma_hip_decoder_prefill; the median
     of TIMING_RUNS calls after a warm-up call that allocates its row buffers,
-    with the attention on the fp64 matrix cores, the default, and on the fp32
-    ones), then `steps` decode steps from the KV cache the fp64 prefill filled
-    are timed (one HIP graph launch each, tokens fed back on the device, one
+    with the attention on the fp32 matrix cores, the default, and on the fp64
+    ones, the verification mode), then `steps` decode steps from the KV cache
+    the default prefill filled are timed (one HIP graph launch each, tokens fed back on the device, one
     readback at the end)."""
     import statistics
     import time
@@ -431,7 +431,7 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
         dec.prefill(ids, 0)
         torch.cuda.synchronize()
         t_mode = {}
-        for mode in (dec.ATTN_F32, dec.ATTN_F64):  # the fp64 prefill last: its cache is decoded
+        for mode in (dec.ATTN_F64, dec.ATTN_F32):  # the default last: its cache is decoded
             dec.set_attention(mode)
             ts = []
             for _ in range(TIMING_RUNS):
@@ -439,7 +439,7 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
                 first = dec.prefill(ids, 0)
                 ts.append(time.perf_counter() - t0)
             t_mode[mode] = statistics.median(ts)
-        t_pf, t_pf32 = t_mode[dec.ATTN_F64], t_mode[dec.ATTN_F32]
+        t_pf, t_pf64 = t_mode[dec.ATTN_F32], t_mode[dec.ATTN_F64]
         best = None
         for _ in range(2):
             t0 = time.perf_counter()
@@ -456,7 +456,7 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     prefill = dict(tokens=prompt, ms=round(1e3 * t_pf, 3), tok_s=round(prompt / t_pf, 1),
                    int8_tops=round(pf_ops / t_pf / 1e12, 1),
                    int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4),
-                   ms_attn_f32=round(1e3 * t_pf32, 3), tok_s_attn_f32=round(prompt / t_pf32, 1))
+                   ms_attn_f64=round(1e3 * t_pf64, 3), tok_s_attn_f64=round(prompt / t_pf64, 1))
     per_layer = (gemv_bytes(q_sz + 2 * kv_sz, c["dim"]) + gemv_bytes(c["dim"], q_sz)
                  + gemv_bytes(2 * c["mlp_dim"], c["dim"]) + gemv_bytes(c["dim"], c["mlp_dim"]))
     weights = c["nl"] * per_layer + gemv_bytes(c["nvocab"], c["dim"])
@@ -482,8 +482,8 @@ def bench_vision(torch, gh) -> dict:
     embedding, 27 encoder layers, post norm, pooling to 256 tokens, RMSNorm,
     projection to the gemma-3-4b width), random weights of that shape; the
     median of five timed images after one untimed, with the attention on the
-    fp64 matrix cores (the default, equal to the fp64 oracle) and on the fp32
-    matrix cores (gemma_hip_vision_set_attention)."""
+    fp32 matrix cores (the default) and on the fp64 matrix cores (the
+    verification mode, equal to the fp64 oracle; gemma_hip_vision_set_attention)."""
     import statistics
     import time
 
@@ -511,9 +511,9 @@ def bench_vision(torch, gh) -> dict:
                      + gemm_ops(n, c["dim"], c["mlp_dim"])) \
         + gemm_ops(c["img_tok"], c["text_dim"], c["dim"])
     return dict(model="siglip (27 layers, 896 px, 4096 patches -> 256 tokens)",
-                ms_per_image=round(ms["f64"], 2), images_s=round(1e3 / ms["f64"], 2),
-                ms_per_image_attn_f32=round(ms["f32"], 2),
-                int8_ops=ops, int8_tops_over_tower=round(ops / ms["f64"] / 1e9, 1))
+                ms_per_image=round(ms["f32"], 2), images_s=round(1e3 / ms["f32"], 2),
+                ms_per_image_attn_f64=round(ms["f64"], 2),
+                int8_ops=ops, int8_tops_over_tower=round(ops / ms["f32"] / 1e9, 1))
 
 
 def measured_traffic(kernel: str) -> dict | None:

@@ -1033,7 +1033,7 @@ struct gemma_hip_decoder {
   gemma_hip_text_config cfg{};
   std::vector<unsigned char> swa;
   int clen = 0, max_blocks = 0, nparts = 256;
-  bool attn_f32 = false;  // prefill attention on the fp32 matrix cores
+  bool attn_f32 = true;  // prefill attention on the fp32 matrix cores (false: fp64)
   struct Layer {
     const int8_t *w[7];  // wq wk wv wo w1(up) w2(gate) w3(down), device
     const float *s[7];
@@ -1618,7 +1618,7 @@ const float *gemma_hip_decoder_logits(const gemma_hip_decoder *dec) {
 struct gemma_hip_vision {
   gemma_hip_vision_config cfg{};
   int npatch = 0, ppi = 0, ksize = 0, hdim = 0;
-  bool attn_f32 = false;  // attention on the fp32 matrix cores (gemma_hip_vision_set_attention)
+  bool attn_f32 = true;  // attention on the fp32 matrix cores (gemma_hip_vision_set_attention)
   struct Layer {
     const int8_t *w[6];  // wq wk wv wo w1 w2, device
     const float *s[6];

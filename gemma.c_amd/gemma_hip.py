@@ -83,6 +83,10 @@ class VisionLayer(ctypes.Structure):
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
+
+# attention arithmetic of the prompt passes and the vision tower
+# (GEMMA_HIP_ATTN_*): fp32 matrix cores (the default) or fp64 (verification)
+ATTN_F64, ATTN_F32 = 0, 1
 _SIGS = {
     "gemma_hip_init": (_I, [_I]),
     "gemma_hip_shutdown": (None, []),
@@ -263,15 +267,28 @@ class GemmaHip:
         return self.lib.gemma_hip_device_ptr(_addr(host))
 
     # device-resident decoder -----------------------------------------------
-    def vision(self, vis) -> "Vision":
+    def vision(self, vis, attention=None) -> "Vision":
         """A vision tower over a dict of VisionEncoder weights
-        (model_bin.synth_vision's layout): registers every int8 tensor."""
-        return Vision(self, vis)
+        (model_bin.synth_vision's layout): registers every int8 tensor.
+        `attention` (ATTN_F32 or ATTN_F64) sets the attention's arithmetic;
+        None keeps the library's default (ATTN_F32)."""
+        return _with_mode(Vision(self, vis), attention)
 
-    def decoder(self, model, clen: int) -> "Decoder":
+    def decoder(self, model, clen: int, attention=None) -> "Decoder":
         """A decoder over a model from model_bin.read_bin(): registers every
-        int8 tensor (each as its own range) and builds the step graph."""
-        return Decoder(self, model, clen)
+        int8 tensor (each as its own range) and builds the step graph.
+        `attention` as for vision(), for the prompt passes."""
+        return _with_mode(Decoder(self, model, clen), attention)
+
+
+def _with_mode(obj, attention):
+    if attention is not None:
+        try:
+            obj.set_attention(attention)
+        except Exception:
+            obj.close()
+            raise
+    return obj
 
 
 class Decoder:
@@ -382,11 +399,11 @@ class Decoder:
                                                            out.ctypes.data))
         return out[:n]
 
-    ATTN_F64, ATTN_F32 = 0, 1
+    ATTN_F64, ATTN_F32 = ATTN_F64, ATTN_F32
 
     def set_attention(self, mode: int):
-        """GEMMA_HIP_ATTN_F64 (0, the default) or GEMMA_HIP_ATTN_F32 (1): the
-        prompt passes' attention on the fp64 or the fp32 matrix cores."""
+        """GEMMA_HIP_ATTN_F32 (1, the default) or GEMMA_HIP_ATTN_F64 (0): the
+        prompt passes' attention on the fp32 or the fp64 matrix cores."""
         self.gh._check(self.lib.gemma_hip_decoder_set_attention(self.handle, int(mode)))
 
     def logits_ptr(self) -> int:
@@ -451,11 +468,11 @@ class Vision:
             self.gh.release_weights(arr)
         self._registered = []
 
-    ATTN_F64, ATTN_F32 = 0, 1
+    ATTN_F64, ATTN_F32 = ATTN_F64, ATTN_F32
 
     def set_attention(self, mode: int):
-        """GEMMA_HIP_ATTN_F64 (0, the default) or GEMMA_HIP_ATTN_F32 (1): the
-        attention's arithmetic, fp64 or fp32 matrix cores."""
+        """GEMMA_HIP_ATTN_F32 (1, the default) or GEMMA_HIP_ATTN_F64 (0): the
+        attention's arithmetic, fp32 or fp64 matrix cores."""
         self.gh._check(self.lib.gemma_hip_vision_set_attention(self.handle, int(mode)))
 
     def forward(self, img):

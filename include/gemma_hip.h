@@ -315,12 +315,14 @@ int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n
                                    int mask, float *logits, int *next);
 
 /* The arithmetic of the prompt passes' attention (prefill, prefill_rows,
- * image): GEMMA_HIP_ATTN_F64 (the default; fp64 matrix cores, each output
- * rounded once, equal to the decode oracle) or GEMMA_HIP_ATTN_F32 (fp32
- * matrix cores at twice the rate, fp32 throughout as the reference's
- * gemm_fpx/softmax/gemm_fpx_nn, gemma.c:5198-5255: agrees to fp32 rounding,
- * amplified where a later int8 quantization flips).  The decode step's
- * attention is fp64 either way.  0 or 1 on an unknown mode. */
+ * image), kept until changed: GEMMA_HIP_ATTN_F32 (the default; fp32 matrix
+ * cores, fp32 throughout as the reference's gemm_fpx/softmax/gemm_fpx_nn,
+ * gemma.c:5198-5255, in its own summation order: agrees with the exact
+ * result to fp32 rounding, amplified where a later int8 quantization flips)
+ * or GEMMA_HIP_ATTN_F64 (fp64 matrix cores at half the rate, each output
+ * rounded once from the exact sum: the verification mode, equal to an fp64
+ * evaluation of the same formulas).  The decode step's attention is fp64
+ * either way.  0 or 1 on an unknown mode. */
 #define GEMMA_HIP_ATTN_F64 0
 #define GEMMA_HIP_ATTN_F32 1
 int gemma_hip_decoder_set_attention(gemma_hip_decoder *dec, int mode);
@@ -387,12 +389,13 @@ int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out
 
 /* The arithmetic of the tower's attention (gemma.c:4533-4561; set before
  * forward, kept until changed):
- *   GEMMA_HIP_ATTN_F64 (the default) -- fp64 matrix cores, every output
- *     rounded once: equal to the fp64 vision oracle;
- *   GEMMA_HIP_ATTN_F32 -- fp32 matrix cores at twice the rate, fp32
- *     throughout as the reference computes it (its summation order differs),
- *     so results agree with the fp64 form to fp32 rounding, amplified where a
- *     later int8 quantization flips.
+ *   GEMMA_HIP_ATTN_F32 (the default) -- fp32 matrix cores, fp32 throughout
+ *     as the reference computes it (its summation order differs), so results
+ *     agree with the exact form to fp32 rounding, amplified where a later
+ *     int8 quantization flips;
+ *   GEMMA_HIP_ATTN_F64 -- fp64 matrix cores at half the rate, every output
+ *     rounded once from the exact sum: the verification mode, equal to an
+ *     fp64 evaluation of the same formulas.
  * The rest of the tower is unchanged.  0 or 1 on an unknown mode. */
 int gemma_hip_vision_set_attention(gemma_hip_vision *vis, int mode);
 

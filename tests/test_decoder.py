@@ -13,7 +13,9 @@ of a teacher-forced run, and the argmax must agree.  A loose tolerance would
 not do: with int8 requantization after every norm, a single 1-ulp difference
 that straddles a rounding boundary moves this random model's logits by ~2%
 from that step on (measured by perturbing the oracle alone), so any fp32
-reassociation would need a percent-level bar.
+reassociation would need a percent-level bar.  The prompt passes therefore
+run with their attention in fp64 (ATTN_F64) where they are held to this bar;
+the library's default, fp32 attention, has its own tests below.
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ import numpy as np
 import pytest
 
 import model_bin
+from gemma_hip import ATTN_F32, ATTN_F64
 from oracle import decode_oracle as dorc
 
 LOGIT_TOL = 1e-5
@@ -152,7 +155,7 @@ def _prefill_vs_oracle(gh, oracle, model, n, more, clen, chunks=None, batched=Fa
     prefill filled."""
     nv = model["config"]["nvocab"]
     prompt = np.random.default_rng(n * 31 + clen).integers(0, nv, n).astype(np.int32)
-    dec = gh.decoder(model, clen)
+    dec = gh.decoder(model, clen, attention=ATTN_F64)
     try:
         ref = dorc.DecodeOracle(model, oracle, clen)
         if batched:
@@ -304,9 +307,8 @@ def test_prefill_f32_attention(gh, oracle, tmp_path, case):
     for n in exact_ns + flip_ns:
         toks = np.random.default_rng(n).integers(0, 1024, n).astype(np.int32)
         want = dorc.DecodeOracle(model, oracle, n + 4).prefill(toks, 0)
-        dec = gh.decoder(model, n + 4)
+        dec = gh.decoder(model, n + 4, attention=ATTN_F32)
         try:
-            dec.set_attention(dec.ATTN_F32)
             lg = np.empty(1024, np.float32)
             nxt = dec.prefill(toks, 0, lg)
         finally:
@@ -315,6 +317,33 @@ def test_prefill_f32_attention(gh, oracle, tmp_path, case):
         print(f"prefill f32 attention {case} n={n}: {rel:.3g}", flush=True)
         assert rel <= (F32_PRE_FLIP if n in exact_ns else F32_FLIP_LEVEL)
         assert nxt == int(np.argmax(want))
+
+
+@pytest.mark.gpu
+def test_prefill_default_attention_is_f32(gh, tmp_path):
+    """A new decoder runs its prompt passes with fp32 attention: the default
+    equals ATTN_F32 bit for bit, and each mode stays set across calls.  The
+    case is F32_CASES' flip case at gemma-3-4b widths (200 tokens), where the
+    two modes' logits are known to part by the flip level."""
+    name, spec, _, (n,) = F32_CASES["4b"]
+    model = model_bin.read_bin(model_bin.write_bin(str(tmp_path / "m.bin"), name, seed=11,
+                                                   nvocab=1024, norm_std=0.1, **spec))
+    toks = np.random.default_rng(n).integers(0, 1024, n).astype(np.int32)
+    out = {}
+    for name, mode in (("default", None), ("f32", ATTN_F32), ("f64", ATTN_F64)):
+        dec = gh.decoder(model, n + 4, attention=mode)
+        try:
+            runs = []
+            for _ in range(2):
+                lg = np.empty(1024, np.float32)
+                dec.prefill(toks, 0, lg)
+                runs.append(lg)
+        finally:
+            dec.close()
+        assert np.array_equal(runs[0], runs[1]), name
+        out[name] = runs[0]
+    assert np.array_equal(out["default"], out["f32"])
+    assert np.abs(out["f32"] - out["f64"]).max() > 1e-3 * np.abs(out["f64"]).max()
 
 
 @pytest.mark.gpu

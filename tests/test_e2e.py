@@ -219,6 +219,11 @@ FLIP_FREE_STEPS = 8
 REL_PRE_FLIP = 1e-5
 REL_MAX = 5e-2
 ARGMAX_AGREE = 0.9
+# The argmax of a flip-perturbed random model disagrees with the reference's
+# on ~7% of rows (measured: 7 of 97 in the decoder comparison below).  Over the
+# 17 rows of the prefill comparison that rate leaves up to 3 disagreements
+# (0.82) inside the binomial 95% range, so that comparison is held to 0.8.
+ARGMAX_AGREE_17 = 0.8
 
 
 def run_reference_decode_only(model_path, prompt_len, steps, tmp_path):
@@ -248,14 +253,15 @@ def compare_to_reference(step_logits, ref_logits):
     return np.array(rel), agree / len(rel)
 
 
-def assert_close_to_reference(rel, agree, what, flip_free=FLIP_FREE_STEPS):
+def assert_close_to_reference(rel, agree, what, flip_free=FLIP_FREE_STEPS,
+                              min_agree=ARGMAX_AGREE):
     """flip_free: leading steps that must agree to REL_PRE_FLIP (0 for
     models deep enough that a requantization flip can come at any step)."""
     if flip_free:
         assert rel[:flip_free].max() <= REL_PRE_FLIP, (
             f"{what}: steps 0..{flip_free - 1} differ by {rel[:flip_free].max():.3g}")
     assert rel.max() <= REL_MAX, f"{what}: max relative difference {rel.max():.3g}"
-    assert agree >= ARGMAX_AGREE, f"{what}: argmax agreement {agree:.2f}"
+    assert agree >= min_agree, f"{what}: argmax agreement {agree:.2f}"
     first = int(np.argmax(rel > REL_PRE_FLIP)) if (rel > REL_PRE_FLIP).any() else len(rel)
     print(f"{what}: first step above {REL_PRE_FLIP:g}: {first} of {len(rel)}, max {rel.max():.3g}, "
           f"median {float(np.median(rel)):.3g}, argmax agreement {agree:.2f}", flush=True)
@@ -347,20 +353,25 @@ def run_reference_prefill(model_path, prompt_len, steps, tmp_path):
 @pytest.mark.gpu
 @needs_e2e
 @pytest.mark.timeout(600)
-def test_device_prefill_follows_reference_program(gh, tmp_path):
+@pytest.mark.parametrize("mode", ["f32", "f64"])
+def test_device_prefill_follows_reference_program(gh, tmp_path, mode):
     """BASELINE.json config 1 (gemma-3-270m, 32 prompt ids): the device's
     batched prefill (gemma_hip_decoder_prefill) against the reference's own
     chunked prefill, then 16 decode steps teacher-forced on the reference's
     tokens.  The reference evaluates the prefill attention in fp32 in its own
-    blockwise order, the device in fp64 (the decode oracle's arithmetic), so
-    the flip-level bounds of the decoder comparison apply."""
+    blockwise order; the device in fp32 in another order (the default) or in
+    fp64 (the decode oracle's arithmetic), so the flip-level bounds of the
+    decoder comparison apply to both."""
     import numpy as np
+
+    from gemma_hip import ATTN_F32, ATTN_F64
 
     path = model_bin.write_bin(str(tmp_path / "m270.bin"), "gemma-3-270m", seed=1234)
     res, ref = run_reference_prefill(path, 32, 16, tmp_path)
     model = model_bin.read_bin(path)
     prompt, toks = res["prompt"], res["tokens"]
-    dec = gh.decoder(model, len(prompt) + len(toks) + 2)
+    dec = gh.decoder(model, len(prompt) + len(toks) + 2,
+                     attention=ATTN_F32 if mode == "f32" else ATTN_F64)
     try:
         lg = np.empty(model["config"]["nvocab"], np.float32)
         dec.prefill(np.array([res["bos"]], np.int32), 0)
@@ -372,5 +383,6 @@ def test_device_prefill_follows_reference_program(gh, tmp_path):
     finally:
         dec.close()
     rel, agree = compare_to_reference(got, ref)
-    assert_close_to_reference(rel, agree, "device prefill vs reference prefill (270m)",
-                              flip_free=0)
+    assert len(rel) == 17
+    assert_close_to_reference(rel, agree, f"device prefill ({mode}) vs reference prefill (270m)",
+                              flip_free=0, min_agree=ARGMAX_AGREE_17)

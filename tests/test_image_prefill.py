@@ -29,6 +29,7 @@ import numpy as np
 import pytest
 
 import model_bin
+from gemma_hip import ATTN_F32, ATTN_F64
 from oracle import decode_oracle as dorc
 from oracle import vision_oracle as vorc
 
@@ -85,11 +86,12 @@ def oracle_chain(model, oracle, img, bos, prompt, tokens, steps, clen):
     return np.array(out), soft
 
 
-def device_chain(gh, model, img, bos, prompt, tokens, steps, clen):
-    """The device through the same stages (gemma_hip_gemma_image for the image)."""
+def device_chain(gh, model, img, bos, prompt, tokens, steps, clen, attention):
+    """The device through the same stages (gemma_hip_gemma_image for the
+    image), the tower's and the prompt passes' attention in `attention`."""
     nv = model["config"]["nvocab"]
-    dec = gh.decoder(model, clen)
-    tower = gh.vision(model["vision"])
+    dec = gh.decoder(model, clen, attention=attention)
+    tower = gh.vision(model["vision"], attention=attention)
     try:
         out, nxt = [], []
         lg = np.empty(nv, np.float32)
@@ -263,7 +265,7 @@ def test_prefill_rows_dense_matches_oracle(gh, oracle, gqa_model, n, pos0):
     rows = (rng.standard_normal((n, dim)) * 0.5).astype(np.float32)
     prefix = rng.integers(0, nv, pos0).astype(np.int32)
     clen = pos0 + n + 4
-    dec = gh.decoder(model, clen)
+    dec = gh.decoder(model, clen, attention=ATTN_F64)
     try:
         ref = dorc.DecodeOracle(model, oracle, clen)
         ref.prefill(prefix, 0)
@@ -348,7 +350,7 @@ def test_gemma_image_matches_oracle(gh, oracle, tmp_path, shape):
     prompt = np.random.default_rng(5).integers(0, 512, 6)
     tokens = np.random.default_rng(6).integers(0, 512, 3)
     clen = 1 + VISION[shape]["img_tok"] + 6 + 3
-    got, nxt, pos = device_chain(gh, model, img, 2, prompt, tokens, 3, clen)
+    got, nxt, pos = device_chain(gh, model, img, 2, prompt, tokens, 3, clen, ATTN_F64)
     want, _ = oracle_chain(model, oracle, img, 2, prompt, tokens, 3, clen)
     assert pos == clen
     worst = max(_check(g, w, f"{shape} stage {i}") for i, (g, w) in enumerate(zip(got, want)))
@@ -359,16 +361,18 @@ def test_gemma_image_matches_oracle(gh, oracle, tmp_path, shape):
 @pytest.mark.gpu
 @needs_e2e
 @pytest.mark.parametrize("case", sorted(REF_CASES))
-def test_device_image_follows_reference_program(gh, tmp_path, case):
+@pytest.mark.parametrize("mode", ["f32", "f64"])
+def test_device_image_follows_reference_program(gh, tmp_path, case, mode):
     """The device chain against forward_gemma_image compiled from the
-    reference's source (flip-free seeds, as above)."""
+    reference's source (flip-free seeds, as above), with the attention in
+    fp32 (the default) and in fp64."""
     model, img, res, ref = run_reference_image(tmp_path, case)
     clen = 1 + res["img_tok"] + len(res["prompt"]) + len(res["tokens"])
     got, nxt, _ = device_chain(gh, model, img, res["bos"], res["prompt"], res["tokens"],
-                               len(ref) - 2, clen)
+                               len(ref) - 2, clen, ATTN_F32 if mode == "f32" else ATTN_F64)
     rel = rel_rows(got, ref)
-    print(f"device vs reference image prompt ({case}): {np.array2string(rel, precision=2)}",
-          flush=True)
+    print(f"device ({mode}) vs reference image prompt ({case}): "
+          f"{np.array2string(rel, precision=2)}", flush=True)
     assert rel.max() <= REL_PRE_FLIP
     assert nxt[1:] == res["tokens"]
 

@@ -7,7 +7,9 @@ bit-exact kernels of test_gpu_parity.py; the fp32 glue (patch-embedding sums,
 layer norms, attention, GELU, pooling, RMSNorm) is evaluated in fp64 by both
 the device and the oracle and rounded once, so the soft tokens must agree to
 |out_gpu - out_oracle| <= TOL * max|out_oracle| -- a bar that a single fp32
-reassociation anywhere upstream of an int8 requantization would fail.
+reassociation anywhere upstream of an int8 requantization would fail.  The
+tower is held to it with its attention in fp64 (ATTN_F64); the library's
+default, fp32 attention, has its own tests below.
 """
 
 from __future__ import annotations
@@ -20,6 +22,7 @@ import numpy as np
 import pytest
 
 import model_bin
+from gemma_hip import ATTN_F32, ATTN_F64
 from oracle import vision_oracle as vorc
 
 TOL = 1e-5
@@ -79,7 +82,7 @@ def test_vision_matches_oracle(gh, oracle, shape):
     vis = model_bin.synth_vision(seed=7, text_dim=64, **SHAPES[shape])
     img = model_bin.synth_image(SHAPES[shape]["img_px"], seed=8)
     want = vorc.VisionOracle(vis, oracle).forward(img)
-    tower = gh.vision(vis)
+    tower = gh.vision(vis, attention=ATTN_F64)
     try:
         got = tower.forward(img)
         again = tower.forward(img)
@@ -111,11 +114,12 @@ def test_vision_f32_attention_matches_oracle(gh, oracle, shape, seed, img_seed):
     want = vorc.VisionOracle(vis, oracle).forward(img)
     tower = gh.vision(vis)
     try:
-        tower.set_attention(tower.ATTN_F32)
-        got = tower.forward(img)
+        got = tower.forward(img)  # the default: ATTN_F32
         again = tower.forward(img)
-        tower.set_attention(tower.ATTN_F64)
+        tower.set_attention(ATTN_F64)
         exact = tower.forward(img)
+        tower.set_attention(ATTN_F32)
+        back = tower.forward(img)
     finally:
         tower.close()
     rel = float(np.abs(got - want).max() / np.abs(want).max())
@@ -123,7 +127,8 @@ def test_vision_f32_attention_matches_oracle(gh, oracle, shape, seed, img_seed):
     assert rel <= F32_PRE_FLIP
     assert np.array_equal(got, again)
     assert np.array_equal(exact, want) or float(np.abs(exact - want).max()) <= TOL * float(
-        np.abs(want).max())  # switching back restores the fp64 path
+        np.abs(want).max())  # switching to the fp64 path
+    assert np.array_equal(back, got)  # and back
 
 
 @pytest.mark.gpu
@@ -131,9 +136,8 @@ def test_vision_f32_attention_siglip_width_flip_level(gh, oracle):
     vis = model_bin.synth_vision(seed=7, text_dim=64, **SHAPES["siglip"])
     img = model_bin.synth_image(SHAPES["siglip"]["img_px"], seed=8)
     want = vorc.VisionOracle(vis, oracle).forward(img)
-    tower = gh.vision(vis)
+    tower = gh.vision(vis, attention=ATTN_F32)
     try:
-        tower.set_attention(tower.ATTN_F32)
         got = tower.forward(img)
     finally:
         tower.close()
@@ -291,13 +295,14 @@ def test_vision_comparison_catches_planted_mistakes(tmp_path, oracle, monkeypatc
 @pytest.mark.gpu
 @needs_e2e
 @pytest.mark.parametrize("case", sorted(REF_CASES))
-def test_device_vision_follows_reference_program(gh, tmp_path, case):
+@pytest.mark.parametrize("mode", ["f32", "f64"])
+def test_device_vision_follows_reference_program(gh, tmp_path, case, mode):
     vis, img, ref = run_reference_vision(tmp_path, case)
-    tower = gh.vision(vis)
+    tower = gh.vision(vis, attention=ATTN_F32 if mode == "f32" else ATTN_F64)
     try:
         got = tower.forward(img)
     finally:
         tower.close()
     rel = rel_to(ref, got)
-    print(f"device vision vs reference ({case}): {rel:.3g}", flush=True)
+    print(f"device vision ({mode}) vs reference ({case}): {rel:.3g}", flush=True)
     assert rel <= REL_PRE_FLIP
