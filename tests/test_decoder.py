@@ -280,6 +280,35 @@ def test_decoder_long_context(gh, oracle, long_ctx, n):
     print(f"long context {n}: worst |d|/max|logit| = {worst:.3g}", flush=True)
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [3100, 8200])
+def test_prefill_f32_attention_long_context(gh, oracle, long_ctx, n):
+    """The default attention (fp32 matrix cores) over a long prompt: 194 and
+    513 row blocks of 16 rows (four q heads per kv head), key ranges in up to
+    8 chunks, on one global layer, against the oracle's prefill, then decode
+    steps on the cache it filled.  Measured free of requantization flips (0
+    and 1.5e-7 of the largest logit), so held to the fp32-rounding bar."""
+    nv = long_ctx["config"]["nvocab"]
+    toks = np.random.default_rng(n).integers(0, nv, n).astype(np.int32)
+    ref = dorc.DecodeOracle(long_ctx, oracle, n + 4)
+    want = ref.prefill(toks, 0)
+    dec = gh.decoder(long_ctx, n + 4, attention=ATTN_F32)
+    try:
+        lg = np.empty(nv, np.float32)
+        nxt = dec.prefill(toks, 0, lg)
+        rel = float(np.abs(lg - want).max() / np.abs(want).max())
+        assert nxt == int(np.argmax(want))
+        for pos in range(n, n + 2):
+            nxt = dec.step(nxt, pos, lg)
+            want = ref.step(int(np.argmax(want)), pos)
+            rel = max(rel, float(np.abs(lg - want).max() / np.abs(want).max()))
+            assert nxt == int(np.argmax(want))
+    finally:
+        dec.close()
+    print(f"long context {n}, fp32 attention: worst |d|/max|logit| = {rel:.3g}", flush=True)
+    assert rel <= F32_PRE_FLIP
+
+
 # The prompt pass with its attention on the fp32 matrix cores
 # (GEMMA_HIP_ATTN_F32).  On cases measured free of int8 requantization flips
 # the logits agree with the fp64 oracle to fp32 rounding (measured 0 ..
