@@ -564,6 +564,14 @@ int env_tile() {
   return t;
 }
 
+// 2221 (128x128, two 128-byte stages) with a tile per CU, else 214 (128x64)
+// with a tile per CU, else 114 (64x64)
+int narrow_tile(int m, int n, const DeviceInfo &dev) {
+  const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+  const long tiles128x64 = (long)((m + 127) / 128) * ((n + 63) / 64);
+  return tiles128 >= dev.cus ? 2221 : tiles128x64 >= dev.cus ? 214 : 114;
+}
+
 template <int WM, int WN, int S, int BKB = 64>
 void launch_dma_segs(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
                      const GemmSegs &bs, int mstr, const int8_t *src, int sstr,
@@ -791,9 +799,10 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
     if (tile == 0) {
       // measured on MI355X at the 1b/4b prefill and SigLIP shapes: 128x128
       // tiles with two 128-byte K stages are fastest once there is a tile
-      // per CU; below that, 128x64 tiles keep more CUs busy
-      const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
-      tile = !dma_ok ? 22 : (tiles128 >= dev.cus ? 2221 : 214);
+      // per CU; below that, 128x64 tiles keep more CUs busy, and 64x64 tiles
+      // where even those leave CUs idle (gemma-3-1b prefill o and q/k/v at
+      // 512 tokens: 9.2 -> 7.6 us and 10.5 -> 9.1 us)
+      tile = !dma_ok ? 22 : narrow_tile(m, n, dev);
     }
     if (tile >= 100 && !dma_ok) tile = 22;
     switch (tile) {
@@ -838,9 +847,9 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
   }
   if (fast && dma_ok && env_tile() == 0) {
     // the tile choice of launch_gemm_i8 for the whole width
-    const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
     const int sp = choose_split(m, n, k, dev, stream, false);
-    const bool wide = sp > 1 || tiles128 >= dev.cus;
+    const int tile = sp > 1 ? 2221 : narrow_tile(m, n, dev);
+    const bool wide = tile == 2221;
     const int bn = wide ? 128 : 64;
     bool aligned = true;
     for (int t = 0; t + 1 < b.nseg; ++t) aligned = aligned && b.end[t] % bn == 0;
@@ -852,8 +861,10 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
       }
       if (wide)
         launch_dma_segs<2, 2, 2, 128>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
-      else
+      else if (tile == 214)
         launch_dma_segs<2, 1, 4>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
+      else
+        launch_dma_segs<1, 1, 4>(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
       return hipGetLastError();
     }
   }
