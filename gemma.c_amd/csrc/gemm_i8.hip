@@ -673,58 +673,105 @@ __global__ __launch_bounds__(kThreads) void gemm_zero_kernel(int *p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// Bytes of workspace a split-K launch over `tiles` 128x128 tiles in `splits`
-// pieces needs: the partial tiles, then the counters on a 256-byte boundary.
-size_t split_bytes(int tiles, int splits) {
-  const size_t part = (size_t)tiles * splits * kThreads * 4 * 16 * sizeof(int);
-  return part + (((size_t)tiles * sizeof(int) + 255) & ~(size_t)255);
+// A split-K launch: square tiles of 64 * wm (wm = 1: 64x64 tiles, four
+// 64-byte K stages; wm = 2: 128x128, two 128-byte stages) in `splits` pieces
+// (1 = no split).
+struct SplitPlan {
+  int wm = 2, splits = 1;
+};
+
+int split_tiles(int m, int n, int wm) {
+  const int t = 64 * wm;
+  return ((m + t - 1) / t) * ((n + t - 1) / t);
 }
 
-// 128x128 tiles, two 128-byte stages, split-K over `splits` workgroups per
-// tile (splits >= 2, at most the number of K stages).
+// int32 partial-tile elements of a split launch: kThreads * wm * wm * 16 per
+// tile and piece
+size_t split_part_ints(int tiles, int splits, int wm) {
+  return (size_t)tiles * splits * kThreads * wm * wm * 16;
+}
+
+// Bytes of workspace a split-K launch needs: the partial tiles, then the
+// tile counters on a 256-byte boundary.
+size_t split_bytes(int tiles, int splits, int wm) {
+  return split_part_ints(tiles, splits, wm) * sizeof(int) +
+         (((size_t)tiles * sizeof(int) + 255) & ~(size_t)255);
+}
+
+// W x W blocks of 32x32 tiles per wave (64W x 64W workgroup tiles), S stages
+// of BKB bytes, split-K over `splits` workgroups per tile (splits >= 2, at
+// most the number of K stages).
+template <int W, int S, int BKB>
 hipError_t launch_dma_split(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
                             const GemmSegs &bs, int mstr, const int8_t *src, int sstr,
                             const float *ssc, int m, int k, int splits, const GemmWs *fixed) {
   const int n = bs.end[bs.nseg - 1];
-  const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
+  const int tiles = split_tiles(m, n, W);
+  const size_t part = split_part_ints(tiles, splits, W);
   SplitK sk{splits, nullptr, nullptr};
   if (fixed != nullptr) {
-    const size_t part = (size_t)tiles * splits * kThreads * 4 * 16;
-    if (split_bytes(tiles, splits) > fixed->bytes) return hipErrorOutOfMemory;
+    if (split_bytes(tiles, splits, W) > fixed->bytes) return hipErrorOutOfMemory;
     sk.ws = fixed->base;
     sk.cnt = fixed->base + ((part * sizeof(int) + 255) & ~(size_t)255) / sizeof(int);
     gemm_zero_kernel<<<(tiles + kThreads - 1) / kThreads, kThreads, 0, stream>>>(sk.cnt, tiles);
   } else {
-    hipError_t e = split_ws(stream, (size_t)tiles * splits * kThreads * 4 * 16, tiles, &sk);
+    hipError_t e = split_ws(stream, part, tiles, &sk);
     if (e != hipSuccess) return e;
   }
   if (heads)
-    gemm_i8_dma_kernel<2, 2, 2, 128, true, true><<<tiles * splits, kThreads, 0, stream>>>(
+    gemm_i8_dma_kernel<W, W, S, BKB, true, true><<<tiles * splits, kThreads, 0, stream>>>(
         dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, sk);
   else
-    gemm_i8_dma_kernel<2, 2, 2, 128, false, true><<<tiles * splits, kThreads, 0, stream>>>(
+    gemm_i8_dma_kernel<W, W, S, BKB, false, true><<<tiles * splits, kThreads, 0, stream>>>(
         dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k, sk);
   return hipGetLastError();
 }
 
-// Splits for the 128x128 kernel (1 = none).  Measured on MI355X, the partial
+hipError_t launch_split(const SplitPlan &p, bool heads, hipStream_t stream, float *dst,
+                        int dstr, int hdim, const GemmSegs &bs, int mstr, const int8_t *src,
+                        int sstr, const float *ssc, int m, int k, const GemmWs *fixed) {
+  return p.wm == 1 ? launch_dma_split<1, 4, 64>(heads, stream, dst, dstr, hdim, bs, mstr, src,
+                                                sstr, ssc, m, k, p.splits, fixed)
+                   : launch_dma_split<2, 2, 128>(heads, stream, dst, dstr, hdim, bs, mstr, src,
+                                                 sstr, ssc, m, k, p.splits, fixed);
+}
+
+// The split-K plan (splits = 1: none).  Measured on MI355X, the partial
 // tiles' round trip through memory costs about as much as 15 K stages, so a
-// split pays only when the grid leaves most CUs idle and K is long: gemma-3-1b
-// down at 512 tokens (36 tiles, 54 stages) goes from 253 to 348 TOPS with 6
-// splits, while every gemma-3-4b and SigLIP shape (>= 128 tiles) lost 15-60%.
-int choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t stream,
-                 bool fixed_ws) {
-  const int tiles = ((m + 127) / 128) * ((n + 127) / 128);
-  const int nk = (k + 127) / 128;
+// split pays only when the grid leaves CUs idle and K is long.  With fewer
+// 64x64 tiles than CUs and K >= 2048, 64x64 tiles in about 1.5 workgroups per
+// CU (at most 6 pieces of at least 8 stages): gemma-3-1b down at 512 tokens
+// 23.3 -> 16.7 us (3 pieces; 128x128 tiles in 6 pieces: 23.3), at 256 tokens
+// 20.5 -> 13.0, gemma-3-4b down at 256 tokens 26.9 -> 22.2.  Otherwise, with
+// at most one 128x128 tile per two CUs and K >= 4096, 128x128 tiles in about
+// two workgroups per CU (at most 8 pieces): gemma-3-1b down at 1024 tokens
+// 28.6 -> 25.8 us, gemma-3-4b down at 512 tokens 40.7 -> 32.5.  Every
+// gemma-3-4b and SigLIP shape at full length (>= 256 tiles of 128x128) lost
+// 15-60% with forced splits.  GEMMA_HIP_GEMM_SPLIT forces 128x128 pieces.
+SplitPlan choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t stream,
+                       bool fixed_ws) {
+  SplitPlan p;
+  const int nk128 = (k + 127) / 128, nk64 = (k + 63) / 64;
   const int forced = env_split();
-  if (forced > 0) return forced > nk ? nk : forced;
-  if (tiles <= 0 || tiles * 4 > dev.cus || nk < 32) return 1;
+  if (forced > 0) {
+    p.splits = forced > nk128 ? nk128 : forced;
+    return p;
+  }
+  const long tiles64 = split_tiles(m, n, 1), tiles128 = split_tiles(m, n, 2);
+  if (tiles64 <= 0) return p;
+  SplitPlan want;
+  if (tiles64 < dev.cus && nk64 >= 32) {
+    want.wm = 1;
+    want.splits = (int)std::min<long>({6, nk64 / 8, (3L * dev.cus + 2 * tiles64 - 1) / (2 * tiles64)});
+  } else if (tiles128 * 2 <= dev.cus && nk128 >= 32) {
+    want.splits = (int)std::min<long>({8, 2L * dev.cus / tiles128, nk128 / 8});
+  }
+  if (want.splits < 2) return p;
   hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
   if (!fixed_ws &&
       (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone))
-    return 1;  // the workspace may have to be allocated: not under capture
-  const int s = std::min(std::min(8, dev.cus / tiles), nk / 8);
-  return s >= 2 ? s : 1;
+    return p;  // the workspace may have to be allocated: not under capture
+  return want;
 }
 
 template <int WM, int WN, int S, int BKB = 64>
@@ -766,8 +813,8 @@ size_t gemm_i8_scratch_bytes(int m, int n, int k, bool heads, const int8_t *mat,
                       ((uint64_t)(m - 1) * dstr + n) * 4 < kOob;
   (void)heads;
   if (!fast || !dma_ok || env_tile() != 0) return 0;
-  const int sp = choose_split(m, n, k, dev, nullptr, true);
-  return sp > 1 ? split_bytes(((m + 127) / 128) * ((n + 127) / 128), sp) : 0;
+  const SplitPlan sp = choose_split(m, n, k, dev, nullptr, true);
+  return sp.splits > 1 ? split_bytes(split_tiles(m, n, sp.wm), sp.splits, sp.wm) : 0;
 }
 
 hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
@@ -784,15 +831,15 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
   if (fast) {
     int tile = env_tile();
     if (tile == 0 && dma_ok) {
-      const int sp = choose_split(m, n, k, dev, stream, fixed != nullptr);
-      if (sp > 1) {
+      const SplitPlan sp = choose_split(m, n, k, dev, stream, fixed != nullptr);
+      if (sp.splits > 1) {
         GemmSegs bs{};
         bs.w[0] = mat;
         bs.s[0] = matsc;
         bs.end[0] = n;
         bs.nseg = 1;
-        const hipError_t e = launch_dma_split(heads, stream, dst, dstr, hdim, bs, mstr, src,
-                                              sstr, ssc, m, k, sp, fixed);
+        const hipError_t e = launch_split(sp, heads, stream, dst, dstr, hdim, bs, mstr, src,
+                                          sstr, ssc, m, k, fixed);
         return e != hipSuccess ? e : hipGetLastError();
       }
     }
@@ -847,16 +894,16 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
   }
   if (fast && dma_ok && env_tile() == 0) {
     // the tile choice of launch_gemm_i8 for the whole width
-    const int sp = choose_split(m, n, k, dev, stream, false);
-    const int tile = sp > 1 ? 2221 : narrow_tile(m, n, dev);
+    const SplitPlan sp = choose_split(m, n, k, dev, stream, false);
+    const int tile = sp.splits > 1 ? (sp.wm == 1 ? 114 : 2221) : narrow_tile(m, n, dev);
     const bool wide = tile == 2221;
     const int bn = wide ? 128 : 64;
     bool aligned = true;
     for (int t = 0; t + 1 < b.nseg; ++t) aligned = aligned && b.end[t] % bn == 0;
     if (aligned) {
-      if (sp > 1) {
+      if (sp.splits > 1) {
         const hipError_t e =
-            launch_dma_split(false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k, sp, nullptr);
+            launch_split(sp, false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k, nullptr);
         return e != hipSuccess ? e : hipGetLastError();
       }
       if (wide)

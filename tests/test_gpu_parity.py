@@ -309,6 +309,42 @@ def test_gemm_split_k(gh, oracle, monkeypatch, splits):
     assert np.array_equal(bits(host(dst)), bits(np.ascontiguousarray(ref)))
 
 
+# The launcher's own split-K plans (no forcing), each bit-exact against the
+# oracle twice in a row: 64x64 tiles in 6, 6, 4 and 3 pieces (10, 40, 20 and
+# 144 tiles; K = 2064 ends in a partial stage), 128x128 tiles in 6 pieces
+# (72 tiles), and 64x64 pieces with the head-major output.
+SPLIT_PLANS = [(77, 301, 4096), (200, 640, 4096), (300, 200, 2064), (512, 1152, 6912),
+               (1024, 1152, 6912)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLIT_PLANS)
+def test_gemm_split_plans(gh, oracle, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    A = outlier_acts(rng, (m, k))
+    qo, so = oracle.quantize_acts(A)
+    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    ref, _ = oracle.gemm_int8(B, bs, qo, so)
+    for rep in range(2):
+        dst = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+        gh.matmul(dst, n, dev(B), k, dev(bs), dev(qo), k, dev(so), m, n, k, stream())
+        assert np.array_equal(bits(host(dst)), bits(ref)), f"launch {rep}"
+
+
+def test_gemm_split_plan_heads(gh, oracle):
+    m, heads, hdim, k = 300, 2, 256, 4096
+    rng = np.random.default_rng(9)
+    A = outlier_acts(rng, (m, k))
+    qh, sh = oracle.quantize_acts(A)
+    B = rng.integers(-127, 128, (heads * hdim, k), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, heads * hdim).astype(np.float32)
+    dst = torch.empty((heads, m, hdim), dtype=torch.float32, device="cuda")
+    gh.matmul_heads(dst, dev(B), dev(bs), dev(qh), dev(sh), m, heads, hdim, k, stream())
+    ref, _ = oracle.gemm_int8(B, bs, qh, sh)
+    ref = ref.reshape(m, heads, hdim).transpose(1, 0, 2)
+    assert np.array_equal(bits(host(dst)), bits(np.ascontiguousarray(ref)))
+
+
 # --------------------------------------------------------------- fp32
 def check_f32(got, mat, src, oracle):
     exact, mag = oracle.gemm_f64(mat, src)

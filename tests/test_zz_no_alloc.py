@@ -49,8 +49,8 @@ def both(gh, m, n, k, seed):
 
 
 def test_noalloc_equals_matmul_twice_then_smaller(gh):
-    # 1b prefill down (36 tiles of 128x128, K = 6912: split 6 ways), then a
-    # smaller shape that also splits (10 tiles, K = 4096: 4 ways)
+    # 1b prefill down (144 tiles of 64x64, K = 6912: split 3 ways), then a
+    # smaller shape that also splits (40 tiles of 64x64, K = 4096: 6 ways)
     for m, n, k, seed in [(512, 1152, 6912, 1), (200, 640, 4096, 2)]:
         note(f"noalloc m={m} n={n} k={k}")
         got, want = both(gh, m, n, k, seed)
