@@ -762,7 +762,8 @@ SplitPlan choose_split(int m, int n, int k, const DeviceInfo &dev, hipStream_t s
   SplitPlan want;
   if (tiles64 < dev.cus && nk64 >= 32) {
     want.wm = 1;
-    want.splits = (int)std::min<long>({6, nk64 / 8, (3L * dev.cus + 2 * tiles64 - 1) / (2 * tiles64)});
+    const long fill = (3L * dev.cus + 2 * tiles64 - 1) / (2 * tiles64);  // ~1.5 per CU
+    want.splits = (int)std::min<long>({6, nk64 / 8, fill});
   } else if (tiles128 * 2 <= dev.cus && nk128 >= 32) {
     want.splits = (int)std::min<long>({8, 2L * dev.cus / tiles128, nk128 / 8});
   }
