@@ -324,6 +324,11 @@ F32_CASES = {
     "hd128": ("test-hd128", dict(layers=2, slide=16), (40, 200), ()),
     "4b": ("gemma-3-4b", dict(layers=2, slide=8, flags=7), (40,), (200,)),
     "1b": ("gemma-3-1b", dict(layers=2, swa=[1, 0]), (40,), (200,)),
+    # attention softcap (the fp32 softmax's tanh branch), no qk norm
+    "softcap": ("gemma-3-270m", dict(layers=2, slide=8, flags=3, sc_att=50.0, sc_log=30.0),
+                (40, 200), ()),
+    # no qk norm, no pre/post FFN norms, no window
+    "plain": ("gemma-3-270m", dict(layers=2, slide=4096, flags=0), (40, 200), ()),
 }
 
 
