@@ -389,6 +389,31 @@ def test_prefill_in_chunks(gh, oracle, models):
 
 
 @pytest.mark.gpu
+def test_prefill_in_chunks_f32_attention(gh, oracle, models):
+    """The chunks of test_prefill_in_chunks with the default fp32 attention:
+    each chunk's queries over the keys the earlier chunks left in the cache,
+    against the oracle fed the whole prompt at once.  Six layers of
+    requantization: measured at the flip level (1.3% of the largest logit),
+    so held to it and to the argmax."""
+    model = models["gemma3"]
+    nv = model["config"]["nvocab"]
+    prompt = np.random.default_rng(45 * 31 + 64).integers(0, nv, 45).astype(np.int32)
+    want = dorc.DecodeOracle(model, oracle, 64).prefill(prompt, 0)
+    dec = gh.decoder(model, 64, attention=ATTN_F32)
+    try:
+        lg = np.empty(nv, np.float32)
+        cuts = [0, 1, 13, 30, 45]
+        for a_, b_ in zip(cuts[:-1], cuts[1:]):
+            nxt = dec.prefill(prompt[a_:b_], a_, lg)
+    finally:
+        dec.close()
+    rel = float(np.abs(lg - want).max() / np.abs(want).max())
+    print(f"prefill in chunks, fp32 attention: {rel:.3g}", flush=True)
+    assert rel <= F32_FLIP_LEVEL
+    assert nxt == int(np.argmax(want))
+
+
+@pytest.mark.gpu
 def test_prefill_argument_errors(gh, models):
     from gemma_hip import GemmaHipError
 
