@@ -559,34 +559,45 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
   __shared__ double red[kWaves];
   __shared__ double2 gsum[kCombGroups][32];
   hold_args(a);
-  int token, pos;
-  if (!step_ok(a.step, a.nvocab, a.clen, &token, &pos)) return;
   const int hd = a.hdim, h = blockIdx.x, tid = threadIdx.x;
-  const int spos = (a.slide > 0 && pos >= a.slide) ? pos + 1 - a.slide : 0;
-  const int nb = (pos + 1 - spos + kAttB - 1) / kAttB;
   const int stride = hd + 2;
   const double *p = a.part + (size_t)h * a.max_blocks * stride;
   const int g = tid / 16, q = tid % 16;
   const int d = blockIdx.y * 64 + 4 * q;
   const bool dv = d < hd;
   // (m, l) of blocks tid and tid + 256, then this group's first kCombBatch
-  // blocks' acc values (indices clamped in range; values past nb unused)
+  // blocks' acc values.  They are issued before the step record is in, so
+  // the two memory round trips overlap: the indices are clamped into the
+  // partials buffer (max_blocks per head), and the values of blocks at or
+  // past the step's block count nb, left from earlier steps or never
+  // written, are selected away or not read once nb is known.
+  const int top = a.max_blocks - 1;
   constexpr int kMl = 2;
-  double mb[kMl], lb[kMl];
+  double mraw[kMl], lb[kMl];
 #pragma unroll
   for (int u = 0; u < kMl; ++u) {
-    const int b = tid + u * kNT;
-    const double *pb = p + (size_t)min(b, nb - 1) * stride;
-    mb[u] = b < nb ? pb[hd] : -DBL_MAX;
+    const double *pb = p + (size_t)min(tid + u * kNT, top) * stride;
+    mraw[u] = pb[hd];
     lb[u] = pb[hd + 1];
   }
+  const int dc = dv ? d : 0;
   double2 x01[kCombBatch], x23[kCombBatch];
 #pragma unroll
   for (int u = 0; u < kCombBatch; ++u) {
-    const double *pb = p + (size_t)min(g + u * kCombGroups, nb - 1) * stride;
-    x01[u] = dv ? *reinterpret_cast<const double2 *>(pb + d) : double2{0.0, 0.0};
-    x23[u] = dv ? *reinterpret_cast<const double2 *>(pb + d + 2) : double2{0.0, 0.0};
+    const double *pb = p + (size_t)min(g + u * kCombGroups, top) * stride;
+    x01[u] = *reinterpret_cast<const double2 *>(pb + dc);
+    x23[u] = *reinterpret_cast<const double2 *>(pb + dc + 2);
   }
+  // No early return on a rejected step (which stores nothing): a branch here
+  // lets the compiler sink the loads above past it, one round trip later.
+  int token, pos;
+  const bool ok = step_ok(a.step, a.nvocab, a.clen, &token, &pos);
+  if (!ok) pos = 0;
+  const int spos = (a.slide > 0 && pos >= a.slide) ? pos + 1 - a.slide : 0;
+  const int nb = (pos + 1 - spos + kAttB - 1) / kAttB;
+  double mb[kMl];
+#pragma unroll
+  for (int u = 0; u < kMl; ++u) mb[u] = tid + u * kNT < nb ? mraw[u] : -DBL_MAX;
   double m = fmax(mb[0], mb[1]);
   for (int b = tid + kMl * kNT; b < nb; b += kNT) m = fmax(m, p[(size_t)b * stride + hd]);
   m = fmax(m, dpp_f64<kDppXor1>(m));
@@ -650,7 +661,7 @@ __global__ __launch_bounds__(kNT) void dec_attn_combine_kernel(DecAttn a) {
       t.x += gsum[gg][tid].x;
       t.y += gsum[gg][tid].y;
     }
-    if (dd < hd) {
+    if (ok && dd < hd) {
       a.xo[(size_t)h * hd + dd] = (float)(t.x / den);
       a.xo[(size_t)h * hd + dd + 1] = (float)(t.y / den);
     }
