@@ -162,6 +162,15 @@ hipError_t launch_dec_argmax(const float *logits, int n, float *pval, int *pidx,
                              int *step, int *tokens, int max_tokens, hipStream_t stream);
 
 // prefill.hip: the batched prompt pass (forward_text_chunk).
+// Byte regions (16-byte aligned) that a kernel reads and discards after its
+// own work, so that a later kernel finds them in the memory-side cache
+// (the Infinity Cache) rather than in HBM.
+constexpr int kMaxWarm = 4;
+struct WarmRegions {
+  const void *p[kMaxWarm];
+  size_t bytes[kMaxWarm];
+  int n;
+};
 // Rows of x [n][dim] (in place), y [n][dim] nullable: the per-row form of
 // DecNorm; h of every row is quantized into xq [n][dim] + xs [n].
 struct PfNorm {
@@ -220,7 +229,7 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
 // f32: on the fp32 matrix cores (otherwise fp64, rounded once)
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t stream);
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
-                                hipStream_t stream);
+                                const WarmRegions &warm, hipStream_t stream);
 
 // vision.hip: the SigLIP tower (forward_vision).
 // x [m][dim] = clamp(patches [m][k] . pe [dim][k] + pe_b) + pos_q * pos_s, in fp64

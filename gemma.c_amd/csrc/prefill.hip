@@ -757,12 +757,32 @@ __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) 
   }
 }
 
+// This workgroup's share (part `part` of `parts`) of the regions, read and
+// discarded: four 16-byte loads in flight per thread, their values fed to an
+// empty asm statement.  Called at the end of a kernel, so that its waits
+// delay only the workgroup's exit.
+__device__ __forceinline__ void warm_share(const WarmRegions &w, int part, int parts, int tid,
+                                           int nt) {
+  for (int j = 0; j < w.n; ++j) {
+    const v4i *p = static_cast<const v4i *>(w.p[j]);
+    const size_t n = w.bytes[j] / 16;
+    const size_t per = (n + parts - 1) / parts;
+    const size_t lo = (size_t)part * per, hi = lo + per < n ? lo + per : n;
+    const size_t st = (size_t)nt;
+    for (size_t i = lo + tid; i < hi; i += 4 * st) {
+      auto at = [&](size_t u) { return i + u * st < hi ? i + u * st : hi - 1; };
+      const v4i x0 = p[i], x1 = p[at(1)], x2 = p[at(2)], x3 = p[at(3)];
+      asm volatile("" ::"v"(x0), "v"(x1), "v"(x2), "v"(x3));
+    }
+  }
+}
+
 // One workgroup per row: out = gelu(gate) * up (gemma.c:4139-4172, the GELU
 // gate fused with the up projection) rounded once, then quantized into
 // xq[r] / xs[r] as quantize_act does.  g is [n][2 mlp], gate columns first.
 template <int NPT, int NT>
 __global__ __launch_bounds__(NT) void pf_gelu_quant_kernel(const float *g, int mlp, int8_t *xq,
-                                                           float *xs) {
+                                                           float *xs, WarmRegions warm) {
   __shared__ float redf[NT / 64];
   __shared__ double etab[128];
   exp_tab_load(etab);
@@ -801,6 +821,7 @@ __global__ __launch_bounds__(NT) void pf_gelu_quant_kernel(const float *g, int m
                 quant_one(out[j].z, qp.inv), quant_one(out[j].w, qp.inv));
   }
   if (tid == 0) xs[blockIdx.x] = qp.scale;
+  warm_share(warm, blockIdx.x, gridDim.x, tid, NT);
 }
 
 template <int C, int CMAX, class F>
@@ -882,14 +903,14 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
 }
 
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
-                                hipStream_t stream) {
+                                const WarmRegions &warm, hipStream_t stream) {
   // the fewest threads per row that cover it in kPfMaxNpt chunks (fewer idle
   // slots: gemma-3-4b's 10240 columns take 512 threads x 5 chunks exactly)
   const int n4 = mlp / 4;
   auto go = [&](auto nt) {
     constexpr int NT = decltype(nt)::value;
     return by_npt<1, kPfMaxNpt>((n4 + NT - 1) / NT, [&](auto c) {
-      pf_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(g, mlp, xq, xs);
+      pf_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(g, mlp, xq, xs, warm);
       return hipGetLastError();
     });
   };
