@@ -297,5 +297,25 @@ __device__ __forceinline__ int32_t dot16(v4i w, v4i x, int32_t acc) {
   return acc;
 }
 
+// This workgroup's share (part `part` of `parts`) of the regions, read and
+// discarded: four 16-byte loads in flight per thread, their values fed to an
+// empty asm statement.  Called at the end of a kernel, so that its waits
+// delay only the workgroup's exit.
+__device__ __forceinline__ void warm_share(const WarmRegions &w, int part, int parts, int tid,
+                                           int nt) {
+  for (int j = 0; j < w.n; ++j) {
+    const v4i *p = static_cast<const v4i *>(w.p[j]);
+    const size_t n = w.bytes[j] / 16;
+    const size_t per = (n + parts - 1) / parts;
+    const size_t lo = (size_t)part * per, hi = lo + per < n ? lo + per : n;
+    const size_t st = (size_t)nt;
+    for (size_t i = lo + tid; i < hi; i += 4 * st) {
+      auto at = [&](size_t u) { return i + u * st < hi ? i + u * st : hi - 1; };
+      const v4i x0 = p[i], x1 = p[at(1)], x2 = p[at(2)], x3 = p[at(3)];
+      asm volatile("" ::"v"(x0), "v"(x1), "v"(x2), "v"(x3));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace gh

@@ -274,7 +274,7 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream);
 // f32: on the fp32 matrix cores (otherwise fp64, rounded once)
 hipError_t launch_vis_attention(const VisAttn &a, int hdim, bool f32, hipStream_t stream);
 hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int mlp, int8_t *xq,
-                                 float *xs, hipStream_t stream);
+                                 float *xs, const WarmRegions &warm, hipStream_t stream);
 hipError_t launch_vis_pool(const VisPool &a, int ntok, hipStream_t stream);
 
 }  // namespace gh

@@ -525,7 +525,8 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_f32_kernel(VisAttn 
 // quantized into xq[r] / xs[r].
 template <int NPT, int NT>
 __global__ __launch_bounds__(NT) void vis_gelu_quant_kernel(const float *hbuf, const float *bias,
-                                                            int mlp, int8_t *xq, float *xs) {
+                                                            int mlp, int8_t *xq, float *xs,
+                                                            WarmRegions warm) {
   __shared__ float redf[NT / 64];
   __shared__ double etab[128];
   exp_tab_load(etab);
@@ -562,6 +563,7 @@ __global__ __launch_bounds__(NT) void vis_gelu_quant_kernel(const float *hbuf, c
                 quant_one(out[j].z, qp.inv), quant_one(out[j].w, qp.inv));
   }
   if (tid == 0) xs[blockIdx.x] = qp.scale;
+  warm_share(warm, blockIdx.x, gridDim.x, tid, NT);
 }
 
 // One workgroup per image token: the mean of its ksize x ksize patches
@@ -678,7 +680,7 @@ hipError_t launch_vis_attention(const VisAttn &a, int hdim, bool f32, hipStream_
 }
 
 hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int mlp, int8_t *xq,
-                                 float *xs, hipStream_t stream) {
+                                 float *xs, const WarmRegions &warm, hipStream_t stream) {
   // the fewest threads per row that cover it in kPfMaxNpt chunks: at SigLIP's
   // 4304 columns, 256 threads leave 16% of the slots empty, 1024 threads 47%
   // (54.7 -> 36.7 us per layer measured)
@@ -686,7 +688,8 @@ hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int m
   auto go = [&](auto nt) {
     constexpr int NT = decltype(nt)::value;
     return by_npt<1, kPfMaxNpt>((n4 + NT - 1) / NT, [&](auto c) {
-      vis_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(h, bias, mlp, xq, xs);
+      vis_gelu_quant_kernel<decltype(c)::value, NT><<<n, NT, 0, stream>>>(h, bias, mlp, xq, xs,
+                                                                             warm);
       return hipGetLastError();
     });
   };
