@@ -30,6 +30,7 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "gh_arith.h"
@@ -525,6 +526,371 @@ __global__ __launch_bounds__(kThreads) void gemm_i8_dma_kernel(
   store_tile<WM, WN, HEADS>(acc, scales, dst, dstr, hdim, m, n, m0, n0, wm, wn, lane);
 }
 
+// ---- ping-pong kernel (8 waves, one workgroup per CU) ----------------------
+//
+// Eight waves in two groups of four (waves 0-3 and 4-7; each SIMD runs one
+// wave of each group).  Period p of the K loop is
+//
+//     group 0: [memory p] [compute p]       group 1: [compute p-1] [memory p]
+//
+// followed by one s_barrier, so on every SIMD one wave issues MFMAs while the
+// other issues its LDS fragment reads and global->LDS DMA, and the two swap
+// halfway through the period without a barrier in between (group 1 runs half
+// a period behind in program order; its compute has the higher s_setprio so
+// its MFMAs go first).  "memory p" issues the DMA of period p+D into the LDS
+// ring, reads this group's fragments of period p and waits for them; each
+// wave then waits until its own DMA of period p+1 has landed, and the barrier
+// makes every wave's DMA of period p+1 visible (and frees the slots period p
+// used) before anyone reads them.
+//
+// Two layouts of the eight waves:
+//  - rows  (KALT = false): the groups split the tile's rows and consume the
+//    same K stage each period (256x320 tiles: 2x2 waves of 64x160 per group);
+//  - K-alternating (KALT = true): each group covers the whole tile with its
+//    own 2x2 (or 4x1) waves and takes every other K stage (intra-workgroup
+//    split-K); at the end the groups add their int32 sums through LDS, each
+//    finishing half of the tile.  This doubles the MFMA work per period for
+//    the 128-row tiles that give the one-tile-per-CU shapes exactly one round.
+// Stages are 64 bytes of K for all BM+BN rows, XOR-swizzled as in the DMA
+// kernel above; the tile's row and column scales come in by DMA with the
+// first stages, so no registers carry them through the loop.  MF selects
+// v_mfma_i32_32x32x32_i8 (32x32 tiles) or v_mfma_i32_16x16x64_i8 (16x16,
+// for tile widths like 144 and 160 that are not multiples of 64).  Integer
+// sums are exact, so every layout gives the same bits as the other kernels.
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// one 64-lane global->LDS DMA: lane i's 16 (or 4) bytes land at lds + 16 i
+// (4 i); m0 carries the LDS address.  Issued from asm so that the compiler's
+// own wait counting does not put a vmcnt(0) between the ring's DMA and the
+// fragment reads of other slots (it cannot tell the slots apart); the
+// kernel's explicit waits order them.
+__device__ __forceinline__ void dma_b128(v4i rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b32(v4i rsrc, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc) : "memory", "m0");
+}
+__device__ __forceinline__ v4i raw_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return v4i{(int)(uint32_t)b, (int)(uint32_t)((b >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+__device__ __forceinline__ void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+// at most a*P of this wave's DMA instructions outstanding, a in [0, A]
+template <int P, int A>
+__device__ __forceinline__ void wait_periods(int a) {
+  if constexpr (A >= 2) { if (a >= 2) { wait_vmcnt<2 * P>(); return; } }
+  if constexpr (A >= 1) { if (a == 1) { wait_vmcnt<P>(); return; } }
+  wait_vmcnt<0>();
+}
+
+template <int MF> struct PpMfma;
+template <> struct PpMfma<32> {
+  typedef v16i Acc;
+  static constexpr int NA = 16, NSUB = 2;  // accumulators per lane, MFMAs per stage
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+  // 16-byte K chunk a lane supplies in sub-step sub
+  static __device__ __forceinline__ int chunk(int sub, int lane) { return 2 * sub + (lane >> 5); }
+  // accumulator r of lane l: row rsub(r) + rlane(l), column l % 32
+  static __device__ __forceinline__ int rlane(int lane) { return 4 * (lane >> 5); }
+  static constexpr int rsub(int r) { return 8 * (r >> 2) + (r & 3); }
+};
+template <> struct PpMfma<16> {
+  typedef v4i Acc;
+  static constexpr int NA = 4, NSUB = 1;
+  static __device__ __forceinline__ Acc mma(v4i a, v4i b, Acc c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int chunk(int, int lane) { return lane >> 4; }
+  static __device__ __forceinline__ int rlane(int lane) { return 4 * (lane >> 4); }
+  static constexpr int rsub(int r) { return r; }
+};
+
+template <int MF, int GWM, int GWN, int TM, int TN, bool KALT>
+struct PpGeo {
+  static constexpr int BM = (KALT ? 1 : 2) * GWM * TM * MF;
+  static constexpr int BN = GWN * TN * MF;
+};
+
+// KS: 64-byte stages per group and period; D: periods of DMA lookahead
+template <int MF, int GWM, int GWN, int TM, int TN, bool KALT, int KS, int D, bool HEADS>
+__global__ __launch_bounds__(512, 1) void gemm_i8_pp_kernel(
+    float *__restrict__ dst, int dstr, int hdim, GemmSegs bs, int mstr,
+    const int8_t *__restrict__ src, int sstr, const float *__restrict__ ssc, int m, int k) {
+  static_assert(GWM * GWN == 4, "four waves per group");
+  typedef PpMfma<MF> M;
+  typedef typename M::Acc Acc;
+  constexpr int BM = PpGeo<MF, GWM, GWN, TM, TN, KALT>::BM;
+  constexpr int BN = PpGeo<MF, GWM, GWN, TM, TN, KALT>::BN;
+  constexpr int C = KALT ? 2 * KS : KS;   // stages per period
+  constexpr int S = C * (D + 1);          // ring depth
+  constexpr int kSlots = (BM + BN) * 4;   // 16-byte slots per stage
+  constexpr int kInstr = kSlots / 64;     // DMA instructions per stage
+  constexpr int kPer = (kInstr + 7) / 8;  // ... per wave (the last ones may be padding)
+  constexpr int kScI = (BM + BN + 511) / 512;
+  static_assert(C * kPer * (D - 1) <= 63, "vmcnt range");
+  static_assert(S * kSlots * 16 + 1024 + kScI * 2048 <= 160 * 1024, "LDS");
+  __shared__ v4i lds[S][kSlots];
+  __shared__ v4i lpad[64];  // target of the padding DMAs (zeros, never read)
+  __shared__ float lsc[kScI * 512];  // [0, BM) row scales, [BM, BM+BN) column scales
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, w4 = wave & 3;
+  const int row_w = ((KALT ? 0 : grp * GWM) + w4 / GWN) * TM * MF;
+  const int col_w = (w4 % GWN) * TN * MF;
+  const int n = bs.end[bs.nseg - 1];
+  int tm, tn;
+  tile_of(blockIdx.x, (m + BM - 1) / BM, (n + BN - 1) / BN, &tm, &tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  // inner segment ends are multiples of BN: the tile's columns are in one segment
+  int sj = 0;
+#pragma unroll
+  for (int t = 0; t < kMaxGemmSegs - 1; ++t)
+    if (t + 1 < bs.nseg && n0 >= bs.end[t]) sj = t + 1;
+  const int c0 = sj == 0 ? 0 : bs.end[sj - 1];
+  const int nb = bs.end[sj] - c0;
+
+  const v4i rs_a = raw_rsrc(src, (uint32_t)(m - 1) * sstr + k);
+  const v4i rs_b = raw_rsrc(bs.w[sj], (uint32_t)(nb - 1) * mstr + k);
+  const uint32_t ring = lds_addr(&lds[0][0]);
+  const uint32_t pad = lds_addr(&lpad[0]);
+  {
+    const v4i rs_as = raw_rsrc(ssc, (uint32_t)m * 4);
+    const v4i rs_bs = raw_rsrc(bs.s[sj], (uint32_t)nb * 4);
+    const uint32_t sc = lds_addr(&lsc[0]);
+#pragma unroll
+    for (int u = 0; u < kScI; ++u) {
+      const int base = u * 512 + wave * 64;  // wave-uniform; BM is a multiple of 64
+      const int s = base + lane;
+      if (base < BM) {
+        dma_b32(rs_as, m0 + s < m ? (uint32_t)(m0 + s) * 4 : kOob, sc + base * 4);
+      } else {
+        const int col = n0 - c0 + s - BM;
+        dma_b32(rs_bs, s - BM < BN && col < nb ? (uint32_t)col * 4 : kOob, sc + base * 4);
+      }
+    }
+  }
+  // this lane's slot in each of its DMA instructions
+  uint32_t row_off[kPer];
+  int chunk16[kPer];
+  bool is_a[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int instr = i * 8 + wave;
+    is_a[i] = instr * 64 < BM * 4;
+    const int slot = instr * 64 + lane - (is_a[i] ? 0 : BM * 4);
+    const int row = slot >> 2;
+    const int chunk = (slot & 3) ^ ((row >> 2) & 3);
+    const int grow = (is_a[i] ? m0 : n0 - c0) + row;
+    const bool in = instr < kInstr && grow < (is_a[i] ? m : nb);
+    row_off[i] = in ? (uint32_t)grow * (uint32_t)(is_a[i] ? sstr : mstr) + chunk * 16 : kOob;
+    chunk16[i] = chunk * 16;
+  }
+  auto issue = [&](int kt) {
+    const int buf = kt % S;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int instr = i * 8 + wave;
+      const int kb = kt * 64;
+      const uint32_t voff = (row_off[i] == kOob || kb + chunk16[i] >= k) ? kOob : row_off[i] + kb;
+      dma_b128(is_a[i] ? rs_a : rs_b, voff,
+               instr < kInstr ? ring + (uint32_t)((buf * kSlots + instr * 64) * 16) : pad);
+    }
+  };
+
+  Acc acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = Acc{};
+  v4i fa[KS][M::NSUB][TM], fb[KS][M::NSUB][TN];
+  auto read_frags = [&](int kt0) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const v4i *st = lds[(kt0 + s) % S];
+#pragma unroll
+      for (int sub = 0; sub < M::NSUB; ++sub) {
+        const int c = M::chunk(sub, lane);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int r = row_w + i * MF + (lane % MF);
+          fa[s][sub][i] = st[r * 4 + (c ^ ((r >> 2) & 3))];
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int r = col_w + j * MF + (lane % MF);
+          fb[s][sub][j] = st[BM * 4 + r * 4 + (c ^ ((r >> 2) & 3))];
+        }
+      }
+    }
+  };
+  auto compute = [&]() {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int sub = 0; sub < M::NSUB; ++sub)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = M::mma(fa[s][sub][i], fb[s][sub][j], acc[i][j]);
+  };
+
+  const int nk = (k + 63) / 64;
+  const int np = (nk + C - 1) / C;  // stages past nk read as zeros
+  for (int p = 0; p < D && p < np; ++p)
+#pragma unroll
+    for (int c = 0; c < C; ++c) issue(p * C + c);
+  wait_periods<C * kPer, D - 1>(min(D - 1, np - 1));  // period 0 (and the scales)
+  pp_barrier();
+  const int own = KALT ? grp * KS : 0;
+  for (int p = 0; p < np; ++p) {
+    if (grp == 1 && p > 0) {
+      __builtin_amdgcn_s_setprio(2);
+      compute();
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (p + D < np) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) issue((p + D) * C + c);
+    }
+    read_frags(p * C + own);
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    if (grp == 0) {
+      __builtin_amdgcn_s_setprio(1);
+      compute();
+      __builtin_amdgcn_s_setprio(0);
+    }
+    wait_periods<C * kPer, D - 1>(max(0, min(D - 1, np - 2 - p)));  // period p+1 landed
+    pp_barrier();
+  }
+  if (grp == 1) compute();
+
+  // The accumulator tiles [I0, I0+NI) x [J0, J0+NJ) this wave finishes:
+  // all of them, or with KALT the half its group keeps after the exchange.
+  constexpr bool kSplitI = TM % 2 == 0;
+  static_assert(!KALT || kSplitI || TN % 2 == 0, "KALT halves the wave tile");
+  constexpr int HI = KALT && kSplitI ? TM / 2 : TM;
+  constexpr int HJ = KALT && !kSplitI ? TN / 2 : TN;
+  static_assert(!KALT || 8 * HI * HJ * M::NA * 64 * 4 <= S * kSlots * 16, "exchange area");
+  if constexpr (KALT) {
+    // every ring read and DMA is complete (last wait was vmcnt(0), the reads
+    // were waited before the last barrier): the ring is reused for the exchange
+    int *xa = reinterpret_cast<int *>(&lds[0][0]);
+    int *mine = xa + (wave * HI * HJ * M::NA) * 64;
+    const int *theirs = xa + ((wave ^ 4) * HI * HJ * M::NA) * 64;
+    auto put = [&](auto G) {
+      constexpr int g = decltype(G)::value;
+      constexpr int gi = kSplitI && g == 0 ? HI : 0, gj = !kSplitI && g == 0 ? HJ : 0;
+#pragma unroll
+      for (int i = 0; i < HI; ++i)
+#pragma unroll
+        for (int j = 0; j < HJ; ++j)
+#pragma unroll
+          for (int r = 0; r < M::NA; ++r)
+            mine[((i * HJ + j) * M::NA + r) * 64 + lane] = acc[gi + i][gj + j][r];
+    };
+    auto take = [&](auto G) {
+      constexpr int g = decltype(G)::value;
+      constexpr int ki = kSplitI && g == 1 ? HI : 0, kj = !kSplitI && g == 1 ? HJ : 0;
+#pragma unroll
+      for (int i = 0; i < HI; ++i)
+#pragma unroll
+        for (int j = 0; j < HJ; ++j)
+#pragma unroll
+          for (int r = 0; r < M::NA; ++r)
+            acc[ki + i][kj + j][r] += theirs[((i * HJ + j) * M::NA + r) * 64 + lane];
+    };
+    if (grp == 0) put(std::integral_constant<int, 0>{}); else put(std::integral_constant<int, 1>{});
+    __syncthreads();
+    if (grp == 0) take(std::integral_constant<int, 0>{}); else take(std::integral_constant<int, 1>{});
+  }
+
+  // epilogue (gemma.c:3854-3865): y = (float)acc * (act_scale * w_scale)
+  auto finish = [&](auto I0c, auto J0c) {
+    constexpr int I0 = decltype(I0c)::value, J0 = decltype(J0c)::value;
+    float amin = __builtin_inff(), wmin = __builtin_inff();
+    bool asub = false, wsub = false;
+#pragma unroll
+    for (int i = 0; i < HI; ++i)
+#pragma unroll
+      for (int r = 0; r < M::NA; ++r)
+        scale_extremes(lsc[row_w + (I0 + i) * MF + M::rsub(r) + M::rlane(lane)], &amin, &asub);
+#pragma unroll
+    for (int j = 0; j < HJ; ++j)
+      scale_extremes(lsc[BM + col_w + (J0 + j) * MF + (lane % MF)], &wmin, &wsub);
+    const bool plain_lane = rescale_all_plain(amin, asub, wmin, wsub);
+    const bool all_plain = __builtin_amdgcn_readfirstlane(__any(!plain_lane) ? 0 : 1) != 0;
+    if (!HEADS && all_plain) {
+      // out-of-range rows and columns fall past the descriptor and are dropped
+      const uint32_t extent = ((uint32_t)(m - 1) * (uint32_t)dstr + (uint32_t)n) * 4u;
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          dst, (short)0, (int)extent, 0x00020000);
+#pragma unroll
+      for (int j = 0; j < HJ; ++j) {
+        const int cl = col_w + (J0 + j) * MF + (lane % MF);
+        const float wsc = lsc[BM + cl];
+        const uint32_t voff =
+            n0 + cl < n ? ((uint32_t)M::rlane(lane) * dstr + n0 + cl) * 4u : kOob;
+#pragma unroll
+        for (int i = 0; i < HI; ++i)
+#pragma unroll
+          for (int r = 0; r < M::NA; ++r) {
+            const int rl = row_w + (I0 + i) * MF + M::rsub(r);
+            const float y = (float)acc[I0 + i][J0 + j][r] * (lsc[rl + M::rlane(lane)] * wsc);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(y), rs, voff,
+                                                  (uint32_t)(m0 + rl) * dstr * 4u, 0);
+          }
+      }
+      return;
+    }
+    // head-major layout, or scales in FTZ/DAZ territory: guarded stores
+#pragma unroll
+    for (int j = 0; j < HJ; ++j) {
+      const int cl = col_w + (J0 + j) * MF + (lane % MF);
+      const int col = n0 + cl;
+      const float wsc = lsc[BM + cl];
+      float *out_col;
+      size_t row_stride;
+      if (HEADS) {
+        out_col = dst + (size_t)(col / hdim) * m * hdim + (col % hdim);
+        row_stride = hdim;
+      } else {
+        out_col = dst + col;
+        row_stride = dstr;
+      }
+#pragma unroll
+      for (int i = 0; i < HI; ++i)
+#pragma unroll
+        for (int r = 0; r < M::NA; ++r) {
+          const int rl = row_w + (I0 + i) * MF + M::rsub(r) + M::rlane(lane);
+          const int32_t a = acc[I0 + i][J0 + j][r];
+          const float y = all_plain ? (float)a * (lsc[rl] * wsc) : rescale(a, lsc[rl], wsc);
+          if (m0 + rl < m && col < n) out_col[(size_t)(m0 + rl) * row_stride] = y;
+        }
+    }
+  };
+  constexpr int kKeepI = KALT && kSplitI ? HI : 0, kKeepJ = KALT && !kSplitI ? HJ : 0;
+  if (KALT && grp == 1)
+    finish(std::integral_constant<int, kKeepI>{}, std::integral_constant<int, kKeepJ>{});
+  else
+    finish(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+}
+
 // Any shape, any alignment: one thread per output, byte loads.  Used only
 // when k % 16 != 0 or a row is not 16-byte aligned.
 template <bool HEADS>
@@ -570,6 +936,106 @@ int narrow_tile(int m, int n, const DeviceInfo &dev) {
   const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
   const long tiles128x64 = (long)((m + 127) / 128) * ((n + 63) / 64);
   return tiles128 >= dev.cus ? 2221 : tiles128x64 >= dev.cus ? 214 : 114;
+}
+
+
+GemmSegs one_seg(const int8_t *mat, const float *matsc, int n) {
+  GemmSegs bs{};
+  bs.w[0] = mat;
+  bs.s[0] = matsc;
+  bs.end[0] = n;
+  bs.nseg = 1;
+  return bs;
+}
+
+// ---- ping-pong kernel: configurations and their choice ---------------------
+//
+// Measured on MI355X (random int8 operands, one launch at a time):
+//   256x320 rows layout (2x2 waves of 64x160 per group, 32x32 MFMA): gemma-3-4b
+//     gate/up 2048x10240x2560 60.5 us (DMA kernel 70.5), SigLIP fc1
+//     4096x4304x1152 33.2 us (36.7);
+//   128x160 K-alternating (2x2 waves of 64x80, 16x16 MFMA): 4b o 19.7 us
+//     (20.4), 4b down 2048x2560x10240 70.3 us (71.5);
+//   128x144 K-alternating (4x1 waves of 32x144): SigLIP q/k/v/o 14.4 us (14.9),
+//     fc2 37.7 us (40.0);
+//   128x128 K-alternating (2x2 waves of 64x64, 32x32 MFMA): 4b q 19.0 us (21.6);
+//   128x64 K-alternating, two stages per group step: 4b k/v 13.9 us (18.0).
+// A launch is worth it when the tiles fill at least 3/4 of the CUs; the cost
+// model below (per round: a fixed 5.5 us of launch, prologue and drain, the
+// tile's stores, and the K loop at the configuration's measured rate per CU)
+// picks among the configurations whose tile width divides the segment ends.
+struct PpConfig {
+  int bm, bn;
+  double tops_per_cu;  // K-loop rate per CU, TOPS
+};
+constexpr PpConfig kPpConfigs[] = {
+    {0, 0, 0.0}, {256, 320, 8.45}, {128, 160, 6.6}, {128, 144, 5.0}, {128, 128, 6.0}, {128, 64, 4.0},
+};
+constexpr int kPpCount = 5;
+
+// GEMMA_HIP_GEMM_PP=0 turns the ping-pong kernel off, 1..5 forces a
+// configuration of kPpConfigs (a launch-shape knob like GEMMA_HIP_GEMM_TILE)
+int env_pp() {
+  const char *e = getenv("GEMMA_HIP_GEMM_PP");
+  return e == nullptr ? -1 : atoi(e);
+}
+
+int choose_pp(int m, int n, int k, const GemmSegs &bs, const DeviceInfo &dev) {
+  const int forced = env_pp();
+  if (forced == 0) return 0;
+  // a forced split-K (GEMMA_HIP_GEMM_SPLIT) asks for the split DMA kernel
+  const char *split = getenv("GEMMA_HIP_GEMM_SPLIT");
+  if (split != nullptr && atoi(split) > 0) return 0;
+  int best = 0;
+  double best_cost = 0.0;
+  for (int id = 1; id <= kPpCount; ++id) {
+    const PpConfig &c = kPpConfigs[id];
+    bool aligned = true;
+    for (int t = 0; t + 1 < bs.nseg; ++t) aligned = aligned && bs.end[t] % c.bn == 0;
+    if (!aligned) continue;
+    if (forced > 0) {
+      if (id == forced) return id;
+      continue;
+    }
+    const long tiles = (long)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn);
+    if (tiles * 4 < 3L * dev.cus) continue;
+    const long rounds = (tiles + dev.cus - 1) / dev.cus;
+    const double area = (double)c.bm * c.bn;
+    const double cost = rounds * (5.5 + 6e-5 * area + 2.0 * area * k / (c.tops_per_cu * 1e6));
+    if (best == 0 || cost < best_cost) {
+      best = id;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+template <int MF, int GWM, int GWN, int TM, int TN, bool KALT, int KS, int D>
+void launch_pp_cfg(bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
+                   const GemmSegs &bs, int mstr, const int8_t *src, int sstr, const float *ssc,
+                   int m, int k) {
+  constexpr int BM = PpGeo<MF, GWM, GWN, TM, TN, KALT>::BM;
+  constexpr int BN = PpGeo<MF, GWM, GWN, TM, TN, KALT>::BN;
+  const int n = bs.end[bs.nseg - 1];
+  const int tiles = ((m + BM - 1) / BM) * ((n + BN - 1) / BN);
+  if (heads)
+    gemm_i8_pp_kernel<MF, GWM, GWN, TM, TN, KALT, KS, D, true><<<tiles, 512, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k);
+  else
+    gemm_i8_pp_kernel<MF, GWM, GWN, TM, TN, KALT, KS, D, false><<<tiles, 512, 0, stream>>>(
+        dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k);
+}
+
+void launch_pp(int id, bool heads, hipStream_t stream, float *dst, int dstr, int hdim,
+               const GemmSegs &bs, int mstr, const int8_t *src, int sstr, const float *ssc, int m,
+               int k) {
+  switch (id) {
+    case 1: launch_pp_cfg<32, 2, 2, 2, 5, false, 1, 2>(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k); break;
+    case 2: launch_pp_cfg<16, 2, 2, 4, 5, true, 1, 2>(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k); break;
+    case 3: launch_pp_cfg<16, 4, 1, 2, 9, true, 1, 2>(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k); break;
+    case 4: launch_pp_cfg<32, 2, 2, 2, 2, true, 1, 3>(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k); break;
+    default: launch_pp_cfg<16, 2, 2, 4, 2, true, 2, 2>(heads, stream, dst, dstr, hdim, bs, mstr, src, sstr, ssc, m, k); break;
+  }
 }
 
 template <int WM, int WN, int S, int BKB = 64>
@@ -814,6 +1280,7 @@ size_t gemm_i8_scratch_bytes(int m, int n, int k, bool heads, const int8_t *mat,
                       ((uint64_t)(m - 1) * dstr + n) * 4 < kOob;
   (void)heads;
   if (!fast || !dma_ok || env_tile() != 0) return 0;
+  if (choose_pp(m, n, k, one_seg(mat, nullptr, n), dev) != 0) return 0;
   const SplitPlan sp = choose_split(m, n, k, dev, nullptr, true);
   return sp.splits > 1 ? split_bytes(split_tiles(m, n, sp.wm), sp.splits, sp.wm) : 0;
 }
@@ -832,6 +1299,12 @@ hipError_t launch_gemm_i8(float *dst, int dstr, int hdim, const int8_t *mat,
   if (fast) {
     int tile = env_tile();
     if (tile == 0 && dma_ok) {
+      const GemmSegs one = one_seg(mat, matsc, n);
+      const int pp = choose_pp(m, n, k, one, dev);
+      if (pp != 0) {
+        launch_pp(pp, heads, stream, dst, dstr, hdim, one, mstr, src, sstr, ssc, m, k);
+        return hipGetLastError();
+      }
       const SplitPlan sp = choose_split(m, n, k, dev, stream, fixed != nullptr);
       if (sp.splits > 1) {
         GemmSegs bs{};
@@ -894,6 +1367,11 @@ hipError_t launch_gemm_i8_segs(float *dst, int dstr, const GemmSegs &b, const in
     dma_ok = dma_ok && (uint64_t)(rows - 1) * k + k < kOob;
   }
   if (fast && dma_ok && env_tile() == 0) {
+    const int pp = choose_pp(m, n, k, b, dev);
+    if (pp != 0) {
+      launch_pp(pp, false, stream, dst, dstr, 0, b, k, src, sstr, ssc, m, k);
+      return hipGetLastError();
+    }
     // the tile choice of launch_gemm_i8 for the whole width
     const SplitPlan sp = choose_split(m, n, k, dev, stream, false);
     const int tile = sp.splits > 1 ? (sp.wm == 1 ? 114 : 2221) : narrow_tile(m, n, dev);

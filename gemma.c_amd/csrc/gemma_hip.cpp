@@ -589,6 +589,38 @@ int gemma_hip_matmul_noalloc(float *dst, int dstr, const int8_t *mat, int mstr,
                      n, k, stream, true);
 }
 
+int gemma_hip_matmul_cols(float *dst, int dstr, const gemma_hip_job *jobs, int njobs,
+                          const int8_t *src, int sstr, const float *ssc, int m, int k,
+                          void *stream) {
+  const char *name = "gemma_hip_matmul_cols";
+  if (need_init()) return 1;
+  if (jobs == nullptr || njobs < 1 || njobs > gh::kMaxGemmSegs)
+    return fail("%s: njobs=%d outside 1..%d", name, njobs, gh::kMaxGemmSegs);
+  gh::GemmSegs bs{};
+  long n = 0;
+  for (int j = 0; j < njobs; ++j) {
+    if (jobs[j].m <= 0) return fail("%s: job %d has m=%d rows", name, j, jobs[j].m);
+    if (jobs[j].w == nullptr || jobs[j].sc == nullptr)
+      return fail("%s: job %d has a null weight or scale pointer", name, j);
+    n += jobs[j].m;
+    if (n > (1l << 30)) return fail("%s: %ld output columns", name, n);
+    bs.w[j] = static_cast<const int8_t *>(jobs[j].w);
+    bs.s[j] = jobs[j].sc;
+    bs.end[j] = (int)n;
+  }
+  bs.nseg = njobs;
+  if (dstr == 0) dstr = (int)n;
+  if (sstr == 0) sstr = k;
+  if (check_matmul_shape(name, m, (int)n, k, dstr, k, sstr)) return 1;
+  if (m == 0) return 0;
+  if (!dst || !src || !ssc) return fail("%s: null pointer", name);
+  hipStream_t s = pick_stream(stream);
+  PerfScope perf(kOpGemmInt8, s);
+  GH_CHECK("gemma_hip_matmul_cols: launch",
+           gh::launch_gemm_i8_segs(dst, dstr, bs, src, sstr, ssc, m, k, g.info, s));
+  return 0;
+}
+
 int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,
                            const int8_t *src, const float *ssc, int m,
                            int heads, int hdim, int k, void *stream) {

@@ -102,6 +102,7 @@ _SIGS = {
     "gemma_hip_perf_phase": (_I, [_I]),
     "gemma_hip_perf_read": (_I, [ctypes.POINTER(PerfEntry), _I, ctypes.POINTER(_I)]),
     "gemma_hip_matmul_heads": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "gemma_hip_matmul_cols": (_I, [_P, _I, ctypes.POINTER(Job), _I, _P, _I, _P, _I, _I, _P]),
     "gemma_hip_matmul_multi": (_I, [ctypes.POINTER(Job), _I, _P, _P, _I, _P]),
     "gemma_hip_quantize_matmul": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P, _P, _P]),
     "gemma_hip_matmul_f32": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
@@ -227,6 +228,12 @@ class GemmaHip:
         self._check(self.lib.gemma_hip_matmul_heads(_addr(dst), _addr(mat), _addr(matsc),
                                                     _addr(src), _addr(ssc), m, heads, hdim, k,
                                                     stream))
+
+    def matmul_cols(self, dst, dstr, specs, src, sstr, ssc, m, k, stream=None):
+        """specs: (w, sc, rows) per job; job j fills the next rows columns."""
+        arr, n = self.jobs((w, sc, None, rows) for w, sc, rows in specs)
+        self._check(self.lib.gemma_hip_matmul_cols(_addr(dst), dstr, arr, n, _addr(src), sstr,
+                                                   _addr(ssc), m, k, stream))
 
     def matmul_multi(self, specs, x, xs, k, stream=None):
         arr, n = self.jobs(specs)

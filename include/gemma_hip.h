@@ -163,6 +163,19 @@ int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,
                            const int8_t *src, const float *ssc, int m,
                            int heads, int hdim, int k, void *stream);
 
+/* gemm_int8 (gemma.c:3937-4054) of one activation block against several
+ * weight matrices that share its K, as adjacent prefill call sites issue
+ * them (up and gate at gemma.c:5365-5372; q, k and v per head at 5084-5087):
+ * the multi-job form of gemma_hip_matmul, as gemma_hip_matmul_multi is of the
+ * GEMV.  Job j (j < njobs <= 3) holds int8 [jobs[j].m][k] dense weights
+ * jobs[j].w and their scales jobs[j].sc, and fills dst columns
+ * [c_j, c_j + jobs[j].m), c_j the sum of the earlier jobs' m; jobs[j].dst is
+ * not used.  src int8 [m][sstr], dst fp32 [m][dstr] (0 strides: dense).
+ * Bit-identical to one gemma_hip_matmul per job. */
+int gemma_hip_matmul_cols(float *dst, int dstr, const gemma_hip_job *jobs, int njobs,
+                          const int8_t *src, int sstr, const float *ssc, int m, int k,
+                          void *stream);
+
 /* gemv_int8_multi (gemma.c:2813-2837): njobs (<= GEMMA_HIP_MAX_JOBS)
  * projections of the one quantized vector x [k] with scale xs (a device
  * pointer to one float). */

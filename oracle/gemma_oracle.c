@@ -160,6 +160,20 @@ void oracle_gemm_int8(float *dst, int dstr, int32_t *acc, const int8_t *mat,
   }
 }
 
+/* The flush of gemm_int8 (gemma.c:3854-3865, scalar tails 3617-3634) over a
+ * matrix of int32 sums computed elsewhere: dst[i][j] = rescale(acc[i][j],
+ * ssc[i], matsc[j]).  Lets a test form the exact sums of a large product with
+ * any exact method and still take every rounding step from this file. */
+void oracle_rescale_matrix(float *dst, const int32_t *acc, const float *ssc,
+                           const float *matsc, int m, int n, int flavor) {
+  for (int i = 0; i < m; i++) {
+    for (int j = 0; j < n; j++) {
+      dst[(size_t)i * n + j] =
+          oracle_rescale(acc[(size_t)i * n + j], ssc[i], matsc[j], flavor);
+    }
+  }
+}
+
 /* gemma.c:2718-2728 / 3074-3112 / 3154-3302, in float64 */
 void oracle_gemm_f64(double *dst, double *absdst, const float *mat, int mstr,
                      const float *src, int sstr, int m, int n, int k) {

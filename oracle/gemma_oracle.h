@@ -63,6 +63,10 @@ void oracle_gemm_int8(float *dst, int dstr, int32_t *acc, const int8_t *mat,
  * compiler vectorises), so the oracle gives the float64 dot product and the
  * float64 sum of |a|*|b| that bounds any fp32 summation's rounding error.
  * Strides of 0 mean dense; dst/absdst are dense [m][n]. */
+/* rescale of precomputed int32 sums (the flush, gemma.c:3854-3865) */
+void oracle_rescale_matrix(float *dst, const int32_t *acc, const float *ssc,
+                           const float *matsc, int m, int n, int flavor);
+
 void oracle_gemm_f64(double *dst, double *absdst, const float *mat, int mstr,
                      const float *src, int sstr, int m, int n, int k);
 

@@ -74,6 +74,8 @@ class Oracle:
         lib.oracle_gemm_int8.restype = None
         lib.oracle_gemm_int8.argtypes = [_f32p, _int, _i32p, _i8p, _int, _f32p, _i8p, _int,
                                          _f32p, _int, _int, _int, _int]
+        lib.oracle_rescale_matrix.restype = None
+        lib.oracle_rescale_matrix.argtypes = [_f32p, _i32p, _f32p, _f32p, _int, _int, _int]
         lib.oracle_gemm_f64.restype = None
         lib.oracle_gemm_f64.argtypes = [_f64p, _f64p, _f32p, _int, _f32p, _int, _int, _int, _int]
         lib.oracle_patch_embed_f64.restype = None
@@ -127,6 +129,33 @@ class Oracle:
                                   _ptr(matsc, _f32p), _ptr(src, _i8p), sstr, _ptr(ssc, _f32p), m,
                                   n, k, flavor)
         return dst, acc
+
+    @staticmethod
+    def int_sums(mat, src) -> np.ndarray:
+        """Exact int32 sums src . mat^T of int8 operands, through a float64
+        product: every product and partial sum is an integer of magnitude at
+        most 127*127*K < 2**53, so any summation order (BLAS blocking, fused
+        multiply-adds) is exact."""
+        k = mat.shape[1]
+        assert 127 * 127 * k < 2 ** 53
+        acc = np.asarray(src, np.float64) @ np.asarray(mat, np.float64).T
+        return np.ascontiguousarray(acc.astype(np.int64).astype(np.int32))
+
+    def rescale_matrix(self, acc, ssc, matsc, flavor: int = GCC):
+        """gemm_int8's flush (gemma.c:3854-3865) of precomputed int32 sums."""
+        acc = np.ascontiguousarray(acc, dtype=np.int32)
+        ssc = np.ascontiguousarray(ssc, dtype=np.float32)
+        matsc = np.ascontiguousarray(matsc, dtype=np.float32)
+        m, n = acc.shape
+        dst = np.empty((m, n), np.float32)
+        self.lib.oracle_rescale_matrix(_ptr(dst, _f32p), _ptr(acc, _i32p), _ptr(ssc, _f32p),
+                                       _ptr(matsc, _f32p), m, n, flavor)
+        return dst
+
+    def gemm_int8_full(self, mat, matsc, src, ssc, flavor: int = GCC):
+        """gemm_int8 (gemma.c:3937-4054) on dense operands at any size: the
+        exact sums of int_sums, then this file's rescale of every cell."""
+        return self.rescale_matrix(self.int_sums(mat, src), ssc, matsc, flavor)
 
     def gemm_f64(self, mat, src, k: int | None = None):
         mat = np.ascontiguousarray(mat, dtype=np.float32)

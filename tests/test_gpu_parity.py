@@ -4,8 +4,9 @@ golden fixtures, every call through the C ABI (include/gemma_hip.h).
 Bar: bit-exact int8 activations, scales, int32 sums (observed through the
 rescale, which is itself bit-exact) and fp32 outputs for the W8A8 path; for
 the fp32 fallback |y - y_exact| <= 1e-5 * sum|a*b| (TOL_F32).
-Large shapes are checked on sampled rows (exact per element) so the oracle
-finishes in seconds.
+GEMM products are compared cell for cell at every size: the oracle forms the
+exact int32 sums of a large product with a float64 matrix product (exact for
+int8 operands, test_oracle.py pins it) and rescales each cell itself.
 """
 
 from __future__ import annotations
@@ -237,31 +238,104 @@ GEMM_SHAPES = [
     ("1b_o", 512, 1152, 1024), ("1b_gate", 512, 6912, 1152), ("1b_down", 512, 1152, 6912),
     ("siglip_qkv", 4096, 1152, 1152), ("siglip_fc1", 4096, 4304, 1152),
     ("siglip_fc2", 4096, 1152, 4304), ("siglip_proj", 256, 2560, 1152),
+    ("4b_q", 2048, 2048, 2560), ("4b_kv", 2048, 1024, 2560), ("4b_o", 2048, 2560, 2048),
     ("4b_gate", 2048, 10240, 2560), ("4b_down", 2048, 2560, 10240),
     ("tiny", 2, 8, 16), ("odd", 77, 333, 112),
 ]
 
 
-@pytest.mark.parametrize("label,m,n,k", GEMM_SHAPES)
-def test_gemm_vs_oracle(gh, oracle, label, m, n, k):
-    note(f"gemm {label} m={m} n={n} k={k}")
-    rng = np.random.default_rng(m * 7 + n + k)
+def quantized_block(gh, oracle, rng, m, k):
+    """m rows of outlier activations quantized on the GPU, checked bit for
+    bit against the oracle's quantize_acts; returns (device q, device
+    scales, oracle q, oracle scales)."""
     A = outlier_acts(rng, (m, k))
-    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
-    bs = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
     Aq = torch.empty((m, k), dtype=torch.int8, device="cuda")
     As = torch.empty(m, dtype=torch.float32, device="cuda")
     gh.quantize(Aq, As, dev(A), k, m, k, stream())
-    dst = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    gh.matmul(dst, n, dev(B), k, dev(bs), Aq, k, As, m, n, k, stream())
     qo, so = oracle.quantize_acts(A)
     assert np.array_equal(host(Aq), qo)
-    # exact check on sampled rows: first/last tile rows and random ones
-    rows = np.unique(np.concatenate([np.arange(min(m, 8)), np.arange(max(0, m - 8), m),
-                                     rng.integers(0, m, min(m, 48))]))
-    ref, _ = oracle.gemm_int8(B, bs, qo[rows], so[rows])
-    got = host(dst)[rows]
-    assert np.array_equal(bits(got), bits(ref)), f"{(bits(got) != bits(ref)).sum()} mismatches"
+    assert np.array_equal(bits(host(As)), bits(so))
+    return Aq, As, qo, so
+
+
+def assert_same(got, ref, what=""):
+    bad = bits(got) != bits(ref)
+    if bad.any():
+        r, c = np.argwhere(bad)[0]
+        raise AssertionError(f"{what}{int(bad.sum())} of {bad.size} cells differ, first at "
+                             f"({r}, {c}): {got[r, c]!r} != {ref[r, c]!r}")
+
+
+@pytest.mark.parametrize("label,m,n,k", GEMM_SHAPES)
+def test_gemm_vs_oracle(gh, oracle, label, m, n, k):
+    """Every cell of the product against the oracle (exact int32 sums through
+    a float64 product, then the oracle's rescale of each cell)."""
+    note(f"gemm {label} m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    Aq, As, qo, so = quantized_block(gh, oracle, rng, m, k)
+    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    dst = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.matmul(dst, n, dev(B), k, dev(bs), Aq, k, As, m, n, k, stream())
+    assert_same(host(dst), oracle.gemm_int8_full(B, bs, qo, so))
+
+
+# The prefill's fused launches over adjacent weight matrices (gemma_hip_matmul_cols):
+# gemma-3-4b q/k/v and gate/up at 2048 tokens, gemma-3-1b at 512, SigLIP
+# q/k/v, and a ragged split whose inner boundaries suit no tile width.
+GEMM_COLS = [
+    ("4b_qkv", 2048, (2048, 1024, 1024), 2560), ("4b_gate_up", 2048, (10240, 10240), 2560),
+    ("1b_qkv", 512, (1024, 256, 256), 1152), ("1b_gate_up", 512, (6912, 6912), 1152),
+    ("siglip_qkv", 4096, (1152, 1152, 1152), 1152), ("ragged", 300, (200, 72, 136), 1040),
+]
+
+
+@pytest.mark.parametrize("label,m,rows,k", GEMM_COLS)
+def test_gemm_cols_vs_oracle(gh, oracle, label, m, rows, k):
+    note(f"gemm cols {label} m={m} rows={rows} k={k}")
+    rng = np.random.default_rng(m + sum(rows) + k)
+    Aq, As, qo, so = quantized_block(gh, oracle, rng, m, k)
+    Bs = [rng.integers(-127, 128, (r, k), dtype=np.int8) for r in rows]
+    bss = [rng.uniform(1e-3, 1e-2, r).astype(np.float32) for r in rows]
+    n = sum(rows)
+    dst = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    gh.matmul_cols(dst, n, [(dev(B), dev(b), r) for B, b, r in zip(Bs, bss, rows)], Aq, k, As,
+                   m, k, stream())
+    ref = oracle.gemm_int8_full(np.concatenate(Bs), np.concatenate(bss), qo, so)
+    assert_same(host(dst), ref)
+
+
+# Every configuration of the ping-pong kernel, forced (GEMMA_HIP_GEMM_PP), on
+# shapes off its tile grid in M, N and K (K = 1040: the last 64-byte stage
+# partial), row-major with a padded stride and head-major, with scales in
+# FTZ/DAZ range so the exact-rescale path runs as well as the plain one.
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_gemm_pp_configs(gh, oracle, monkeypatch, cfg):
+    monkeypatch.setenv("GEMMA_HIP_GEMM_PP", str(cfg))
+    rng = np.random.default_rng(70 + cfg)
+    m, n, k, dstr = 300, 700, 1040, 712
+    qa = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    sa = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
+    B = rng.integers(-127, 128, (n, k), dtype=np.int8)
+    bs = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    for rep in range(2):
+        if rep == 1:  # FTZ products and DAZ (subnormal) scales
+            sa[::7] = 1e-36
+            bs[3::11] = np.float32(5e-39)
+        dst = torch.full((m, dstr), -7.0, dtype=torch.float32, device="cuda")
+        gh.matmul(dst, dstr, dev(B), k, dev(bs), dev(qa), k, dev(sa), m, n, k, stream())
+        got = host(dst)
+        ref, _ = oracle.gemm_int8(B, bs, qa, sa)
+        assert_same(got[:, :n], ref, f"config {cfg} rep {rep}: ")
+        assert np.all(got[:, n:] == -7.0), "cells past n of the padded stride were written"
+    heads, hdim = 3, 256
+    Bh = rng.integers(-127, 128, (heads * hdim, k), dtype=np.int8)
+    bh = rng.uniform(1e-3, 1e-2, heads * hdim).astype(np.float32)
+    dst = torch.full((heads, m, hdim), -7.0, dtype=torch.float32, device="cuda")
+    gh.matmul_heads(dst, dev(Bh), dev(bh), dev(qa), dev(sa), m, heads, hdim, k, stream())
+    ref, _ = oracle.gemm_int8(Bh, bh, qa, sa)
+    ref = np.ascontiguousarray(ref.reshape(m, heads, hdim).transpose(1, 0, 2))
+    assert np.array_equal(bits(host(dst)), bits(ref)), f"config {cfg} head-major"
 
 
 def test_gemm_heads_vs_oracle(gh, oracle):

@@ -80,6 +80,39 @@ def test_gemm_int8_matches_reference(oracle, golden, tag):
     assert np.array_equal(acc.astype(np.int64), brute)
 
 
+@pytest.mark.parametrize("tag", ["tails", "blocks", "m1"])
+def test_gemm_int8_full_matches_reference(oracle, golden, tag):
+    """The large-shape path of the GPU tests (exact sums by a float64 product,
+    then the file's own rescale of every cell) against the reference's
+    fixtures and the scalar restatement, with FTZ-range scales added."""
+    g = golden("gemm_int8")
+    m, n, k, ds, ms, ss = (int(v) for v in g[tag + "_shape"])
+    a, b = g[tag + "_a"][:, :k], g[tag + "_b"][:, :k]
+    full = oracle.gemm_int8_full(b, g[tag + "_bs"], a, g[tag + "_as"])
+    assert np.array_equal(bits(full), bits(g[tag + "_dst"][:, :n]))
+    rng = np.random.default_rng(3)
+    asc = g[tag + "_as"].copy()
+    bsc = g[tag + "_bs"].copy()
+    asc[::3] = 1e-20  # products of 1e-20 and 1e-3..1e-2 scales fall below FLT_MIN
+    bsc[1::4] = rng.uniform(1e-39, 1e-38, bsc[1::4].shape).astype(np.float32)  # subnormal: DAZ
+    slow, _ = oracle.gemm_int8(b, bsc, a, asc)
+    assert np.array_equal(bits(oracle.gemm_int8_full(b, bsc, a, asc)), bits(slow))
+
+
+def test_int_sums_exact_at_full_length(oracle):
+    """int_sums against an int64 brute force at the longest K of the path
+    (gemma-3-4b down, K = 10240) with all-extreme operands, where every
+    partial sum is largest."""
+    rng = np.random.default_rng(5)
+    k = 10240
+    a = rng.choice(np.array([-127, 127], np.int8), (3, k))
+    b = rng.choice(np.array([-127, 127], np.int8), (4, k))
+    b[0] = a[0]  # a sum of exactly 127*127*k
+    got = oracle.int_sums(b, a)
+    assert got[0, 0] == 127 * 127 * k
+    assert np.array_equal(got.astype(np.int64), a.astype(np.int64) @ b.astype(np.int64).T)
+
+
 def test_fpx_reference_within_tolerance_of_exact(oracle, golden):
     """The fp32 fallback has no bit-exact target; the reference's own fp32
     results lie within 1e-5 * sum|a*b| of the exact product, which is the
