@@ -960,10 +960,13 @@ GemmSegs one_seg(const int8_t *mat, const float *matsc, int n) {
 //     fc2 37.7 us (40.0);
 //   128x128 K-alternating (2x2 waves of 64x64, 32x32 MFMA): 4b q 19.0 us (21.6);
 //   128x64 K-alternating, two stages per group step: 4b k/v 13.9 us (18.0).
-// A launch is worth it when the tiles fill at least 3/4 of the CUs; the cost
-// model below (per round: a fixed 5.5 us of launch, prologue and drain, the
-// tile's stores, and the K loop at the configuration's measured rate per CU)
-// picks among the configurations whose tile width divides the segment ends.
+//   gemma-3-4b gate/up as one launch (2048x20480x2560, two rounds of 256x320):
+//     111.6 us (132.5).
+// A launch is worth it when the tiles fill at least 3/4 of the CUs in one
+// round (two for 256x320); the cost model below (per round: a fixed 5.5 us
+// of launch, prologue and drain, the tile's stores, and the K loop at the
+// configuration's measured rate per CU) picks among the configurations whose
+// tile width divides the segment ends.
 struct PpConfig {
   int bm, bn;
   double tops_per_cu;  // K-loop rate per CU, TOPS
@@ -1000,6 +1003,12 @@ int choose_pp(int m, int n, int k, const GemmSegs &bs, const DeviceInfo &dev) {
     const long tiles = (long)((m + c.bm - 1) / c.bm) * ((n + c.bn - 1) / c.bn);
     if (tiles * 4 < 3L * dev.cus) continue;
     const long rounds = (tiles + dev.cus - 1) / dev.cus;
+    // one workgroup per CU pays its prologue and drain every round: past one
+    // round (two for the 256x320 tiles) the DMA kernel, two workgroups per CU,
+    // measured faster (gemma-3-4b q/k/v at 2048 tokens 29.0 us against 38.5
+    // for 128x128 tiles in two rounds; gemma-3-1b gate/up at 512 tokens 16.4
+    // against 21.1; SigLIP q/k/v 28.9 against 35.7)
+    if (rounds > (id == 1 ? 2 : 1)) continue;
     const double area = (double)c.bm * c.bn;
     const double cost = rounds * (5.5 + 6e-5 * area + 2.0 * area * k / (c.tops_per_cu * 1e6));
     if (best == 0 || cost < best_cost) {
