@@ -26,8 +26,7 @@ constexpr int kRowChunks = kBK / 4 + 1;   // float4 chunks per LDS row (+1 pad)
 template <int WM, int WN>
 __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
     float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
-    const float *__restrict__ src, int sstr, int m, int n, int k,
-    const float *__restrict__ bias, bool clamp) {
+    const float *__restrict__ src, int sstr, int m, int n, int k, F32Epilogue ep) {
   constexpr int kBM = 64 * WM, kBN = 64 * WN;
   __shared__ v4f lds_a[2][kBM][kRowChunks];
   __shared__ v4f lds_b[2][kBN][kRowChunks];
@@ -110,16 +109,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
   for (int j = 0; j < WN; ++j) {
     const int col = n0 + wn * 32 * WN + j * 32 + (lane & 31);
     if (col >= n) continue;
-    const float b = bias != nullptr ? bias[col] : 0.0f;
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row =
             m0 + wm * 32 * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        float y = bias != nullptr ? acc[i][j][r] + b : acc[i][j][r];
-        if (clamp) y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y));
-        if (row < m) dst[(size_t)row * dstr + col] = y;
+        if (row < m) dst[(size_t)row * dstr + col] = ep.apply(acc[i][j][r], row, col, dstr);
       }
   }
 }
@@ -127,8 +123,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 // Any shape, any alignment: one thread per output.
 __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
     float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
-    const float *__restrict__ src, int sstr, int m, int n, int k,
-    const float *__restrict__ bias, bool clamp) {
+    const float *__restrict__ src, int sstr, int m, int n, int k, F32Epilogue ep) {
   const int col = blockIdx.x * 64 + (threadIdx.x & 63);
   const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
   if (row >= m || col >= n) return;
@@ -136,9 +131,55 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
   const float *b = mat + (size_t)col * mstr;
   float acc = 0.0f;
   for (int l = 0; l < k; ++l) acc = __builtin_fmaf(a[l], b[l], acc);
-  if (bias != nullptr) acc += bias[col];
-  if (clamp) acc = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, acc));
-  dst[(size_t)row * dstr + col] = acc;
+  dst[(size_t)row * dstr + col] = ep.apply(acc, row, col, dstr);
+}
+
+// The fp64 twin of the fp32 GEMM for the verification modes: each output is
+// the fp64 sum, rounded once by the epilogue.  A workgroup computes a 32 x 64
+// tile, each thread 2 x 4 outputs, over K in LDS chunks of 32.
+constexpr int kF64M = 32, kF64N = 64, kF64K = 32;
+
+__global__ __launch_bounds__(kThreads) void gemm_f64_kernel(
+    float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
+    const float *__restrict__ src, int sstr, int m, int n, int k, F32Epilogue ep) {
+  __shared__ float as[kF64M][kF64K + 1];
+  __shared__ float bs[kF64N][kF64K + 1];
+  const int tid = threadIdx.x;
+  const int m0 = blockIdx.y * kF64M, n0 = blockIdx.x * kF64N;
+  const int tm = tid / 16, tn = tid % 16;  // outputs (m0 + 2 tm + i, n0 + tn + 16 j)
+  double acc[2][4] = {};
+  for (int k0 = 0; k0 < k; k0 += kF64K) {
+    for (int i = tid; i < kF64M * kF64K; i += kThreads) {
+      const int r = i / kF64K, c = i % kF64K;
+      as[r][c] = (m0 + r < m && k0 + c < k) ? src[(size_t)(m0 + r) * sstr + k0 + c] : 0.0f;
+    }
+    for (int i = tid; i < kF64N * kF64K; i += kThreads) {
+      const int r = i / kF64K, c = i % kF64K;
+      bs[r][c] = (n0 + r < n && k0 + c < k) ? mat[(size_t)(n0 + r) * mstr + k0 + c] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int c = 0; c < kF64K; ++c) {
+      const double x0 = as[2 * tm][c], x1 = as[2 * tm + 1][c];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const double w = bs[tn + 16 * j][c];
+        acc[0][j] = fma(x0, w, acc[0][j]);
+        acc[1][j] = fma(x1, w, acc[1][j]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = m0 + 2 * tm + i;
+    if (row >= m) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = n0 + tn + 16 * j;
+      if (col < n) dst[(size_t)row * dstr + col] = ep.apply_f64(acc[i][j], row, col, dstr);
+    }
+  }
 }
 
 }  // namespace
@@ -148,8 +189,13 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_generic_kernel(
 // the GPU idle at 128x128).  GEMMA_HIP_GEMM_F32_TILE=128 or 64 forces one.
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const float *src, int sstr, int m, int n, int k,
-                           const float *bias, bool clamp,
-                           const DeviceInfo &dev, hipStream_t stream) {
+                           const F32Epilogue &ep, const DeviceInfo &dev, hipStream_t stream,
+                           bool f64) {
+  if (f64) {
+    const dim3 grid((n + kF64N - 1) / kF64N, (m + kF64M - 1) / kF64M);
+    gemm_f64_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m, n, k, ep);
+    return hipGetLastError();
+  }
   const bool fast = k % 4 == 0 && mstr % 4 == 0 && sstr % 4 == 0 &&
                     (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
   if (fast) {
@@ -162,18 +208,28 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
     if (big) {
       const dim3 grid((n + 127) / 128, (m + 127) / 128);
       gemm_f32_kernel<2, 2><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
-                                                          n, k, bias, clamp);
+                                                          n, k, ep);
     } else {
       const dim3 grid((n + 63) / 64, (m + 63) / 64);
       gemm_f32_kernel<1, 1><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
-                                                          n, k, bias, clamp);
+                                                          n, k, ep);
     }
   } else {
     const dim3 grid((n + 63) / 64, (m + 3) / 4);
     gemm_f32_generic_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr,
-                                                           src, sstr, m, n, k, bias, clamp);
+                                                           src, sstr, m, n, k, ep);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
+                           const float *src, int sstr, int m, int n, int k,
+                           const float *bias, bool clamp,
+                           const DeviceInfo &dev, hipStream_t stream) {
+  F32Epilogue ep{};
+  ep.bias = bias;
+  ep.clamp = clamp;
+  return launch_gemm_f32(dst, dstr, mat, mstr, src, sstr, m, n, k, ep, dev, stream, false);
 }
 
 }  // namespace gh

@@ -805,6 +805,36 @@ int gemma_hip_vision_attention(float *out, const float *qkv, const float *bias, 
   return 0;
 }
 
+int gemma_hip_prefill_attention(float *out, const float *q, int q_stride, const float *kc,
+                                const float *vc, int n, int pos0, int n_heads, int nkv,
+                                int hdim, int clen, int slide, float asc, float sc_att,
+                                int dense, int mode, void *stream) {
+  const char *name = "gemma_hip_prefill_attention";
+  if (need_init()) return 1;
+  if (!out || !q || !kc || !vc) return fail("%s: null pointer", name);
+  const int hn = nkv > 0 && n_heads % nkv == 0 ? n_heads / nkv : 0;
+  if (n < 1 || pos0 < 0 || hn < 1 || 32 % hn != 0 || (hdim != 128 && hdim != 256) ||
+      n_heads > gh::kPfMaxMergeHeads || (long)n_heads * hdim > q_stride ||
+      (long)pos0 + n > clen || slide < 0 || (long)n * q_stride > (1l << 30) ||
+      (long)nkv * clen * hdim > (1l << 30))
+    return fail("%s: unsupported shape n=%d pos0=%d heads=%d/%d hdim=%d clen=%d stride=%d",
+                name, n, pos0, n_heads, nkv, hdim, clen, q_stride);
+  if (mode != GEMMA_HIP_ATTN_F64 && mode != GEMMA_HIP_ATTN_F32)
+    return fail("%s: unknown mode %d", name, mode);
+  hipStream_t s = pick_stream(stream);
+  double *part = nullptr;
+  GH_CHECK("gemma_hip_prefill_attention: workspace",
+           hipMalloc(&part, gh::pf_attn_part_doubles(n, n_heads, hdim) * sizeof(double)));
+  const gh::PfAttn at{q, q_stride, kc, vc, out, n_heads * hdim, n, pos0, n_heads, nkv, clen,
+                      slide, asc, sc_att, part, 0, 0, 0, dense ? 1 : 0};
+  hipError_t e = gh::launch_pf_attention(at, hdim, mode == GEMMA_HIP_ATTN_F32, s);
+  const hipError_t e2 = hipStreamSynchronize(s);
+  (void)hipFree(part);
+  if (e != hipSuccess || (e = e2) != hipSuccess)
+    return fail("%s: %s", name, hipGetErrorString(e));
+  return 0;
+}
+
 /* ---- host drop-ins ------------------------------------------------------ */
 
 // Inputs up to this size are read by the kernels straight from pinned host
@@ -1697,9 +1727,17 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
   // patch embedding + position embedding (4411-4468)
   if ((e = gh::launch_im2col(v->patches, v->img, c.img_px, c.psize, st)) != hipSuccess)
     return e;
-  const gh::VisPatch pa{v->patches, v->pe, v->pe_b, v->pos_q, v->pos_s, v->x, n,
-                        3 * c.psize * c.psize, dim};
-  if ((e = gh::launch_vis_patch(pa, st)) != hipSuccess) return e;
+  // the patch GEMM (the a9 path: fp32 matrix cores; fp64 in the verification
+  // mode) with the bias, clamp and position embedding in its epilogue
+  gh::F32Epilogue pe{};
+  pe.bias = v->pe_b;
+  pe.clamp = true;
+  pe.pos_q = v->pos_q;
+  pe.pos_s = v->pos_s;
+  const int kdim = 3 * c.psize * c.psize;
+  if ((e = gh::launch_gemm_f32(v->x, dim, v->pe, kdim, v->patches, kdim, n, dim, kdim, pe,
+                               g.info, st, !v->attn_f32)) != hipSuccess)
+    return e;
   for (int l = 0; l < c.nl; ++l) {
     const auto &L = v->layers[l];
     // residual of the previous layer's MLP (fc2 bias), first layer norm (4474-4484)

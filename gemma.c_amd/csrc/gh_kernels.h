@@ -97,6 +97,40 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const float *bias, bool clamp,
                            const DeviceInfo &dev, hipStream_t stream);
 
+// What the fp32 GEMM does with a finished sum s of output (row, col):
+//   y = s (+ bias[col]), clamped to [-FLT_MAX, FLT_MAX] when clamp is set;
+//   with pos_q: y = clamp(y + (float)pos_q[row][col] * pos_s[row]) -- the
+//   dequantized position embedding of the SigLIP patch embedding
+//   (gemma.c:4411-4468), whose rows are dstr wide.
+struct F32Epilogue {
+  const float *bias;
+  bool clamp;
+  const int8_t *pos_q;
+  const float *pos_s;
+  __device__ __forceinline__ float finish(float y, int row, int col, int dstr) const {
+    if (clamp) y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y));
+    if (pos_q != nullptr) {
+      const float pos = (float)pos_q[(size_t)row * dstr + col] * pos_s[row];
+      y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y + pos));
+    }
+    return y;
+  }
+  // an fp32 sum: the bias is one fp32 addition
+  __device__ __forceinline__ float apply(float s, int row, int col, int dstr) const {
+    return finish(bias != nullptr ? s + bias[col] : s, row, col, dstr);
+  }
+  // an fp64 sum: the sum and the bias rounded once
+  __device__ __forceinline__ float apply_f64(double s, int row, int col, int dstr) const {
+    return finish((float)(bias != nullptr ? s + (double)bias[col] : s), row, col, dstr);
+  }
+};
+// ... with a full epilogue; f64 selects the fp64 twin (every output rounded
+// once from its fp64 sum), the verification mode of the vision tower.
+hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
+                           const float *src, int sstr, int m, int n, int k,
+                           const F32Epilogue &ep, const DeviceInfo &dev, hipStream_t stream,
+                           bool f64);
+
 // patch.hip: a [npatch][3*psize*psize] = patches of the HWC image, in the K
 // order of the SigLIP patch-embedding weight [dim][3][psize][psize].
 hipError_t launch_im2col(float *a, const float *img, int img_px, int psize,
@@ -213,6 +247,7 @@ struct PfAttn {
   int dense;
 };
 constexpr int kPfMaxSplit = 8;
+constexpr int kPfMaxMergeHeads = 64;  // q heads the key-split merge handles
 // doubles of PfAttn::part for n rows
 inline size_t pf_attn_part_doubles(size_t n, size_t n_heads, size_t hdim) {
   return (size_t)kPfMaxSplit * n * n_heads * (hdim + 2);
@@ -232,14 +267,6 @@ hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, floa
                                 const WarmRegions &warm, hipStream_t stream);
 
 // vision.hip: the SigLIP tower (forward_vision).
-// x [m][dim] = clamp(patches [m][k] . pe [dim][k] + pe_b) + pos_q * pos_s, in fp64
-struct VisPatch {
-  const float *patches, *pe, *pe_b;
-  const int8_t *pos_q;
-  const float *pos_s;
-  float *x;
-  int m, k, dim;
-};
 // per row: x = clamp((y + bias) + x) when y is given; LayerNorm(x; w, b) into
 // xq/xs (quantized) or, when xq is null, into h
 struct VisLn {
@@ -268,7 +295,6 @@ struct VisPool {
   int dim, ppi, ksize;
   float eps;
 };
-hipError_t launch_vis_patch(const VisPatch &a, hipStream_t stream);
 hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream);
 // head dim 16, 32, 64, 72 or 128
 // f32: on the fp32 matrix cores (otherwise fp64, rounded once)

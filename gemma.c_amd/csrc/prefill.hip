@@ -144,7 +144,6 @@ __global__ __launch_bounds__(64) void pf_qk_rope_kernel(PfRope a) {
 constexpr int kPaQ = 64;              // query vectors per workgroup (head dim 128)
 constexpr int kPaPairWaves = 8;       // waves per workgroup (head dim 256): 4 pairs
 constexpr int kPaQPair = kPaPairWaves * 8;  // query vectors per workgroup (16 per pair)
-constexpr int kPfMaxMergeHeads = 64;  // q heads the merge handles
 constexpr int kPaKeys = 32;           // keys per tile (register-staged kernel)
 constexpr double kPaSlack = 64.0;     // p <= e^64: sums stay far below DBL_MAX
 constexpr double kPaFloor = -1e300;   // |score| <= 256 * FLT_MAX^2 << 1e300

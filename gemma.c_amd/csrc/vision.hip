@@ -17,60 +17,6 @@
 namespace gh {
 namespace {
 
-// Patch embedding as a GEMM over im2col patches (gemma.c:4411-4448), in fp64:
-// x[p][oc] = clamp((float)(sum_k a[p][k] * pe[oc][k] + pe_b[oc])), then the
-// position embedding row p dequantized in fp32 and added (4452-4468):
-// x = clamp(x + (float)q * scale).  A workgroup computes a 32 x 64 tile,
-// each thread 2 x 4 outputs, over K in LDS chunks of 32.
-constexpr int kVpM = 32, kVpN = 64, kVpK = 32;
-
-__global__ __launch_bounds__(kNT) void vis_patch_kernel(VisPatch a) {
-  __shared__ float as[kVpM][kVpK + 1];
-  __shared__ float bs[kVpN][kVpK + 1];
-  const int tid = threadIdx.x;
-  const int m0 = blockIdx.x * kVpM, n0 = blockIdx.y * kVpN;
-  const int tm = tid / 16, tn = tid % 16;  // outputs (m0 + 2 tm + i, n0 + tn + 16 j)
-  double acc[2][4] = {};
-  for (int k0 = 0; k0 < a.k; k0 += kVpK) {
-    for (int i = tid; i < kVpM * kVpK; i += kNT) {
-      const int r = i / kVpK, c = i % kVpK;
-      as[r][c] = (m0 + r < a.m && k0 + c < a.k) ? a.patches[(size_t)(m0 + r) * a.k + k0 + c]
-                                                 : 0.0f;
-    }
-    for (int i = tid; i < kVpN * kVpK; i += kNT) {
-      const int r = i / kVpK, c = i % kVpK;
-      bs[r][c] = (n0 + r < a.dim && k0 + c < a.k) ? a.pe[(size_t)(n0 + r) * a.k + k0 + c]
-                                                   : 0.0f;
-    }
-    lds_barrier();
-#pragma unroll 4
-    for (int c = 0; c < kVpK; ++c) {
-      const double x0 = as[2 * tm][c], x1 = as[2 * tm + 1][c];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const double w = bs[tn + 16 * j][c];
-        acc[0][j] = fma(x0, w, acc[0][j]);
-        acc[1][j] = fma(x1, w, acc[1][j]);
-      }
-    }
-    lds_barrier();
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int p = m0 + 2 * tm + i;
-    if (p >= a.m) continue;
-    const float scale = a.pos_s[p];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int oc = n0 + tn + 16 * j;
-      if (oc >= a.dim) continue;
-      const float e = clamp_f32((float)(acc[i][j] + (double)a.pe_b[oc]));
-      const float pos = (float)a.pos_q[(size_t)p * a.dim + oc] * scale;
-      a.x[(size_t)p * a.dim + oc] = clamp_f32(e + pos);
-    }
-  }
-}
-
 // One workgroup per row.  With y: x[r] = clamp((y[r] + bias) + x[r]) (the
 // output bias and the residual, gemma.c:4575-4590, 4641-4656), stored back
 // as the new residual.  Then LayerNorm (layernorm, gemma.c:2526-2549) in
@@ -631,12 +577,6 @@ hipError_t by_npt(int npt, F &&launch) {
 }
 
 }  // namespace
-
-hipError_t launch_vis_patch(const VisPatch &a, hipStream_t stream) {
-  const dim3 grid((a.m + kVpM - 1) / kVpM, (a.dim + kVpN - 1) / kVpN);
-  vis_patch_kernel<<<grid, kNT, 0, stream>>>(a);
-  return hipGetLastError();
-}
 
 hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
   // the fewest threads per row that cover it in kPfMaxNpt chunks: more rows

@@ -103,6 +103,8 @@ _SIGS = {
     "gemma_hip_perf_read": (_I, [ctypes.POINTER(PerfEntry), _I, ctypes.POINTER(_I)]),
     "gemma_hip_matmul_heads": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "gemma_hip_matmul_cols": (_I, [_P, _I, ctypes.POINTER(Job), _I, _P, _I, _P, _I, _I, _P]),
+    "gemma_hip_prefill_attention": (_I, [_P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                                         ctypes.c_float, ctypes.c_float, _I, _I, _P]),
     "gemma_hip_matmul_multi": (_I, [ctypes.POINTER(Job), _I, _P, _P, _I, _P]),
     "gemma_hip_quantize_matmul": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P, _P, _P]),
     "gemma_hip_matmul_f32": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
@@ -258,6 +260,13 @@ class GemmaHip:
                                                    _addr(work), stream))
 
     # weights ---------------------------------------------------------------
+    def prefill_attention(self, out, q, q_stride, kc, vc, n, pos0, n_heads, nkv, hdim, clen,
+                          slide, asc, sc_att, dense, mode, stream=None):
+        """gemma_hip_prefill_attention on device pointers."""
+        self._check(self.lib.gemma_hip_prefill_attention(
+            _addr(out), _addr(q), q_stride, _addr(kc), _addr(vc), n, pos0, n_heads, nkv, hdim,
+            clen, slide, float(asc), float(sc_att), 1 if dense else 0, mode, stream))
+
     def vision_attention(self, out, qkv, bias, n, n_heads, dim, mode=0, stream=None):
         """gemma_hip_vision_attention on device pointers."""
         self._check(self.lib.gemma_hip_vision_attention(_addr(out), _addr(qkv), _addr(bias), n,

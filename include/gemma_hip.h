@@ -400,15 +400,17 @@ void gemma_hip_vision_destroy(gemma_hip_vision *vis);
  * soft tokens, what forward_vision leaves in tb->x) out. */
 int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out);
 
-/* The arithmetic of the tower's attention (gemma.c:4533-4561; set before
- * forward, kept until changed):
+/* The arithmetic of the tower's two fp32 products, its attention
+ * (gemma.c:4533-4561) and its patch embedding (4411-4448, im2col and a GEMM
+ * with the bias, clamp and position embedding of 4452-4468 in its epilogue);
+ * set before forward, kept until changed:
  *   GEMMA_HIP_ATTN_F32 (the default) -- fp32 matrix cores, fp32 throughout
  *     as the reference computes it (its summation order differs), so results
  *     agree with the exact form to fp32 rounding, amplified where a later
  *     int8 quantization flips;
- *   GEMMA_HIP_ATTN_F64 -- fp64 matrix cores at half the rate, every output
- *     rounded once from the exact sum: the verification mode, equal to an
- *     fp64 evaluation of the same formulas.
+ *   GEMMA_HIP_ATTN_F64 -- fp64 (matrix cores for the attention), every
+ *     output rounded once from the exact sum: the verification mode, equal
+ *     to an fp64 evaluation of the same formulas.
  * The rest of the tower is unchanged.  0 or 1 on an unknown mode. */
 int gemma_hip_vision_set_attention(gemma_hip_vision *vis, int mode);
 
@@ -420,6 +422,24 @@ int gemma_hip_vision_set_attention(gemma_hip_vision *vis, int mode);
  * (NULL: the library's). */
 int gemma_hip_vision_attention(float *out, const float *qkv, const float *bias, int n,
                                int n_heads, int dim, int mode, void *stream);
+
+/* The prompt pass's attention block alone (forward_text_chunk's blockwise
+ * attention, gemma.c:5152-5293, and its dense form 5258-5290), as
+ * gemma_hip_vision_attention is for the tower, so that its kernels can be
+ * checked before any int8 requantization: no counterpart function in the
+ * reference.  q [n][q_stride] holds the n rows' q heads after RoPE (head h
+ * at column h*hdim, n_heads*hdim <= q_stride); kc / vc [nkv][clen][hdim]
+ * hold the keys and values of positions 0 .. pos0+n-1 (the rows' own at
+ * pos0 .. pos0+n-1); out [n][n_heads*hdim].  Row i sits at position pos0+i:
+ * dense == 0 attends causally to keys max(0, pos0+i+1-slide) .. pos0+i
+ * (slide 0: no window), dense == 1 to every key 0 .. pos0+n-1.  Scores are
+ * q.k * asc, capped as tanh(s / sc_att) * sc_att when sc_att != 0; mode is
+ * GEMMA_HIP_ATTN_F32 or GEMMA_HIP_ATTN_F64 as for the decoder.  hdim 128 or
+ * 256; n_heads / nkv must divide 32.  Allocates its key-split workspace. */
+int gemma_hip_prefill_attention(float *out, const float *q, int q_stride, const float *kc,
+                                const float *vc, int n, int pos0, int n_heads, int nkv,
+                                int hdim, int clen, int slide, float asc, float sc_att,
+                                int dense, int mode, void *stream);
 
 /* forward_gemma_image (gemma.c:5561-5595) on the device: the vision tower on
  * img, its img_tok soft tokens handed to the decoder in HBM, and the dense

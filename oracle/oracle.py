@@ -57,6 +57,7 @@ class Oracle:
     """ctypes binding of gemma_oracle.c."""
 
     def __init__(self, path: str = LIB_PATH):
+        self.margins = None  # requantization margins while tracking (track_margins)
         if not os.path.exists(path):
             raise FileNotFoundError(f"oracle library not built: {path}")
         lib = ctypes.CDLL(path)
@@ -82,10 +83,40 @@ class Oracle:
         lib.oracle_patch_embed_f64.argtypes = [_f64p, _f64p, _f32p, _f32p, _f32p, _int, _int, _int]
         self.lib = lib
 
+    # -- requantization margins -------------------------------------------
+    # While tracking, every quantize_act(s) call records the smallest distance,
+    # over its rows' elements, of t = |v| * 127 / amax (the quantizer's
+    # argument before rounding, gemma.c:2621-2646, in exact arithmetic) from a
+    # rounding boundary k + 1/2.  An input that differs from the oracle's by
+    # at most eps * amax moves every t by at most 254 eps (plus the fp32
+    # rounding of v * inv on both sides), so a pass whose smallest margin
+    # exceeds that bound quantizes every element to the oracle's int8 value.
+    def track_margins(self) -> None:
+        self.margins = []
+
+    def min_margin(self) -> float:
+        """Smallest margin since track_margins (inf when nothing was quantized)."""
+        return min(self.margins) if self.margins else float("inf")
+
+    @staticmethod
+    def row_margins(rows: np.ndarray) -> float:
+        rows = np.atleast_2d(np.asarray(rows, np.float64))
+        amax = np.abs(rows).max(axis=1, keepdims=True)
+        live = amax[:, 0] > 0
+        if not live.any():
+            return float("inf")
+        t = np.abs(rows[live]) * (127.0 / amax[live])
+        return float(np.abs(t - np.floor(t) - 0.5).min())
+
+    def _record(self, rows) -> None:
+        if getattr(self, "margins", None) is not None:
+            self.margins.append(self.row_margins(rows))
+
     def quantize_act(self, vec: np.ndarray, flavor: int = GCC):
         vec = np.ascontiguousarray(vec, dtype=np.float32)
         q = np.empty(vec.shape[0], np.int8)
         s = self.lib.oracle_quantize_act(_ptr(q, _i8p), _ptr(vec, _f32p), vec.shape[0], flavor)
+        self._record(vec)
         return q, np.float32(s)
 
     def quantize_acts(self, src: np.ndarray, n: int | None = None, flavor: int = GCC):
@@ -97,6 +128,7 @@ class Oracle:
         s = np.empty(m, np.float32)
         self.lib.oracle_quantize_acts(_ptr(q, _i8p), _ptr(s, _f32p), _ptr(src, _f32p), sstr, m,
                                       n, flavor)
+        self._record(src[:, :n])
         return q, s
 
     def gemv_int8(self, mat, matsc, vec, vsc, flavor: int = GCC):

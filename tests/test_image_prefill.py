@@ -12,11 +12,13 @@ same argmax).  Oracle or device against the reference program: the reference
 evaluates the glue in fp32, so the two agree to fp32 rounding (measured
 6e-8 .. 3.2e-7 of the largest logit) until an fp32 difference straddles an
 int8 requantization boundary, which moves this random model's logits by 1%
-to 4% from there on; the comparison runs on seeds measured flip-free, with
-the bound REL_PRE_FLIP (among them a 256-token image, as gemma 3 feeds one).
-It is sharp: causal attention over the image block moves the logits by 13% to
-20%, and a sliding window kept in the dense path (16 image tokens under a
-window of 8) by 48%.
+to 4% from there on.  Which applies is decided before the run from the
+oracle's requantization margins over the whole chain (tests/flips.py): a
+chain the criterion clears is held to REL_PRE_FLIP, any other to the flip
+level, with the argmax wherever the reference's lead exceeds what that level
+can move.  The tight bound is sharp: causal attention over the image block
+moves the logits by 13% to 20%, and a sliding window kept in the dense path
+(16 image tokens under a window of 8) by 48%.
 """
 
 from __future__ import annotations
@@ -33,8 +35,11 @@ from gemma_hip import ATTN_F32, ATTN_F64
 from oracle import decode_oracle as dorc
 from oracle import vision_oracle as vorc
 
+import flips
+
 LOGIT_TOL = 1e-5
 REL_PRE_FLIP = 1e-5
+REL_FLIP_LEVEL = 5e-2
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 E2E_CPU = os.path.join(REPO, "oracle", "_ref", "gemma_e2e_cpu")
@@ -51,11 +56,11 @@ VISION = {
     # 256 patches, unpooled: a gemma-3 image's 256 soft tokens
     "tok256": dict(nl=1, n_heads=2, img_px=224, psize=14, dim=64, mlp_dim=128, img_tok=256),
 }
-# shape, vision weight seed, image seed, text layers (measured flip-free against
-# the reference; with 256 image tokens only a single text layer stays clear of
-# requantization flips on some seeds)
+# shape, vision weight seed, image seed, text layers (the bar of each comes
+# from the margin criterion; hd72_s7 and hd16_s8 are seeds taken as they come)
 REF_CASES = {"hd72": ("hd72", 1, 101, 2), "hd16": ("hd16", 4, 104, 2),
-             "tok256": ("tok256", 2, 102, 1)}
+             "tok256": ("tok256", 2, 102, 1), "hd72_s7": ("hd72", 7, 107, 2),
+             "hd16_s8": ("hd16", 8, 108, 2)}
 
 
 def mm_model(path, shape, seed, layers=2, text="gemma-3-270m"):
@@ -115,6 +120,20 @@ def device_chain(gh, model, img, bos, prompt, tokens, steps, clen, attention):
 
 def rel_rows(got, ref):
     return np.abs(got - ref).max(axis=1) / np.abs(ref).max(axis=1)
+
+
+def check_against_reference(got, ref, margin, what):
+    """Every stage's logits within the bar the oracle's margin sets, and the
+    argmax of every stage where the reference's lead is clear of that bar."""
+    free = margin > flips.MARGIN_BOUND
+    bar = REL_PRE_FLIP if free else REL_FLIP_LEVEL
+    rel = rel_rows(got, ref)
+    print(f"{what} ({'flip-free' if free else 'may flip'}): "
+          f"{np.array2string(rel, precision=2)}", flush=True)
+    assert rel.max() <= bar
+    for i, (g, r) in enumerate(zip(got, ref)):
+        if flips.clear_argmax(r, bar):
+            assert int(np.argmax(g)) == int(np.argmax(r)), f"{what}: stage {i}"
 
 
 def run_reference_image(tmp_path, case, prompt_len=5, steps=3):
@@ -195,13 +214,9 @@ def test_oracle_image_follows_reference_program(tmp_path, oracle, case):
     reference's source, against the oracle's chain, stage by stage."""
     model, img, res, ref = run_reference_image(tmp_path, case)
     clen = 1 + res["img_tok"] + len(res["prompt"]) + len(res["tokens"])
-    got, _ = oracle_chain(model, oracle, img, res["bos"], res["prompt"], res["tokens"],
-                          len(ref) - 2, clen)
-    rel = rel_rows(got, ref)
-    print(f"oracle vs reference image prompt ({case}): {np.array2string(rel, precision=2)}",
-          flush=True)
-    assert rel.max() <= REL_PRE_FLIP
-    assert res["tokens"][0] == int(np.argmax(got[1]))
+    (got, _), margin = flips.tracked(oracle, oracle_chain, model, oracle, img, res["bos"],
+                                     res["prompt"], res["tokens"], len(ref) - 2, clen)
+    check_against_reference(got, ref, margin, f"oracle vs reference image prompt ({case})")
 
 
 @needs_e2e
@@ -289,20 +304,16 @@ def test_prefill_rows_dense_matches_oracle(gh, oracle, gqa_model, n, pos0):
 
 # The dense rows with the prompt pass's attention on the fp32 matrix cores
 # (GEMMA_HIP_ATTN_F32: the fp32 kernel's bidirectional form, head dims 256
-# and 128).  Where no int8 requantization flips, the logits agree with the
-# fp64 oracle to fp32 rounding (the flip-free cases measured 0: the last
-# row's logits come out bit-identical); the cases measured with a flip (the
-# 256 rows at gemma-3-270m widths, 1.2% of the largest logit, and the
-# multi-row ones at gemma-3-4b widths, 1.7% and 1.8%: in the dense form every
-# row's flips reach the last row through its keys and values in the next
-# layer) are held to the flip level and the argmax, as the causal fp32 cases
-# of test_decoder.py.
+# and 128) against the fp64 oracle, the bar from the margin criterion as in
+# test_decoder.py (fp32 rounding where the oracle's pass is clear of every
+# requantization boundary; else the flip level, measured 1.2% .. 1.8%, and
+# the argmax where its lead is clear).  The dense kernels themselves are
+# pinned before any requantization in tests/test_attention.py.
 F32_PRE_FLIP = 1e-6
 F32_FLIP_LEVEL = 5e-2
-F32_DENSE_CASES = [  # model, rows, first position, measured with a flip
-    ("two", 77, 30, False), ("two", 256, 1, True), ("hd128", 77, 30, False),
-    ("hd128", 200, 3, False), ("gqa", 1, 5, False), ("gqa", 77, 30, True),
-    ("gqa", 256, 1, True)]
+F32_DENSE_CASES = [  # model, rows, first position
+    ("two", 77, 30), ("two", 256, 1), ("hd128", 77, 30), ("hd128", 200, 3), ("gqa", 1, 5),
+    ("gqa", 77, 30), ("gqa", 256, 1)]
 
 
 @pytest.fixture(scope="module")
@@ -314,9 +325,9 @@ def hd128_model(tmp_path_factory):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("key,n,pos0,flip", F32_DENSE_CASES)
+@pytest.mark.parametrize("key,n,pos0", F32_DENSE_CASES)
 def test_prefill_rows_dense_f32_attention(gh, oracle, text_models, hd128_model, gqa_model, key,
-                                          n, pos0, flip):
+                                          n, pos0):
     model = {"two": text_models.get("two"), "hd128": hd128_model, "gqa": gqa_model}[key]
     nv, dim = model["config"]["nvocab"], model["config"]["dim"]
     rng = np.random.default_rng(n)
@@ -327,17 +338,25 @@ def test_prefill_rows_dense_f32_attention(gh, oracle, text_models, hd128_model, 
     try:
         dec.set_attention(dec.ATTN_F32)
         ref = dorc.DecodeOracle(model, oracle, clen)
-        ref.prefill(prefix, 0)
-        want = ref.prefill(None, pos0, rows=rows, mask=False)
+        oracle.track_margins()
+        try:
+            ref.prefill(prefix, 0)
+            want = ref.prefill(None, pos0, rows=rows, mask=False)
+            free = oracle.min_margin() > flips.MARGIN_BOUND
+        finally:
+            oracle.margins = None
         lg = np.empty(nv, np.float32)
         dec.prefill(prefix, 0)
         nxt = dec.prefill_rows(rows, pos0, False, lg)
     finally:
         dec.close()
+    bar = F32_PRE_FLIP if free else F32_FLIP_LEVEL
     rel = float(np.abs(lg - want).max() / np.abs(want).max())
-    print(f"dense rows {key} {n} at {pos0}, fp32 attention: {rel:.3g}", flush=True)
-    assert rel <= (F32_FLIP_LEVEL if flip else F32_PRE_FLIP)
-    assert nxt == int(np.argmax(want))
+    print(f"dense rows {key} {n} at {pos0}, fp32 attention "
+          f"({'flip-free' if free else 'may flip'}): {rel:.3g}", flush=True)
+    assert rel <= bar
+    if flips.clear_argmax(want, bar):
+        assert nxt == int(np.argmax(want))
 
 
 @pytest.mark.gpu
@@ -362,19 +381,17 @@ def test_gemma_image_matches_oracle(gh, oracle, tmp_path, shape):
 @needs_e2e
 @pytest.mark.parametrize("case", sorted(REF_CASES))
 @pytest.mark.parametrize("mode", ["f32", "f64"])
-def test_device_image_follows_reference_program(gh, tmp_path, case, mode):
+def test_device_image_follows_reference_program(gh, oracle, tmp_path, case, mode):
     """The device chain against forward_gemma_image compiled from the
-    reference's source (flip-free seeds, as above), with the attention in
-    fp32 (the default) and in fp64."""
+    reference's source (bars from the margin criterion, as above), with the
+    attention in fp32 (the default) and in fp64."""
     model, img, res, ref = run_reference_image(tmp_path, case)
     clen = 1 + res["img_tok"] + len(res["prompt"]) + len(res["tokens"])
+    _, margin = flips.tracked(oracle, oracle_chain, model, oracle, img, res["bos"],
+                              res["prompt"], res["tokens"], len(ref) - 2, clen)
     got, nxt, _ = device_chain(gh, model, img, res["bos"], res["prompt"], res["tokens"],
                                len(ref) - 2, clen, ATTN_F32 if mode == "f32" else ATTN_F64)
-    rel = rel_rows(got, ref)
-    print(f"device ({mode}) vs reference image prompt ({case}): "
-          f"{np.array2string(rel, precision=2)}", flush=True)
-    assert rel.max() <= REL_PRE_FLIP
-    assert nxt[1:] == res["tokens"]
+    check_against_reference(got, ref, margin, f"device ({mode}) vs reference image prompt ({case})")
 
 
 @pytest.mark.gpu

@@ -113,6 +113,34 @@ def test_int_sums_exact_at_full_length(oracle):
     assert np.array_equal(got.astype(np.int64), a.astype(np.int64) @ b.astype(np.int64).T)
 
 
+def test_requantization_margins(oracle):
+    """The margin record (tests/flips.py) in closed form: an element whose
+    scaled magnitude sits exactly on a boundary has margin 0; one at an
+    integer has 1/2; perturbing a vector by less than its margin keeps every
+    int8 value, and by more than the margin changes one."""
+    amax = np.float32(127.0)  # t = |v|
+    oracle.track_margins()
+    oracle.quantize_act(np.array([amax, 3.5, -2.0], np.float32))
+    assert oracle.min_margin() == 0.0
+    oracle.track_margins()
+    oracle.quantize_acts(np.array([[amax, 3.0, -2.0], [0, 0, 0]], np.float32))
+    assert oracle.min_margin() == 0.5
+    oracle.margins = None
+    rng = np.random.default_rng(1)
+    v = rng.standard_normal(512).astype(np.float32)
+    m = oracle.row_margins(v)
+    q, _ = oracle.quantize_act(v)
+    amx = float(np.abs(v).max())
+    safe = v + np.float32(0.4 * m * amx / 127.0) * np.sign(rng.standard_normal(512)).astype(np.float32)
+    safe[np.argmax(np.abs(v))] = v[np.argmax(np.abs(v))]  # keep amax
+    assert np.array_equal(oracle.quantize_act(safe)[0], q)
+    i = int(np.argmin(np.abs(np.abs(v) * 127.0 / amx - np.floor(np.abs(v) * 127.0 / amx) - 0.5)))
+    t = abs(float(v[i])) * 127.0 / amx
+    push = v.copy()
+    push[i] = np.float32(np.sign(v[i]) * (np.floor(t) + 0.5 + (0.01 if t < np.floor(t) + 0.5 else -0.01)) * amx / 127.0)
+    assert not np.array_equal(oracle.quantize_act(push)[0], q)
+
+
 def test_fpx_reference_within_tolerance_of_exact(oracle, golden):
     """The fp32 fallback has no bit-exact target; the reference's own fp32
     results lie within 1e-5 * sum|a*b| of the exact product, which is the

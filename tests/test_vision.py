@@ -25,6 +25,8 @@ import model_bin
 from gemma_hip import ATTN_F32, ATTN_F64
 from oracle import vision_oracle as vorc
 
+import flips
+
 TOL = 1e-5
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -73,6 +75,10 @@ SHAPES = {
     # runs), the 1152-wide layer-norm rows and multi-chunk GELU rows of
     # config 4, pooled 4x4 to 16 tokens
     "siglip": dict(nl=2, n_heads=16, img_px=224, psize=14, dim=1152, mlp_dim=4304, img_tok=16),
+    # one layer over 1 and 4 patches: few enough quantized values that the
+    # margin criterion (tests/flips.py) can clear whole passes
+    "tiny": dict(nl=1, n_heads=2, img_px=28, psize=14, dim=32, mlp_dim=64, img_tok=4),
+    "small": dict(nl=1, n_heads=2, img_px=56, psize=14, dim=32, mlp_dim=64, img_tok=4),
 }
 
 
@@ -95,23 +101,39 @@ def test_vision_matches_oracle(gh, oracle, shape):
     assert np.array_equal(got, again)  # deterministic
 
 
-# The fp32-matrix-core attention (GEMMA_HIP_ATTN_F32) in the whole tower: on
-# seeds measured free of int8 requantization flips it agrees with the fp64
-# oracle to fp32 rounding (measured 5e-8 .. 1.5e-7 of the largest output); at
-# SigLIP's widths a flip is certain somewhere, and one moves the pooled soft
-# tokens by ~1% (measured 1.0% .. 1.4% max, 0.2% median), so there the bar is
-# the flip level.  The attention kernel itself is pinned directly below.
-F32_TOWER_CASES = [("hd16", 7, 8), ("hd16", 8, 9), ("hd72", 8, 9), ("hd72", 9, 10)]
+# The default arithmetic (GEMMA_HIP_ATTN_F32: the patch embedding and the
+# attention on the fp32 matrix cores) in the whole tower, against the fp64
+# oracle.  The bar of each case is decided before the device runs, from the
+# oracle's requantization margins (tests/flips.py): a pass with no quantizer
+# argument within reach of fp32 rounding of a boundary agrees to fp32
+# rounding (F32_PRE_FLIP); any other may flip an int8 activation, which moves
+# the pooled soft tokens by ~1% (F32_FLIP_LEVEL).  The attention and patch
+# kernels themselves are pinned directly (below, and test_gpu_parity.py).
+F32_TOWER_CASES = [("tiny", 2, 102), ("tiny", 4, 104), ("small", 1, 101), ("small", 5, 105),
+                   ("hd16", 7, 8), ("hd72", 8, 9)]
 F32_PRE_FLIP = 1e-6
 F32_FLIP_LEVEL = 5e-2
 
 
+def oracle_tower(oracle, shape, seed, img_seed, text_dim=64):
+    """(weights, image, the oracle's soft tokens, whether the pass is flip-free)"""
+    vis = model_bin.synth_vision(seed=seed, text_dim=text_dim, **SHAPES[shape])
+    img = model_bin.synth_image(SHAPES[shape]["img_px"], seed=img_seed)
+    want, margin = flips.tracked(oracle, vorc.VisionOracle(vis, oracle).forward, img)
+    return vis, img, want, margin > flips.MARGIN_BOUND
+
+
+def test_f32_tower_cases_exercise_both_bars(oracle):
+    """The case list holds passes the criterion clears (so the fp32-rounding
+    bar is really applied) and passes it does not."""
+    free = [oracle_tower(oracle, *case)[3] for case in F32_TOWER_CASES]
+    assert sum(free) >= 2 and not all(free)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("shape,seed,img_seed", F32_TOWER_CASES)
-def test_vision_f32_attention_matches_oracle(gh, oracle, shape, seed, img_seed):
-    vis = model_bin.synth_vision(seed=seed, text_dim=64, **SHAPES[shape])
-    img = model_bin.synth_image(SHAPES[shape]["img_px"], seed=img_seed)
-    want = vorc.VisionOracle(vis, oracle).forward(img)
+def test_vision_f32_matches_oracle(gh, oracle, shape, seed, img_seed):
+    vis, img, want, free = oracle_tower(oracle, shape, seed, img_seed)
     tower = gh.vision(vis)
     try:
         got = tower.forward(img)  # the default: ATTN_F32
@@ -123,11 +145,11 @@ def test_vision_f32_attention_matches_oracle(gh, oracle, shape, seed, img_seed):
     finally:
         tower.close()
     rel = float(np.abs(got - want).max() / np.abs(want).max())
-    print(f"vision f32 attention {shape} seed {seed}: {rel:.3g}", flush=True)
-    assert rel <= F32_PRE_FLIP
+    print(f"vision f32 {shape} seed {seed} ({'flip-free' if free else 'may flip'}): {rel:.3g}",
+          flush=True)
+    assert rel <= (F32_PRE_FLIP if free else F32_FLIP_LEVEL)
     assert np.array_equal(got, again)
-    assert np.array_equal(exact, want) or float(np.abs(exact - want).max()) <= TOL * float(
-        np.abs(want).max())  # switching to the fp64 path
+    assert float(np.abs(exact - want).max()) <= TOL * float(np.abs(want).max())  # fp64 mode
     assert np.array_equal(back, got)  # and back
 
 
@@ -220,14 +242,17 @@ def test_vision_argument_errors(gh):
 # ------------------------------------------------- against the reference program
 # forward_vision itself (compiled from the reference's source by oracle/Makefile,
 # run by oracle/e2e_harness.c on a multimodal .bin written by model_bin) on the
-# same weights and image.  The reference evaluates the glue in fp32; below the
-# first int8 requantization flip the two agree to ~2e-7 of the largest output
-# (measured: 1e-7 .. 3e-7 over 12 seeds at head dim 72), which is the bound
-# here, on seeds measured flip-free.  The planted-mistake test shows the bound
-# is sharp: a dropped bias, a squared attention scale or transposed pooling
-# moves the output by 1.5% to 100%.
+# same weights and image.  The reference evaluates the glue in fp32, so where
+# the oracle's margin criterion (tests/flips.py) clears the pass the two agree
+# to fp32 rounding (measured 1e-7 .. 3e-7 of the largest output; bound
+# REL_PRE_FLIP), and elsewhere to the flip level.  The planted-mistake test
+# shows the tight bound is sharp: a dropped bias, a squared attention scale or
+# transposed pooling moves the output by 1.5% to 100%.
 REL_PRE_FLIP = 1e-5
-REF_CASES = {"hd72": ("hd72", 1, 101), "hd16": ("hd16", 3, 8)}  # shape, weight seed, image seed
+REL_FLIP_LEVEL = 5e-2
+REF_CASES = {  # shape, weight seed, image seed
+    "tiny": ("tiny", 2, 102), "small": ("small", 1, 101),
+    "hd72": ("hd72", 1, 101), "hd16": ("hd16", 3, 8), "hd72_s5": ("hd72", 5, 105)}
 
 
 def run_reference_vision(tmp_path, case):
@@ -271,9 +296,12 @@ def test_multimodal_bin_round_trip(tmp_path):
 @pytest.mark.parametrize("case", sorted(REF_CASES))
 def test_vision_oracle_follows_reference_program(tmp_path, oracle, case):
     vis, img, ref = run_reference_vision(tmp_path, case)
-    rel = rel_to(ref, vorc.VisionOracle(vis, oracle).forward(img))
-    print(f"vision oracle vs reference ({case}): {rel:.3g}", flush=True)
-    assert rel <= REL_PRE_FLIP
+    want, margin = flips.tracked(oracle, vorc.VisionOracle(vis, oracle).forward, img)
+    free = margin > flips.MARGIN_BOUND
+    rel = rel_to(ref, want)
+    print(f"vision oracle vs reference ({case}, {'flip-free' if free else 'may flip'}): "
+          f"{rel:.3g}", flush=True)
+    assert rel <= (REL_PRE_FLIP if free else REL_FLIP_LEVEL)
 
 
 @needs_e2e
@@ -296,13 +324,16 @@ def test_vision_comparison_catches_planted_mistakes(tmp_path, oracle, monkeypatc
 @needs_e2e
 @pytest.mark.parametrize("case", sorted(REF_CASES))
 @pytest.mark.parametrize("mode", ["f32", "f64"])
-def test_device_vision_follows_reference_program(gh, tmp_path, case, mode):
+def test_device_vision_follows_reference_program(gh, oracle, tmp_path, case, mode):
     vis, img, ref = run_reference_vision(tmp_path, case)
+    _, margin = flips.tracked(oracle, vorc.VisionOracle(vis, oracle).forward, img)
+    free = margin > flips.MARGIN_BOUND
     tower = gh.vision(vis, attention=ATTN_F32 if mode == "f32" else ATTN_F64)
     try:
         got = tower.forward(img)
     finally:
         tower.close()
     rel = rel_to(ref, got)
-    print(f"device vision ({mode}) vs reference ({case}): {rel:.3g}", flush=True)
-    assert rel <= REL_PRE_FLIP
+    print(f"device vision ({mode}) vs reference ({case}, {'flip-free' if free else 'may flip'}): "
+          f"{rel:.3g}", flush=True)
+    assert rel <= (REL_PRE_FLIP if free else REL_FLIP_LEVEL)
