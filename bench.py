@@ -394,7 +394,7 @@ def bench_decode_1b(torch, gh, gen, timer, tokens):
         for _ in range(tokens):
             graph.replay()
 
-    ms = min(timer.elapsed_ms(run) for _ in range(3)) / tokens
+    ms = statistics.median(timer.elapsed_ms(run) for _ in range(TIMING_RUNS)) / tokens
     return dict(tok_s=round(1e3 / ms, 1), ms_per_token=round(ms, 4),
                 bytes_per_token=total_bytes,
                 gbs=round(total_bytes / (ms * 1e-3) / 1e9, 1),
@@ -415,7 +415,7 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     with the attention on the fp32 matrix cores, the default, and on the fp64
     ones, the verification mode), then `steps` decode steps from the KV cache
     the default prefill filled are timed (one HIP graph launch each, tokens fed back on the device, one
-    readback at the end)."""
+    readback at the end; the median of TIMING_RUNS generations)."""
     import statistics
     import time
 
@@ -440,12 +440,14 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
                 ts.append(time.perf_counter() - t0)
             t_mode[mode] = statistics.median(ts)
         t_pf, t_pf64 = t_mode[dec.ATTN_F32], t_mode[dec.ATTN_F64]
-        best = None
-        for _ in range(2):
+        # the median of TIMING_RUNS generations, each from the same cache
+        # state (the steps overwrite the positions after the prompt)
+        runs = []
+        for _ in range(TIMING_RUNS):
             t0 = time.perf_counter()
             toks = dec.generate(first, prompt, steps)
-            dt = time.perf_counter() - t0
-            best = dt if best is None else min(best, dt)
+            runs.append(time.perf_counter() - t0)
+        t_gen = statistics.median(runs)
     finally:
         dec.close()
     q_sz, kv_sz = c["n_heads"] * c["hdim"], c["nkv"] * c["hdim"]
@@ -466,11 +468,11 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
             keys = min(pos + 1, c["slide"]) if sw else pos + 1
             kv += 2 * kv_sz * 4 * keys
     per_token = weights + kv / steps
-    tok_s = steps / best
+    tok_s = steps / t_gen
     gbs = per_token * tok_s / 1e9
     return dict(model=name, context=f"{prompt}->{prompt + steps}", prefill=prefill,
                 tok_s=round(tok_s, 1),
-                ms_per_token=round(1e3 * best / steps, 4), bytes_per_token=int(per_token),
+                ms_per_token=round(1e3 * t_gen / steps, 4), bytes_per_token=int(per_token),
                 gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
                 hbm_bound_tok_s=round(HBM_PEAK_GBS * 1e9 / per_token, 1),
                 distinct_tokens=int(len(set(toks.tolist()))))

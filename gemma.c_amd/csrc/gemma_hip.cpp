@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -97,15 +98,23 @@ State g;
 // When enabled, every device entry point records a HIP event before and
 // after its launches on its stream; the pairs are resolved into totals per
 // (phase, op) lazily (when many are pending, and on read).  Launches on a
-// stream that is being captured into a graph are not timed.
-enum PerfOp { kOpQuantizeAct, kOpGemvInt8, kOpGemmInt8, kOpGemvFpx, kOpGemmFpx, kOpCount };
-const char *const kOpName[kOpCount] = {"quantize_act", "gemv_int8", "gemm_int8", "gemv_fpx",
-                                       "gemm_fpx"};
-constexpr int kPhases = 3;  // PerfPhase: prefill, decode, vision (gemma.c:2402-2407)
+// stream that is being captured into a graph are not timed, so the decoder
+// runs its steps eagerly while timing is on.  The ops are the reference's,
+// in its report order (gemma.c:2409-2431).
+enum PerfOp {
+  kOpRmsnorm, kOpLayernorm, kOpQuantizeAct, kOpGemvFpx, kOpGemvInt8, kOpGemvFpxNn,
+  kOpGemmFpx, kOpGemmFpxNn, kOpGemmInt8, kOpSoftmax, kOpGelu, kOpRope, kOpSample, kOpCount
+};
+const char *const kOpName[kOpCount] = {
+    "rmsnorm",     "layernorm", "quantize_act", "gemv_fpx",  "gemv_int8",
+    "gemv_fpx_nn", "gemm_fpx",  "gemm_fpx_nn",  "gemm_int8", "softmax",
+    "gelu",        "rope",      "sample_from_logits"};
+// PerfPhase (gemma.c:2402-2407)
+enum PerfPhase { kPhasePrefill, kPhaseDecode, kPhaseVision, kPhases };
 
 struct Perf {
   std::mutex mu;
-  bool on = false;
+  std::atomic<bool> on{false};  // read unlocked by every PerfScope
   int phase = 0;
   struct Pending {
     int op, phase;
@@ -152,11 +161,13 @@ struct Perf {
 };
 Perf g_perf;
 
-// Times the launches made during its lifetime on `stream` as one call of op.
+// Times the launches made during its lifetime on `stream` as one call of op,
+// in `phase` (default: the current one).
 class PerfScope {
  public:
-  PerfScope(int op, hipStream_t stream) : op_(op), stream_(stream) {
-    if (!g_perf.on) return;
+  PerfScope(int op, hipStream_t stream, int phase = -1)
+      : op_(op), phase_(phase), stream_(stream) {
+    if (!g_perf.on.load(std::memory_order_relaxed)) return;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
       return;
@@ -177,17 +188,32 @@ class PerfScope {
       g_perf.pool.push_back(b_);
       return;
     }
-    g_perf.pending.push_back(Perf::Pending{op_, g_perf.phase, a_, b_});
+    g_perf.pending.push_back(Perf::Pending{op_, phase_ >= 0 ? phase_ : g_perf.phase, a_, b_});
     if (g_perf.pending.size() >= 512) (void)g_perf.drain();
   }
   PerfScope(const PerfScope &) = delete;
   PerfScope &operator=(const PerfScope &) = delete;
 
  private:
-  int op_;
+  int op_, phase_;
   hipStream_t stream_;
   hipEvent_t a_ = nullptr, b_ = nullptr;
 };
+
+// One launch (or a few that make one op) timed as one call of op.
+template <class F>
+hipError_t timed(int op, hipStream_t stream, F &&launch, int phase = -1) {
+  PerfScope perf(op, stream, phase);
+  return launch();
+}
+
+// A whole-forward entry point attributes the ops that follow to its phase,
+// as the reference's forward_gemma_* do with PERF_PHASE (gemma.c:5463,
+// 5509, 5568).
+void perf_enter(int phase) {
+  std::lock_guard<std::mutex> lock(g_perf.mu);
+  g_perf.phase = phase;
+}
 
 // NULL is HIP's default (null) stream, so work on it is ordered with the
 // caller's own default-stream copies.
@@ -542,7 +568,7 @@ int matmul_impl(const char *name, float *dst, int dstr, const int8_t *mat, int m
   if (m == 0) return 0;
   if (!dst || !mat || !matsc || !src || !ssc) return fail("%s: null pointer", name);
   hipStream_t s = pick_stream(stream);
-  PerfScope perf(op >= 0 ? op : m == 1 ? kOpGemvInt8 : kOpGemmInt8, s);
+  const int perf_op = op >= 0 ? op : m == 1 ? kOpGemvInt8 : kOpGemmInt8;
   if (m == 1 && mstr == k && k <= kMaxGemvK8) {
     gh::GemvJobs jobs{};
     jobs.w[0] = mat;
@@ -550,6 +576,7 @@ int matmul_impl(const char *name, float *dst, int dstr, const int8_t *mat, int m
     jobs.dst[0] = dst;
     for (int j = 0; j < gh::kMaxJobs; ++j) jobs.end[j] = n;
     jobs.njobs = 1;
+    PerfScope perf(perf_op, s);
     const hipError_t e =
         gh::launch_gemv_i8(jobs, k, src, ssc, nullptr, nullptr, nullptr, g.info, s);
     if (e != hipSuccess) return fail("%s: gemv launch: %s", name, hipGetErrorString(e));
@@ -565,6 +592,7 @@ int matmul_impl(const char *name, float *dst, int dstr, const int8_t *mat, int m
       return fail("%s: m=%d n=%d k=%d needs %zu bytes of scratch, more than the %zu it has",
                   name, m, n, k, need, ws.bytes);
   }
+  PerfScope perf(perf_op, s);  // after the checks: a refused call is not timed
   const hipError_t e = gh::launch_gemm_i8(dst, dstr, 0, mat, mstr, matsc, src, sstr, ssc, m,
                                           n, k, g.info, s, noalloc ? &ws : nullptr);
   if (e != hipSuccess) return fail("%s: gemm launch: %s", name, hipGetErrorString(e));
@@ -1182,6 +1210,11 @@ int prefill_reserve(gemma_hip_decoder *d, int n) {
 // last row, with no sliding window (gemma.c:5258-5290).
 constexpr int kWarmRows = 256;  // rows from which a GEMM's weights are read ahead of it
 
+// Each launch is timed as the reference op it stands for when timing is on
+// (fused kernels as the op they open with; the attention kernels, which hold
+// the reference's score and value products too, as softmax).
+#define GH_OP(op, expr) timed((op), st, [&] { return (expr); })
+
 hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, bool dense,
                            hipStream_t st) {
   const gemma_hip_text_config &c = d->cfg;
@@ -1190,8 +1223,8 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
   const size_t cache = (size_t)d->clen * kv_sz;
   hipError_t e;
   auto gemm = [&](float *dst, int dstr, const int8_t *w, const float *ws, int nout, int k) {
-    return gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, d->pf_a8, k, d->pf_as, n, nout, k, g.info,
-                              st);
+    return GH_OP(kOpGemmInt8, gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, d->pf_a8, k, d->pf_as,
+                                                 n, nout, k, g.info, st));
   };
   if (embed && (e = gh::launch_pf_embed(d->pf_tok, n, d->emb, d->emb_s, d->pf_x, dim,
                                         c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
@@ -1202,12 +1235,13 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
     const gh::PfNorm n1{d->pf_x, l > 0 ? d->pf_y : nullptr,
                         (l > 0 && c.mlp_pst) ? d->layers[l - 1].n4 : nullptr, L.n1, d->pf_a8,
                         d->pf_as, dim, c.eps};
-    if ((e = gh::launch_pf_norm_rows(n1, n, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpRmsnorm, gh::launch_pf_norm_rows(n1, n, st))) != hipSuccess) return e;
     // q, k, v rows (gemma.c:5045-5089)
     const gh::GemmSegs qkv{{L.w[0], L.w[1], L.w[2]}, {L.s[0], L.s[1], L.s[2]},
                            {q_sz, q_sz + kv_sz, q_sz + 2 * kv_sz}, 3};
-    if ((e = gh::launch_gemm_i8_segs(d->pf_qkv, stride, qkv, d->pf_a8, dim, d->pf_as, n, dim,
-                                     g.info, st)) != hipSuccess)
+    if ((e = GH_OP(kOpGemmInt8, gh::launch_gemm_i8_segs(d->pf_qkv, stride, qkv, d->pf_a8, dim,
+                                                        d->pf_as, n, dim, g.info, st))) !=
+        hipSuccess)
       return e;
     // q/k norm, RoPE, KV append, attention
     const bool sliding = d->swa[l] != 0;
@@ -1215,21 +1249,24 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
     const gh::PfRope rp{d->pf_qkv, stride, q_sz, c.qk_norm ? L.nq : nullptr,
                         c.qk_norm ? L.nk : nullptr, sliding ? d->rope_l : d->rope_g, kc,
                         kc + cache, d->clen, pos, c.n_heads, c.nkv, c.eps};
-    if ((e = gh::launch_pf_qk_rope(rp, n, c.hdim, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpRope, gh::launch_pf_qk_rope(rp, n, c.hdim, st))) != hipSuccess) return e;
     const gh::PfAttn at{d->pf_qkv, stride, kc, kc + cache, d->pf_xo, q_sz, n, pos, c.n_heads,
                         c.nkv, d->clen, sliding ? c.slide : 0,
                         (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
                         0, dense ? 1 : 0};
-    if ((e = gh::launch_pf_attention(at, c.hdim, d->attn_f32, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, st))) !=
+        hipSuccess)
+      return e;
     // o projection
-    if ((e = gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st)) !=
+    if ((e = GH_OP(kOpQuantizeAct,
+                   gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st))) !=
             hipSuccess ||
         (e = gemm(d->pf_y, dim, L.w[3], L.s[3], dim, q_sz)) != hipSuccess)
       return e;
     // residual of the attention (post-attention norm), pre-FFN norm, quantize
     const gh::PfNorm n3{d->pf_x, d->pf_y, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
                         d->pf_a8, d->pf_as, dim, c.eps};
-    if ((e = gh::launch_pf_norm_rows(n3, n, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpRmsnorm, gh::launch_pf_norm_rows(n3, n, st))) != hipSuccess) return e;
     // The GELU kernel reads the down weights after its rows, so that the down
     // GEMM finds them in the Infinity Cache: a GEMM whose weights stream from
     // HBM runs latency-bound on them (gemma-3-4b down alone: 70 us with its
@@ -1241,10 +1278,11 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
     // gate (w2), up (w1) (gemma.c:5365-5373), GELU(gate) * up, quantize, down
     const gh::GemmSegs gu{{L.w[5], L.w[4], nullptr}, {L.s[5], L.s[4], nullptr},
                           {mlp, 2 * mlp, 2 * mlp}, 2};
-    if ((e = gh::launch_gemm_i8_segs(d->pf_g, 2 * mlp, gu, d->pf_a8, dim, d->pf_as, n, dim,
-                                     g.info, st)) != hipSuccess ||
-        (e = gh::launch_pf_gelu_quant(d->pf_g, n, mlp, d->pf_a8, d->pf_as, wdown, st)) !=
+    if ((e = GH_OP(kOpGemmInt8, gh::launch_gemm_i8_segs(d->pf_g, 2 * mlp, gu, d->pf_a8, dim,
+                                                        d->pf_as, n, dim, g.info, st))) !=
             hipSuccess ||
+        (e = GH_OP(kOpGelu, gh::launch_pf_gelu_quant(d->pf_g, n, mlp, d->pf_a8, d->pf_as, wdown,
+                                                     st))) != hipSuccess ||
         (e = gemm(d->pf_y, dim, L.w[6], L.s[6], dim, mlp)) != hipSuccess)
       return e;
   }
@@ -1253,19 +1291,23 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
   gh::DecNorm fn{d->pf_x + last, d->pf_y + last,
                  c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm, nullptr, d->h, dim,
                  c.eps};
-  if ((e = gh::launch_dec_final_norm(fn, st)) != hipSuccess) return e;
+  if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(fn, st))) != hipSuccess) return e;
   gh::GemvJobs lm{};
   lm.w[0] = d->emb; lm.sc[0] = d->emb_s; lm.dst[0] = d->logits;
   for (int j = 0; j < gh::kMaxJobs; ++j) lm.end[j] = c.nvocab;
   lm.njobs = 1;
-  if ((e = gh::launch_gemv_i8(lm, dim, nullptr, nullptr, d->h, nullptr, nullptr, g.info, st)) !=
-      hipSuccess)
+  if ((e = GH_OP(kOpGemvInt8, gh::launch_gemv_i8(lm, dim, nullptr, nullptr, d->h, nullptr,
+                                                  nullptr, g.info, st))) != hipSuccess)
     return e;
-  if (c.sc_log != 0.0f &&
-      (e = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st)) != hipSuccess)
-    return e;
-  return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
-                               d->tokens, d->clen, st);
+  // the softcap and argmax are sample_from_logits, which the reference
+  // counts in the decode phase (gemma.c:5776)
+  return timed(kOpSample, st, [&] {
+    hipError_t es = hipSuccess;
+    if (c.sc_log != 0.0f) es = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st);
+    if (es != hipSuccess) return es;
+    return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
+                                 d->tokens, d->clen, st);
+  }, kPhaseDecode);
 }
 
 // The checks every prefill entry point makes of n rows at pos.
@@ -1335,8 +1377,8 @@ hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
     qkv.dst[0] = d->xq; qkv.dst[1] = d->xk; qkv.dst[2] = d->xv;
     qkv.end[0] = q_sz; qkv.end[1] = q_sz + kv_sz; qkv.end[2] = qkv.end[3] = q_sz + 2 * kv_sz;
     qkv.njobs = 3;
-    if ((e = gh::launch_dec_norm_gemv(n1, qkv, q_sz + 2 * kv_sz, c.dim, false, g.info, st)) !=
-        hipSuccess)
+    if ((e = GH_OP(kOpGemvInt8, gh::launch_dec_norm_gemv(n1, qkv, q_sz + 2 * kv_sz, c.dim,
+                                                         false, g.info, st))) != hipSuccess)
       return e;
     cur ^= 1;
     // attention
@@ -1348,14 +1390,14 @@ hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
                    c.n_heads, c.nkv, c.hdim, d->clen, sliding ? c.slide : 0,
                    d->max_blocks, c.nvocab, (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att,
                    c.eps};
-    if ((e = gh::launch_dec_attention(at, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpSoftmax, gh::launch_dec_attention(at, st))) != hipSuccess) return e;
     // o projection (quantize fused)
     gh::GemvJobs o{};
     o.w[0] = L.w[3]; o.sc[0] = L.s[3]; o.dst[0] = d->yattn;
     for (int j = 0; j < gh::kMaxJobs; ++j) o.end[j] = c.dim;
     o.njobs = 1;
-    if ((e = gh::launch_gemv_i8(o, q_sz, nullptr, nullptr, d->xo, nullptr, nullptr, g.info, st)) !=
-        hipSuccess)
+    if ((e = GH_OP(kOpGemvInt8, gh::launch_gemv_i8(o, q_sz, nullptr, nullptr, d->xo, nullptr,
+                                                   nullptr, g.info, st))) != hipSuccess)
       return e;
     // residual of the attention (post-attention norm), pre-FFN norm, gate/up + GELU
     gh::DecNorm n3{d->x[cur], d->yattn, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
@@ -1366,8 +1408,8 @@ hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
     gu.dst[0] = d->gbuf; gu.dst[1] = d->gbuf;
     gu.end[0] = gu.end[1] = gu.end[2] = gu.end[3] = 2 * c.mlp_dim;
     gu.njobs = 2;
-    if ((e = gh::launch_dec_norm_gemv(n3, gu, 2 * c.mlp_dim, c.dim, true, g.info, st)) !=
-        hipSuccess)
+    if ((e = GH_OP(kOpGemvInt8, gh::launch_dec_norm_gemv(n3, gu, 2 * c.mlp_dim, c.dim, true,
+                                                         g.info, st))) != hipSuccess)
       return e;
     cur ^= 1;
     // down projection (quantize fused)
@@ -1375,26 +1417,28 @@ hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
     dn.w[0] = L.w[6]; dn.sc[0] = L.s[6]; dn.dst[0] = d->ymlp;
     for (int j = 0; j < gh::kMaxJobs; ++j) dn.end[j] = c.dim;
     dn.njobs = 1;
-    if ((e = gh::launch_gemv_i8(dn, c.mlp_dim, nullptr, nullptr, d->gbuf, nullptr, nullptr,
-                                g.info, st)) != hipSuccess)
+    if ((e = GH_OP(kOpGemvInt8, gh::launch_gemv_i8(dn, c.mlp_dim, nullptr, nullptr, d->gbuf,
+                                                   nullptr, nullptr, g.info, st))) != hipSuccess)
       return e;
   }
   // last residual, final norm, LM head (tied embedding), softcap, argmax
   gh::DecNorm fn{d->x[cur], d->ymlp, c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm,
                  nullptr, d->h, c.dim, c.eps};
-  if ((e = gh::launch_dec_final_norm(fn, st)) != hipSuccess) return e;
+  if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(fn, st))) != hipSuccess) return e;
   gh::GemvJobs lm{};
   lm.w[0] = d->emb; lm.sc[0] = d->emb_s; lm.dst[0] = d->logits;
   for (int j = 0; j < gh::kMaxJobs; ++j) lm.end[j] = c.nvocab;
   lm.njobs = 1;
-  if ((e = gh::launch_gemv_i8(lm, c.dim, nullptr, nullptr, d->h, nullptr, nullptr, g.info, st)) !=
-      hipSuccess)
+  if ((e = GH_OP(kOpGemvInt8, gh::launch_gemv_i8(lm, c.dim, nullptr, nullptr, d->h, nullptr,
+                                                  nullptr, g.info, st))) != hipSuccess)
     return e;
-  if (c.sc_log != 0.0f &&
-      (e = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st)) != hipSuccess)
-    return e;
-  return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
-                               d->tokens, d->clen, st);
+  return GH_OP(kOpSample, [&] {
+    hipError_t es = hipSuccess;
+    if (c.sc_log != 0.0f) es = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st);
+    if (es != hipSuccess) return es;
+    return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
+                                 d->tokens, d->clen, st);
+  }());
 }
 
 }  // namespace
@@ -1592,6 +1636,20 @@ void gemma_hip_decoder_destroy(gemma_hip_decoder *dec) {
   decoder_free(dec);
 }
 
+}  // extern "C"
+
+namespace {
+// One decode step on the library's stream: the captured graph, or the same
+// launches made eagerly while per-op timing is on (a graph's kernels cannot
+// be timed one by one).
+hipError_t run_step(gemma_hip_decoder *dec) {
+  if (g_perf.on.load(std::memory_order_relaxed)) return decoder_enqueue(dec, g.stream);
+  return hipGraphLaunch(dec->exec, g.stream);
+}
+}  // namespace
+
+extern "C" {
+
 int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos, float *logits,
                            int *next) {
   if (need_init()) return 1;
@@ -1606,7 +1664,8 @@ int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos, float *lo
   dec->pin[3] = 0;
   GH_CHECK("gemma_hip_decoder_step: H2D",
            hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
-  GH_CHECK("gemma_hip_decoder_step: graph", hipGraphLaunch(dec->exec, g.stream));
+  perf_enter(kPhaseDecode);
+  GH_CHECK("gemma_hip_decoder_step: step", run_step(dec));
   if (logits != nullptr)
     GH_CHECK("gemma_hip_decoder_step: logits D2H",
              hipMemcpyAsync(logits, dec->logits, (size_t)dec->cfg.nvocab * 4,
@@ -1634,8 +1693,8 @@ int gemma_hip_decoder_generate(gemma_hip_decoder *dec, int token, int pos, int n
   dec->pin[3] = 0;
   GH_CHECK("gemma_hip_decoder_generate: H2D",
            hipMemcpyAsync(dec->step, dec->pin, 16, hipMemcpyHostToDevice, g.stream));
-  for (int i = 0; i < n; ++i)
-    GH_CHECK("gemma_hip_decoder_generate: graph", hipGraphLaunch(dec->exec, g.stream));
+  perf_enter(kPhaseDecode);
+  for (int i = 0; i < n; ++i) GH_CHECK("gemma_hip_decoder_generate: step", run_step(dec));
   GH_CHECK("gemma_hip_decoder_generate: D2H",
            hipMemcpyAsync(tokens, dec->tokens, (size_t)n * 4, hipMemcpyDeviceToHost, g.stream));
   GH_CHECK("gemma_hip_decoder_generate: sync", hipStreamSynchronize(g.stream));
@@ -1658,6 +1717,7 @@ int gemma_hip_decoder_prefill(gemma_hip_decoder *dec, const int *tokens, int n, 
   if (prefill_stage(dec, kName, n)) return 1;
   PF_CHECK("tokens H2D",
            hipMemcpyAsync(dec->pf_tok, tokens, (size_t)n * 4, hipMemcpyHostToDevice, g.stream));
+  perf_enter(kPhasePrefill);
   return prefill_run(dec, kName, n, pos, tokens[n - 1], true, false, logits, next);
 }
 
@@ -1669,6 +1729,9 @@ int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n
   if (prefill_check(dec, kName, n, pos) || prefill_stage(dec, kName, n)) return 1;
   PF_CHECK("rows copy", hipMemcpyAsync(dec->pf_x, x, (size_t)n * dec->cfg.dim * 4,
                                        hipMemcpyDefault, g.stream));
+  // text rows belong to the prefill phase, image soft tokens (the dense
+  // pass of forward_gemma_image) to the vision phase
+  perf_enter(mask != 0 ? kPhasePrefill : kPhaseVision);
   return prefill_run(dec, kName, n, pos, 0, false, mask == 0, logits, next);
 }
 
@@ -1722,11 +1785,10 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
   hipError_t e;
   auto gemm = [&](float *dst, int dstr, const int8_t *w, const float *ws, int m, int nout,
                   int k) {
-    return gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, v->a8, k, v->as, m, nout, k, g.info, st);
+    return GH_OP(kOpGemmInt8,
+                 gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, v->a8, k, v->as, m, nout, k, g.info, st));
   };
   // patch embedding + position embedding (4411-4468)
-  if ((e = gh::launch_im2col(v->patches, v->img, c.img_px, c.psize, st)) != hipSuccess)
-    return e;
   // the patch GEMM (the a9 path: fp32 matrix cores; fp64 in the verification
   // mode) with the bias, clamp and position embedding in its epilogue
   gh::F32Epilogue pe{};
@@ -1735,30 +1797,37 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
   pe.pos_q = v->pos_q;
   pe.pos_s = v->pos_s;
   const int kdim = 3 * c.psize * c.psize;
-  if ((e = gh::launch_gemm_f32(v->x, dim, v->pe, kdim, v->patches, kdim, n, dim, kdim, pe,
-                               g.info, st, !v->attn_f32)) != hipSuccess)
+  if ((e = GH_OP(kOpGemmFpx, [&] {
+         const hipError_t ei = gh::launch_im2col(v->patches, v->img, c.img_px, c.psize, st);
+         if (ei != hipSuccess) return ei;
+         return gh::launch_gemm_f32(v->x, dim, v->pe, kdim, v->patches, kdim, n, dim, kdim, pe,
+                                    g.info, st, !v->attn_f32);
+       }())) != hipSuccess)
     return e;
   for (int l = 0; l < c.nl; ++l) {
     const auto &L = v->layers[l];
     // residual of the previous layer's MLP (fc2 bias), first layer norm (4474-4484)
     const gh::VisLn n1{v->x, l > 0 ? v->y : nullptr, l > 0 ? v->layers[l - 1].b2 : nullptr,
                        L.n1, L.n1b, v->a8, v->as, nullptr, dim, c.eps};
-    if ((e = gh::launch_vis_ln_rows(n1, n, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(n1, n, st))) != hipSuccess) return e;
     // q, k, v (4487-4511); their biases are added inside the attention
     const gh::GemmSegs qkv{{L.w[0], L.w[1], L.w[2]}, {L.s[0], L.s[1], L.s[2]},
                            {dim, 2 * dim, 3 * dim}, 3};
-    if ((e = gh::launch_gemm_i8_segs(v->qkv, 3 * dim, qkv, v->a8, dim, v->as, n, dim, g.info,
-                                     st)) != hipSuccess)
+    if ((e = GH_OP(kOpGemmInt8, gh::launch_gemm_i8_segs(v->qkv, 3 * dim, qkv, v->a8, dim,
+                                                        v->as, n, dim, g.info, st))) != hipSuccess)
       return e;
     const gh::VisAttn at{v->qkv, 3 * dim, L.bqkv, v->att, n, c.n_heads, dim,
                          1.0f / sqrtf((float)v->hdim)};
-    if ((e = gh::launch_vis_attention(at, v->hdim, v->attn_f32, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpSoftmax, gh::launch_vis_attention(at, v->hdim, v->attn_f32, st))) !=
+        hipSuccess)
+      return e;
     // o (4563-4573), then its bias, the residual and the second layer norm
-    if ((e = gh::launch_quantize(v->a8, v->as, v->att, dim, n, dim, st)) != hipSuccess ||
+    if ((e = GH_OP(kOpQuantizeAct, gh::launch_quantize(v->a8, v->as, v->att, dim, n, dim,
+                                                       st))) != hipSuccess ||
         (e = gemm(v->y, dim, L.w[3], L.s[3], n, dim, dim)) != hipSuccess)
       return e;
     const gh::VisLn n2{v->x, v->y, L.bo, L.n2, L.n2b, v->a8, v->as, nullptr, dim, c.eps};
-    if ((e = gh::launch_vis_ln_rows(n2, n, st)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(n2, n, st))) != hipSuccess) return e;
     // The GELU kernel reads fc2's weights after its rows, as the decoder's
     // prefill does for down: the tower's 27 layers hold more weights than the
     // Infinity Cache, so each layer's come from HBM.  Measured at 896 px:
@@ -1768,8 +1837,8 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
     if (n >= kWarmRows) w_fc2 = {{L.w[5]}, {(size_t)mlp * dim}, 1};
     // fc1, bias + GELU, fc2 (4604-4644)
     if ((e = gemm(v->hbuf, mlp, L.w[4], L.s[4], n, mlp, dim)) != hipSuccess ||
-        (e = gh::launch_vis_gelu_quant(v->hbuf, L.b1, n, mlp, v->a8, v->as, w_fc2, st)) !=
-            hipSuccess ||
+        (e = GH_OP(kOpGelu, gh::launch_vis_gelu_quant(v->hbuf, L.b1, n, mlp, v->a8, v->as,
+                                                      w_fc2, st))) != hipSuccess ||
         (e = gemm(v->y, dim, L.w[5], L.s[5], n, dim, mlp)) != hipSuccess)
       return e;
   }
@@ -1777,11 +1846,13 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
   // projection (4708-4721)
   const gh::VisLn pn{v->x, v->y, v->layers[c.nl - 1].b2, v->post_n, v->post_nb, nullptr,
                      nullptr, v->hln, dim, c.eps};
-  if ((e = gh::launch_vis_ln_rows(pn, n, st)) != hipSuccess) return e;
+  if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(pn, n, st))) != hipSuccess) return e;
   const gh::VisPool po{v->hln, v->norm, v->a8, v->as, dim, v->ppi, v->ksize, c.eps};
-  if ((e = gh::launch_vis_pool(po, c.img_tok, st)) != hipSuccess) return e;
+  if ((e = GH_OP(kOpRmsnorm, gh::launch_vis_pool(po, c.img_tok, st))) != hipSuccess) return e;
   return gemm(v->out, c.text_dim, v->proj, v->proj_s, c.img_tok, c.text_dim, dim);
 }
+
+#undef GH_OP
 
 }  // namespace
 
@@ -1943,6 +2014,7 @@ int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out
   GH_CHECK("gemma_hip_vision_forward: image H2D",
            hipMemcpyAsync(vis->img, img, (size_t)c.img_px * c.img_px * 3 * 4,
                           hipMemcpyHostToDevice, g.stream));
+  perf_enter(kPhaseVision);
   GH_CHECK("gemma_hip_vision_forward: launch", vision_enqueue(vis, g.stream));
   GH_CHECK("gemma_hip_vision_forward: D2H",
            hipMemcpyAsync(out, vis->out, (size_t)c.img_tok * c.text_dim * 4,
@@ -1973,6 +2045,7 @@ int gemma_hip_gemma_image(gemma_hip_decoder *dec, gemma_hip_vision *vis, const f
     return 1;
   PF_CHECK("image H2D", hipMemcpyAsync(vis->img, img, (size_t)c.img_px * c.img_px * 3 * 4,
                                        hipMemcpyHostToDevice, g.stream));
+  perf_enter(kPhaseVision);
   PF_CHECK("vision", vision_enqueue(vis, g.stream));
   PF_CHECK("soft tokens", hipMemcpyAsync(dec->pf_x, vis->out, (size_t)c.img_tok * c.text_dim * 4,
                                          hipMemcpyDeviceToDevice, g.stream));

@@ -85,12 +85,29 @@ int gemma_hip_sync(void *stream);
  * 2468-2476) on the device: while enabled, the GPU time of every device
  * entry point's launches (HIP events on its stream, so PCIe copies of the
  * _host calls are not included) is summed per phase and op, under the
- * reference's op names: "quantize_act" (gemma_hip_quantize and the _host
- * quantizes), "gemv_int8" (matmul with m == 1, matmul_multi, and
- * quantize_matmul, whose quantize is fused into the GEMV launch), "gemm_int8"
- * (matmul with m > 1, matmul_heads), "gemv_fpx" and "gemm_fpx" (the fp32
- * entry points).  Launches on a stream under graph capture are not timed;
- * the device-resident decoder and vision tower are not broken down. */
+ * reference's op names and report order: "quantize_act" (gemma_hip_quantize
+ * and the _host quantizes), "gemv_int8" (matmul with m == 1, matmul_multi,
+ * and quantize_matmul, whose quantize is fused into the GEMV launch),
+ * "gemm_int8" (matmul with m > 1, matmul_cols, matmul_heads), "gemv_fpx" and
+ * "gemm_fpx" (the fp32 entry points).
+ *
+ * The device-resident decoder and vision tower time each launch as the
+ * reference op it stands for, fused kernels as the op they open with:
+ * "rmsnorm" (the residual + norm (+ quantize) rows, the final norm, the
+ * tower's pooling RMSNorm), "layernorm" (the tower's residual + layer norm
+ * rows), "gemv_int8" (the decode GEMVs, their norm-fused forms and the LM
+ * head), "gemm_int8" (the prompt pass's and the tower's GEMMs),
+ * "quantize_act", "gelu" (GELU(gate) * up + quantize, bias + GELU +
+ * quantize), "rope" (the prompt pass's q/k norm + RoPE + cache append),
+ * "softmax" (the attention kernels, which also hold the reference's score
+ * and value products and, in the decode step, its RoPE), "gemm_fpx" (the
+ * tower's im2col + patch GEMM) and "sample_from_logits" (softcap + argmax,
+ * counted in the decode phase as the reference does).  They set the phase
+ * themselves as the reference's forward_gemma_* do: decoder_prefill and
+ * prefill_rows with mask != 0 prefill; decoder_step and decoder_generate
+ * decode (run eagerly, not as the captured graph, while timing is on);
+ * vision_forward, gemma_image and prefill_rows with mask == 0 vision.
+ * Launches on a stream under graph capture are not timed. */
 
 /* One (phase, op) total: seconds of GPU time over `calls` calls. */
 typedef struct {

@@ -272,6 +272,27 @@ def long_ctx(tmp_path_factory):
                                                   norm_std=0.1))
 
 
+@pytest.fixture(scope="module")
+def long_gqa_4b(tmp_path_factory):
+    """gemma-3-4b widths (dim 2560, mlp 10240, 8 q heads over 4 kv heads of
+    256), one global layer: config 5's attention shape past 2048 keys."""
+    d = tmp_path_factory.mktemp("long4b")
+    return model_bin.read_bin(model_bin.write_bin(str(d / "long4b.bin"), "gemma-3-4b", seed=17,
+                                                  nvocab=1024, layers=1, swa=[0],
+                                                  norm_std=0.1))
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(300)
+def test_decoder_4b_gqa_long_prompt(gh, oracle, long_gqa_4b):
+    """Config 5's attention at its own widths: a 2100-token prompt through
+    the global layer (the prefill's GQA attention over 2100 keys, in several
+    key-split chunks), then decode steps at positions 2100 .. 2105, past
+    2048, on the cache it filled -- against the oracle."""
+    worst = _prefill_vs_oracle(gh, oracle, long_gqa_4b, 2100, 6, 2112, batched=True)
+    print(f"4b GQA long prompt: worst |d|/max|logit| = {worst:.3g}", flush=True)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("n", [3100, 8200])
 def test_decoder_long_context(gh, oracle, long_ctx, n):
@@ -460,6 +481,48 @@ def test_decoder_generate_equals_steps(gh, models):
             token = dec.step(token, pos)
             seq.append(token)
         assert list(toks) == seq
+    finally:
+        dec.close()
+
+
+@pytest.mark.gpu
+def test_decoder_perf_breakdown(gh, models):
+    """The device-resident decoder under per-op timing: the prompt pass and
+    the decode steps broken down under the reference's PerfBench names
+    (gemma.c:2409-2431), each launch counted once in its phase, and the
+    eager steps timing runs giving the graph's tokens."""
+    model = models["gemma3"]
+    nl = model["config"]["nl"]
+    prompt = [5, 9, 2, 7, 11, 3, 8]
+    dec = gh.decoder(model, 48)
+    try:
+        dec.prefill(prompt, 0)
+        want = list(dec.generate(4, len(prompt), 12))
+        gh.perf_enable(True)
+        try:
+            dec.prefill(prompt, 0)
+            got = list(dec.generate(4, len(prompt), 12))
+            perf = gh.perf_read()
+        finally:
+            gh.perf_enable(False)
+        assert got == want
+        calls = {ph: {op: c for op, (sec, c) in ops.items()} for ph, ops in perf.items()}
+        assert calls["prefill"] == {"rmsnorm": 2 * nl + 1, "gemm_int8": 4 * nl, "rope": nl,
+                                    "softmax": nl, "quantize_act": nl, "gelu": nl,
+                                    "gemv_int8": 1}
+        assert calls["decode"] == {"gemv_int8": 12 * (4 * nl + 1), "softmax": 12 * nl,
+                                   "rmsnorm": 12, "sample_from_logits": 12 + 1}
+        for ops in perf.values():
+            for op, (sec, c) in ops.items():
+                assert 0 < sec < 1.0, op
+        # timing off again: the graph runs, the totals stay cleared on the
+        # next enable
+        assert list(dec.generate(4, len(prompt), 12)) == want
+        gh.perf_enable(True)
+        try:
+            assert gh.perf_read() == {}
+        finally:
+            gh.perf_enable(False)
     finally:
         dec.close()
 

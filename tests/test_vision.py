@@ -101,6 +101,33 @@ def test_vision_matches_oracle(gh, oracle, shape):
     assert np.array_equal(got, again)  # deterministic
 
 
+@pytest.mark.gpu
+def test_vision_perf_breakdown(gh):
+    """The tower under per-op timing: one forward broken down in the vision
+    phase under the reference's PerfBench names (gemma.c:2409-2431)."""
+    vis = model_bin.synth_vision(seed=7, text_dim=64, **SHAPES["tiny"])
+    img = model_bin.synth_image(SHAPES["tiny"]["img_px"], seed=8)
+    nl = vis["config"]["nl"]
+    tower = gh.vision(vis)
+    try:
+        want = tower.forward(img)
+        gh.perf_enable(True)
+        try:
+            got = tower.forward(img)
+            perf = gh.perf_read()
+        finally:
+            gh.perf_enable(False)
+    finally:
+        tower.close()
+    assert np.array_equal(got, want)
+    assert set(perf) == {"vision"}
+    calls = {op: c for op, (sec, c) in perf["vision"].items()}
+    assert calls == {"gemm_fpx": 1, "layernorm": 2 * nl + 1, "gemm_int8": 4 * nl + 1,
+                     "softmax": nl, "quantize_act": nl, "gelu": nl, "rmsnorm": 1}
+    for op, (sec, c) in perf["vision"].items():
+        assert 0 < sec < 1.0, op
+
+
 # The default arithmetic (GEMMA_HIP_ATTN_F32: the patch embedding and the
 # attention on the fp32 matrix cores) in the whole tower, against the fp64
 # oracle.  The bar of each case is decided before the device runs, from the
