@@ -591,6 +591,56 @@ def cpu_baseline(threads: int, seconds_per_shape: float) -> dict | None:
                 per_gemv_gbs=parts)
 
 
+def perf_report(torch, gh, decoder_runs) -> str:
+    """The reference's per-op report (PerfBench) for the device-resident
+    paths: each decoder model's prompt pass and decode steps (one prefill of
+    the prompt, then the steps, eagerly so that each launch is timed), and one
+    896 px image through the SigLIP tower.  Each launch's GPU time comes from
+    HIP events around it, so the event pairs add a little to each total."""
+    import numpy as np
+
+    import gemma_hip
+    import model_bin
+
+    out = []
+    for name, prompt, steps in decoder_runs:
+        model = model_bin.synth_model(name, seed=1234)
+        ids = np.random.default_rng(1234).integers(0, model["config"]["nvocab"],
+                                                   prompt).astype(np.int32)
+        dec = gh.decoder(model, prompt + steps + 1)
+        try:
+            first = dec.prefill(ids, 0)
+            dec.generate(first, prompt, 4)
+            gh.perf_enable(True)
+            try:
+                first = dec.prefill(ids, 0)
+                dec.generate(first, prompt, steps)
+                perf = gh.perf_read()
+            finally:
+                gh.perf_enable(False)
+        finally:
+            dec.close()
+        out.append(f"== {name}: prefill {prompt} tokens, decode {steps} steps ==")
+        out.append(gemma_hip.perf_table(perf))
+    vis = model_bin.synth_vision(seed=1234, text_dim=2560)
+    img = model_bin.synth_image(vis["config"]["img_px"], seed=1234)
+    tower = gh.vision(vis)
+    try:
+        tower.forward(img)
+        gh.perf_enable(True)
+        try:
+            tower.forward(img)
+            perf = gh.perf_read()
+        finally:
+            gh.perf_enable(False)
+    finally:
+        tower.close()
+    out.append("== siglip: one 896 px image ==")
+    out.append(gemma_hip.perf_table(perf))
+    torch.cuda.synchronize()
+    return "\n".join(out)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -606,6 +656,9 @@ def main() -> int:
     ap.add_argument("--decoder-models", default="gemma-3-270m,gemma-3-1b,gemma-3-4b",
                     help="models of the decoder timing (comma list of gemma-3-270m, "
                          "gemma-3-1b, gemma-3-4b)")
+    ap.add_argument("--perf-report", action="store_true",
+                    help="print the reference's per-op report (PerfBench names) of the "
+                         "decoder models and the vision tower, then exit")
     ap.add_argument("--copy-probe", action="store_true",
                     help="profiling aid: 3 dispatches of an elementwise kernel that reads "
                          "and writes exactly 1 GiB (calibrates FETCH_SIZE / WRITE_SIZE)")
@@ -632,6 +685,10 @@ def main() -> int:
 
     gh = gemma_hip.GemmaHip(0)
     decoder_runs = [r for r in DECODER_RUNS if r[0] in args.decoder_models.split(",")]
+    if args.perf_report:
+        print(perf_report(torch, gh, decoder_runs), flush=True)
+        gh.close()
+        return 0
     if args.only == "decoder":
         for name, prompt, nsteps in decoder_runs:
             print(json.dumps(bench_decoder(torch, gh, name, prompt, nsteps)), flush=True)

@@ -35,6 +35,34 @@ class PerfEntry(ctypes.Structure):
 
 
 PERF_PHASES = ("prefill", "decode", "vision")  # the reference's PerfPhase order
+# the reference's PerfOp names in report order (gemma.c:2409-2431)
+PERF_OPS = ("rmsnorm", "layernorm", "quantize_act", "gemv_fpx", "gemv_int8", "gemv_fpx_nn",
+            "gemm_fpx", "gemm_fpx_nn", "gemm_int8", "softmax", "gelu", "rope",
+            "sample_from_logits")
+
+
+def perf_table(perf) -> str:
+    """perf_read()'s totals as the per-phase tables of the reference's report
+    (perf_print, gemma.c:6824-6862: function, calls, total ms, avg us, share of
+    the phase's recorded time)."""
+    lines = []
+    for ph in PERF_PHASES:
+        ops = perf.get(ph)
+        if not ops:
+            continue
+        total = sum(sec for sec, _ in ops.values())
+        lines.append(f"{ph}: {total * 1e3:.3f} ms of GPU time")
+        lines.append(f"  {'function':<18} {'calls':>8} {'total ms':>10} {'avg us':>9} {'share':>7}")
+        lines.append("  " + "-" * 18 + " " + "-" * 8 + " " + "-" * 10 + " " + "-" * 9 + " " + "-" * 7)
+        for op in PERF_OPS:
+            if op not in ops:
+                continue
+            sec, calls = ops[op]
+            share = 100.0 * sec / total if total > 0 else 0.0
+            lines.append(f"  {op:<18} {calls:>8} {sec * 1e3:>10.3f} {sec * 1e6 / calls:>9.2f} "
+                         f"{share:>6.1f}%")
+        lines.append(f"  {'total':<18} {'':>8} {total * 1e3:>10.3f}")
+    return "\n".join(lines)
 
 
 class Job(ctypes.Structure):
