@@ -282,10 +282,16 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
   }
 }
 
-// x = dequantized embedding row of the step's token (gemma.c:5468-5493)
+// x = dequantized embedding row of the step's token, or its fp32 row times
+// the embedding scale (gemma.c:5468-5493)
 __global__ __launch_bounds__(kNT) void dec_embed_kernel(DecEmbed a) {
   int token, pos;
   if (!step_ok(a.step, a.nvocab, a.clen, &token, &pos)) return;
+  if (a.emb_f != nullptr) {
+    const float *row = a.emb_f + (size_t)token * a.dim;
+    for (int i = threadIdx.x; i < a.dim; i += kNT) a.x[i] = row[i] * a.esc;
+    return;
+  }
   const float esc = a.esc * a.emb_s[token];
   const int8_t *row = a.emb_q + (size_t)token * a.dim;
   for (int i = threadIdx.x; i < a.dim; i += kNT) a.x[i] = (float)row[i] * esc;

@@ -1124,14 +1124,17 @@ struct gemma_hip_decoder {
   std::vector<unsigned char> swa;
   int clen = 0, max_blocks = 0, nparts = 256;
   bool attn_f32 = true;  // prefill attention on the fp32 matrix cores (false: fp64)
+  bool quant = true;     // W8A8 weights; false: an fp32 ('U') model
   struct Layer {
     const int8_t *w[7];  // wq wk wv wo w1(up) w2(gate) w3(down), device
     const float *s[7];
+    const float *wf[7];  // the same, fp32 ('U'), device
     float *nq, *nk, *n1, *n2, *n3, *n4;  // device copies
   };
   std::vector<Layer> layers;
   const int8_t *emb = nullptr;
   const float *emb_s = nullptr;
+  const float *emb_f = nullptr;  // fp32 embedding / LM head ('U')
   float *fnorm = nullptr;
   char *mem = nullptr;  // every device buffer below lives in this allocation
   float *x[2]{}, *xq = nullptr, *xk = nullptr, *xv = nullptr, *xo = nullptr;
@@ -1149,6 +1152,7 @@ struct gemma_hip_decoder {
   float *pf_x = nullptr, *pf_y = nullptr, *pf_qkv = nullptr, *pf_xo = nullptr, *pf_g = nullptr;
   float *pf_as = nullptr;
   int8_t *pf_a8 = nullptr;
+  float *pf_h = nullptr;  // normalized rows ('U': the fp32 GEMMs' input)
   int *pf_tok = nullptr;
   double *pf_part = nullptr;  // attention key-split partials
 };
@@ -1179,7 +1183,8 @@ int prefill_reserve(gemma_hip_decoder *d, int n) {
                o_qkv = cv.take(rows * (q_sz + 2 * kv_sz) * 4), o_xo = cv.take(rows * q_sz * 4),
                o_g = cv.take(rows * 2 * mlp * 4), o_a8 = cv.take(rows * kmax),
                o_as = cv.take(rows * 4), o_tok = cv.take(rows * 4),
-               o_part = cv.take(gh::pf_attn_part_doubles(rows, c.n_heads, c.hdim) * 8);
+               o_part = cv.take(gh::pf_attn_part_doubles(rows, c.n_heads, c.hdim) * 8),
+               o_h = cv.take(d->quant ? 0 : rows * dim * 4);
   if (d->pf_mem != nullptr) {
     (void)hipStreamSynchronize(g.stream);
     (void)hipFree(d->pf_mem);
@@ -1198,6 +1203,7 @@ int prefill_reserve(gemma_hip_decoder *d, int n) {
   d->pf_as = (float *)(m + o_as);
   d->pf_tok = (int *)(m + o_tok);
   d->pf_part = (double *)(m + o_part);
+  d->pf_h = d->quant ? nullptr : (float *)(m + o_h);
   d->pf_rows = n;
   return 0;
 }
@@ -1215,6 +1221,10 @@ constexpr int kWarmRows = 256;  // rows from which a GEMM's weights are read ahe
 // the reference's score and value products too, as softmax).
 #define GH_OP(op, expr) timed((op), st, [&] { return (expr); })
 
+hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed, bool dense,
+                               hipStream_t st);
+hipError_t decoder_enqueue_f32(gemma_hip_decoder *d, hipStream_t st);
+
 hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, bool dense,
                            hipStream_t st) {
   const gemma_hip_text_config &c = d->cfg;
@@ -1226,7 +1236,8 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
     return GH_OP(kOpGemmInt8, gh::launch_gemm_i8(dst, dstr, 0, w, k, ws, d->pf_a8, k, d->pf_as,
                                                  n, nout, k, g.info, st));
   };
-  if (embed && (e = gh::launch_pf_embed(d->pf_tok, n, d->emb, d->emb_s, d->pf_x, dim,
+  if (!d->quant) return prefill_enqueue_f32(d, n, pos, embed, dense, st);
+  if (embed && (e = gh::launch_pf_embed(d->pf_tok, n, d->emb, d->emb_s, nullptr, d->pf_x, dim,
                                         c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
     return e;
   for (int l = 0; l < c.nl; ++l) {
@@ -1358,6 +1369,7 @@ int prefill_run(gemma_hip_decoder *dec, const char *kName, int n, int pos, int l
 
 // Enqueues one decode step on `st` (captured into the decoder's graph).
 hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
+  if (!d->quant) return decoder_enqueue_f32(d, st);
   const gemma_hip_text_config &c = d->cfg;
   const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim;
   hipError_t e;
@@ -1441,18 +1453,181 @@ hipError_t decoder_enqueue(gemma_hip_decoder *d, hipStream_t st) {
   }());
 }
 
+// The fp32 ('U') model's prompt pass: forward_text_chunk's !quant branches
+// (gemma.c:5079, 5297, 5358, 5384, 5431): the norms store fp32 rows, the
+// projections are fp32 GEMMs on the matrix cores (gemm_fpx), GELU(gate) * up
+// is computed in place, and the LM head is an fp32 GEMV; everything else is
+// the W8A8 pass's kernels.
+hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed, bool dense,
+                               hipStream_t st) {
+  const gemma_hip_text_config &c = d->cfg;
+  const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim, dim = c.dim, mlp = c.mlp_dim;
+  const int stride = q_sz + 2 * kv_sz;
+  const size_t cache = (size_t)d->clen * kv_sz;
+  hipError_t e;
+  // dst[r][0..nout) = src[r] . w rows (gemm_fpx, gemma.c:3308)
+  auto gemm = [&](float *dst, int dstr, const float *w, int nout, const float *src, int sstr,
+                  int k) {
+    return GH_OP(kOpGemmFpx, gh::launch_gemm_f32(dst, dstr, w, k, src, sstr, n, nout, k, nullptr,
+                                                 false, g.info, st));
+  };
+  if (embed && (e = gh::launch_pf_embed(d->pf_tok, n, nullptr, nullptr, d->emb_f, d->pf_x, dim,
+                                        c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
+    return e;
+  for (int l = 0; l < c.nl; ++l) {
+    const auto &L = d->layers[l];
+    gh::PfNorm n1{d->pf_x, l > 0 ? d->pf_y : nullptr,
+                  (l > 0 && c.mlp_pst) ? d->layers[l - 1].n4 : nullptr, L.n1, nullptr, nullptr,
+                  dim, c.eps, d->pf_h};
+    if ((e = GH_OP(kOpRmsnorm, gh::launch_pf_norm_rows(n1, n, st))) != hipSuccess) return e;
+    // q, k, v into the fused rows (gemma.c:5079)
+    if ((e = gemm(d->pf_qkv, stride, L.wf[0], q_sz, d->pf_h, dim, dim)) != hipSuccess ||
+        (e = gemm(d->pf_qkv + q_sz, stride, L.wf[1], kv_sz, d->pf_h, dim, dim)) != hipSuccess ||
+        (e = gemm(d->pf_qkv + q_sz + kv_sz, stride, L.wf[2], kv_sz, d->pf_h, dim, dim)) !=
+            hipSuccess)
+      return e;
+    const bool sliding = d->swa[l] != 0;
+    float *kc = d->kv + (size_t)l * 2 * cache;
+    const gh::PfRope rp{d->pf_qkv, stride, q_sz, c.qk_norm ? L.nq : nullptr,
+                        c.qk_norm ? L.nk : nullptr, sliding ? d->rope_l : d->rope_g, kc,
+                        kc + cache, d->clen, pos, c.n_heads, c.nkv, c.eps};
+    if ((e = GH_OP(kOpRope, gh::launch_pf_qk_rope(rp, n, c.hdim, st))) != hipSuccess) return e;
+    const gh::PfAttn at{d->pf_qkv, stride, kc, kc + cache, d->pf_xo, q_sz, n, pos, c.n_heads,
+                        c.nkv, d->clen, sliding ? c.slide : 0,
+                        (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
+                        0, dense ? 1 : 0};
+    if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, st))) !=
+        hipSuccess)
+      return e;
+    // o (gemma.c:5297), residual, norms
+    if ((e = gemm(d->pf_y, dim, L.wf[3], dim, d->pf_xo, q_sz, q_sz)) != hipSuccess) return e;
+    const gh::PfNorm n3{d->pf_x, d->pf_y, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
+                        nullptr, nullptr, dim, c.eps, d->pf_h};
+    if ((e = GH_OP(kOpRmsnorm, gh::launch_pf_norm_rows(n3, n, st))) != hipSuccess) return e;
+    // gate (w2) and up (w1) side by side in pf_g (gemma.c:5358), GELU, down (5384)
+    if ((e = gemm(d->pf_g, 2 * mlp, L.wf[5], mlp, d->pf_h, dim, dim)) != hipSuccess ||
+        (e = gemm(d->pf_g + mlp, 2 * mlp, L.wf[4], mlp, d->pf_h, dim, dim)) != hipSuccess ||
+        (e = GH_OP(kOpGelu, gh::launch_gelu_mul_rows(d->pf_g, n, mlp, st))) != hipSuccess ||
+        (e = gemm(d->pf_y, dim, L.wf[6], dim, d->pf_g, 2 * mlp, mlp)) != hipSuccess)
+      return e;
+  }
+  // the last row: last residual, final norm, LM head (gemma.c:5431), softcap, argmax
+  const size_t last = (size_t)(n - 1) * dim;
+  gh::DecNorm fn{d->pf_x + last, d->pf_y + last,
+                 c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm, nullptr, d->h, dim,
+                 c.eps};
+  if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(fn, st))) != hipSuccess) return e;
+  gh::GemvJobs lm{};
+  lm.w[0] = d->emb_f; lm.dst[0] = d->logits;
+  for (int j = 0; j < gh::kMaxJobs; ++j) lm.end[j] = c.nvocab;
+  lm.njobs = 1;
+  if ((e = GH_OP(kOpGemvFpx, gh::launch_gemv_f32(lm, dim, d->h, g.info, st))) != hipSuccess)
+    return e;
+  return timed(kOpSample, st, [&] {
+    hipError_t es = hipSuccess;
+    if (c.sc_log != 0.0f) es = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st);
+    if (es != hipSuccess) return es;
+    return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
+                                 d->tokens, d->clen, st);
+  }, kPhaseDecode);
+}
+
+// The fp32 ('U') model's decode step: forward_text_decode's !quant branches
+// (gemma.c:4762, 4855, 4906, 4925, 4960).  Each norm is one workgroup that
+// stores the new residual and the normalized vector, which the fp32 GEMVs
+// (gemv_fpx / gemv_fpx_multi) read; GELU(gate) * up is its own launch.
+hipError_t decoder_enqueue_f32(gemma_hip_decoder *d, hipStream_t st) {
+  const gemma_hip_text_config &c = d->cfg;
+  const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim, mlp = c.mlp_dim;
+  hipError_t e;
+  gh::DecEmbed em{nullptr, nullptr, d->x[0], d->step, c.dim, c.nvocab, d->clen,
+                  c.mlp_pre ? 1.0f : sqrtf((float)c.dim), d->emb_f};
+  if ((e = gh::launch_dec_embed(em, st)) != hipSuccess) return e;
+  auto gemv = [&](const gh::GemvJobs &jobs, int k, const float *x) {
+    return GH_OP(kOpGemvFpx, gh::launch_gemv_f32(jobs, k, x, g.info, st));
+  };
+  auto one_job = [](const float *w, float *dst, int rows) {
+    gh::GemvJobs j{};
+    j.w[0] = w; j.dst[0] = dst;
+    for (int t = 0; t < gh::kMaxJobs; ++t) j.end[t] = rows;
+    j.njobs = 1;
+    return j;
+  };
+  int cur = 0;
+  for (int l = 0; l < c.nl; ++l) {
+    const auto &L = d->layers[l];
+    gh::DecNorm n1{d->x[cur], l > 0 ? d->ymlp : nullptr,
+                   (l > 0 && c.mlp_pst) ? d->layers[l - 1].n4 : nullptr, L.n1,
+                   d->x[cur ^ 1], d->h, c.dim, c.eps};
+    if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(n1, st))) != hipSuccess) return e;
+    cur ^= 1;
+    gh::GemvJobs qkv{};
+    qkv.w[0] = L.wf[0]; qkv.w[1] = L.wf[1]; qkv.w[2] = L.wf[2];
+    qkv.dst[0] = d->xq; qkv.dst[1] = d->xk; qkv.dst[2] = d->xv;
+    qkv.end[0] = q_sz; qkv.end[1] = q_sz + kv_sz; qkv.end[2] = qkv.end[3] = q_sz + 2 * kv_sz;
+    qkv.njobs = 3;
+    if ((e = gemv(qkv, c.dim, d->h)) != hipSuccess) return e;
+    const size_t cache = (size_t)d->clen * kv_sz;
+    float *kc = d->kv + (size_t)l * 2 * cache;
+    const bool sliding = d->swa[l] != 0;
+    gh::DecAttn at{d->xq, d->xk, d->xv, c.qk_norm ? L.nq : nullptr, c.qk_norm ? L.nk : nullptr,
+                   sliding ? d->rope_l : d->rope_g, kc, kc + cache, d->part, d->xo, d->step,
+                   c.n_heads, c.nkv, c.hdim, d->clen, sliding ? c.slide : 0,
+                   d->max_blocks, c.nvocab, (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att,
+                   c.eps};
+    if ((e = GH_OP(kOpSoftmax, gh::launch_dec_attention(at, st))) != hipSuccess) return e;
+    if ((e = gemv(one_job(L.wf[3], d->yattn, c.dim), q_sz, d->xo)) != hipSuccess) return e;
+    gh::DecNorm n3{d->x[cur], d->yattn, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
+                   d->x[cur ^ 1], d->h, c.dim, c.eps};
+    if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(n3, st))) != hipSuccess) return e;
+    cur ^= 1;
+    gh::GemvJobs gu{};
+    gu.w[0] = L.wf[5]; gu.w[1] = L.wf[4];  // gate (w2), up (w1): gemma.c:4906-4910
+    gu.dst[0] = d->gbuf; gu.dst[1] = d->gbuf + mlp;
+    gu.end[0] = mlp; gu.end[1] = gu.end[2] = gu.end[3] = 2 * mlp;
+    gu.njobs = 2;
+    if ((e = gemv(gu, c.dim, d->h)) != hipSuccess ||
+        (e = GH_OP(kOpGelu, gh::launch_gelu_mul_rows(d->gbuf, 1, mlp, st))) != hipSuccess ||
+        (e = gemv(one_job(L.wf[6], d->ymlp, c.dim), mlp, d->gbuf)) != hipSuccess)
+      return e;
+  }
+  gh::DecNorm fn{d->x[cur], d->ymlp, c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm,
+                 nullptr, d->h, c.dim, c.eps};
+  if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(fn, st))) != hipSuccess) return e;
+  if ((e = gemv(one_job(d->emb_f, d->logits, c.nvocab), c.dim, d->h)) != hipSuccess) return e;
+  return GH_OP(kOpSample, [&] {
+    hipError_t es = hipSuccess;
+    if (c.sc_log != 0.0f) es = gh::launch_dec_softcap(d->logits, c.nvocab, c.sc_log, st);
+    if (es != hipSuccess) return es;
+    return gh::launch_dec_argmax(d->logits, c.nvocab, d->pval, d->pidx, d->nparts, d->step,
+                                 d->tokens, d->clen, st);
+  }());
+}
+
 }  // namespace
 
 extern "C" {
 
-gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
-                                            const gemma_hip_layer *layers,
-                                            const int8_t *emb, const float *emb_s,
-                                            const float *fnorm, int clen) {
-  if (need_init()) return nullptr;
-  if (cfg == nullptr || layers == nullptr || emb == nullptr || emb_s == nullptr ||
+}  // extern "C"
+
+namespace {
+
+// One layer's tensors as a create entry point passes them: the seven
+// projections (int8 with row scales, or fp32), the norm weights.
+struct LayerSrc {
+  const void *w[7];  // wq wk wv wo w1 w2 w3
+  const float *s[7];
+  const float *norm[6];  // nq nk n1 n2 n3 n4
+};
+
+// gemma_hip_decoder_create(_f32): quant selects W8A8 weights (emb int8 with
+// emb_s) or fp32 ones (emb fp32, emb_s unused).
+gemma_hip_decoder *decoder_build(const char *name, const gemma_hip_text_config *cfg,
+                                 const LayerSrc *layers, bool quant, const void *emb,
+                                 const float *emb_s, const float *fnorm, int clen) {
+  if (cfg == nullptr || layers == nullptr || emb == nullptr || (quant && emb_s == nullptr) ||
       fnorm == nullptr || cfg->swa == nullptr) {
-    fail("gemma_hip_decoder_create: null argument");
+    fail("%s: null argument", name);
     return nullptr;
   }
   const gemma_hip_text_config c = *cfg;
@@ -1460,18 +1635,19 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
       c.hdim % 2 != 0 || c.dim <= 0 || c.dim % 16 != 0 || c.dim > 6144 || c.mlp_dim <= 0 ||
       c.mlp_dim % 16 != 0 || c.nvocab <= 0 || c.q_scale <= 0 || clen <= 0 || c.slide < 0 ||
       (c.n_heads * c.hdim) % 16 != 0) {
-    fail("gemma_hip_decoder_create: unsupported config (nl=%d heads=%d/%d hdim=%d dim=%d "
-         "mlp=%d vocab=%d clen=%d)", c.nl, c.n_heads, c.nkv, c.hdim, c.dim, c.mlp_dim, c.nvocab,
+    fail("%s: unsupported config (nl=%d heads=%d/%d hdim=%d dim=%d "
+         "mlp=%d vocab=%d clen=%d)", name, c.nl, c.n_heads, c.nkv, c.hdim, c.dim, c.mlp_dim, c.nvocab,
          clen);
     return nullptr;
   }
   for (int l = 0; l < c.nl; ++l)
     if (c.swa[l] && c.slide <= 0) {
-      fail("gemma_hip_decoder_create: layer %d slides but slide = %d", l, c.slide);
+      fail("%s: layer %d slides but slide = %d", name, l, c.slide);
       return nullptr;
     }
   gemma_hip_decoder *d = new gemma_hip_decoder();
   d->cfg = c;
+  d->quant = quant;
   d->swa.assign(c.swa, c.swa + c.nl);
   d->cfg.swa = nullptr;
   d->clen = clen;
@@ -1479,8 +1655,9 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   const int hn = c.n_heads / c.nkv;
   if (gh::dec_attn_lds(hn, c.hdim) > 65536 || (size_t)d->max_blocks * 8 > 65536 ||
       c.hdim % 128 != 0 || c.hdim > 512) {
-    fail("gemma_hip_decoder_create: unsupported attention shape (head dim %d must be a "
-         "multiple of 128 up to 512; %d q heads per kv head; context %d)", c.hdim, hn, clen);
+    fail("%s: unsupported attention shape (head dim %d must be a "
+         "multiple of 128 up to 512; %d q heads per kv head; context %d)", name, c.hdim, hn,
+         clen);
     decoder_free(d);
     return nullptr;
   }
@@ -1489,35 +1666,52 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   // resolve every weight; rows must be 16-byte aligned on the device
   auto weight = [&](const void *host, size_t bytes, const char *what, const void **out) {
     const char *p = resolve(host, bytes);
-    if (p == nullptr) return fail("gemma_hip_decoder_create: %s is not registered", what);
+    if (p == nullptr) return fail("%s: %s is not registered", name, what);
     if ((uintptr_t)p % 16 != 0)
-      return fail("gemma_hip_decoder_create: %s is not 16-byte aligned on the device "
-                  "(register each tensor as its own range)", what);
+      return fail("%s: %s is not 16-byte aligned on the device "
+                  "(register each tensor as its own range)", name, what);
     *out = p;
     return 0;
   };
   const void *ptr = nullptr;
-  if (weight(emb, (size_t)c.nvocab * dim, "emb", &ptr)) { decoder_free(d); return nullptr; }
-  d->emb = (const int8_t *)ptr;
-  if (weight(emb_s, (size_t)c.nvocab * 4, "emb scales", &ptr)) { decoder_free(d); return nullptr; }
-  d->emb_s = (const float *)ptr;
+  const size_t wbytes = quant ? 1 : 4;  // bytes per weight
+  if (weight(emb, (size_t)c.nvocab * dim * wbytes, "emb", &ptr)) {
+    decoder_free(d);
+    return nullptr;
+  }
+  if (quant) {
+    d->emb = (const int8_t *)ptr;
+    if (weight(emb_s, (size_t)c.nvocab * 4, "emb scales", &ptr)) {
+      decoder_free(d);
+      return nullptr;
+    }
+    d->emb_s = (const float *)ptr;
+  } else {
+    d->emb_f = (const float *)ptr;
+  }
   d->layers.resize(c.nl);
   for (int l = 0; l < c.nl; ++l) {
-    const gemma_hip_layer &src = layers[l];
-    const int8_t *ws[7] = {src.wq, src.wk, src.wv, src.wo, src.w1, src.w2, src.w3};
-    const float *ss[7] = {src.wq_s, src.wk_s, src.wv_s, src.wo_s, src.w1_s, src.w2_s, src.w3_s};
+    const LayerSrc &src = layers[l];
     const size_t rows[7] = {q_sz, kv_sz, kv_sz, dim, mlp, mlp, dim};
     const size_t cols[7] = {dim, dim, dim, q_sz, dim, dim, mlp};
     static const char *names[7] = {"wq", "wk", "wv", "wo", "w1", "w2", "w3"};
     for (int t = 0; t < 7; ++t) {
-      if (weight(ws[t], rows[t] * cols[t], names[t], &ptr)) { decoder_free(d); return nullptr; }
+      if (weight(src.w[t], rows[t] * cols[t] * wbytes, names[t], &ptr)) {
+        decoder_free(d);
+        return nullptr;
+      }
+      if (!quant) {
+        d->layers[l].wf[t] = (const float *)ptr;
+        continue;
+      }
       d->layers[l].w[t] = (const int8_t *)ptr;
-      if (weight(ss[t], rows[t] * 4, names[t], &ptr)) { decoder_free(d); return nullptr; }
+      if (weight(src.s[t], rows[t] * 4, names[t], &ptr)) { decoder_free(d); return nullptr; }
       d->layers[l].s[t] = (const float *)ptr;
     }
-    if (src.n1 == nullptr || src.n2 == nullptr || (c.qk_norm && (!src.nq || !src.nk)) ||
-        (c.mlp_pre && !src.n3) || (c.mlp_pst && !src.n4)) {
-      fail("gemma_hip_decoder_create: layer %d lacks a norm weight", l);
+    const float *const *nm = src.norm;  // nq nk n1 n2 n3 n4
+    if (nm[2] == nullptr || nm[3] == nullptr || (c.qk_norm && (!nm[0] || !nm[1])) ||
+        (c.mlp_pre && !nm[4]) || (c.mlp_pst && !nm[5])) {
+      fail("%s: layer %d lacks a norm weight", name, l);
       decoder_free(d);
       return nullptr;
     }
@@ -1529,7 +1723,7 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   for (int l = 0; l < c.nl; ++l) o_norm[l] = cv.take(norm_floats * 4);
   const size_t o_fnorm = cv.take(dim * 4), o_x0 = cv.take(dim * 4), o_x1 = cv.take(dim * 4),
                o_xq = cv.take(q_sz * 4), o_xk = cv.take(kv_sz * 4), o_xv = cv.take(kv_sz * 4),
-               o_xo = cv.take(q_sz * 4), o_ya = cv.take(dim * 4), o_g = cv.take(mlp * 4),
+               o_xo = cv.take(q_sz * 4), o_ya = cv.take(dim * 4), o_g = cv.take((quant ? 1 : 2) * mlp * 4),
                o_ym = cv.take(dim * 4), o_h = cv.take(dim * 4),
                o_lg = cv.take((size_t)c.nvocab * 4),
                o_part = cv.take((size_t)c.n_heads * d->max_blocks * (c.hdim + 2) * 8),
@@ -1540,7 +1734,7 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   hipError_t e = hipMalloc((void **)&d->mem, cv.used);
   if (e == hipSuccess) e = hipHostMalloc((void **)&d->pin, 64, hipHostMallocDefault);
   if (e != hipSuccess) {
-    hip_fail("gemma_hip_decoder_create: alloc", e);
+    hip_fail(name, e);
     decoder_free(d);
     return nullptr;
   }
@@ -1569,8 +1763,7 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   std::vector<float> host(norm_floats * c.nl + dim, 0.0f);
   for (int l = 0; l < c.nl; ++l) {
     float *dst = host.data() + norm_floats * l;
-    const gemma_hip_layer &src = layers[l];
-    const float *parts[6] = {src.nq, src.nk, src.n1, src.n2, src.n3, src.n4};
+    const float *const *parts = layers[l].norm;
     const size_t lens[6] = {(size_t)c.hdim, (size_t)c.hdim, dim, dim, dim, dim};
     float *devp[6];
     size_t off = 0;
@@ -1610,7 +1803,7 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
     }
   }
   if (e != hipSuccess) {
-    hip_fail("gemma_hip_decoder_create: upload", e);
+    hip_fail(name, e);
     decoder_free(d);
     return nullptr;
   }
@@ -1623,11 +1816,55 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
   }
   if (e == hipSuccess) e = hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0);
   if (e != hipSuccess) {
-    hip_fail("gemma_hip_decoder_create: graph capture", e);
+    hip_fail(name, e);
     decoder_free(d);
     return nullptr;
   }
   return d;
+}
+
+}  // namespace
+
+extern "C" {
+
+gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
+                                            const gemma_hip_layer *layers,
+                                            const int8_t *emb, const float *emb_s,
+                                            const float *fnorm, int clen) {
+  static const char *kName = "gemma_hip_decoder_create";
+  if (need_init()) return nullptr;
+  if (cfg == nullptr || layers == nullptr || cfg->nl <= 0) {
+    fail("%s: null argument", kName);
+    return nullptr;
+  }
+  std::vector<LayerSrc> src(cfg->nl);
+  for (int l = 0; l < cfg->nl; ++l) {
+    const gemma_hip_layer &a = layers[l];
+    src[l] = LayerSrc{{a.wq, a.wk, a.wv, a.wo, a.w1, a.w2, a.w3},
+                      {a.wq_s, a.wk_s, a.wv_s, a.wo_s, a.w1_s, a.w2_s, a.w3_s},
+                      {a.nq, a.nk, a.n1, a.n2, a.n3, a.n4}};
+  }
+  return decoder_build(kName, cfg, src.data(), true, emb, emb_s, fnorm, clen);
+}
+
+gemma_hip_decoder *gemma_hip_decoder_create_f32(const gemma_hip_text_config *cfg,
+                                                const gemma_hip_layer_f32 *layers,
+                                                const float *emb, const float *fnorm,
+                                                int clen) {
+  static const char *kName = "gemma_hip_decoder_create_f32";
+  if (need_init()) return nullptr;
+  if (cfg == nullptr || layers == nullptr || cfg->nl <= 0) {
+    fail("%s: null argument", kName);
+    return nullptr;
+  }
+  std::vector<LayerSrc> src(cfg->nl);
+  for (int l = 0; l < cfg->nl; ++l) {
+    const gemma_hip_layer_f32 &a = layers[l];
+    src[l] = LayerSrc{{a.wq, a.wk, a.wv, a.wo, a.w1, a.w2, a.w3},
+                      {},
+                      {a.nq, a.nk, a.n1, a.n2, a.n3, a.n4}};
+  }
+  return decoder_build(kName, cfg, src.data(), false, emb, nullptr, fnorm, clen);
 }
 
 void gemma_hip_decoder_destroy(gemma_hip_decoder *dec) {

@@ -152,7 +152,8 @@ struct DecNorm {
   float eps;
 };
 
-// x = emb_q[token] * (esc * emb_s[token]); step = {token, pos, count}
+// x = emb_q[token] * (esc * emb_s[token]), or emb_f[token] * esc for an
+// fp32 table (emb_f non-null); step = {token, pos, count}
 struct DecEmbed {
   const int8_t *emb_q;
   const float *emb_s;
@@ -160,6 +161,7 @@ struct DecEmbed {
   const int *step;
   int dim, nvocab, clen;
   float esc;
+  const float *emb_f;
 };
 
 // Keys per attention workgroup, and its LDS bytes for hn q heads per kv head.
@@ -207,6 +209,8 @@ struct WarmRegions {
 };
 // Rows of x [n][dim] (in place), y [n][dim] nullable: the per-row form of
 // DecNorm; h of every row is quantized into xq [n][dim] + xs [n].
+// per row: x = clamp(x + post(y)), h = rmsnorm(x; w_pre) quantized into
+// xq/xs, or, when xq is null, stored to h (fp32 rows [n][dim])
 struct PfNorm {
   float *x;
   const float *y;
@@ -216,6 +220,7 @@ struct PfNorm {
   float *xs;
   int dim;
   float eps;
+  float *h;
 };
 // qkv [n][stride]: q heads at column h*hdim, k heads from q_sz, v heads from
 // q_sz + kv_sz; rows sit at positions pos0 .. pos0+n-1; kc/vc [nkv][clen][hdim]
@@ -255,8 +260,10 @@ inline size_t pf_attn_part_doubles(size_t n, size_t n_heads, size_t hdim) {
 // float4 chunks per thread of the row kernels: dim <= 6144 (256 threads),
 // mlp <= 24576 (1024 threads)
 constexpr int kPfMaxNpt = 6;
+// emb_f non-null: an fp32 table (rows emb_f[token] * esc), else int8 rows
+// scaled by esc * emb_s[token]
 hipError_t launch_pf_embed(const int *tokens, int n, const int8_t *emb_q, const float *emb_s,
-                           float *x, int dim, float esc, hipStream_t stream);
+                           const float *emb_f, float *x, int dim, float esc, hipStream_t stream);
 hipError_t launch_pf_norm_rows(const PfNorm &a, int n, hipStream_t stream);
 hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t stream);
 // hdim 128 or 256; the q heads per kv head must divide 32; a.part must hold
@@ -265,6 +272,9 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t stream);
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
                                 const WarmRegions &warm, hipStream_t stream);
+// rows g [n][2 * mlp] = (gate | up): gate = gelu(gate) * up in place (the
+// fp32-weight path, where no quantize follows); mlp % 4 == 0
+hipError_t launch_gelu_mul_rows(float *g, int n, int mlp, hipStream_t stream);
 
 // vision.hip: the SigLIP tower (forward_vision).
 // per row: x = clamp((y + bias) + x) when y is given; LayerNorm(x; w, b) into

@@ -39,29 +39,37 @@ namespace {
 // x[r] = emb_q[tokens[r]] * (esc * emb_s[tokens[r]]) (gemma.c:5468-5493,
 // per token); the host range-checks every token
 __global__ __launch_bounds__(kNT) void pf_embed_kernel(const int *tokens, const int8_t *emb_q,
-                                                       const float *emb_s, float *x, int dim,
-                                                       float esc) {
+                                                       const float *emb_s, const float *emb_f,
+                                                       float *x, int dim, float esc) {
   const int token = tokens[blockIdx.x];
+  float *xr = x + (size_t)blockIdx.x * dim;
+  if (emb_f != nullptr) {
+    const float *row = emb_f + (size_t)token * dim;
+    for (int i = threadIdx.x; i < dim; i += kNT) xr[i] = row[i] * esc;
+    return;
+  }
   const float s = esc * emb_s[token];
   const int8_t *row = emb_q + (size_t)token * dim;
-  float *xr = x + (size_t)blockIdx.x * dim;
   for (int i = threadIdx.x; i < dim; i += kNT) xr[i] = (float)row[i] * s;
 }
 
 // One workgroup per row: x[r] = clamp(x[r] + post(y[r])), h = rmsnorm(x[r],
-// w_pre), h quantized into xq[r] / xs[r] (quantize_acts, gemma.c:2652-2674).
+// w_pre), h quantized into xq[r] / xs[r] (quantize_acts, gemma.c:2652-2674),
+// or stored to h[r] when xq is null.
 template <int NPT>
 __global__ __launch_bounds__(kNT) void pf_norm_rows_kernel(PfNorm a) {
   __shared__ double red[kWaves];
   __shared__ float redf[kWaves];
   const size_t r = blockIdx.x;
   float *xr = a.x + r * a.dim;
+  const bool quant = a.xq != nullptr;
   const DecNorm na{xr, a.y != nullptr ? a.y + r * a.dim : nullptr, a.w_post, a.w_pre, xr,
-                   nullptr, a.dim, a.eps};
+                   quant ? nullptr : a.h + r * a.dim, a.dim, a.eps};
   NormIn<NPT> in;
   norm_load<NPT, kNT>(na, in);
-  const float s = norm_quant<NPT, kNT, true>(na, in, a.xq + r * a.dim, red, redf);
-  if (threadIdx.x == 0) a.xs[r] = s;
+  const float s = norm_quant<NPT, kNT, true>(na, in, quant ? a.xq + r * a.dim : nullptr, red,
+                                             redf);
+  if (quant && threadIdx.x == 0) a.xs[r] = s;
 }
 
 // One wave per (row, head): q heads are normalized (nq) and rotated in place;
@@ -756,6 +764,30 @@ __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) 
   }
 }
 
+// gate = gelu(gate) * up in place over rows [gate (mlp) | up (mlp)], grid
+// (ceil(mlp / 4 / kNT), rows): the fp32-weight path's GELU (gemma.c:
+// 4139-4172 with mul), each value evaluated in fp64 and rounded once as the
+// quantizing kernels do.
+__global__ __launch_bounds__(kNT) void gelu_mul_rows_kernel(float *g, int mlp) {
+  __shared__ double etab[128];
+  exp_tab_load(etab);
+  const ExpConsts ec = exp_consts();
+  const int c = blockIdx.x * kNT + threadIdx.x;
+  float *gate = g + (size_t)blockIdx.y * 2 * mlp;
+  const bool ok = c < mlp / 4;
+  v4f gv = {0.f, 0.f, 0.f, 0.f}, uv = gv;
+  if (ok) {
+    gv = reinterpret_cast<const v4f *>(gate)[c];
+    uv = reinterpret_cast<const v4f *>(gate + mlp)[c];
+  }
+  lds_barrier();  // the exp table
+  if (!ok) return;
+  v4f out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = (float)(gelu((double)gv[e], etab, ec) * (double)uv[e]);
+  reinterpret_cast<v4f *>(gate)[c] = out;
+}
+
 // One workgroup per row: out = gelu(gate) * up (gemma.c:4139-4172, the GELU
 // gate fused with the up projection) rounded once, then quantized into
 // xq[r] / xs[r] as quantize_act does.  g is [n][2 mlp], gate columns first.
@@ -813,8 +845,15 @@ hipError_t by_npt(int npt, F &&launch) {
 }  // namespace
 
 hipError_t launch_pf_embed(const int *tokens, int n, const int8_t *emb_q, const float *emb_s,
-                           float *x, int dim, float esc, hipStream_t stream) {
-  pf_embed_kernel<<<n, kNT, 0, stream>>>(tokens, emb_q, emb_s, x, dim, esc);
+                           const float *emb_f, float *x, int dim, float esc, hipStream_t stream) {
+  pf_embed_kernel<<<n, kNT, 0, stream>>>(tokens, emb_q, emb_s, emb_f, x, dim, esc);
+  return hipGetLastError();
+}
+
+hipError_t launch_gelu_mul_rows(float *g, int n, int mlp, hipStream_t stream) {
+  if (n <= 0 || mlp <= 0 || mlp % 4 != 0) return hipErrorInvalidValue;
+  const int n4 = mlp / 4;
+  gelu_mul_rows_kernel<<<dim3((n4 + kNT - 1) / kNT, n), kNT, 0, stream>>>(g, mlp);
   return hipGetLastError();
 }
 

@@ -91,6 +91,13 @@ class Layer(ctypes.Structure):
         "nq", "nk", "n1", "n2", "n3", "n4")]
 
 
+class LayerF32(ctypes.Structure):
+    """gemma_hip_layer_f32: one TextDecoderLayer of an fp32 ('U') file."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "wq", "wk", "wv", "wo", "w1", "w2", "w3", "nq", "nk", "n1", "n2", "n3", "n4")]
+
+
 class VisionConfig(ctypes.Structure):
     """gemma_hip_vision_config: the reference's VisionConfig (gemma.c:713-721)
     plus TextConfig's img_tok and dim (here text_dim)."""
@@ -149,6 +156,8 @@ _SIGS = {
     "gemma_hip_patch_embed_host": (_I, [_P, _P, _P, _P, _I, _I, _I]),
     "gemma_hip_decoder_create": (_P, [ctypes.POINTER(TextConfig), ctypes.POINTER(Layer), _P, _P,
                                       _P, _I]),
+    "gemma_hip_decoder_create_f32": (_P, [ctypes.POINTER(TextConfig), ctypes.POINTER(LayerF32),
+                                          _P, _P, _I]),
     "gemma_hip_decoder_destroy": (None, [_P]),
     "gemma_hip_decoder_step": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
     "gemma_hip_decoder_generate": (_I, [_P, _I, _I, _I, _P]),
@@ -364,20 +373,28 @@ class Decoder:
                          c["q_scale"], c["slide"], c["nvocab"], c["theta_l"], c["theta_g"],
                          c["eps"], c["sc_att"], c["sc_log"], int(c["qk_norm"]),
                          int(c["mlp_pre"]), int(c["mlp_pst"]), swa.ctypes.data)
-        layers = (Layer * c["nl"])()
+        quant = c.get("quant", True)
+        layers = ((Layer if quant else LayerF32) * c["nl"])()
         try:
             for i, ly in enumerate(model["layers"]):
                 f = {}
                 for w in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
-                    f[w] = reg(ly[w][0])
-                    f[w + "_s"] = reg(ly[w][1])
+                    if quant:
+                        f[w] = reg(ly[w][0])
+                        f[w + "_s"] = reg(ly[w][1])
+                    else:  # 'U': one fp32 [out][in] array
+                        f[w] = reg(ly[w])
                 for n in ("nq", "nk", "n1", "n2", "n3", "n4"):
                     f[n] = host(ly[n]) if ly.get(n) is not None else None
-                layers[i] = Layer(**f)
-            emb_q, emb_s = reg(model["emb"][0]), reg(model["emb"][1])
+                layers[i] = (Layer if quant else LayerF32)(**f)
             fnorm = host(model["fnorm"])
-            self.handle = self.lib.gemma_hip_decoder_create(ctypes.byref(cfg), layers, emb_q,
-                                                            emb_s, fnorm, clen)
+            if quant:
+                emb_q, emb_s = reg(model["emb"][0]), reg(model["emb"][1])
+                self.handle = self.lib.gemma_hip_decoder_create(ctypes.byref(cfg), layers,
+                                                                emb_q, emb_s, fnorm, clen)
+            else:
+                self.handle = self.lib.gemma_hip_decoder_create_f32(
+                    ctypes.byref(cfg), layers, reg(model["emb"]), fnorm, clen)
             if not self.handle:
                 raise GemmaHipError(self.lib.gemma_hip_last_error().decode())
         except Exception:

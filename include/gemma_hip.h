@@ -316,6 +316,26 @@ gemma_hip_decoder *gemma_hip_decoder_create(const gemma_hip_text_config *cfg,
                                             const float *fnorm, int clen);
 void gemma_hip_decoder_destroy(gemma_hip_decoder *dec);
 
+/* One TextDecoderLayer of an unquantized ('U') file: fp32 weights [out][in]
+ * (QTensor.fpx, gemma.c:1125-1131) as host pointers inside registered
+ * ranges; the norms as for gemma_hip_layer. */
+typedef struct {
+  const float *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+  const float *nq, *nk, *n1, *n2, *n3, *n4;
+} gemma_hip_layer_f32;
+
+/* gemma_hip_decoder_create for a 'U' file: the reference's !quant branches
+ * (decode gemma.c:4762, 4855, 4906, 4925, 4960; prefill 5079, 5297, 5358,
+ * 5384, 5431) on the device: emb is the fp32 [nvocab][dim] table (also the
+ * tied LM head), the projections run as fp32 GEMVs (gemv_fpx) in the step
+ * and as fp32 matrix-core GEMMs (gemm_fpx) in the prompt pass, with no
+ * activation quantize.  Every other decoder entry point takes the result as
+ * it takes a W8A8 decoder. */
+gemma_hip_decoder *gemma_hip_decoder_create_f32(const gemma_hip_text_config *cfg,
+                                                const gemma_hip_layer_f32 *layers,
+                                                const float *emb, const float *fnorm,
+                                                int clen);
+
 /* One step at position pos (0 <= pos < clen, token < nvocab): logits (host,
  * nvocab floats) and next (the argmax) are written when non-NULL. */
 int gemma_hip_decoder_step(gemma_hip_decoder *dec, int token, int pos,

@@ -100,14 +100,23 @@ class DecodeOracle:
         self.clen = clen
 
     def gemv(self, w, x_f32):
-        """quantize_act + gemv_int8 (gemma.c:2590-2788): exact."""
+        """quantize_act + gemv_int8 (gemma.c:2590-2788): exact.  For an fp32
+        ('U') model, gemv_fpx (2734-2757): the fp32 dot products evaluated in
+        float64 and rounded once (the reference sums in its compiler's fp32
+        order, so no fp32 result is canonical; the exact one is what both
+        are checked against)."""
+        if not self.c.get("quant", True):
+            return (np.asarray(w, F64) @ np.asarray(x_f32, F64)).astype(F32)
         q, xs = self.o.quantize_act(np.ascontiguousarray(x_f32, F32))
         acc = int_dot(q, w[0])
         return acc.astype(F32) * (F32(xs) * np.asarray(w[1], F32))
 
     def gemm(self, w, x_f32):
         """quantize_acts + gemm_int8 (gemma.c:2652-2674, 3937-4054) over the
-        rows of x_f32, exact; row i equals gemv(w, x_f32[i])."""
+        rows of x_f32, exact; row i equals gemv(w, x_f32[i]) (for a 'U' model
+        gemm_fpx, gemma.c:3308, as gemv does it)."""
+        if not self.c.get("quant", True):
+            return (np.asarray(x_f32, F64) @ np.asarray(w, F64).T).astype(F32)
         q, xs = self.o.quantize_acts(np.ascontiguousarray(x_f32, F32))
         acc = int_dot(q, w[0])
         return acc.astype(F32) * (xs[:, None] * np.asarray(w[1], F32)[None, :])
@@ -117,8 +126,11 @@ class DecodeOracle:
         dim, hd, nh, nkv = c["dim"], c["hdim"], c["n_heads"], c["nkv"]
         eps = c["eps"]
         esc = F32(1.0) if c["mlp_pre"] else F32(np.sqrt(F32(dim)))
-        esc = F32(esc * m["emb"][1][token])
-        x = (m["emb"][0][token].astype(F32) * esc).astype(F32)
+        if c.get("quant", True):
+            esc = F32(esc * m["emb"][1][token])
+            x = (m["emb"][0][token].astype(F32) * esc).astype(F32)
+        else:  # the fp32 row (gemma.c:5484-5486)
+            x = (np.asarray(m["emb"][token], F32) * esc).astype(F32)
         asc = F32(1.0) / F32(np.sqrt(F32(c["q_scale"])))
         for li, ly in enumerate(m["layers"]):
             resid = x
@@ -181,8 +193,11 @@ class DecodeOracle:
         else:
             toks = np.asarray(tokens, np.int64)
             esc0 = F32(1.0) if c["mlp_pre"] else F32(np.sqrt(F32(dim)))
-            esc = (esc0 * np.asarray(m["emb"][1], F32)[toks]).astype(F32)
-            x = (np.asarray(m["emb"][0])[toks].astype(F32) * esc[:, None]).astype(F32)
+            if c.get("quant", True):
+                esc = (esc0 * np.asarray(m["emb"][1], F32)[toks]).astype(F32)
+                x = (np.asarray(m["emb"][0])[toks].astype(F32) * esc[:, None]).astype(F32)
+            else:
+                x = (np.asarray(m["emb"], F32)[toks] * esc0).astype(F32)
         n = len(x)
         asc = F32(1.0) / F32(np.sqrt(F32(c["q_scale"])))
         pos = pos0 + np.arange(n)
