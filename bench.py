@@ -38,7 +38,10 @@ The JSON line also carries, measured in the same run:
                 tokens/s and int8 TOPS of its GEMMs, then tokens/s of the
                 device-resident greedy decode step (gemma_hip_decoder_generate:
                 embedding, norms, q/k/v, RoPE, KV cache, attention, o, GELU,
-                down, LM head, argmax)
+                down, LM head, argmax); "gemma-3-1b:U" is config 3 as an
+                unquantized ('U') model (gemma_hip_decoder_create_f32: fp32
+                GEMVs, ~4 GB of weights per token; fp32 matrix-core GEMMs in
+                the prompt pass)
   vision        config 4 end to end: one 896x896 image through the SigLIP
                 tower on the GPU (gemma_hip_vision_forward), ms per image
   cpu_baseline  the reference's own quantize_act + gemv_int8(_multi), compiled
@@ -405,7 +408,9 @@ def bench_decode_1b(torch, gh, gen, timer, tokens):
 
 # decode phases of BASELINE.json configs 3 and 5: (model, context before, timed steps)
 # BASELINE.json configs 1, 3 and 5: (model, prompt tokens, greedy decode steps)
-DECODER_RUNS = (("gemma-3-270m", 32, 64), ("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512))
+# name[:U] (":U": an unquantized fp32 model file), prompt tokens, decode steps
+DECODER_RUNS = (("gemma-3-270m", 32, 64), ("gemma-3-1b", 512, 256), ("gemma-3-4b", 2048, 512),
+                ("gemma-3-1b:U", 512, 256))
 
 
 def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
@@ -423,7 +428,9 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
 
     import model_bin
 
-    model = model_bin.synth_model(name, seed=1234)
+    base, _, kind = name.partition(":")
+    quant = kind != "U"
+    model = model_bin.synth_model(base, seed=1234, quant=quant)
     c = model["config"]
     ids = np.random.default_rng(1234).integers(0, c["nvocab"], prompt).astype(np.int32)
     dec = gh.decoder(model, prompt + steps + 1)
@@ -456,12 +463,17 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
                         + gemm_ops(prompt, 2 * c["mlp_dim"], c["dim"])
                         + gemm_ops(prompt, c["dim"], c["mlp_dim"]))
     prefill = dict(tokens=prompt, ms=round(1e3 * t_pf, 3), tok_s=round(prompt / t_pf, 1),
-                   int8_tops=round(pf_ops / t_pf / 1e12, 1),
-                   int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4),
                    ms_attn_f64=round(1e3 * t_pf64, 3), tok_s_attn_f64=round(prompt / t_pf64, 1))
-    per_layer = (gemv_bytes(q_sz + 2 * kv_sz, c["dim"]) + gemv_bytes(c["dim"], q_sz)
-                 + gemv_bytes(2 * c["mlp_dim"], c["dim"]) + gemv_bytes(c["dim"], c["mlp_dim"]))
-    weights = c["nl"] * per_layer + gemv_bytes(c["nvocab"], c["dim"])
+    if quant:
+        prefill.update(int8_tops=round(pf_ops / t_pf / 1e12, 1),
+                       int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4))
+    else:  # the fp32 GEMMs on the fp32 matrix cores
+        prefill.update(fp32_tflops=round(pf_ops / t_pf / 1e12, 1),
+                       fp32_frac=round(pf_ops / t_pf / 1e12 / FP32_PEAK_TFLOPS, 4))
+    gb = gemv_bytes if quant else gemv_f32_bytes
+    per_layer = (gb(q_sz + 2 * kv_sz, c["dim"]) + gb(c["dim"], q_sz)
+                 + gb(2 * c["mlp_dim"], c["dim"]) + gb(c["dim"], c["mlp_dim"]))
+    weights = c["nl"] * per_layer + gb(c["nvocab"], c["dim"])
     kv = 0
     for pos in range(prompt, prompt + steps):
         for sw in c["swa"]:
@@ -604,7 +616,8 @@ def perf_report(torch, gh, decoder_runs) -> str:
 
     out = []
     for name, prompt, steps in decoder_runs:
-        model = model_bin.synth_model(name, seed=1234)
+        base, _, kind = name.partition(":")
+        model = model_bin.synth_model(base, seed=1234, quant=kind != "U")
         ids = np.random.default_rng(1234).integers(0, model["config"]["nvocab"],
                                                    prompt).astype(np.int32)
         dec = gh.decoder(model, prompt + steps + 1)
@@ -653,9 +666,10 @@ def main() -> int:
                     default=None,
                     help="profiling aid: run just the timed sweep, the LM-head timing, "
                          "the device-resident decoder, the vision tower or the GEMM shapes")
-    ap.add_argument("--decoder-models", default="gemma-3-270m,gemma-3-1b,gemma-3-4b",
+    ap.add_argument("--decoder-models",
+                    default="gemma-3-270m,gemma-3-1b,gemma-3-4b,gemma-3-1b:U",
                     help="models of the decoder timing (comma list of gemma-3-270m, "
-                         "gemma-3-1b, gemma-3-4b)")
+                         "gemma-3-1b, gemma-3-4b, gemma-3-1b:U; ':U' an fp32 model)")
     ap.add_argument("--perf-report", action="store_true",
                     help="print the reference's per-op report (PerfBench names) of the "
                          "decoder models and the vision tower, then exit")

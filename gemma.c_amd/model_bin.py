@@ -280,28 +280,34 @@ def read_bin(path: str) -> dict:
     return out
 
 
-def synth_model(name: str, seed: int = 1234, nvocab: int = NVOCAB) -> dict:
+def synth_model(name: str, seed: int = 1234, nvocab: int = NVOCAB, quant: bool = True) -> dict:
     """A random W8A8 model of shape `name` in memory, in read_bin()'s layout,
     for throughput runs where writing a multi-GB file would dominate: int8
     weights are tiles of one 64 MB random block (each tensor starting at its
     own offset), row scales U(4e-4, 8e-4) (the scale of N(0, 0.02) weights
-    quantized per row), norm weights 0."""
+    quantized per row), norm weights 0.  quant=False: an fp32 ('U') model,
+    weights tiles of one 64 MB block of N(0, 0.02) floats."""
     c = CONFIGS[name]
     nl, dim, hdim, mlp = c["nl"], c["dim"], c["hdim"], c["mlp"]
     q_sz, kv_sz = c["n_heads"] * hdim, c["nkv"] * hdim
     rng = np.random.default_rng(seed)
-    block = np.frombuffer(rng.bytes(64 << 20), np.int8)
-    block = np.where(block == -128, np.int8(127), block).astype(np.int8)
+    if quant:
+        block = np.frombuffer(rng.bytes(64 << 20), np.int8)
+        block = np.where(block == -128, np.int8(127), block).astype(np.int8)
+    else:
+        block = (rng.standard_normal(16 << 20) * 0.02).astype(np.float32)
     twice = np.concatenate([block, block])
 
     def qt(rows, cols):
         n = rows * cols
-        q = np.empty(n, np.int8)
+        q = np.empty(n, block.dtype)
         start, done = int(rng.integers(0, len(block))), 0
         while done < n:
             take = min(n - done, len(block))
             q[done:done + take] = twice[start:start + take]
             done += take
+        if not quant:
+            return q.reshape(rows, cols)
         return q.reshape(rows, cols), rng.uniform(4e-4, 8e-4, rows).astype(np.float32)
 
     zeros = lambda n: np.zeros(n, np.float32)  # noqa: E731
@@ -309,7 +315,7 @@ def synth_model(name: str, seed: int = 1234, nvocab: int = NVOCAB) -> dict:
                q_scale=hdim, slide=c["slide"], nvocab=nvocab, theta_l=10000.0,
                theta_g=1000000.0, eps=float(np.float32(1e-6)), sc_att=0.0, sc_log=0.0,
                qk_norm=True, mlp_pre=True, mlp_pst=True,
-               swa=[int((i + 1) % 6 != 0) for i in range(nl)], max_seq=32768)
+               swa=[int((i + 1) % 6 != 0) for i in range(nl)], max_seq=32768, quant=quant)
     layers = [{"wq": qt(q_sz, dim), "wk": qt(kv_sz, dim), "wv": qt(kv_sz, dim),
                "wo": qt(dim, q_sz), "nq": zeros(hdim), "nk": zeros(hdim),
                "w1": qt(mlp, dim), "w2": qt(mlp, dim), "w3": qt(dim, mlp),
