@@ -1992,14 +1992,17 @@ struct gemma_hip_vision {
   gemma_hip_vision_config cfg{};
   int npatch = 0, ppi = 0, ksize = 0, hdim = 0;
   bool attn_f32 = true;  // attention on the fp32 matrix cores (gemma_hip_vision_set_attention)
+  bool quant = true;     // int8 projections; false: an fp32 ('U') model
   struct Layer {
     const int8_t *w[6];  // wq wk wv wo w1 w2, device
     const float *s[6];
+    const float *wf[6];  // the same, fp32 ('U'), device
     float *bqkv, *bo, *b1, *b2, *n1, *n1b, *n2, *n2b;  // device copies
   };
   std::vector<Layer> layers;
   const int8_t *pos_q = nullptr, *proj = nullptr;
   const float *pos_s = nullptr, *proj_s = nullptr;
+  const float *pos_f = nullptr, *proj_f = nullptr;  // fp32 ('U')
   float *pe = nullptr, *pe_b = nullptr, *post_n = nullptr, *post_nb = nullptr, *norm = nullptr;
   char *mem = nullptr;  // parameters and activations
   float *img = nullptr, *patches = nullptr, *x = nullptr, *y = nullptr, *qkv = nullptr;
@@ -2016,7 +2019,10 @@ void vision_free(gemma_hip_vision *v) {
 }
 
 // forward_vision (gemma.c:4394-4725) on `st`; the image is already in v->img
+hipError_t vision_enqueue_f32(gemma_hip_vision *v, hipStream_t st);
+
 hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
+  if (!v->quant) return vision_enqueue_f32(v, st);
   const gemma_hip_vision_config &c = v->cfg;
   const int n = v->npatch, dim = c.dim, mlp = c.mlp_dim;
   hipError_t e;
@@ -2089,24 +2095,93 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
   return gemm(v->out, c.text_dim, v->proj, v->proj_s, c.img_tok, c.text_dim, dim);
 }
 
+// The fp32 ('U') tower: forward_vision's !quant branches (gemma.c:4454, 4488,
+// 4562, 4604, 4626, 4709): the fp32 position embedding in the patch GEMM's
+// epilogue, the layer norms and the pooling store fp32 rows, the projections
+// are fp32 matrix-core GEMMs (fp64 in the verification mode, as the patch
+// GEMM), the fc1 bias + GELU its own launch.
+hipError_t vision_enqueue_f32(gemma_hip_vision *v, hipStream_t st) {
+  const gemma_hip_vision_config &c = v->cfg;
+  const int n = v->npatch, dim = c.dim, mlp = c.mlp_dim;
+  const bool f64 = !v->attn_f32;
+  hipError_t e;
+  auto gemm = [&](float *dst, int dstr, const float *w, int m, int nout, const float *src,
+                  int sstr, int k) {
+    return GH_OP(kOpGemmFpx, gh::launch_gemm_f32(dst, dstr, w, k, src, sstr, m, nout, k,
+                                                 gh::F32Epilogue{}, g.info, st, f64));
+  };
+  gh::F32Epilogue pe{};
+  pe.bias = v->pe_b;
+  pe.clamp = true;
+  pe.pos_f = v->pos_f;
+  const int kdim = 3 * c.psize * c.psize;
+  if ((e = GH_OP(kOpGemmFpx, [&] {
+         const hipError_t ei = gh::launch_im2col(v->patches, v->img, c.img_px, c.psize, st);
+         if (ei != hipSuccess) return ei;
+         return gh::launch_gemm_f32(v->x, dim, v->pe, kdim, v->patches, kdim, n, dim, kdim, pe,
+                                    g.info, st, f64);
+       }())) != hipSuccess)
+    return e;
+  for (int l = 0; l < c.nl; ++l) {
+    const auto &L = v->layers[l];
+    const gh::VisLn n1{v->x, l > 0 ? v->y : nullptr, l > 0 ? v->layers[l - 1].b2 : nullptr,
+                       L.n1, L.n1b, nullptr, nullptr, v->hln, dim, c.eps};
+    if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(n1, n, st))) != hipSuccess) return e;
+    if ((e = gemm(v->qkv, 3 * dim, L.wf[0], n, dim, v->hln, dim, dim)) != hipSuccess ||
+        (e = gemm(v->qkv + dim, 3 * dim, L.wf[1], n, dim, v->hln, dim, dim)) != hipSuccess ||
+        (e = gemm(v->qkv + 2 * dim, 3 * dim, L.wf[2], n, dim, v->hln, dim, dim)) != hipSuccess)
+      return e;
+    const gh::VisAttn at{v->qkv, 3 * dim, L.bqkv, v->att, n, c.n_heads, dim,
+                         1.0f / sqrtf((float)v->hdim)};
+    if ((e = GH_OP(kOpSoftmax, gh::launch_vis_attention(at, v->hdim, v->attn_f32, st))) !=
+        hipSuccess)
+      return e;
+    if ((e = gemm(v->y, dim, L.wf[3], n, dim, v->att, dim, dim)) != hipSuccess) return e;
+    const gh::VisLn n2{v->x, v->y, L.bo, L.n2, L.n2b, nullptr, nullptr, v->hln, dim, c.eps};
+    if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(n2, n, st))) != hipSuccess) return e;
+    if ((e = gemm(v->hbuf, mlp, L.wf[4], n, mlp, v->hln, dim, dim)) != hipSuccess ||
+        (e = GH_OP(kOpGelu, gh::launch_vis_bias_gelu(v->hbuf, L.b1, n, mlp, st))) !=
+            hipSuccess ||
+        (e = gemm(v->y, dim, L.wf[5], n, dim, v->hbuf, mlp, mlp)) != hipSuccess)
+      return e;
+  }
+  const gh::VisLn pn{v->x, v->y, v->layers[c.nl - 1].b2, v->post_n, v->post_nb, nullptr,
+                     nullptr, v->hln, dim, c.eps};
+  if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(pn, n, st))) != hipSuccess) return e;
+  gh::VisPool po{v->hln, v->norm, nullptr, nullptr, dim, v->ppi, v->ksize, c.eps, v->att};
+  if ((e = GH_OP(kOpRmsnorm, gh::launch_vis_pool(po, c.img_tok, st))) != hipSuccess) return e;
+  return gemm(v->out, c.text_dim, v->proj_f, c.img_tok, c.text_dim, v->att, dim, dim);
+}
+
 #undef GH_OP
 
 }  // namespace
 
 extern "C" {
 
-gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
-                                          const gemma_hip_vision_layer *layers,
-                                          const float *pe, const float *pe_b,
-                                          const int8_t *pos_q, const float *pos_s,
-                                          const float *post_n, const float *post_nb,
-                                          const float *norm, const int8_t *proj,
-                                          const float *proj_s) {
-  if (need_init()) return nullptr;
+}  // extern "C"
+
+namespace {
+
+// One encoder layer's tensors as a create entry point passes them.
+struct VisLayerSrc {
+  const void *w[6];  // wq wk wv wo w1 w2: int8 (with s) or fp32
+  const float *s[6];
+  const float *b[6];  // bq bk bv bo b1 b2
+  const float *n[4];  // n1 n1_b n2 n2_b
+};
+
+// gemma_hip_vision_create(_f32): quant selects int8 projections, position
+// embedding and projection (with their row scales) or fp32 ones.
+gemma_hip_vision *vision_build(const char *name, const gemma_hip_vision_config *cfg,
+                               const VisLayerSrc *layers, bool quant, const float *pe,
+                               const float *pe_b, const void *pos, const float *pos_s,
+                               const float *post_n, const float *post_nb, const float *norm,
+                               const void *proj, const float *proj_s) {
   if (cfg == nullptr || layers == nullptr || pe == nullptr || pe_b == nullptr ||
-      pos_q == nullptr || pos_s == nullptr || post_n == nullptr || post_nb == nullptr ||
-      norm == nullptr || proj == nullptr || proj_s == nullptr) {
-    fail("gemma_hip_vision_create: null argument");
+      pos == nullptr || (quant && (pos_s == nullptr || proj_s == nullptr)) ||
+      post_n == nullptr || post_nb == nullptr || norm == nullptr || proj == nullptr) {
+    fail("%s: null argument", name);
     return nullptr;
   }
   const gemma_hip_vision_config c = *cfg;
@@ -2120,13 +2195,14 @@ gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
       c.mlp_dim <= 0 || c.mlp_dim % 16 != 0 || c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt ||
       c.psize <= 0 || c.img_px <= 0 || c.img_px % c.psize != 0 || c.img_tok <= 0 ||
       side * side != c.img_tok || ppi % side != 0 || c.text_dim <= 0 || c.text_dim % 16 != 0) {
-    fail("gemma_hip_vision_create: unsupported config (nl=%d heads=%d dim=%d mlp=%d img=%d "
-         "patch=%d img_tok=%d text_dim=%d)", c.nl, c.n_heads, c.dim, c.mlp_dim, c.img_px,
+    fail("%s: unsupported config (nl=%d heads=%d dim=%d mlp=%d img=%d "
+         "patch=%d img_tok=%d text_dim=%d)", name, c.nl, c.n_heads, c.dim, c.mlp_dim, c.img_px,
          c.psize, c.img_tok, c.text_dim);
     return nullptr;
   }
   gemma_hip_vision *v = new gemma_hip_vision();
   v->cfg = c;
+  v->quant = quant;
   v->hdim = hdim;
   v->ppi = ppi;
   v->npatch = ppi * ppi;
@@ -2134,45 +2210,63 @@ gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
   const size_t dim = c.dim, mlp = c.mlp_dim, n = v->npatch, kpe = 3 * (size_t)c.psize * c.psize;
   auto weight = [&](const void *host, size_t bytes, const char *what, const void **out) {
     const char *p = resolve(host, bytes);
-    if (p == nullptr) return fail("gemma_hip_vision_create: %s is not registered", what);
-    if ((uintptr_t)p % 16 != 0)
-      return fail("gemma_hip_vision_create: %s is not 16-byte aligned on the device", what);
+    if (p == nullptr) return fail("%s: %s is not registered", name, what);
+    if ((uintptr_t)p % 16 != 0) return fail("%s: %s is not 16-byte aligned on the device", name, what);
     *out = p;
     return 0;
   };
   const void *ptr = nullptr;
+  const size_t wbytes = quant ? 1 : 4;  // bytes per weight
   v->layers.resize(c.nl);
   for (int l = 0; l < c.nl; ++l) {
-    const gemma_hip_vision_layer &src = layers[l];
-    const int8_t *ws[6] = {src.wq, src.wk, src.wv, src.wo, src.w1, src.w2};
-    const float *ss[6] = {src.wq_s, src.wk_s, src.wv_s, src.wo_s, src.w1_s, src.w2_s};
+    const VisLayerSrc &src = layers[l];
     const size_t rows[6] = {dim, dim, dim, dim, mlp, dim};
     const size_t cols[6] = {dim, dim, dim, dim, dim, mlp};
     static const char *names[6] = {"wq", "wk", "wv", "wo", "w1", "w2"};
     for (int t = 0; t < 6; ++t) {
-      if (weight(ws[t], rows[t] * cols[t], names[t], &ptr)) { vision_free(v); return nullptr; }
+      if (weight(src.w[t], rows[t] * cols[t] * wbytes, names[t], &ptr)) {
+        vision_free(v);
+        return nullptr;
+      }
+      if (!quant) {
+        v->layers[l].wf[t] = (const float *)ptr;
+        continue;
+      }
       v->layers[l].w[t] = (const int8_t *)ptr;
-      if (weight(ss[t], rows[t] * 4, names[t], &ptr)) { vision_free(v); return nullptr; }
+      if (weight(src.s[t], rows[t] * 4, names[t], &ptr)) { vision_free(v); return nullptr; }
       v->layers[l].s[t] = (const float *)ptr;
     }
-    if (!src.bq || !src.bk || !src.bv || !src.bo || !src.b1 || !src.b2 || !src.n1 ||
-        !src.n1_b || !src.n2 || !src.n2_b) {
-      fail("gemma_hip_vision_create: layer %d lacks a bias or norm weight", l);
+    bool have = true;
+    for (int t = 0; t < 6; ++t) have = have && src.b[t] != nullptr;
+    for (int t = 0; t < 4; ++t) have = have && src.n[t] != nullptr;
+    if (!have) {
+      fail("%s: layer %d lacks a bias or norm weight", name, l);
       vision_free(v);
       return nullptr;
     }
   }
-  if (weight(pos_q, n * dim, "pos_emb", &ptr)) { vision_free(v); return nullptr; }
-  v->pos_q = (const int8_t *)ptr;
-  if (weight(pos_s, n * 4, "pos_emb scales", &ptr)) { vision_free(v); return nullptr; }
-  v->pos_s = (const float *)ptr;
-  if (weight(proj, (size_t)c.text_dim * dim, "proj", &ptr)) { vision_free(v); return nullptr; }
-  v->proj = (const int8_t *)ptr;
-  if (weight(proj_s, (size_t)c.text_dim * 4, "proj scales", &ptr)) {
+  if (weight(pos, n * dim * wbytes, "pos_emb", &ptr)) { vision_free(v); return nullptr; }
+  if (quant) {
+    v->pos_q = (const int8_t *)ptr;
+    if (weight(pos_s, n * 4, "pos_emb scales", &ptr)) { vision_free(v); return nullptr; }
+    v->pos_s = (const float *)ptr;
+  } else {
+    v->pos_f = (const float *)ptr;
+  }
+  if (weight(proj, (size_t)c.text_dim * dim * wbytes, "proj", &ptr)) {
     vision_free(v);
     return nullptr;
   }
-  v->proj_s = (const float *)ptr;
+  if (quant) {
+    v->proj = (const int8_t *)ptr;
+    if (weight(proj_s, (size_t)c.text_dim * 4, "proj scales", &ptr)) {
+      vision_free(v);
+      return nullptr;
+    }
+    v->proj_s = (const float *)ptr;
+  } else {
+    v->proj_f = (const float *)ptr;
+  }
   // one device allocation: copied parameters, then the activations
   Carver cv;
   const size_t per_layer = 3 * dim + dim + mlp + dim + 4 * dim;  // bqkv bo b1 b2 n1 n1b n2 n2b
@@ -2185,7 +2279,7 @@ gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
                o_a8 = cv.take(n * std::max(dim, mlp)), o_as = cv.take(n * 4);
   hipError_t e = hipMalloc((void **)&v->mem, cv.used);
   if (e != hipSuccess) {
-    hip_fail("gemma_hip_vision_create: alloc", e);
+    hip_fail(name, e);
     vision_free(v);
     return nullptr;
   }
@@ -2203,22 +2297,22 @@ gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
   v->post_nb = put(post_nb, dim);
   v->norm = put(norm, dim);
   for (int l = 0; l < c.nl; ++l) {
-    const gemma_hip_vision_layer &src = layers[l];
+    const VisLayerSrc &src = layers[l];
     auto &L = v->layers[l];
-    L.bqkv = put(src.bq, dim);
-    put(src.bk, dim);
-    put(src.bv, dim);
-    L.bo = put(src.bo, dim);
-    L.b1 = put(src.b1, mlp);
-    L.b2 = put(src.b2, dim);
-    L.n1 = put(src.n1, dim);
-    L.n1b = put(src.n1_b, dim);
-    L.n2 = put(src.n2, dim);
-    L.n2b = put(src.n2_b, dim);
+    L.bqkv = put(src.b[0], dim);
+    put(src.b[1], dim);
+    put(src.b[2], dim);
+    L.bo = put(src.b[3], dim);
+    L.b1 = put(src.b[4], mlp);
+    L.b2 = put(src.b[5], dim);
+    L.n1 = put(src.n[0], dim);
+    L.n1b = put(src.n[1], dim);
+    L.n2 = put(src.n[2], dim);
+    L.n2b = put(src.n[3], dim);
   }
   e = hipMemcpy(m + o_par, host.data(), host.size() * 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
-    hip_fail("gemma_hip_vision_create: upload", e);
+    hip_fail(name, e);
     vision_free(v);
     return nullptr;
   }
@@ -2234,6 +2328,59 @@ gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
   v->a8 = (int8_t *)(m + o_a8);
   v->as = (float *)(m + o_as);
   return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
+                                          const gemma_hip_vision_layer *layers,
+                                          const float *pe, const float *pe_b,
+                                          const int8_t *pos_q, const float *pos_s,
+                                          const float *post_n, const float *post_nb,
+                                          const float *norm, const int8_t *proj,
+                                          const float *proj_s) {
+  static const char *kName = "gemma_hip_vision_create";
+  if (need_init()) return nullptr;
+  if (cfg == nullptr || layers == nullptr || cfg->nl <= 0) {
+    fail("%s: null argument", kName);
+    return nullptr;
+  }
+  std::vector<VisLayerSrc> src(cfg->nl);
+  for (int l = 0; l < cfg->nl; ++l) {
+    const gemma_hip_vision_layer &a = layers[l];
+    src[l] = VisLayerSrc{{a.wq, a.wk, a.wv, a.wo, a.w1, a.w2},
+                         {a.wq_s, a.wk_s, a.wv_s, a.wo_s, a.w1_s, a.w2_s},
+                         {a.bq, a.bk, a.bv, a.bo, a.b1, a.b2},
+                         {a.n1, a.n1_b, a.n2, a.n2_b}};
+  }
+  return vision_build(kName, cfg, src.data(), true, pe, pe_b, pos_q, pos_s, post_n, post_nb,
+                      norm, proj, proj_s);
+}
+
+gemma_hip_vision *gemma_hip_vision_create_f32(const gemma_hip_vision_config *cfg,
+                                              const gemma_hip_vision_layer_f32 *layers,
+                                              const float *pe, const float *pe_b,
+                                              const float *pos, const float *post_n,
+                                              const float *post_nb, const float *norm,
+                                              const float *proj) {
+  static const char *kName = "gemma_hip_vision_create_f32";
+  if (need_init()) return nullptr;
+  if (cfg == nullptr || layers == nullptr || cfg->nl <= 0) {
+    fail("%s: null argument", kName);
+    return nullptr;
+  }
+  std::vector<VisLayerSrc> src(cfg->nl);
+  for (int l = 0; l < cfg->nl; ++l) {
+    const gemma_hip_vision_layer_f32 &a = layers[l];
+    src[l] = VisLayerSrc{{a.wq, a.wk, a.wv, a.wo, a.w1, a.w2},
+                         {},
+                         {a.bq, a.bk, a.bv, a.bo, a.b1, a.b2},
+                         {a.n1, a.n1_b, a.n2, a.n2_b}};
+  }
+  return vision_build(kName, cfg, src.data(), false, pe, pe_b, pos, nullptr, post_n, post_nb,
+                      norm, proj, nullptr);
 }
 
 void gemma_hip_vision_destroy(gemma_hip_vision *vis) {

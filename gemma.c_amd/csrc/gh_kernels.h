@@ -107,10 +107,12 @@ struct F32Epilogue {
   bool clamp;
   const int8_t *pos_q;
   const float *pos_s;
+  const float *pos_f;  // an fp32 position embedding [rows][dstr] ('U' files)
   __device__ __forceinline__ float finish(float y, int row, int col, int dstr) const {
     if (clamp) y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y));
-    if (pos_q != nullptr) {
-      const float pos = (float)pos_q[(size_t)row * dstr + col] * pos_s[row];
+    if (pos_q != nullptr || pos_f != nullptr) {
+      const float pos = pos_f != nullptr ? pos_f[(size_t)row * dstr + col]
+                                         : (float)pos_q[(size_t)row * dstr + col] * pos_s[row];
       y = fminf(3.40282347e38f, fmaxf(-3.40282347e38f, y + pos));
     }
     return y;
@@ -297,13 +299,15 @@ struct VisAttn {
   int n, n_heads, dim;
   float scale;
 };
-// h [ppi*ppi][dim] -> xq/xs [(ppi/ksize)^2][dim]: mean pooling, RMSNorm(w)
+// h [ppi*ppi][dim] -> xq/xs [(ppi/ksize)^2][dim]: mean pooling, RMSNorm(w);
+// when xq is null the normalized rows go to out (fp32)
 struct VisPool {
   const float *h, *w;
   int8_t *xq;
   float *xs;
   int dim, ppi, ksize;
   float eps;
+  float *out;
 };
 hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream);
 // head dim 16, 32, 64, 72 or 128
@@ -312,5 +316,8 @@ hipError_t launch_vis_attention(const VisAttn &a, int hdim, bool f32, hipStream_
 hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int mlp, int8_t *xq,
                                  float *xs, const WarmRegions &warm, hipStream_t stream);
 hipError_t launch_vis_pool(const VisPool &a, int ntok, hipStream_t stream);
+// h [n][mlp] = gelu(h + bias) in place (the fp32-weight tower, where no
+// quantize follows); mlp % 4 == 0
+hipError_t launch_vis_bias_gelu(float *h, const float *bias, int n, int mlp, hipStream_t stream);
 
 }  // namespace gh

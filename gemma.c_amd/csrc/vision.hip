@@ -555,6 +555,14 @@ __global__ __launch_bounds__(kNT) void vis_pool_kernel(VisPool a) {
       amax = fmaxf(amax, abs_daz(pv[j][e]));
     }
   }
+  if (a.xq == nullptr) {  // fp32 rows for an fp32 projection
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int c = tid + j * kNT;
+      if (c < n4) reinterpret_cast<v4f *>(a.out + (size_t)blockIdx.x * a.dim)[c] = pv[j];
+    }
+    return;
+  }
   amax = block_max<kNT>(amax, redf);
   const QuantParams qp = quant_params(amax);
   int8_t *row = a.xq + (size_t)blockIdx.x * a.dim;
@@ -567,6 +575,29 @@ __global__ __launch_bounds__(kNT) void vis_pool_kernel(VisPool a) {
                 quant_one(pv[j].z, qp.inv), quant_one(pv[j].w, qp.inv));
   }
   if (tid == 0) a.xs[blockIdx.x] = qp.scale;
+}
+
+// h = gelu(h + bias) in place, grid (ceil(mlp / 4 / kNT), rows): the fp32
+// tower's fc1 epilogue (gemma.c:4620-4622), each value as the quantizing
+// kernel computes it.
+__global__ __launch_bounds__(kNT) void vis_bias_gelu_kernel(float *h, const float *bias, int mlp) {
+  __shared__ double etab[128];
+  exp_tab_load(etab);
+  const ExpConsts ec = exp_consts();
+  const int c = blockIdx.x * kNT + threadIdx.x;
+  float *row = h + (size_t)blockIdx.y * mlp;
+  const bool ok = c < mlp / 4;
+  v4f hv = {0.f, 0.f, 0.f, 0.f}, bv = hv;
+  if (ok) {
+    hv = reinterpret_cast<const v4f *>(row)[c];
+    bv = reinterpret_cast<const v4f *>(bias)[c];
+  }
+  lds_barrier();  // the exp table
+  if (!ok) return;
+  v4f out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = (float)gelu((double)(hv[e] + bv[e]), etab, ec);
+  reinterpret_cast<v4f *>(row)[c] = out;
 }
 
 template <int C, int CMAX, class F>
@@ -636,6 +667,12 @@ hipError_t launch_vis_gelu_quant(const float *h, const float *bias, int n, int m
   if ((n4 + 255) / 256 <= kPfMaxNpt) return go(std::integral_constant<int, 256>{});
   if ((n4 + 511) / 512 <= kPfMaxNpt) return go(std::integral_constant<int, 512>{});
   return go(std::integral_constant<int, 1024>{});
+}
+
+hipError_t launch_vis_bias_gelu(float *h, const float *bias, int n, int mlp, hipStream_t stream) {
+  if (n <= 0 || mlp <= 0 || mlp % 4 != 0) return hipErrorInvalidValue;
+  vis_bias_gelu_kernel<<<dim3((mlp / 4 + kNT - 1) / kNT, n), kNT, 0, stream>>>(h, bias, mlp);
+  return hipGetLastError();
 }
 
 hipError_t launch_vis_pool(const VisPool &a, int ntok, hipStream_t stream) {

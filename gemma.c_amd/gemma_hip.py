@@ -116,6 +116,14 @@ class VisionLayer(ctypes.Structure):
         "bq", "bk", "bv", "bo", "b1", "b2", "n1", "n1_b", "n2", "n2_b")]
 
 
+class VisionLayerF32(ctypes.Structure):
+    """gemma_hip_vision_layer_f32: one VisionEncoderLayer of an fp32 ('U') file."""
+
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "wq", "wk", "wv", "wo", "w1", "w2",
+        "bq", "bk", "bv", "bo", "b1", "b2", "n1", "n1_b", "n2", "n2_b")]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 
@@ -167,6 +175,7 @@ _SIGS = {
     "gemma_hip_decoder_logits": (_P, [_P]),
     "gemma_hip_decoder_set_attention": (_I, [_P, _I]),
     "gemma_hip_vision_create": (_P, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "gemma_hip_vision_create_f32": (_P, [_P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "gemma_hip_vision_destroy": (None, [_P]),
     "gemma_hip_vision_forward": (_I, [_P, _P, _P]),
     "gemma_hip_vision_set_attention": (_I, [_P, _I]),
@@ -503,21 +512,32 @@ class Vision:
 
         cfg = VisionConfig(c["nl"], c["n_heads"], c["img_px"], c["psize"], c["dim"],
                            c["mlp_dim"], c["eps"], c["img_tok"], c["text_dim"])
-        layers = (VisionLayer * c["nl"])()
+        quant = c.get("quant", True)
+        kind = VisionLayer if quant else VisionLayerF32
+        layers = (kind * c["nl"])()
         try:
             for i, ly in enumerate(vis["layers"]):
                 f = {}
                 for w in ("wq", "wk", "wv", "wo", "w1", "w2"):
-                    f[w] = reg(ly[w][0])
-                    f[w + "_s"] = reg(ly[w][1])
+                    if quant:
+                        f[w] = reg(ly[w][0])
+                        f[w + "_s"] = reg(ly[w][1])
+                    else:  # 'U': one fp32 [out][in] array
+                        f[w] = reg(ly[w])
                 for b in ("bq", "bk", "bv", "bo", "b1", "b2", "n1", "n1_b", "n2", "n2_b"):
                     f[b] = host(ly[b])
-                layers[i] = VisionLayer(**f)
-            self.handle = self.lib.gemma_hip_vision_create(
-                ctypes.byref(cfg), layers, host(vis["pe"]), host(vis["pe_b"]),
-                reg(vis["pos"][0]), reg(vis["pos"][1]), host(vis["post_n"]),
-                host(vis["post_nb"]), host(vis["norm"]), reg(vis["proj"][0]),
-                reg(vis["proj"][1]))
+                layers[i] = kind(**f)
+            if quant:
+                self.handle = self.lib.gemma_hip_vision_create(
+                    ctypes.byref(cfg), layers, host(vis["pe"]), host(vis["pe_b"]),
+                    reg(vis["pos"][0]), reg(vis["pos"][1]), host(vis["post_n"]),
+                    host(vis["post_nb"]), host(vis["norm"]), reg(vis["proj"][0]),
+                    reg(vis["proj"][1]))
+            else:
+                self.handle = self.lib.gemma_hip_vision_create_f32(
+                    ctypes.byref(cfg), layers, host(vis["pe"]), host(vis["pe_b"]),
+                    reg(vis["pos"]), host(vis["post_n"]), host(vis["post_nb"]),
+                    host(vis["norm"]), reg(vis["proj"]))
             if not self.handle:
                 raise GemmaHipError(self.lib.gemma_hip_last_error().decode())
         except Exception:

@@ -104,8 +104,8 @@ def write_bin(path: str, name: str, seed: int = 1234, nvocab: int = NVOCAB,
         c["slide"] = slide
     q_sz, kv_sz = c["n_heads"] * hdim, c["nkv"] * hdim
     rng = np.random.default_rng(seed)
-    if not quant and vision is not None:
-        raise ValueError("the writer's vision tower is W8A8 only")
+    if vision is not None and vision["config"].get("quant", True) != quant:
+        raise ValueError("the vision tower and the decoder must both be W8A8 or both fp32")
     linear = _write_qtensor if quant else _write_ftensor
     tmp = path + ".tmp"
     with open(tmp, "wb") as f:
@@ -168,6 +168,9 @@ def _write_vision(f, v: dict) -> None:
         f.write(np.ascontiguousarray(a, np.float32).tobytes())
 
     def q(w):
+        if isinstance(w, np.ndarray):  # 'U': fp32 [rows][cols]
+            t(w)
+            return
         f.write(np.ascontiguousarray(w[0], np.int8).tobytes())
         t(w[1])
 
@@ -259,7 +262,7 @@ def read_bin(path: str) -> dict:
     if vcfg is not None:
         vd, vm, p = vcfg["dim"], vcfg["mlp_dim"], vcfg["psize"]
         npatch = (vcfg["img_px"] // p) ** 2
-        vis = {"config": dict(vcfg, text_dim=dim)}
+        vis = {"config": dict(vcfg, text_dim=dim, quant=quant)}
         vis["pe"] = f32(vd * 3 * p * p).reshape(vd, 3 * p * p)
         vis["pe_b"] = f32(vd)
         vis["pos"] = qt(npatch, vd)
@@ -331,18 +334,23 @@ VISION_CONFIGS = {
 }
 
 
-def synth_vision(seed: int = 1234, text_dim: int = 2560, eps: float = 1e-6, **shape) -> dict:
+def synth_vision(seed: int = 1234, text_dim: int = 2560, eps: float = 1e-6, quant: bool = True,
+                 **shape) -> dict:
     """Random W8A8 VisionEncoder weights (gemma.c:1565-1585) in memory: int8
     tensors uniform in [-127, 127] with row scales U(4e-4, 8e-4), the fp32
     patch embedding and biases N(0, 0.02), layer-norm weights N(1, 0.05) and
     biases N(0, 0.05), the soft-embedding RMSNorm weight N(0, 0.1) (applied as
-    w + 1).  `shape` overrides VISION_CONFIGS["siglip"]'s fields."""
+    w + 1).  quant=False: an fp32 ('U') tower, the projections, position
+    embedding and output projection N(0, 0.02) fp32.  `shape` overrides
+    VISION_CONFIGS["siglip"]'s fields."""
     c = dict(VISION_CONFIGS["siglip"], **shape)
     rng = np.random.default_rng(seed)
     dim, mlp, p = c["dim"], c["mlp_dim"], c["psize"]
     npatch = (c["img_px"] // p) ** 2
 
     def qt(rows, cols):
+        if not quant:
+            return (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(0.02))
         q = rng.integers(-127, 128, (rows, cols), dtype=np.int8)
         return q, rng.uniform(4e-4, 8e-4, rows).astype(np.float32)
 
@@ -356,7 +364,7 @@ def synth_vision(seed: int = 1234, text_dim: int = 2560, eps: float = 1e-6, **sh
                "n1": nrm(dim, 1, 0.05), "n1_b": nrm(dim, 0, 0.05),
                "n2": nrm(dim, 1, 0.05), "n2_b": nrm(dim, 0, 0.05)}
               for _ in range(c["nl"])]
-    cfg = dict(c, eps=float(np.float32(eps)), text_dim=text_dim)
+    cfg = dict(c, eps=float(np.float32(eps)), text_dim=text_dim, quant=quant)
     return {"config": cfg, "pe": nrm(dim * 3 * p * p, 0, 0.02).reshape(dim, 3 * p * p),
             "pe_b": nrm(dim, 0, 0.02), "pos": qt(npatch, dim), "layers": layers,
             "post_n": nrm(dim, 1, 0.05), "post_nb": nrm(dim, 0, 0.05), "norm": nrm(dim, 0, 0.1),

@@ -432,6 +432,27 @@ gemma_hip_vision *gemma_hip_vision_create(const gemma_hip_vision_config *cfg,
                                           const float *proj_s);
 void gemma_hip_vision_destroy(gemma_hip_vision *vis);
 
+/* One VisionEncoderLayer of an unquantized ('U') file: fp32 projections
+ * [out][in] (registered), biases and norms as for gemma_hip_vision_layer. */
+typedef struct {
+  const float *wq, *wk, *wv, *wo, *w1, *w2;
+  const float *bq, *bk, *bv, *bo, *b1, *b2;
+  const float *n1, *n1_b, *n2, *n2_b;
+} gemma_hip_vision_layer_f32;
+
+/* gemma_hip_vision_create for a 'U' file: forward_vision's !quant branches
+ * (gemma.c:4454, 4488, 4562, 4604, 4626, 4709) on the device: pos
+ * [npatch][dim] and proj [text_dim][dim] fp32 (registered), every
+ * projection an fp32 matrix-core GEMM (gemm_fpx; fp64 in the verification
+ * mode of gemma_hip_vision_set_attention), no activation quantize.  Every
+ * other vision entry point takes the result as it takes a W8A8 tower. */
+gemma_hip_vision *gemma_hip_vision_create_f32(const gemma_hip_vision_config *cfg,
+                                              const gemma_hip_vision_layer_f32 *layers,
+                                              const float *pe, const float *pe_b,
+                                              const float *pos, const float *post_n,
+                                              const float *post_nb, const float *norm,
+                                              const float *proj);
+
 /* One image: img (host, [img_px][img_px][3] fp32, normalized as gemma.c:
  * 4271-4273 leaves it) in, out (host, [img_tok][text_dim] fp32: the image's
  * soft tokens, what forward_vision leaves in tb->x) out. */

@@ -62,7 +62,11 @@ class VisionOracle:
         self.o = oracle
 
     def gemm(self, w, x_f32):
-        """quantize_acts + gemm_int8 (gemma.c:2652-2674, 3937-4054): exact."""
+        """quantize_acts + gemm_int8 (gemma.c:2652-2674, 3937-4054): exact.
+        For an fp32 ('U') tower, gemm_fpx (3308): the float64 product rounded
+        once."""
+        if not self.c.get("quant", True):
+            return (np.asarray(x_f32, F64) @ np.asarray(w, F64).T).astype(F32)
         q, xs = self.o.quantize_acts(np.ascontiguousarray(x_f32, F32))
         acc = int_dot(q, w[0])
         return acc.astype(F32) * (xs[:, None] * np.asarray(w[1], F32)[None, :])
@@ -76,7 +80,10 @@ class VisionOracle:
         eps = c["eps"]
         emb, _ = self.o.patch_embed_f64(img, v["pe"], v["pe_b"], c["psize"])
         x = clamp_f32(emb)
-        pos = v["pos"][0].astype(F32) * v["pos"][1][:, None].astype(F32)
+        if c.get("quant", True):
+            pos = v["pos"][0].astype(F32) * v["pos"][1][:, None].astype(F32)
+        else:  # the fp32 table (gemma.c:4453-4456)
+            pos = np.asarray(v["pos"], F32)
         x = clamp_f32(x + pos)
         scale = F32(1.0) / F32(np.sqrt(F32(hd)))
         for ly in v["layers"]:

@@ -364,3 +364,92 @@ def test_device_vision_follows_reference_program(gh, oracle, tmp_path, case, mod
     print(f"device vision ({mode}) vs reference ({case}, {'flip-free' if free else 'may flip'}): "
           f"{rel:.3g}", flush=True)
     assert rel <= (REL_PRE_FLIP if free else REL_FLIP_LEVEL)
+
+
+# ------------------------------------------------- unquantized ('U') towers
+# forward_vision's !quant branches (gemma.c:4454, 4488, 4562, 4604, 4626,
+# 4709): fp32 projections, position embedding and output projection, no
+# activation quantize.  With no int8 requantization to amplify a rounding
+# difference, the oracle (float64 products rounded once) agrees with the
+# reference program to fp32 rounding, and the device (fp32 matrix-core GEMMs
+# and attention by default) with the oracle to U_TOL of the largest output;
+# in the verification mode (fp64 GEMMs and attention, every output rounded
+# once) to the W8A8 tower's TOL.
+U_TOL = 1e-4
+U_CASES = {"tiny": ("tiny", 2, 102), "hd72": ("hd72", 1, 101), "hd16": ("hd16", 3, 8),
+           "siglip": ("siglip", 4, 7)}
+
+
+def u_tower(case, text_dim=640):
+    shape, seed, img_seed = U_CASES[case]
+    vis = model_bin.synth_vision(seed=seed, text_dim=text_dim, quant=False, **SHAPES[shape])
+    return vis, model_bin.synth_image(SHAPES[shape]["img_px"], seed=img_seed)
+
+
+def test_u_multimodal_bin_round_trip(tmp_path):
+    vis, _ = u_tower("hd16")
+    path = model_bin.write_bin(str(tmp_path / "mmu.bin"), "gemma-3-270m", seed=5, nvocab=512,
+                               layers=2, vision=vis, quant=False)
+    back = model_bin.read_bin(path)
+    assert back["end"] == os.path.getsize(path)
+    v = back["vision"]
+    assert v["config"] == dict(vis["config"]) and v["config"]["quant"] is False
+    assert np.array_equal(v["pos"], vis["pos"]) and np.array_equal(v["proj"], vis["proj"])
+    for a, b in zip(v["layers"], vis["layers"]):
+        for key in ("wq", "wo", "w1", "w2", "b1", "n2_b"):
+            assert np.array_equal(a[key], b[key])
+    with pytest.raises(ValueError):
+        model_bin.write_bin(str(tmp_path / "mix.bin"), "gemma-3-270m", seed=5, nvocab=512,
+                            layers=2, vision=vis, quant=True)
+
+
+@needs_e2e
+@pytest.mark.parametrize("case", ["tiny", "hd72", "hd16"])
+def test_u_vision_oracle_follows_reference_program(tmp_path, oracle, case):
+    vis, img = u_tower(case)
+    path = model_bin.write_bin(str(tmp_path / f"mmu_{case}.bin"), "gemma-3-270m", seed=5,
+                               nvocab=512, layers=2, vision=vis, quant=False)
+    img_path, out_path = str(tmp_path / "img.f32"), str(tmp_path / "soft.f32")
+    img.tofile(img_path)
+    env = dict(os.environ, GEMMA_E2E_VISION_IMAGE=img_path, GEMMA_E2E_VISION_OUT=out_path)
+    out = subprocess.run([E2E_CPU, path, "1", "0", "1", "4"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    ref = np.fromfile(out_path, np.float32).reshape(vis["config"]["img_tok"], 640)
+    want = vorc.VisionOracle(model_bin.read_bin(path)["vision"], oracle).forward(img)
+    rel = rel_to(ref, want)
+    print(f"U vision oracle vs reference ({case}): {rel:.3g}", flush=True)
+    assert rel <= REL_PRE_FLIP  # no requantization: fp32 rounding throughout
+    # sharp: the fp32 position embedding left out moves the output far past it
+    bad = copy.deepcopy(model_bin.read_bin(path)["vision"])
+    bad["pos"] = np.zeros_like(bad["pos"])
+    assert rel_to(ref, vorc.VisionOracle(bad, oracle).forward(img)) > 100 * REL_PRE_FLIP
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", sorted(U_CASES))
+@pytest.mark.parametrize("mode", ["f32", "f64"])
+def test_u_vision_matches_oracle(gh, oracle, case, mode):
+    vis, img = u_tower(case)
+    want = vorc.VisionOracle(vis, oracle).forward(img)
+    tower = gh.vision(vis, attention=ATTN_F32 if mode == "f32" else ATTN_F64)
+    try:
+        got = tower.forward(img)
+        again = tower.forward(img)
+        if case == "tiny" and mode == "f32":
+            gh.perf_enable(True)
+            try:
+                tower.forward(img)
+                perf = gh.perf_read()
+            finally:
+                gh.perf_enable(False)
+            nl = vis["config"]["nl"]
+            calls = {op: c for op, (s, c) in perf["vision"].items()}
+            assert calls == {"gemm_fpx": 1 + 6 * nl + 1, "layernorm": 2 * nl + 1,
+                             "softmax": nl, "gelu": nl, "rmsnorm": 1}
+    finally:
+        tower.close()
+    rel = rel_to(want, got)
+    print(f"U vision {case} ({mode}): |d|/max|out| = {rel:.3g}", flush=True)
+    assert rel <= (U_TOL if mode == "f32" else TOL)
+    assert np.array_equal(got, again)
