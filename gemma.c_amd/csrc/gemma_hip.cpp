@@ -843,6 +843,7 @@ int gemma_hip_prefill_attention(float *out, const float *q, int q_stride, const 
   const int hn = nkv > 0 && n_heads % nkv == 0 ? n_heads / nkv : 0;
   if (n < 1 || pos0 < 0 || hn < 1 || 32 % hn != 0 || (hdim != 128 && hdim != 256) ||
       n_heads > gh::kPfMaxMergeHeads || (long)n_heads * hdim > q_stride ||
+      n_heads * hdim > 4 * 256 * gh::kPfMaxNpt ||
       (long)pos0 + n > clen || slide < 0 || (long)n * q_stride > (1l << 30) ||
       (long)nkv * clen * hdim > (1l << 30))
     return fail("%s: unsupported shape n=%d pos0=%d heads=%d/%d hdim=%d clen=%d stride=%d",
@@ -1261,19 +1262,16 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
                         c.qk_norm ? L.nk : nullptr, sliding ? d->rope_l : d->rope_g, kc,
                         kc + cache, d->clen, pos, c.n_heads, c.nkv, c.eps};
     if ((e = GH_OP(kOpRope, gh::launch_pf_qk_rope(rp, n, c.hdim, st))) != hipSuccess) return e;
+    // the attention's merge pass also quantizes its rows for the o projection
     const gh::PfAttn at{d->pf_qkv, stride, kc, kc + cache, d->pf_xo, q_sz, n, pos, c.n_heads,
                         c.nkv, d->clen, sliding ? c.slide : 0,
                         (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
-                        0, dense ? 1 : 0};
+                        0, dense ? 1 : 0, d->pf_a8, d->pf_as};
     if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, st))) !=
         hipSuccess)
       return e;
     // o projection
-    if ((e = GH_OP(kOpQuantizeAct,
-                   gh::launch_quantize(d->pf_a8, d->pf_as, d->pf_xo, q_sz, n, q_sz, st))) !=
-            hipSuccess ||
-        (e = gemm(d->pf_y, dim, L.w[3], L.s[3], dim, q_sz)) != hipSuccess)
-      return e;
+    if ((e = gemm(d->pf_y, dim, L.w[3], L.s[3], dim, q_sz)) != hipSuccess) return e;
     // residual of the attention (post-attention norm), pre-FFN norm, quantize
     const gh::PfNorm n3{d->pf_x, d->pf_y, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
                         d->pf_a8, d->pf_as, dim, c.eps};
@@ -1327,10 +1325,12 @@ int prefill_check(const gemma_hip_decoder *dec, const char *name, int n, int pos
   if (n < 1 || pos < 0 || pos > dec->clen - n)
     return fail("%s: %d rows at pos %d out of range (clen %d)", name, n, pos, dec->clen);
   const int hn = c.n_heads / c.nkv;
-  if ((c.hdim != 128 && c.hdim != 256) || 32 % hn != 0 || c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt)
+  if ((c.hdim != 128 && c.hdim != 256) || 32 % hn != 0 || c.mlp_dim > 4 * 1024 * gh::kPfMaxNpt ||
+      c.n_heads * c.hdim > 4 * 256 * gh::kPfMaxNpt)
     return fail("%s: unsupported shape (head dim %d must be 128 or 256, "
-                "%d q heads per kv head must divide 32, mlp %d at most %d)",
-                name, c.hdim, hn, c.mlp_dim, 4 * 1024 * gh::kPfMaxNpt);
+                "%d q heads per kv head must divide 32, mlp %d at most %d, q width %d at "
+                "most %d)", name, c.hdim, hn, c.mlp_dim, 4 * 1024 * gh::kPfMaxNpt,
+                c.n_heads * c.hdim, 4 * 256 * gh::kPfMaxNpt);
   return 0;
 }
 

@@ -173,6 +173,16 @@ inline size_t dec_attn_lds(int hn, int hdim) {
          ((size_t)hn * hdim + 2 * (size_t)hdim + (size_t)kDecAttnBlock * (2 * hdim + 16)) * 4;
 }
 
+// Byte regions (16-byte aligned) that a kernel reads and discards after its
+// own work, so that a later kernel finds them in the memory-side cache
+// (the Infinity Cache) rather than in HBM.
+constexpr int kMaxWarm = 4;
+struct WarmRegions {
+  const void *p[kMaxWarm];
+  size_t bytes[kMaxWarm];
+  int n;
+};
+
 // One layer's attention: q/k/v rows in, xo out; kc/vc are the layer's cache
 // [nkv][clen][hdim]; rope the table [clen][hdim] (cos, sin interleaved) of
 // the layer's base; part holds [n_heads][max_blocks][hdim + 2] fp64 partials.
@@ -200,15 +210,6 @@ hipError_t launch_dec_argmax(const float *logits, int n, float *pval, int *pidx,
                              int *step, int *tokens, int max_tokens, hipStream_t stream);
 
 // prefill.hip: the batched prompt pass (forward_text_chunk).
-// Byte regions (16-byte aligned) that a kernel reads and discards after its
-// own work, so that a later kernel finds them in the memory-side cache
-// (the Infinity Cache) rather than in HBM.
-constexpr int kMaxWarm = 4;
-struct WarmRegions {
-  const void *p[kMaxWarm];
-  size_t bytes[kMaxWarm];
-  int n;
-};
 // Rows of x [n][dim] (in place), y [n][dim] nullable: the per-row form of
 // DecNorm; h of every row is quantized into xq [n][dim] + xs [n].
 // per row: x = clamp(x + post(y)), h = rmsnorm(x; w_pre) quantized into
@@ -252,6 +253,11 @@ struct PfAttn {
   // 1: every row sees keys 0 .. pos0+n-1, no window (mask=false, the image
   // tokens' bidirectional attention, gemma.c:5258-5290)
   int dense;
+  // non-null: every output row is quantized into xq [n][q_sz] / xs [n] as
+  // quantize_acts does (the o projection's input), in the merge pass, and
+  // xo then holds only the rows the attention kernel wrote whole
+  int8_t *xq;
+  float *xs;
 };
 constexpr int kPfMaxSplit = 8;
 constexpr int kPfMaxMergeHeads = 64;  // q heads the key-split merge handles

@@ -29,6 +29,7 @@
 // attention in fp32 with a different order (blockwise gemm_fpx, softmax,
 // gemm_fpx_nn), which no fp32 bit pattern here could follow anyway.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "dec_common.h"
@@ -730,38 +731,102 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void pf_attn_pair_kernel(PfAttn a)
 // and m = kPaFloor (kPaFloorF), so it adds nothing.  Rows whose row block
 // took a single chunk were written by the attention kernel.  P: the
 // partials' type (double from the fp64 kernels, float from the fp32 one).
-template <class P>
+// With a.xq the row (merged, or as the attention kernel wrote it) is
+// quantized as quantize_acts does (gemma.c:2652-2674) instead of stored:
+// the o projection's quantize, fused.  NPT float4 of the row per thread.
+template <class P, int NPT>
 __global__ __launch_bounds__(kNT) void pf_attn_merge_kernel(PfAttn a, int hdim) {
-  __shared__ double wt[kPfMaxMergeHeads][kPfMaxSplit + 1];  // weights, then 1 / denominator
-  const int row = blockIdx.x;
+  __shared__ double wt[kPfMaxMergeHeads][kPfMaxSplit + 1];  // weights, then the denominator
+  __shared__ float redf[kWaves];
+  const int row = blockIdx.x, tid = threadIdx.x;
   const int hn = a.n_heads / a.nkv, qb = a.qpb / hn;
   const int r0 = row / qb * qb;
   const auto [k_base, p_last] = pa_range(a, r0, min(qb, a.n - r0));
-  const int nchunks = (p_last - k_base + a.chunk) / a.chunk;
-  if (nchunks == 1) return;
-  const P *part = reinterpret_cast<const P *>(a.part);
-  const P *ml = part + (size_t)kPfMaxSplit * a.n * a.q_sz;
-  for (int h = threadIdx.x; h < a.n_heads; h += kNT) {
-    double m = -DBL_MAX;
-    for (int c = 0; c < nchunks; ++c)
-      m = fmax(m, (double)ml[(((size_t)c * a.n + row) * a.n_heads + h) * 2]);
-    double den = 0.0;
-    for (int c = 0; c < nchunks; ++c) {
-      const size_t at = ((size_t)c * a.n + row) * a.n_heads + h;
-      const double w = exp((double)ml[at * 2] - m);
-      wt[h][c] = w;
-      den += w * (double)ml[at * 2 + 1];
+  const int nchunks = a.nsplit > 1 ? (p_last - k_base + a.chunk) / a.chunk : 1;
+  if (nchunks == 1 && a.xq == nullptr) return;
+  const int n4 = a.q_sz >> 2;
+  v4f out[NPT];
+  if (nchunks == 1) {
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int c = tid + j * kNT;
+      out[j] = c < n4 ? reinterpret_cast<const v4f *>(a.xo + (size_t)row * a.q_sz)[c]
+                      : v4f{0.f, 0.f, 0.f, 0.f};
     }
-    wt[h][kPfMaxSplit] = den;
+  } else {
+    const P *part = reinterpret_cast<const P *>(a.part);
+    const P *ml = part + (size_t)kPfMaxSplit * a.n * a.q_sz;
+    for (int h = tid; h < a.n_heads; h += kNT) {
+      double m = -DBL_MAX;
+      for (int c = 0; c < nchunks; ++c)
+        m = fmax(m, (double)ml[(((size_t)c * a.n + row) * a.n_heads + h) * 2]);
+      double den = 0.0;
+      for (int c = 0; c < nchunks; ++c) {
+        const size_t at = ((size_t)c * a.n + row) * a.n_heads + h;
+        const double w = exp((double)ml[at * 2] - m);
+        wt[h][c] = w;
+        den += w * (double)ml[at * 2 + 1];
+      }
+      wt[h][kPfMaxSplit] = den;
+    }
+    __syncthreads();
+    // every chunk's 4 values of a float4 are loaded before any is summed (the
+    // loads of a row are all in flight at once), then summed in chunk order
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int c4 = tid + j * kNT;
+      out[j] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (c4 >= n4) continue;
+      const int h = 4 * c4 / hdim;
+      double v[kPfMaxSplit][4];
+#pragma unroll
+      for (int c = 0; c < kPfMaxSplit; ++c) {
+        const P *src = part + ((size_t)min(c, nchunks - 1) * a.n + row) * a.q_sz + 4 * c4;
+        if constexpr (sizeof(P) == 4) {
+          const v4f x = *reinterpret_cast<const v4f *>(src);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[c][e] = (double)x[e];
+        } else {
+          const double2 x0 = reinterpret_cast<const double2 *>(src)[0];
+          const double2 x1 = reinterpret_cast<const double2 *>(src)[1];
+          v[c][0] = x0.x; v[c][1] = x0.y; v[c][2] = x1.x; v[c][3] = x1.y;
+        }
+      }
+      double num[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+      for (int c = 0; c < kPfMaxSplit; ++c)
+        if (c < nchunks)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) num[e] += wt[h][c] * v[c][e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[j][e] = (float)(num[e] / wt[h][kPfMaxSplit]);
+    }
   }
-  __syncthreads();
-  for (int i = threadIdx.x; i < a.q_sz; i += kNT) {
-    const int h = i / hdim;
-    double num = 0.0;
-    for (int c = 0; c < nchunks; ++c)
-      num += wt[h][c] * (double)part[((size_t)c * a.n + row) * a.q_sz + i];
-    a.xo[(size_t)row * a.q_sz + i] = (float)(num / wt[h][kPfMaxSplit]);
+  if (a.xq == nullptr) {
+#pragma unroll
+    for (int j = 0; j < NPT; ++j) {
+      const int c = tid + j * kNT;
+      if (c < n4) reinterpret_cast<v4f *>(a.xo + (size_t)row * a.q_sz)[c] = out[j];
+    }
+    return;
   }
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) amax = fmaxf(amax, abs_daz(out[j][e]));
+  amax = block_max<kNT>(amax, redf);
+  const QuantParams qp = quant_params(amax);
+  int8_t *dst = a.xq + (size_t)row * a.q_sz;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int c = tid + j * kNT;
+    if (c < n4)
+      reinterpret_cast<uint32_t *>(dst)[c] =
+          pack4(quant_one(out[j].x, qp.inv), quant_one(out[j].y, qp.inv),
+                quant_one(out[j].z, qp.inv), quant_one(out[j].w, qp.inv));
+  }
+  if (tid == 0) a.xs[row] = qp.scale;
 }
 
 // gate = gelu(gate) * up in place over rows [gate (mlp) | up (mlp)], grid
@@ -889,8 +954,14 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
     kmax = std::max(kmax, r.p_last - r.k_base + 1);
   }
   // split the key ranges until there are about 2048 blocks (half of them
-  // empty for causal rows), in chunks of at least one tile
-  const int want = (2048 + nrb * a.nkv - 1) / (nrb * a.nkv);
+  // empty for causal rows), in chunks of at least one tile;
+  // GEMMA_HIP_PF_BLOCKS overrides the target (a tuning knob, read once)
+  static const int target = [] {
+    const char *e = getenv("GEMMA_HIP_PF_BLOCKS");
+    const int v = e != nullptr ? atoi(e) : 0;
+    return v >= 64 && v <= (1 << 16) ? v : 2048;
+  }();
+  const int want = (target + nrb * a.nkv - 1) / (nrb * a.nkv);
   const int split = std::max(1, std::min({kPfMaxSplit, want, (kmax + kPaKeys - 1) / kPaKeys}));
   PfAttn b = a;
   b.qpb = qpb;
@@ -911,13 +982,17 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
       default: return hipErrorInvalidValue;
     }
   }
-  if (b.nsplit > 1) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || (b.nsplit == 1 && b.xq == nullptr)) return e;
+  if (a.q_sz % 4 != 0) return hipErrorInvalidValue;
+  return by_npt<1, kPfMaxNpt>((a.q_sz / 4 + kNT - 1) / kNT, [&](auto c) {
+    constexpr int NPT = decltype(c)::value;
     if (f32)
-      pf_attn_merge_kernel<float><<<a.n, kNT, 0, stream>>>(b, hdim);
+      pf_attn_merge_kernel<float, NPT><<<a.n, kNT, 0, stream>>>(b, hdim);
     else
-      pf_attn_merge_kernel<double><<<a.n, kNT, 0, stream>>>(b, hdim);
-  }
-  return hipGetLastError();
+      pf_attn_merge_kernel<double, NPT><<<a.n, kNT, 0, stream>>>(b, hdim);
+    return hipGetLastError();
+  });
 }
 
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,

@@ -493,7 +493,8 @@ int gemma_hip_vision_attention(float *out, const float *qkv, const float *bias, 
  * (slide 0: no window), dense == 1 to every key 0 .. pos0+n-1.  Scores are
  * q.k * asc, capped as tanh(s / sc_att) * sc_att when sc_att != 0; mode is
  * GEMMA_HIP_ATTN_F32 or GEMMA_HIP_ATTN_F64 as for the decoder.  hdim 128 or
- * 256; n_heads / nkv must divide 32.  Allocates its key-split workspace. */
+ * 256; n_heads / nkv must divide 32; n_heads * hdim <= 6144.  Allocates its
+ * key-split workspace. */
 int gemma_hip_prefill_attention(float *out, const float *q, int q_stride, const float *kc,
                                 const float *vc, int n, int pos0, int n_heads, int nkv,
                                 int hdim, int clen, int slide, float asc, float sc_att,
