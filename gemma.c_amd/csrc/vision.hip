@@ -12,6 +12,9 @@
 // are.
 #include <type_traits>
 
+#include <cstdlib>
+#include <cstring>
+
 #include "dec_common.h"
 
 namespace gh {
@@ -625,9 +628,293 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
   return go(std::integral_constant<int, 256>{});
 }
 
+// The fp32 mode's attention on the bf16 matrix cores: every fp32 operand x
+// of the two products (q, k, the probabilities p and v) is split into three
+// bf16 pieces x = x0 + x1 + x2 (each rounded to nearest from the remainder,
+// so together they hold x's 24 significant bits), and each product a.b is
+// summed from the six piece products whose orders add up to at most 2
+// (a0 b0, a0 b1, a1 b0, a0 b2, a1 b1, a2 b0): the dropped ones are below
+// 3 * 2^-24 |a b|, fp32 rounding.  bf16 x bf16 products are exact in the
+// fp32 accumulators.  v_mfma_f32_16x16x32_bf16 (lane l: A[l%16][8(l/16) ..
+// +7], B[8(l/16) .. +7][l%16], D[4(l/16) + r][l%16], checked on the GPU)
+// runs 14x the fp32 MFMA's rate here, so the six cost ~0.4 of one fp32 MFMA
+// step.  Geometry as vis_attn_f32_kernel: NW waves x 16 queries of one head,
+// 32-key tiles.  The next tile's fp32 K and V rows go by LDS DMA into a
+// staging buffer while the current tile's planes are in use; at a tile's
+// start the staged rows get their bias and are split into the planes (once
+// per workgroup, not per wave; with no prefetch registers the kernel fits
+// two workgroups per CU at head dim 72).  Scores per 16-key
+// block b: S[key 16b + 4g + r][query col] over 32-dim chunks of the head dim
+// (padded with zeros to CH * 32); K in LDS as three bf16 planes [key][dim].
+// Values: the PV product's k index is 8g + 4b + r, the key 16b + 4g + r,
+// so a lane's own eight probabilities are its B operand as they stand; V^T
+// is staged in LDS as three bf16 planes [dim][k] in that key order.
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+struct Bf3 {
+  __bf16 p0, p1, p2;
+};
+__device__ __forceinline__ Bf3 split3(float x) {
+  Bf3 r;
+  r.p0 = (__bf16)x;
+  const float r1 = x - (float)r.p0;  // exact: x and p0 agree in their leading bits
+  r.p1 = (__bf16)r1;
+  r.p2 = (__bf16)(r1 - (float)r.p1);
+  return r;
+}
+
+// One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
+// wave-uniform); from inline asm so that the compiler does not wait for the
+// pending load before later LDS reads (the kernel waits itself).  m0 has no
+// other user in the kernel that calls this.
+__device__ __forceinline__ void vis_dma16(const float *g, void *lds) {
+  const uint32_t m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(g)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+template <int HD, int NW>
+__global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn a) {
+  constexpr int TK = 32;              // keys per tile
+  constexpr int CH = (HD + 31) / 32;  // 32-dim chunks of the score product
+  constexpr int DP = CH * 32;         // padded head dim of the K planes
+  constexpr int NB = (HD + 15) / 16;  // 16-dim output blocks
+  constexpr int RK = DP + 8;          // K plane row (bf16): 16 rows in distinct banks
+  constexpr int RV = TK + 8;          // V^T plane row (bf16)
+  constexpr int NT = NW * 64, QB = NW * 16;
+  constexpr int C4 = HD / 4;
+  constexpr int PF = (TK * C4 + NT - 1) / NT;  // K float4 per thread
+  static_assert(HD % 8 == 0 && HD <= 128, "head dim");
+  __shared__ __attribute__((aligned(16))) __bf16 kt[3][TK * RK];
+  __shared__ __attribute__((aligned(16))) __bf16 vt[3][NB * 16 * RV];
+  __shared__ v4f kvb[2][C4];
+  // the next tile's fp32 K and V rows land here by LDS DMA, key-major [key][C4]
+  constexpr int SG = TK * C4;
+  __shared__ v4f stg[2][SG];
+  static_assert(SG % 64 == 0, "whole DMA instructions per tile");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nqb = (a.n + QB - 1) / QB, nblk = nqb * a.n_heads;
+  int blk = blockIdx.x;
+  if (nblk % 8 == 0) blk = (blk % 8) * (nblk / 8) + blk / 8;
+  const int h = blk / nqb;
+  const int q0 = (blk - h * nqb) * QB + wave * 16;
+  const int col = lane & 15, grp = lane >> 4;
+
+  // the query's pieces: lane (col, g) holds dims 32 c + 8 g .. + 7
+  bf8 qa[3][CH];
+  {
+    const int qr = min(q0 + col, a.n - 1);
+    const float *qrow = a.qkv + (size_t)qr * a.stride + h * HD;
+    const float *bq = a.bias + h * HD;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 32 * c + 8 * grp + e;
+        const float x = d < HD ? qrow[d] + bq[d] : 0.0f;
+        const Bf3 sp = split3(x);
+        qa[0][c][e] = sp.p0;
+        qa[1][c][e] = sp.p1;
+        qa[2][c][e] = sp.p2;
+      }
+  }
+  v4f o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_ref = -FLT_MAX, l_part = 0.0f;
+  const float *bk = a.bias + a.dim + h * HD;
+  const float *bv = a.bias + 2 * a.dim + h * HD;
+  const float *kbase = a.qkv + a.dim + h * HD;
+  const float *vbase = a.qkv + 2 * a.dim + h * HD;
+
+  // zero padding: K dims HD .. DP-1 and V^T rows HD .. 16 NB - 1, never staged
+  const __bf16 bz = (__bf16)0.0f;
+  for (int i = tid; i < 3 * TK * (DP - HD); i += NT) {
+    const int p = i / (TK * (DP - HD)), j = i % (TK * (DP - HD));
+    kt[p][(j / (DP - HD)) * RK + HD + j % (DP - HD)] = bz;
+  }
+  for (int i = tid; i < 3 * (16 * NB - HD) * RV; i += NT) {
+    const int p = i / ((16 * NB - HD) * RV), j = i % ((16 * NB - HD) * RV);
+    vt[p][HD * RV + j] = bz;
+  }
+  for (int i = tid; i < 2 * C4; i += NT)
+    kvb[i / C4][i % C4] = reinterpret_cast<const v4f *>(i < C4 ? bk : bv)[i % C4];
+
+  static_assert(TK / 4 == 8, "V blocks: 8 key quads per tile");
+  constexpr int VB = 8 * C4;              // V blocks (4 keys x 4 dims) per tile
+  constexpr int PV = (VB + NT - 1) / NT;  // V blocks per thread
+  constexpr int NI = 2 * SG / 64;  // DMA instructions per tile (K, then V)
+  auto fetch = [&](int t0) {  // rows clamped into range: every load is unconditional
+    for (int i = wave; i < NI; i += NW) {  // wave-uniform
+      const int kv = i / (SG / 64), ch = (i % (SG / 64)) * 64 + lane;
+      const int t = ch / C4, c4 = ch - t * C4;
+      vis_dma16((kv == 0 ? kbase : vbase) + (size_t)min(t0 + t, a.n - 1) * a.stride + 4 * c4,
+                &stg[kv][(i % (SG / 64)) * 64]);
+    }
+  };
+  fetch(0);
+  for (int t0 = 0; t0 < a.n; t0 += TK) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's DMAs landed
+    lds_barrier();  // every wave is done with the previous tile (and every DMA landed)
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * NT;
+      if (i >= TK * C4) break;
+      const int t = i / C4, c4 = i - t * C4;
+      const v4f kv = t0 + t < a.n ? stg[0][i] + kvb[0][c4] : zero;
+      bf4 k0, k1, k2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const Bf3 sp = split3(kv[e]);
+        k0[e] = sp.p0;
+        k1[e] = sp.p1;
+        k2[e] = sp.p2;
+      }
+      *reinterpret_cast<bf4 *>(&kt[0][t * RK + 4 * c4]) = k0;
+      *reinterpret_cast<bf4 *>(&kt[1][t * RK + 4 * c4]) = k1;
+      *reinterpret_cast<bf4 *>(&kt[2][t * RK + 4 * c4]) = k2;
+    }
+#pragma unroll
+    for (int j = 0; j < PV; ++j) {
+      const int b = tid + j * NT;
+      if (b >= VB) break;
+      const int tq = b % 8, c4 = b / 8;
+      const int k0i = 8 * (tq % 4) + 4 * (tq / 4);  // PV index of key 4 tq
+      v4f r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        r[u] = t0 + 4 * tq + u < a.n ? stg[1][(4 * tq + u) * C4 + c4] + kvb[1][c4] : zero;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf4 v0, v1, v2;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const Bf3 sp = split3(r[u][e]);
+          v0[u] = sp.p0;
+          v1[u] = sp.p1;
+          v2[u] = sp.p2;
+        }
+        const int at = (4 * c4 + e) * RV + k0i;
+        *reinterpret_cast<bf4 *>(&vt[0][at]) = v0;
+        *reinterpret_cast<bf4 *>(&vt[1][at]) = v1;
+        *reinterpret_cast<bf4 *>(&vt[2][at]) = v2;
+      }
+    }
+    lds_barrier();
+    if (t0 + TK < a.n) fetch(t0 + TK);
+
+    // scores: sc[b][r] = q(col) . k(t0 + 16 b + 4 grp + r), the small piece
+    // products first
+    v4f sc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int at = (16 * b + col) * RK + 32 * c + 8 * grp;
+        const bf8 k0 = *reinterpret_cast<const bf8 *>(&kt[0][at]);
+        const bf8 k1 = *reinterpret_cast<const bf8 *>(&kt[1][at]);
+        const bf8 k2 = *reinterpret_cast<const bf8 *>(&kt[2][at]);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qa[0][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qa[1][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qa[2][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qa[0][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qa[1][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qa[0][c], sc[b], 0, 0, 0);
+      }
+    }
+    float tmax = -FLT_MAX;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = t0 + 16 * b + 4 * grp + r < a.n;
+        sc[b][r] = ok ? sc[b][r] * a.scale : -FLT_MAX;
+        tmax = fmaxf(tmax, sc[b][r]);
+      }
+    if (__any(tmax > m_ref + kVaSlackF)) {
+      float rmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+      rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+      const float m_new = fmaxf(m_ref, rmax);
+      const float alpha = __expf(m_ref - m_new);
+      m_ref = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
+    }
+    // probabilities, their pieces (k = 4 b + r of this lane's eight)
+    bf8 p0, p1, p2;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = sc[b][r] > -FLT_MAX ? __expf(sc[b][r] - m_ref) : 0.0f;
+        l_part += pr;
+        const Bf3 sp = split3(pr);
+        p0[4 * b + r] = sp.p0;
+        p1[4 * b + r] = sp.p1;
+        p2[4 * b + r] = sp.p2;
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int at = (16 * nb + col) * RV + 8 * grp;
+      const bf8 v0 = *reinterpret_cast<const bf8 *>(&vt[0][at]);
+      const bf8 v1 = *reinterpret_cast<const bf8 *>(&vt[1][at]);
+      const bf8 v2 = *reinterpret_cast<const bf8 *>(&vt[2][at]);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v2, p0, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, p1, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, p2, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, p0, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, p1, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, p0, o[nb], 0, 0, 0);
+    }
+  }
+  float l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  const int qr = q0 + col;
+  if (qr < a.n) {
+    float *orow = a.out + (size_t)qr * a.dim + h * HD;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int d = 16 * nb + 4 * grp + r;
+        if (d < HD) orow[d] = o[nb][r] / l;
+      }
+  }
+}
+
+// The fp32 mode's kernel: the split bf16 one by default, the fp32-MFMA one
+// with GEMMA_HIP_VIS_ATTN=f32 (read once)
+// Read at every launch (one getenv per layer), so that a process can time or
+// check both fp32-mode kernels.
+bool vis_attn_split() {
+  const char *e = getenv("GEMMA_HIP_VIS_ATTN");
+  return e == nullptr || strcmp(e, "f32") != 0;
+}
+
 hipError_t launch_vis_attention(const VisAttn &a, int hdim, bool f32, hipStream_t stream) {
   constexpr int NW = kVaWaves;
   const dim3 grid((a.n + NW * 16 - 1) / (NW * 16) * a.n_heads);
+  if (f32 && vis_attn_split()) {
+    switch (hdim) {
+      case 16: vis_attn_bf3_kernel<16, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 32: vis_attn_bf3_kernel<32, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 64: vis_attn_bf3_kernel<64, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 72: vis_attn_bf3_kernel<72, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      case 128: vis_attn_bf3_kernel<128, NW><<<grid, NW * 64, 0, stream>>>(a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (f32) {
     switch (hdim) {
       case 16: vis_attn_f32_kernel<16, NW, kVaKeysF><<<grid, NW * 64, 0, stream>>>(a); break;

@@ -462,10 +462,16 @@ int gemma_hip_vision_forward(gemma_hip_vision *vis, const float *img, float *out
  * (gemma.c:4533-4561) and its patch embedding (4411-4448, im2col and a GEMM
  * with the bias, clamp and position embedding of 4452-4468 in its epilogue);
  * set before forward, kept until changed:
- *   GEMMA_HIP_ATTN_F32 (the default) -- fp32 matrix cores, fp32 throughout
- *     as the reference computes it (its summation order differs), so results
- *     agree with the exact form to fp32 rounding, amplified where a later
- *     int8 quantization flips;
+ *   GEMMA_HIP_ATTN_F32 (the default) -- fp32 throughout as the reference
+ *     computes it (its summation order differs), so results agree with the
+ *     exact form to fp32 rounding, amplified where a later int8 quantization
+ *     flips.  The patch GEMM runs on the fp32 matrix cores; the attention on
+ *     the bf16 ones in split precision: each fp32 operand is the sum of three
+ *     bf16 pieces and every product is summed from the six piece products
+ *     down to 2^-16 of the leading one, which leaves an error per product of
+ *     order 2^-23 relative, the size of an fp32 rounding, with fp32
+ *     accumulation (the environment variable GEMMA_HIP_VIS_ATTN=f32, read
+ *     once, selects the plain fp32 matrix-core kernel instead);
  *   GEMMA_HIP_ATTN_F64 -- fp64 (matrix cores for the attention), every
  *     output rounded once from the exact sum: the verification mode, equal
  *     to an fp64 evaluation of the same formulas.

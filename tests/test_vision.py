@@ -228,22 +228,29 @@ def _attention_inputs(n, heads, dim, seed):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", sorted(ATT_CASES))
-def test_vision_attention_kernels_match_oracle(gh, case):
+def test_vision_attention_kernels_match_oracle(gh, case, monkeypatch):
     import torch
 
     n, heads, dim = ATT_CASES[case]
     qkv, bias, want = _attention_inputs(n, heads, dim, seed=n + heads)
     dq, db = torch.from_numpy(qkv).cuda(), torch.from_numpy(bias).cuda()
     scale = float(np.abs(want).max())
-    for mode, tol in ((0, ATT_F64_TOL), (1, ATT_F32_TOL)):
+    # mode 1 twice: the split-bf16 kernel (the default) and the plain fp32
+    # matrix-core kernel that GEMMA_HIP_VIS_ATTN=f32 selects per launch
+    for mode, kernel, tol in ((0, "f64", ATT_F64_TOL), (1, "split", ATT_F32_TOL),
+                              (1, "f32", ATT_F32_TOL)):
+        if kernel == "f32":
+            monkeypatch.setenv("GEMMA_HIP_VIS_ATTN", "f32")
+        else:
+            monkeypatch.delenv("GEMMA_HIP_VIS_ATTN", raising=False)
         out = torch.full((n, dim), float("nan"), device="cuda")
         gh.vision_attention(out, dq, db, n, heads, dim, mode,
                             stream=torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         rel = float(np.abs(got - want).max()) / scale
-        print(f"vision attention {case} mode {mode}: |d|/max = {rel:.3g}", flush=True)
-        assert rel <= tol, (case, mode, rel)
+        print(f"vision attention {case} {kernel}: |d|/max = {rel:.3g}", flush=True)
+        assert rel <= tol, (case, kernel, rel)
 
 
 @pytest.mark.gpu
