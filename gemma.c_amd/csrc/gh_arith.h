@@ -249,4 +249,26 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+// Split precision on the bf16 matrix cores: x = p0 + p1 + p2, each piece
+// rounded to nearest bf16 from the remainder of the ones before it (the
+// subtractions are exact: x and p0 agree in their leading bits, and so do the
+// remainder and p1), so the three together carry x's 24 significant bits.
+// A product a.b summed from the six piece products whose orders add up to at
+// most 2 (a0 b0, a0 b1, a1 b0, a0 b2, a1 b1, a2 b0) drops terms below
+// 3 * 2^-24 |a b|; each bf16 x bf16 product is exact in fp32.
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+struct Bf3 {
+  __bf16 p0, p1, p2;
+};
+__device__ __forceinline__ Bf3 split3(float x) {
+  Bf3 r;
+  r.p0 = (__bf16)x;
+  const float r1 = x - (float)r.p0;
+  r.p1 = (__bf16)r1;
+  r.p2 = (__bf16)(r1 - (float)r.p1);
+  return r;
+}
+
 }  // namespace gh

@@ -30,6 +30,7 @@
 // gemm_fpx_nn), which no fp32 bit pattern here could follow anyway.
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "dec_common.h"
@@ -584,6 +585,201 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
   }
 }
 
+// The same attention on the bf16 matrix cores in split precision: q, k, the
+// weights p and v each as three bf16 pieces (split3), every product summed
+// from its six leading piece products (v_mfma_f32_16x16x32_bf16, the small
+// ones first) with fp32 accumulation, so the error per product is of the
+// size of an fp32 rounding and the result agrees with the fp64 form to fp32
+// rounding, as pf_attn_f32_kernel's does, at ~2.5x its matrix-core rate.
+// A workgroup is kPbWaves waves x 16 query vectors (one workgroup per CU:
+// the planes below take most of the LDS).  Key tiles of 32, whose K rows go
+// by LDS DMA into an fp32 staging buffer and whose V rows (4 keys x 4 dims
+// per thread) into registers while the tile before is in use; at a tile's
+// start the workgroup splits both, once for all its waves, into three bf16
+// planes each: K [key][dim] and V^T [dim][k], where k = 8 g + 4 b + r is the
+// value product's index of key 16 b + 4 g + r -- the key whose score lane
+// (query, g) holds in element r of block b, so a lane's eight weights are
+// its operand of that product as they stand.  Lane (query col, g) holds the
+// query's dims 32 c + 8 g .. + 7 of every piece and the outputs' dims
+// 16 nb + 4 g .. + 3.  Masks, softmax and partials as pf_attn_f32_kernel.
+constexpr int kPbWaves = 8;
+constexpr int kPbQ = kPbWaves * 16;  // query vectors per workgroup
+
+template <int HD>
+__global__ __launch_bounds__(kPbWaves * 64) void pf_attn_bf3_kernel(PfAttn a) {
+  constexpr int NT = kPbWaves * 64;
+  constexpr int TK = 32;          // keys per tile
+  constexpr int CH = HD / 32;     // 32-dim chunks of the score product
+  constexpr int NB = HD / 16;     // 16-dim output blocks
+  constexpr int C4 = HD / 4;      // float4 per key row
+  constexpr int RK = HD + 8;      // K plane row (bf16): 8 rows in distinct banks
+  constexpr int RV = TK + 8;      // V^T plane row (bf16)
+  constexpr int SG = TK * C4;     // float4 of a K tile
+  constexpr int NIW = SG / 64 / kPbWaves;  // K DMA instructions per wave and tile
+  constexpr int PF = (SG + NT - 1) / NT;   // K float4 split per thread
+  constexpr int VB = 8 * C4;               // V blocks (4 keys x 4 dims) per tile
+  static_assert(HD % 64 == 0 && TK == kPaKeys && NIW * 64 * kPbWaves == SG && VB <= NT,
+                "tile staging");
+  __shared__ __attribute__((aligned(16))) __bf16 kt[3][TK * RK];
+  __shared__ __attribute__((aligned(16))) __bf16 vt[3][HD * RV];
+  __shared__ v4f stg[SG];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const PaLane L = pa_lane(a, wave, col);
+  if (L.empty) return;  // the whole block: before any barrier
+  bf8 qa[3][CH];
+  {
+    const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + 8 * grp;
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const v4f q4 = *reinterpret_cast<const v4f *>(qrow + 32 * c + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const Bf3 sp = split3(q4[e]);
+          qa[0][c][4 * h + e] = sp.p0;
+          qa[1][c][4 * h + e] = sp.p1;
+          qa[2][c][4 * h + e] = sp.p2;
+        }
+      }
+  }
+  v4f o[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) o[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m_ref = kPaFloorF, l_part = 0.0f;
+  const float *kc = a.kc + (size_t)L.hk * a.clen * HD;
+  const float *vc = a.vc + (size_t)L.hk * a.clen * HD;
+
+  // rows past the chunk's last key repeat it: their weights are exactly 0
+  const int vtq = tid % 8, vc4 = tid / 8;  // this thread's V block (tid < VB)
+  v4f vr[4];
+  auto fetch = [&](int t0) {
+#pragma unroll
+    for (int j = 0; j < NIW; ++j) {
+      const int i = wave * NIW + j;  // wave-uniform
+      const int ch = 64 * i + lane, t = ch / C4;
+      lds_dma16(kc + (size_t)min(t0 + t, L.k_end) * HD + 4 * (ch - t * C4),
+                reinterpret_cast<float *>(&stg[64 * i]));
+    }
+    if (tid < VB) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        vr[u] = *reinterpret_cast<const v4f *>(vc + (size_t)min(t0 + 4 * vtq + u, L.k_end) * HD +
+                                               4 * vc4);
+    }
+  };
+  fetch(L.k_lo);
+  for (int t0 = L.k_lo; t0 <= L.k_end; t0 += TK) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's K DMAs and V rows are in
+    lds_barrier();  // every wave's DMAs landed, every wave is done with the planes
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const int i = tid + j * NT;
+      if (i >= SG) break;
+      const int t = i / C4, c4 = i - t * C4;
+      const v4f kv = stg[i];
+      bf4 k0, k1, k2;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const Bf3 sp = split3(kv[e]);
+        k0[e] = sp.p0;
+        k1[e] = sp.p1;
+        k2[e] = sp.p2;
+      }
+      *reinterpret_cast<bf4 *>(&kt[0][t * RK + 4 * c4]) = k0;
+      *reinterpret_cast<bf4 *>(&kt[1][t * RK + 4 * c4]) = k1;
+      *reinterpret_cast<bf4 *>(&kt[2][t * RK + 4 * c4]) = k2;
+    }
+    if (tid < VB) {
+      const int k0i = 8 * (vtq % 4) + 4 * (vtq / 4);  // the value product's k of key 4 vtq
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        bf4 v0, v1, v2;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const Bf3 sp = split3(vr[u][e]);
+          v0[u] = sp.p0;
+          v1[u] = sp.p1;
+          v2[u] = sp.p2;
+        }
+        const int at = (4 * vc4 + e) * RV + k0i;
+        *reinterpret_cast<bf4 *>(&vt[0][at]) = v0;
+        *reinterpret_cast<bf4 *>(&vt[1][at]) = v1;
+        *reinterpret_cast<bf4 *>(&vt[2][at]) = v2;
+      }
+    }
+    lds_barrier();  // the planes are complete; the staging buffer is free
+    if (t0 + TK <= L.k_end) fetch(t0 + TK);
+
+    if (t0 > L.w_hi || t0 + TK - 1 < L.w_lo) continue;  // wave-uniform
+    v4f sc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int at = (16 * b + col) * RK + 32 * c + 8 * grp;
+        const bf8 k0 = *reinterpret_cast<const bf8 *>(&kt[0][at]);
+        const bf8 k1 = *reinterpret_cast<const bf8 *>(&kt[1][at]);
+        const bf8 k2 = *reinterpret_cast<const bf8 *>(&kt[2][at]);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k2, qa[0][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qa[1][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qa[2][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qa[0][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qa[1][c], sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qa[0][c], sc[b], 0, 0, 0);
+      }
+    }
+    pa_softmax_f32<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o);
+    bf8 p0, p1, p2;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const Bf3 sp = split3(sc[b][r]);
+        p0[4 * b + r] = sp.p0;
+        p1[4 * b + r] = sp.p1;
+        p2[4 * b + r] = sp.p2;
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int at = (16 * nb + col) * RV + 8 * grp;
+      const bf8 v0 = *reinterpret_cast<const bf8 *>(&vt[0][at]);
+      const bf8 v1 = *reinterpret_cast<const bf8 *>(&vt[1][at]);
+      const bf8 v2 = *reinterpret_cast<const bf8 *>(&vt[2][at]);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v2, p0, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, p1, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, p2, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v1, p0, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, p1, o[nb], 0, 0, 0);
+      o[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v0, p0, o[nb], 0, 0, 0);
+    }
+  }
+  float l = l_part + __shfl_xor(l_part, 16, 64);
+  l = l + __shfl_xor(l, 32, 64);
+  if (!L.valid) return;
+  // dims 16 nb + 4 grp .. + 3 are o[nb]
+  if (L.nchunks == 1) {
+    float *orow = a.xo + (size_t)L.row * a.q_sz + L.head * HD + 4 * grp;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) *reinterpret_cast<v4f *>(orow + 16 * nb) = o[nb] / l;
+    return;
+  }
+  float *pf = reinterpret_cast<float *>(a.part);
+  const size_t at = (size_t)L.chunk_id * a.n + L.row;
+  float *prow = pf + at * a.q_sz + L.head * HD + 4 * grp;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) *reinterpret_cast<v4f *>(prow + 16 * nb) = o[nb];
+  if (grp == 0) {
+    float *ml = pf + (size_t)kPfMaxSplit * a.n * a.q_sz + (at * a.n_heads + L.head) * 2;
+    ml[0] = m_ref;
+    ml[1] = l;
+  }
+}
+
 // HD 256 on wave pairs.  A whole head dim per wave needs 64 fp64 output
 // accumulators and 64 fp64 query operands per lane, i.e. one wave per SIMD,
 // and then nothing overlaps a wave's softmax, barriers and operand reads with
@@ -940,9 +1136,18 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
   return hipGetLastError();
 }
 
+// The fp32 mode's kernel: the split bf16 one by default, the fp32-MFMA one
+// with GEMMA_HIP_PF_ATTN=f32.  Read at every launch, so that one process can
+// time or check both.
+bool pf_attn_split() {
+  const char *e = getenv("GEMMA_HIP_PF_ATTN");
+  return e == nullptr || strcmp(e, "f32") != 0;
+}
+
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t stream) {
   const int hn = a.n_heads / a.nkv;
-  const int qpb = f32 ? kPaQ : hdim == 256 ? kPaQPair : kPaQ;
+  const bool bf3 = f32 && pf_attn_split();
+  const int qpb = bf3 ? kPbQ : f32 ? kPaQ : hdim == 256 ? kPaQPair : kPaQ;
   if (hn <= 0 || qpb % hn != 0 || a.n <= 0 || a.part == nullptr ||
       a.n_heads > kPfMaxMergeHeads)
     return hipErrorInvalidValue;
@@ -968,7 +1173,13 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
   b.chunk = ((kmax + split - 1) / split + kPaKeys - 1) / kPaKeys * kPaKeys;
   b.nsplit = (kmax + b.chunk - 1) / b.chunk;
   const dim3 grid(nrb * b.nsplit * a.nkv);
-  if (f32) {
+  if (bf3) {
+    switch (hdim) {
+      case 128: pf_attn_bf3_kernel<128><<<grid, kPbWaves * 64, 0, stream>>>(b); break;
+      case 256: pf_attn_bf3_kernel<256><<<grid, kPbWaves * 64, 0, stream>>>(b); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else if (f32) {
     switch (hdim) {
       case 128: pf_attn_f32_kernel<128><<<grid, kNT, 0, stream>>>(b); break;
       case 256: pf_attn_f32_kernel<256><<<grid, kNT, 0, stream>>>(b); break;

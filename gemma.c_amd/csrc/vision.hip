@@ -649,21 +649,6 @@ hipError_t launch_vis_ln_rows(const VisLn &a, int n, hipStream_t stream) {
 // Values: the PV product's k index is 8g + 4b + r, the key 16b + 4g + r,
 // so a lane's own eight probabilities are its B operand as they stand; V^T
 // is staged in LDS as three bf16 planes [dim][k] in that key order.
-typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-
-struct Bf3 {
-  __bf16 p0, p1, p2;
-};
-__device__ __forceinline__ Bf3 split3(float x) {
-  Bf3 r;
-  r.p0 = (__bf16)x;
-  const float r1 = x - (float)r.p0;  // exact: x and p0 agree in their leading bits
-  r.p1 = (__bf16)r1;
-  r.p2 = (__bf16)(r1 - (float)r.p1);
-  return r;
-}
-
 // One LDS DMA load: every lane's 16 bytes at g land at lds + 16 * lane (lds
 // wave-uniform); from inline asm so that the compiler does not wait for the
 // pending load before later LDS reads (the kernel waits itself).  m0 has no
@@ -893,9 +878,8 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
 }
 
 // The fp32 mode's kernel: the split bf16 one by default, the fp32-MFMA one
-// with GEMMA_HIP_VIS_ATTN=f32 (read once)
-// Read at every launch (one getenv per layer), so that a process can time or
-// check both fp32-mode kernels.
+// with GEMMA_HIP_VIS_ATTN=f32.  Read at every launch (one getenv per layer),
+// so that one process can time or check both.
 bool vis_attn_split() {
   const char *e = getenv("GEMMA_HIP_VIS_ATTN");
   return e == nullptr || strcmp(e, "f32") != 0;

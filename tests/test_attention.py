@@ -72,6 +72,10 @@ def inputs(case):
     clen = pos0 + n + 3
     kc = rng.standard_normal((nkv, clen, hd)).astype(F32)
     vc = rng.standard_normal((nkv, clen, hd)).astype(F32)
+    # cache rows past the last row's position are never read: NaN there
+    # would reach every output of a kernel that multiplies one by a zero weight
+    kc[:, pos0 + n:] = np.nan
+    vc[:, pos0 + n:] = np.nan
     asc = F32(1.0) / np.sqrt(F32(hd))
     return q, kc, vc, clen, asc
 
@@ -107,7 +111,7 @@ def test_attention_bars_catch_planted_mistakes():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", sorted(CASES))
-def test_prefill_attention_kernels_match_oracle(gh, case):
+def test_prefill_attention_kernels_match_oracle(gh, case, monkeypatch):
     import torch
 
     from gemma_hip import ATTN_F32, ATTN_F64
@@ -117,12 +121,19 @@ def test_prefill_attention_kernels_match_oracle(gh, case):
     want = reference(q, kc, vc, n, pos0, nh, nkv, hd, slide, asc, sc_att, dense)
     dq, dk, dv = (torch.from_numpy(a).cuda() for a in (q, kc, vc))
     scale = float(np.abs(want).max())
-    for mode, tol in ((ATTN_F64, ATT_F64_TOL), (ATTN_F32, ATT_F32_TOL)):
+    # ATTN_F32 twice: the split-bf16 kernel (the default) and the plain fp32
+    # matrix-core kernel that GEMMA_HIP_PF_ATTN=f32 selects per launch
+    for mode, kernel, tol in ((ATTN_F64, "f64", ATT_F64_TOL), (ATTN_F32, "split", ATT_F32_TOL),
+                              (ATTN_F32, "f32", ATT_F32_TOL)):
+        if kernel == "f32":
+            monkeypatch.setenv("GEMMA_HIP_PF_ATTN", "f32")
+        else:
+            monkeypatch.delenv("GEMMA_HIP_PF_ATTN", raising=False)
         out = torch.full((n, nh * hd), float("nan"), device="cuda")
         gh.prefill_attention(out, dq, q.shape[1], dk, dv, n, pos0, nh, nkv, hd, clen, slide, asc,
                              sc_att, dense, mode, stream=torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         rel = float(np.abs(got - want).max()) / scale
-        print(f"prefill attention {case} mode {mode}: |d|/max = {rel:.3g}", flush=True)
-        assert rel <= tol, (case, mode, rel)
+        print(f"prefill attention {case} {kernel}: |d|/max = {rel:.3g}", flush=True)
+        assert rel <= tol, (case, kernel, rel)
