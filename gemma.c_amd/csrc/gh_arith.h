@@ -259,16 +259,30 @@ __device__ __forceinline__ float wave_max_dpp(float v) {
 typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
-struct Bf3 {
-  __bf16 p0, p1, p2;
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// The pieces of two values a, b, each piece pair packed as a bf16x2 dword (a
+// in the low half): one v_cvt_pk_bf16_f32 per piece pair, and each piece's
+// fp32 value taken back from the packed dword by a shift or a mask.
+struct Bf3x2 {
+  uint32_t q0, q1, q2;
 };
-__device__ __forceinline__ Bf3 split3(float x) {
-  Bf3 r;
-  r.p0 = (__bf16)x;
-  const float r1 = x - (float)r.p0;
-  r.p1 = (__bf16)r1;
-  r.p2 = (__bf16)(r1 - (float)r.p1);
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{a, b}, h2));
+}
+__device__ __forceinline__ float bf16_lo(uint32_t q) { return __uint_as_float(q << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t q) { return __uint_as_float(q & 0xffff0000u); }
+__device__ __forceinline__ Bf3x2 split3x2(float a, float b) {
+  Bf3x2 r;
+  r.q0 = cvt_pk_bf16(a, b);
+  const float a1 = a - bf16_lo(r.q0), b1 = b - bf16_hi(r.q0);
+  r.q1 = cvt_pk_bf16(a1, b1);
+  r.q2 = cvt_pk_bf16(a1 - bf16_lo(r.q1), b1 - bf16_hi(r.q1));
   return r;
 }
+__device__ __forceinline__ bf8 as_bf8(u4 v) { return __builtin_bit_cast(bf8, v); }
 
 }  // namespace gh

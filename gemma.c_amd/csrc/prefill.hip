@@ -586,7 +586,7 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_f32_kernel(PfAttn a) {
 }
 
 // The same attention on the bf16 matrix cores in split precision: q, k, the
-// weights p and v each as three bf16 pieces (split3), every product summed
+// weights p and v each as three bf16 pieces (split3x2), every product summed
 // from its six leading piece products (v_mfma_f32_16x16x32_bf16, the small
 // ones first) with fp32 accumulation, so the error per product is of the
 // size of an fp32 rounding and the result agrees with the fp64 form to fp32
@@ -633,18 +633,23 @@ __global__ __launch_bounds__(kPbWaves * 64) void pf_attn_bf3_kernel(PfAttn a) {
   {
     const float *qrow = a.qkv + (size_t)L.row * a.stride + L.head * HD + 8 * grp;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
+    for (int c = 0; c < CH; ++c) {
+      u4 w0, w1, w2;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const v4f q4 = *reinterpret_cast<const v4f *>(qrow + 32 * c + 4 * h);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const Bf3 sp = split3(q4[e]);
-          qa[0][c][4 * h + e] = sp.p0;
-          qa[1][c][4 * h + e] = sp.p1;
-          qa[2][c][4 * h + e] = sp.p2;
+        for (int e = 0; e < 4; e += 2) {
+          const Bf3x2 sp = split3x2(q4[e], q4[e + 1]);
+          w0[2 * h + e / 2] = sp.q0;
+          w1[2 * h + e / 2] = sp.q1;
+          w2[2 * h + e / 2] = sp.q2;
         }
       }
+      qa[0][c] = as_bf8(w0);
+      qa[1][c] = as_bf8(w1);
+      qa[2][c] = as_bf8(w2);
+    }
   }
   v4f o[NB];
 #pragma unroll
@@ -681,34 +686,20 @@ __global__ __launch_bounds__(kPbWaves * 64) void pf_attn_bf3_kernel(PfAttn a) {
       if (i >= SG) break;
       const int t = i / C4, c4 = i - t * C4;
       const v4f kv = stg[i];
-      bf4 k0, k1, k2;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const Bf3 sp = split3(kv[e]);
-        k0[e] = sp.p0;
-        k1[e] = sp.p1;
-        k2[e] = sp.p2;
-      }
-      *reinterpret_cast<bf4 *>(&kt[0][t * RK + 4 * c4]) = k0;
-      *reinterpret_cast<bf4 *>(&kt[1][t * RK + 4 * c4]) = k1;
-      *reinterpret_cast<bf4 *>(&kt[2][t * RK + 4 * c4]) = k2;
+      const Bf3x2 lo = split3x2(kv[0], kv[1]), hi = split3x2(kv[2], kv[3]);
+      *reinterpret_cast<u2 *>(&kt[0][t * RK + 4 * c4]) = u2{lo.q0, hi.q0};
+      *reinterpret_cast<u2 *>(&kt[1][t * RK + 4 * c4]) = u2{lo.q1, hi.q1};
+      *reinterpret_cast<u2 *>(&kt[2][t * RK + 4 * c4]) = u2{lo.q2, hi.q2};
     }
     if (tid < VB) {
       const int k0i = 8 * (vtq % 4) + 4 * (vtq / 4);  // the value product's k of key 4 vtq
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        bf4 v0, v1, v2;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const Bf3 sp = split3(vr[u][e]);
-          v0[u] = sp.p0;
-          v1[u] = sp.p1;
-          v2[u] = sp.p2;
-        }
+        const Bf3x2 lo = split3x2(vr[0][e], vr[1][e]), hi = split3x2(vr[2][e], vr[3][e]);
         const int at = (4 * vc4 + e) * RV + k0i;
-        *reinterpret_cast<bf4 *>(&vt[0][at]) = v0;
-        *reinterpret_cast<bf4 *>(&vt[1][at]) = v1;
-        *reinterpret_cast<bf4 *>(&vt[2][at]) = v2;
+        *reinterpret_cast<u2 *>(&vt[0][at]) = u2{lo.q0, hi.q0};
+        *reinterpret_cast<u2 *>(&vt[1][at]) = u2{lo.q1, hi.q1};
+        *reinterpret_cast<u2 *>(&vt[2][at]) = u2{lo.q2, hi.q2};
       }
     }
     lds_barrier();  // the planes are complete; the staging buffer is free
@@ -734,16 +725,17 @@ __global__ __launch_bounds__(kPbWaves * 64) void pf_attn_bf3_kernel(PfAttn a) {
       }
     }
     pa_softmax_f32<NB, 2>(a, L, sc, t0, grp, m_ref, l_part, o);
-    bf8 p0, p1, p2;
+    u4 w0, w1, w2;  // weight k = 4 b + r of the lane's eight is dword 2 b + r / 2
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const Bf3 sp = split3(sc[b][r]);
-        p0[4 * b + r] = sp.p0;
-        p1[4 * b + r] = sp.p1;
-        p2[4 * b + r] = sp.p2;
+      for (int r = 0; r < 4; r += 2) {
+        const Bf3x2 sp = split3x2(sc[b][r], sc[b][r + 1]);
+        w0[2 * b + r / 2] = sp.q0;
+        w1[2 * b + r / 2] = sp.q1;
+        w2[2 * b + r / 2] = sp.q2;
       }
+    const bf8 p0 = as_bf8(w0), p1 = as_bf8(w1), p2 = as_bf8(w2);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const int at = (16 * nb + col) * RV + 8 * grp;

@@ -698,16 +698,22 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
     const float *qrow = a.qkv + (size_t)qr * a.stride + h * HD;
     const float *bq = a.bias + h * HD;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
+    for (int c = 0; c < CH; ++c) {
+      u4 w0, w1, w2;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 32 * c + 8 * grp + e;
-        const float x = d < HD ? qrow[d] + bq[d] : 0.0f;
-        const Bf3 sp = split3(x);
-        qa[0][c][e] = sp.p0;
-        qa[1][c][e] = sp.p1;
-        qa[2][c][e] = sp.p2;
+      for (int e = 0; e < 8; e += 2) {
+        const int d = 32 * c + 8 * grp + e;  // HD is even: d and d + 1 are both in or out
+        const float x0 = d < HD ? qrow[d] + bq[d] : 0.0f;
+        const float x1 = d < HD ? qrow[d + 1] + bq[d + 1] : 0.0f;
+        const Bf3x2 sp = split3x2(x0, x1);
+        w0[e / 2] = sp.q0;
+        w1[e / 2] = sp.q1;
+        w2[e / 2] = sp.q2;
       }
+      qa[0][c] = as_bf8(w0);
+      qa[1][c] = as_bf8(w1);
+      qa[2][c] = as_bf8(w2);
+    }
   }
   v4f o[NB];
 #pragma unroll
@@ -754,17 +760,10 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
       if (i >= TK * C4) break;
       const int t = i / C4, c4 = i - t * C4;
       const v4f kv = t0 + t < a.n ? stg[0][i] + kvb[0][c4] : zero;
-      bf4 k0, k1, k2;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const Bf3 sp = split3(kv[e]);
-        k0[e] = sp.p0;
-        k1[e] = sp.p1;
-        k2[e] = sp.p2;
-      }
-      *reinterpret_cast<bf4 *>(&kt[0][t * RK + 4 * c4]) = k0;
-      *reinterpret_cast<bf4 *>(&kt[1][t * RK + 4 * c4]) = k1;
-      *reinterpret_cast<bf4 *>(&kt[2][t * RK + 4 * c4]) = k2;
+      const Bf3x2 lo = split3x2(kv[0], kv[1]), hi = split3x2(kv[2], kv[3]);
+      *reinterpret_cast<u2 *>(&kt[0][t * RK + 4 * c4]) = u2{lo.q0, hi.q0};
+      *reinterpret_cast<u2 *>(&kt[1][t * RK + 4 * c4]) = u2{lo.q1, hi.q1};
+      *reinterpret_cast<u2 *>(&kt[2][t * RK + 4 * c4]) = u2{lo.q2, hi.q2};
     }
 #pragma unroll
     for (int j = 0; j < PV; ++j) {
@@ -779,18 +778,11 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        bf4 v0, v1, v2;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const Bf3 sp = split3(r[u][e]);
-          v0[u] = sp.p0;
-          v1[u] = sp.p1;
-          v2[u] = sp.p2;
-        }
+        const Bf3x2 lo = split3x2(r[0][e], r[1][e]), hi = split3x2(r[2][e], r[3][e]);
         const int at = (4 * c4 + e) * RV + k0i;
-        *reinterpret_cast<bf4 *>(&vt[0][at]) = v0;
-        *reinterpret_cast<bf4 *>(&vt[1][at]) = v1;
-        *reinterpret_cast<bf4 *>(&vt[2][at]) = v2;
+        *reinterpret_cast<u2 *>(&vt[0][at]) = u2{lo.q0, hi.q0};
+        *reinterpret_cast<u2 *>(&vt[1][at]) = u2{lo.q1, hi.q1};
+        *reinterpret_cast<u2 *>(&vt[2][at]) = u2{lo.q2, hi.q2};
       }
     }
     lds_barrier();
@@ -836,18 +828,21 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
       for (int nb = 0; nb < NB; ++nb) o[nb] *= alpha;
     }
     // probabilities, their pieces (k = 4 b + r of this lane's eight)
-    bf8 p0, p1, p2;
+    u4 w0, w1, w2;  // weight k = 4 b + r of the lane's eight is dword 2 b + r / 2
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float pr = sc[b][r] > -FLT_MAX ? __expf(sc[b][r] - m_ref) : 0.0f;
-        l_part += pr;
-        const Bf3 sp = split3(pr);
-        p0[4 * b + r] = sp.p0;
-        p1[4 * b + r] = sp.p1;
-        p2[4 * b + r] = sp.p2;
+      for (int r = 0; r < 4; r += 2) {
+        const float pa = sc[b][r] > -FLT_MAX ? __expf(sc[b][r] - m_ref) : 0.0f;
+        const float pb = sc[b][r + 1] > -FLT_MAX ? __expf(sc[b][r + 1] - m_ref) : 0.0f;
+        l_part += pa;
+        l_part += pb;
+        const Bf3x2 sp = split3x2(pa, pb);
+        w0[2 * b + r / 2] = sp.q0;
+        w1[2 * b + r / 2] = sp.q1;
+        w2[2 * b + r / 2] = sp.q2;
       }
+    const bf8 p0 = as_bf8(w0), p1 = as_bf8(w1), p2 = as_bf8(w2);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const int at = (16 * nb + col) * RV + 8 * grp;
