@@ -856,7 +856,7 @@ int gemma_hip_prefill_attention(float *out, const float *q, int q_stride, const 
            hipMalloc(&part, gh::pf_attn_part_doubles(n, n_heads, hdim) * sizeof(double)));
   const gh::PfAttn at{q, q_stride, kc, vc, out, n_heads * hdim, n, pos0, n_heads, nkv, clen,
                       slide, asc, sc_att, part, 0, 0, 0, dense ? 1 : 0};
-  hipError_t e = gh::launch_pf_attention(at, hdim, mode == GEMMA_HIP_ATTN_F32, s);
+  hipError_t e = gh::launch_pf_attention(at, hdim, mode == GEMMA_HIP_ATTN_F32, g.info, s);
   const hipError_t e2 = hipStreamSynchronize(s);
   (void)hipFree(part);
   if (e != hipSuccess || (e = e2) != hipSuccess)
@@ -1267,7 +1267,7 @@ hipError_t prefill_enqueue(gemma_hip_decoder *d, int n, int pos, bool embed, boo
                         c.nkv, d->clen, sliding ? c.slide : 0,
                         (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
                         0, dense ? 1 : 0, d->pf_a8, d->pf_as};
-    if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, st))) !=
+    if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, g.info, st))) !=
         hipSuccess)
       return e;
     // o projection
@@ -1496,7 +1496,7 @@ hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed,
                         c.nkv, d->clen, sliding ? c.slide : 0,
                         (float)(1.0f / sqrtf((float)c.q_scale)), c.sc_att, d->pf_part, 0, 0,
                         0, dense ? 1 : 0};
-    if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, st))) !=
+    if ((e = GH_OP(kOpSoftmax, gh::launch_pf_attention(at, c.hdim, d->attn_f32, g.info, st))) !=
         hipSuccess)
       return e;
     // o (gemma.c:5297), residual, norms

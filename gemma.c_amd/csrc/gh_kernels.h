@@ -277,7 +277,8 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
 // hdim 128 or 256; the q heads per kv head must divide 32; a.part must hold
 // pf_attn_part_doubles(n, n_heads, hdim) doubles
 // f32: on the fp32 matrix cores (otherwise fp64, rounded once)
-hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t stream);
+hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, const DeviceInfo &dev,
+                               hipStream_t stream);
 hipError_t launch_pf_gelu_quant(const float *g, int n, int mlp, int8_t *xq, float *xs,
                                 const WarmRegions &warm, hipStream_t stream);
 // rows g [n][2 * mlp] = (gate | up): gate = gelu(gate) * up in place (the

@@ -32,6 +32,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
+#include <vector>
 
 #include "dec_common.h"
 
@@ -1128,6 +1129,92 @@ hipError_t launch_pf_qk_rope(const PfRope &a, int n, int hdim, hipStream_t strea
   return hipGetLastError();
 }
 
+// Keys per chunk when a row block's range of at most kmax keys is split in
+// `split`: whole tiles.
+int pf_chunk(int kmax, int split) {
+  return ((kmax + split - 1) / split + kPaKeys - 1) / kPaKeys * kPaKeys;
+}
+
+// The key split for the split-bf16 kernel, which runs one workgroup per CU:
+// each candidate split's blocks are dealt, in launch order (pa_lane's block
+// order), to the CU that frees first, each costing its chunk's tiles plus a
+// fixed prologue and epilogue of about two tiles (empty blocks next to
+// nothing), and the merge pass reads and writes the partials once per chunk.
+// Measured at the gemma-3-4b prefill (2048 rows, 8 q heads on 4 kv heads):
+// sliding layers 147 -> 124 us with two chunks instead of seven, global
+// layers 182 -> 146 us with three instead of eight (kernel + merge); this
+// model ranks the splits as the measurements do.
+// The plan is a host computation of a few thousand heap operations, and a
+// decoder asks for the same few shapes at every layer: the last plans are
+// kept (per thread).
+int pf_bf3_split_plan(const PfAttn &b0, int hdim, int qb, int nrb, int kmax, int cus);
+int pf_bf3_split(const PfAttn &b, int hdim, int qb, int nrb, int kmax, int cus) {
+  struct Key {
+    int n, pos0, n_heads, nkv, q_sz, slide, dense, hdim, cus;
+    bool operator==(const Key &o) const {
+      return n == o.n && pos0 == o.pos0 && n_heads == o.n_heads && nkv == o.nkv &&
+             q_sz == o.q_sz && slide == o.slide && dense == o.dense && hdim == o.hdim &&
+             cus == o.cus;
+    }
+  };
+  constexpr int kKeep = 8;
+  thread_local Key keys[kKeep];
+  thread_local int plans[kKeep], used = 0, next = 0;
+  const Key key{b.n, b.pos0, b.n_heads, b.nkv, b.q_sz, b.slide, b.dense, hdim, cus};
+  for (int i = 0; i < used; ++i)
+    if (keys[i] == key) return plans[i];
+  const int split = pf_bf3_split_plan(b, hdim, qb, nrb, kmax, cus);
+  keys[next] = key;
+  plans[next] = split;
+  next = (next + 1) % kKeep;
+  used = std::min(used + 1, kKeep);
+  return split;
+}
+
+int pf_bf3_split_plan(const PfAttn &b0, int hdim, int qb, int nrb, int kmax, int cus) {
+  const double tile_us = 6.0 * hdim / 256.0, fixed_tiles = 2.0;
+  const double merge_us = 0.143e-6 * 4.0 * (double)b0.n * b0.q_sz;  // per chunk
+  const int max_split = std::min(kPfMaxSplit, (kmax + kPaKeys - 1) / kPaKeys);
+  int best = 1, last_nsplit = 0;
+  double best_cost = 0.0;
+  // free_at: a min-heap of the CUs' busy-until times
+  std::vector<double> free_at((size_t)std::max(cus, 1));
+  const auto later = [](double x, double y) { return x > y; };
+  for (int s = 1; s <= max_split; ++s) {
+    PfAttn b = b0;
+    b.chunk = pf_chunk(kmax, s);
+    b.nsplit = (kmax + b.chunk - 1) / b.chunk;
+    if (b.nsplit == last_nsplit) continue;
+    last_nsplit = b.nsplit;
+    std::fill(free_at.begin(), free_at.end(), 0.0);
+    double makespan = 0.0;
+    const int blocks = nrb * b.nsplit * b.nkv;
+    for (int blk = 0; blk < blocks; ++blk) {
+      // pa_lane's mapping of a block to its row block and chunk
+      const int rot = (b.nkv * b.nsplit) % 8 == 0 ? blk / b.nkv / b.nsplit : 0;
+      const int cid = ((blk / b.nkv) % b.nsplit + rot) % b.nsplit;
+      const int r0 = (nrb - 1 - blk / b.nkv / b.nsplit) * qb;
+      const PaRange r = pa_range(b, r0, std::min(qb, b.n - r0));
+      const int nch = (r.p_last - r.k_base + b.chunk) / b.chunk;
+      double cost = 0.05;
+      if (cid < nch) {
+        const int lo = r.k_base + cid * b.chunk, hi = std::min(lo + b.chunk - 1, r.p_last);
+        cost = (hi - lo + kPaKeys) / kPaKeys + fixed_tiles;
+      }
+      std::pop_heap(free_at.begin(), free_at.end(), later);
+      free_at.back() += cost;
+      makespan = std::max(makespan, free_at.back());
+      std::push_heap(free_at.begin(), free_at.end(), later);
+    }
+    const double us = makespan * tile_us + merge_us * b.nsplit;
+    if (s == 1 || us < best_cost) {
+      best = s;
+      best_cost = us;
+    }
+  }
+  return best;
+}
+
 // The fp32 mode's kernel: the split bf16 one by default, the fp32-MFMA one
 // with GEMMA_HIP_PF_ATTN=f32.  Read at every launch, so that one process can
 // time or check both.
@@ -1136,7 +1223,8 @@ bool pf_attn_split() {
   return e == nullptr || strcmp(e, "f32") != 0;
 }
 
-hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t stream) {
+hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, const DeviceInfo &dev,
+                               hipStream_t stream) {
   const int hn = a.n_heads / a.nkv;
   const bool bf3 = f32 && pf_attn_split();
   const int qpb = bf3 ? kPbQ : f32 ? kPaQ : hdim == 256 ? kPaQPair : kPaQ;
@@ -1150,19 +1238,27 @@ hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, hipStream_t 
     const PaRange r = pa_range(a, rb * qb, std::min(qb, a.n - rb * qb));
     kmax = std::max(kmax, r.p_last - r.k_base + 1);
   }
-  // split the key ranges until there are about 2048 blocks (half of them
-  // empty for causal rows), in chunks of at least one tile;
-  // GEMMA_HIP_PF_BLOCKS overrides the target (a tuning knob, read once)
-  static const int target = [] {
+  // GEMMA_HIP_PF_BLOCKS (a tuning knob, read once): split the key ranges
+  // until there are about that many blocks.  Otherwise the fp32-MFMA and fp64
+  // kernels (two workgroups per CU) take about 2048 blocks (half of them
+  // empty for causal rows), and the split-bf16 kernel the split of
+  // pf_bf3_split.
+  static const int knob = [] {
     const char *e = getenv("GEMMA_HIP_PF_BLOCKS");
     const int v = e != nullptr ? atoi(e) : 0;
-    return v >= 64 && v <= (1 << 16) ? v : 2048;
+    return v >= 64 && v <= (1 << 16) ? v : 0;
   }();
-  const int want = (target + nrb * a.nkv - 1) / (nrb * a.nkv);
-  const int split = std::max(1, std::min({kPfMaxSplit, want, (kmax + kPaKeys - 1) / kPaKeys}));
   PfAttn b = a;
   b.qpb = qpb;
-  b.chunk = ((kmax + split - 1) / split + kPaKeys - 1) / kPaKeys * kPaKeys;
+  int split;
+  if (bf3 && knob == 0) {
+    split = pf_bf3_split(b, hdim, qb, nrb, kmax, dev.cus);
+  } else {
+    const int target = knob > 0 ? knob : 2048;
+    const int want = (target + nrb * a.nkv - 1) / (nrb * a.nkv);
+    split = std::max(1, std::min({kPfMaxSplit, want, (kmax + kPaKeys - 1) / kPaKeys}));
+  }
+  b.chunk = pf_chunk(kmax, split);
   b.nsplit = (kmax + b.chunk - 1) / b.chunk;
   const dim3 grid(nrb * b.nsplit * a.nkv);
   if (bf3) {
