@@ -2073,9 +2073,10 @@ hipError_t vision_enqueue(gemma_hip_vision *v, hipStream_t st) {
     if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(n2, n, st))) != hipSuccess) return e;
     // The GELU kernel reads fc2's weights after its rows, as the decoder's
     // prefill does for down: the tower's 27 layers hold more weights than the
-    // Infinity Cache, so each layer's come from HBM.  Measured at 896 px:
-    // 27.6 -> 27.3 ms per image (the same read of fc1's weights in the layer
-    // norm in front of fc1: 29.8 ms).
+    // Infinity Cache, so each layer's come from HBM.  Measured at 896 px,
+    // five alternating runs each on one box: 19.47 -> 19.24 ms per image
+    // (the same read of fc1's weights in the layer norm in front of fc1 was
+    // slower).
     gh::WarmRegions w_fc2{};
     if (n >= kWarmRows) w_fc2 = {{L.w[5]}, {(size_t)mlp * dim}, 1};
     // fc1, bias + GELU, fc2 (4604-4644)
