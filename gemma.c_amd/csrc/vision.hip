@@ -667,6 +667,12 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
   constexpr int TK = 32;              // keys per tile
   constexpr int CH = (HD + 31) / 32;  // 32-dim chunks of the score product
   constexpr int DP = CH * 32;         // padded head dim of the K planes
+  // A last chunk of 8 dims (head dim 72) takes two MFMAs instead of six: its
+  // k index carries four piece products over the 8 dims, k = 8 g + e for
+  // dim 32 CF + e of piece pair g (first MFMA: k2 q0, k1 q1, k0 q2, k1 q0;
+  // second: k0 q1, k0 q0 and two zero pairs)
+  constexpr bool kTail8 = HD % 32 == 8;
+  constexpr int CF = kTail8 ? CH - 1 : CH;  // chunks summed piece by piece
   constexpr int NB = (HD + 15) / 16;  // 16-dim output blocks
   constexpr int RK = DP + 8;          // K plane row (bf16): 16 rows in distinct banks
   constexpr int RV = TK + 8;          // V^T plane row (bf16)
@@ -674,7 +680,9 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
   constexpr int C4 = HD / 4;
   constexpr int PF = (TK * C4 + NT - 1) / NT;  // K float4 per thread
   static_assert(HD % 8 == 0 && HD <= 128, "head dim");
-  __shared__ __attribute__((aligned(16))) __bf16 kt[3][TK * RK];
+  // planes 16 bytes apart in the banks: the first tail MFMA reads three of
+  // them at one offset
+  __shared__ __attribute__((aligned(16))) __bf16 kt[3][TK * RK + 8];
   __shared__ __attribute__((aligned(16))) __bf16 vt[3][NB * 16 * RV];
   __shared__ v4f kvb[2][C4];
   // the next tile's fp32 K and V rows land here by LDS DMA, key-major [key][C4]
@@ -714,6 +722,22 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
       qa[1][c] = as_bf8(w1);
       qa[2][c] = as_bf8(w2);
     }
+  }
+  // the tail chunk's operands: lane (col, 0) holds dims 32 CF .. + 7 of
+  // every piece in qa[p][CF]; lane (col, g) takes the piece of pair g
+  bf8 qt1 = {}, qt2 = {};
+  int tsel = 0;  // the K plane lane (col, g) reads in the first tail MFMA
+  if constexpr (kTail8) {
+    u4 t[3];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      const u4 v = __builtin_bit_cast(u4, qa[p][CF]);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) t[p][d] = (uint32_t)__shfl((int)v[d], col, 64);
+    }
+    qt1 = as_bf8(grp == 1 ? t[1] : grp == 2 ? t[2] : t[0]);          // q0 q1 q2 q0
+    qt2 = as_bf8(grp == 0 ? t[1] : grp == 1 ? t[0] : u4{0, 0, 0, 0});  // q1 q0 0 0
+    tsel = grp == 0 ? 2 : grp == 2 ? 0 : 1;                            // k2 k1 k0 k1
   }
   v4f o[NB];
 #pragma unroll
@@ -794,8 +818,15 @@ __global__ __launch_bounds__(NW * 64, 16 / NW) void vis_attn_bf3_kernel(VisAttn 
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       sc[b] = v4f{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kTail8) {
+        const int at = (16 * b + col) * RK + 32 * CF;
+        const bf8 a1 = *reinterpret_cast<const bf8 *>(&kt[tsel][at]);
+        const bf8 a2 = *reinterpret_cast<const bf8 *>(&kt[0][at]);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qt1, sc[b], 0, 0, 0);
+        sc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, qt2, sc[b], 0, 0, 0);
+      }
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
+      for (int c = 0; c < CF; ++c) {
         const int at = (16 * b + col) * RK + 32 * c + 8 * grp;
         const bf8 k0 = *reinterpret_cast<const bf8 *>(&kt[0][at]);
         const bf8 k1 = *reinterpret_cast<const bf8 *>(&kt[1][at]);
