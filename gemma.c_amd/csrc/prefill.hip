@@ -1215,29 +1215,56 @@ int pf_bf3_split_plan(const PfAttn &b0, int hdim, int qb, int nrb, int kmax, int
   return best;
 }
 
-// The fp32 mode's kernel: the split bf16 one by default, the fp32-MFMA one
-// with GEMMA_HIP_PF_ATTN=f32.  Read at every launch, so that one process can
-// time or check both.
-bool pf_attn_split() {
+// The fp32 mode's kernel, read at every launch so that one process can time
+// or check both: GEMMA_HIP_PF_ATTN=f32 the fp32-MFMA one, =bf3 the split-bf16
+// one; unset, the split-bf16 one unless the pass is so small that it would
+// have fewer than kPbMinBlocks workgroups, where the fp32-MFMA kernel's
+// smaller workgroups, two per CU, finish first (gemma-3-270m, 32 rows: one
+// split-bf16 workgroup, 19.8 us per layer against 13.5).
+constexpr int kPbMinBlocks = 32;
+enum PfKind { kPfF32, kPfBf3, kPfAuto };
+PfKind pf_attn_kind() {
   const char *e = getenv("GEMMA_HIP_PF_ATTN");
-  return e == nullptr || strcmp(e, "f32") != 0;
+  if (e == nullptr) return kPfAuto;
+  return strcmp(e, "f32") == 0 ? kPfF32 : strcmp(e, "bf3") == 0 ? kPfBf3 : kPfAuto;
+}
+
+// Row blocks of qpb query vectors and the longest key range among them.
+struct PaGeo {
+  int qb, nrb, kmax;
+};
+PaGeo pa_geo(const PfAttn &a, int qpb) {
+  PaGeo g;
+  g.qb = qpb / (a.n_heads / a.nkv);
+  g.nrb = (a.n + g.qb - 1) / g.qb;
+  g.kmax = 0;
+  for (int rb = 0; rb < g.nrb; ++rb) {
+    const PaRange r = pa_range(a, rb * g.qb, std::min(g.qb, a.n - rb * g.qb));
+    g.kmax = std::max(g.kmax, r.p_last - r.k_base + 1);
+  }
+  return g;
 }
 
 hipError_t launch_pf_attention(const PfAttn &a, int hdim, bool f32, const DeviceInfo &dev,
                                hipStream_t stream) {
-  const int hn = a.n_heads / a.nkv;
-  const bool bf3 = f32 && pf_attn_split();
-  const int qpb = bf3 ? kPbQ : f32 ? kPaQ : hdim == 256 ? kPaQPair : kPaQ;
-  if (hn <= 0 || qpb % hn != 0 || a.n <= 0 || a.part == nullptr ||
-      a.n_heads > kPfMaxMergeHeads)
+  const int hn = a.nkv > 0 ? a.n_heads / a.nkv : 0;
+  if (hn <= 0 || kPbQ % hn != 0 || kPaQ % hn != 0 || kPaQPair % hn != 0 || a.n <= 0 ||
+      a.part == nullptr || a.n_heads > kPfMaxMergeHeads)
     return hipErrorInvalidValue;
-  const int qb = qpb / hn, nrb = (a.n + qb - 1) / qb;
-  // the longest key range of a row block
-  int kmax = 0;
-  for (int rb = 0; rb < nrb; ++rb) {
-    const PaRange r = pa_range(a, rb * qb, std::min(qb, a.n - rb * qb));
-    kmax = std::max(kmax, r.p_last - r.k_base + 1);
+  bool bf3 = false;
+  PaGeo geo{};
+  if (f32) {
+    const PfKind kind = pf_attn_kind();
+    if (kind != kPfF32) {
+      geo = pa_geo(a, kPbQ);
+      const int most = geo.nrb * a.nkv *
+                       std::min(kPfMaxSplit, (geo.kmax + kPaKeys - 1) / kPaKeys);
+      bf3 = kind == kPfBf3 || most >= kPbMinBlocks;
+    }
   }
+  const int qpb = bf3 ? kPbQ : f32 ? kPaQ : hdim == 256 ? kPaQPair : kPaQ;
+  if (!bf3) geo = pa_geo(a, qpb);
+  const int qb = geo.qb, nrb = geo.nrb, kmax = geo.kmax;
   // GEMMA_HIP_PF_BLOCKS (a tuning knob, read once): split the key ranges
   // until there are about that many blocks.  Otherwise the fp32-MFMA and fp64
   // kernels (two workgroups per CU) take about 2048 blocks (half of them

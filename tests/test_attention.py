@@ -121,12 +121,13 @@ def test_prefill_attention_kernels_match_oracle(gh, case, monkeypatch):
     want = reference(q, kc, vc, n, pos0, nh, nkv, hd, slide, asc, sc_att, dense)
     dq, dk, dv = (torch.from_numpy(a).cuda() for a in (q, kc, vc))
     scale = float(np.abs(want).max())
-    # ATTN_F32 twice: the split-bf16 kernel (the default) and the plain fp32
-    # matrix-core kernel that GEMMA_HIP_PF_ATTN=f32 selects per launch
-    for mode, kernel, tol in ((ATTN_F64, "f64", ATT_F64_TOL), (ATTN_F32, "split", ATT_F32_TOL),
-                              (ATTN_F32, "f32", ATT_F32_TOL)):
-        if kernel == "f32":
-            monkeypatch.setenv("GEMMA_HIP_PF_ATTN", "f32")
+    # ATTN_F32 three times: the default choice (the split-bf16 kernel, or the
+    # fp32-MFMA one for the smallest passes) and each kernel forced per launch
+    # by GEMMA_HIP_PF_ATTN
+    for mode, kernel, tol in ((ATTN_F64, "f64", ATT_F64_TOL), (ATTN_F32, "default", ATT_F32_TOL),
+                              (ATTN_F32, "bf3", ATT_F32_TOL), (ATTN_F32, "f32", ATT_F32_TOL)):
+        if kernel in ("bf3", "f32"):
+            monkeypatch.setenv("GEMMA_HIP_PF_ATTN", kernel)
         else:
             monkeypatch.delenv("GEMMA_HIP_PF_ATTN", raising=False)
         out = torch.full((n, nh * hd), float("nan"), device="cuda")
