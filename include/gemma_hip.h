@@ -365,14 +365,19 @@ int gemma_hip_decoder_prefill_rows(gemma_hip_decoder *dec, const float *x, int n
                                    int mask, float *logits, int *next);
 
 /* The arithmetic of the prompt passes' attention (prefill, prefill_rows,
- * image), kept until changed: GEMMA_HIP_ATTN_F32 (the default; fp32 matrix
- * cores, fp32 throughout as the reference's gemm_fpx/softmax/gemm_fpx_nn,
+ * image), kept until changed: GEMMA_HIP_ATTN_F32 (the default; fp32
+ * throughout as the reference's gemm_fpx/softmax/gemm_fpx_nn,
  * gemma.c:5198-5255, in its own summation order: agrees with the exact
  * result to fp32 rounding, amplified where a later int8 quantization flips)
- * or GEMMA_HIP_ATTN_F64 (fp64 matrix cores at half the rate, each output
- * rounded once from the exact sum: the verification mode, equal to an fp64
- * evaluation of the same formulas).  The decode step's attention is fp64
- * either way.  0 or 1 on an unknown mode. */
+ * or GEMMA_HIP_ATTN_F64 (fp64 matrix cores, each output rounded once from
+ * the exact sum: the verification mode, equal to an fp64 evaluation of the
+ * same formulas).  The fp32 mode runs on the bf16 matrix cores in split
+ * precision (each fp32 operand three bf16 pieces, each product summed from
+ * the six piece products down to 2^-16 of the leading one, fp32
+ * accumulation), or, for passes too small to give that kernel 32 workgroups,
+ * on the fp32 matrix cores; the environment variable GEMMA_HIP_PF_ATTN=bf3
+ * or =f32, read at every launch, forces either.  The decode step's attention
+ * is fp64 either way.  0 or 1 on an unknown mode. */
 #define GEMMA_HIP_ATTN_F64 0
 #define GEMMA_HIP_ATTN_F32 1
 int gemma_hip_decoder_set_attention(gemma_hip_decoder *dec, int mode);
