@@ -405,6 +405,22 @@ __global__ __launch_bounds__(kNT, 2) void pf_attn_kernel(PfAttn a) {
 constexpr float kPaSlackF = 16.0f;    // p <= e^16
 constexpr float kPaFloorF = -1e30f;   // far below any score, far above -FLT_MAX
 
+// e^x for the softmax (x <= kPaSlackF) in seven instructions: 2^(x log2 e)
+// by v_exp_f32 at h = fl(x * L), times 2^l ~ 1 + l ln 2 for the remainder
+// l = x log2 e - h (the product's rounding error, exact by fma, plus x times
+// the error of L = fl(log2 e)); |l| <= ~|x| 2^-24, so the neglected
+// (l ln 2)^2 / 2 is below 2^-40 and the result is within about one ulp of
+// v_exp_f32's own.  Below e^-87 the result may be 0 (the weight is then
+// negligible beside the row's largest, which is at least e^-16).
+__device__ __forceinline__ float exp_pa(float x) {
+  constexpr float L = 1.44269502162933349609375f;       // fl(log2 e)
+  constexpr float L_lo = 1.92596298909109e-8f;  // log2 e - L
+  const float h = x * L;
+  const float l = fmaf(x, L, -h) + x * L_lo;
+  const float r = __builtin_amdgcn_exp2f(h);
+  return fmaf(r, l * 0.693147182464599609375f, r);
+}
+
 template <int NB, int NS>
 __device__ __forceinline__ void pa_softmax_f32(const PfAttn &a, const PaLane &L, v4f (&sc)[NS],
                                                int key0, int grp, float &m_ref, float &l_part,
@@ -424,7 +440,7 @@ __device__ __forceinline__ void pa_softmax_f32(const PfAttn &a, const PaLane &L,
     float rmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
     const float m_new = fmaxf(m_ref, rmax);
-    const float alpha = expf(m_ref - m_new);
+    const float alpha = exp_pa(m_ref - m_new);
     m_ref = m_new;
     l_part *= alpha;
 #pragma unroll
@@ -434,7 +450,7 @@ __device__ __forceinline__ void pa_softmax_f32(const PfAttn &a, const PaLane &L,
   for (int b = 0; b < NS; ++b)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      sc[b][r] = sc[b][r] > -FLT_MAX ? expf(sc[b][r] - m_ref) : 0.0f;
+      sc[b][r] = sc[b][r] > -FLT_MAX ? exp_pa(sc[b][r] - m_ref) : 0.0f;
       l_part += sc[b][r];
     }
 }
