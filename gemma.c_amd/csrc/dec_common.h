@@ -142,13 +142,23 @@ __device__ __forceinline__ double exp_tab(double x, const double *tab, const Exp
 // gelu_tanh (gemma.c:4139-4145) with the reference's fp32 constants, in
 // fp64: 0.5 x (1 + tanh(u)) with u = c (x + k x^3) is the same function as
 // x / (1 + e^(-2u)) (1 + tanh(u) = 2 / (1 + e^(-2u))), which costs one table
-// exponential and one division instead of tanh.  The two forms differ only
+// exponential and one reciprocal instead of tanh.  The two forms differ only
 // by fp64 rounding; at x -> -inf both give -0, at x -> +inf both give x.
 __device__ __forceinline__ double gelu(double x, const double *etab, const ExpConsts &ec) {
   const double c = (double)0.79788456080287f;
   const double k = (double)0.044715f;
   const double u = c * (x + k * x * x * x);
-  return x / (1.0 + exp_tab(-2.0 * u, etab, ec));
+  // x / d by v_rcp_f64 and two Newton steps (each squares the relative
+  // error, so the reciprocal is within an ulp or two of fp64), instead of
+  // the correctly rounded fp64 division sequence: the result is rounded to
+  // fp32 once anyway.  d is capped at 1e300, where x / d and x * (1 / d)
+  // both round to a zero of x's sign in fp32 (d = inf would give NaN in
+  // the Newton steps).
+  const double d = fmin(1.0 + exp_tab(-2.0 * u, etab, ec), 1e300);
+  double r = __builtin_amdgcn_rcp(d);
+  r = fma(r, fma(-d, r, 1.0), r);
+  r = fma(r, fma(-d, r, 1.0), r);
+  return x * r;
 }
 
 // Reads the step's token and position; false when they are out of range
