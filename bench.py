@@ -28,7 +28,10 @@ The JSON line also carries, measured in the same run:
   per_gemv_f32  the fp32 fallback ('U' files, gemv_fpx): the sweep's launches
                 with fp32 weights, GB/s per launch
   gemm_f32      the fp32 GEMM (gemm_fpx) at the gemma-3-4b prefill shapes,
-                TFLOP/s against the 157.3 TFLOP/s fp32 matrix peak
+                TFLOP/s of fp32 work; by default split-bf16 on the bf16
+                matrix cores (six bf16 products per multiply-add: bound
+                2500 / 6 = 416.7 TF/s), with GEMMA_HIP_GEMM_F32=mfma the
+                fp32-MFMA kernel (bound 157.3 TF/s)
   decode_1b     tokens/s of the full W8A8 matmul path of one gemma-3-1b
                 decode token (26 layers x {qkv, o, gate/up, down} + LM head)
   decoder       configs 3 (gemma-3-1b: 512 prompt tokens, then 256 decode
@@ -70,6 +73,7 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
 LM_KERNEL = "gemv_i8_stream_kernel<8, 9, 1, true, 256>"
 INT8_PEAK_TOPS = 5000.0    # MI355X dense int8 MFMA
 FP32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 ROTATE_BYTES = 512 << 20   # > 2x the 256 MB Infinity Cache
 ROT_STEPS = 8              # steps per captured graph
 TIMING_RUNS = 5            # per-launch and GEMM timings: median of this many runs
@@ -320,8 +324,13 @@ def bench_gemm(torch, gh, gen, timer, reps):
 
 def bench_gemm_f32(torch, gh, gen, timer, reps):
     """The fp32 GEMM (gemm_fpx, gemma.c:3304-3399; 'U' model files) at the
-    gemma-3-4b prefill shapes, TFLOP/s against the 157.3 TFLOP/s fp32 matrix
-    peak."""
+    gemma-3-4b prefill shapes, TFLOP/s of fp32 work against the bound of the
+    kernel that runs: the split-bf16 one (the library's default) spends six
+    bf16 MFMA products per fp32 multiply-add, so its bound is a sixth of the
+    bf16 peak; the fp32-MFMA one (GEMMA_HIP_GEMM_F32=mfma) is bound by the
+    fp32 matrix peak."""
+    split = os.environ.get("GEMMA_HIP_GEMM_F32") != "mfma"
+    peak = BF16_PEAK_TFLOPS / 6 if split else FP32_PEAK_TFLOPS
     out = {}
     stream = torch.cuda.current_stream().cuda_stream
     for name, m, n, k in GEMM_SHAPES[:5]:
@@ -337,9 +346,10 @@ def bench_gemm_f32(torch, gh, gen, timer, reps):
         ms = statistics.median(timer.elapsed_ms(run) for _ in range(TIMING_RUNS)) / reps
         tf = gemm_ops(m, n, k) / (ms * 1e-3) / 1e12
         out[name] = dict(m=m, n=n, k=k, us=round(ms * 1e3, 2), tflops=round(tf, 1),
-                         frac=round(tf / FP32_PEAK_TFLOPS, 4))
+                         frac=round(tf / peak, 4))
         del a, b, d
-    return {"peak_tflops": FP32_PEAK_TFLOPS, "shapes": out}
+    return {"kernel": "split-bf16" if split else "fp32-mfma", "peak_tflops": round(peak, 1),
+            "shapes": out}
 
 
 def bench_decode_1b(torch, gh, gen, timer, tokens):
@@ -467,9 +477,11 @@ def bench_decoder(torch, gh, name: str, prompt: int, steps: int) -> dict:
     if quant:
         prefill.update(int8_tops=round(pf_ops / t_pf / 1e12, 1),
                        int8_frac=round(pf_ops / t_pf / 1e12 / INT8_PEAK_TOPS, 4))
-    else:  # the fp32 GEMMs on the fp32 matrix cores
+    else:  # the fp32 GEMMs (split-bf16 by default: bound a sixth of the bf16 peak)
+        split = os.environ.get("GEMMA_HIP_GEMM_F32") != "mfma"
+        peak = BF16_PEAK_TFLOPS / 6 if split else FP32_PEAK_TFLOPS
         prefill.update(fp32_tflops=round(pf_ops / t_pf / 1e12, 1),
-                       fp32_frac=round(pf_ops / t_pf / 1e12 / FP32_PEAK_TFLOPS, 4))
+                       fp32_frac=round(pf_ops / t_pf / 1e12 / peak, 4))
     gb = gemv_bytes if quant else gemv_f32_bytes
     per_layer = (gb(q_sz + 2 * kv_sz, c["dim"]) + gb(c["dim"], q_sz)
                  + gb(2 * c["mlp_dim"], c["dim"]) + gb(c["dim"], c["mlp_dim"]))

@@ -427,7 +427,14 @@ def check_f32(got, mat, src, oracle):
     assert np.all(err <= TOL_F32 * mag), f"worst relative error {worst:.3e}"
 
 
-def test_f32_golden(gh, golden, oracle):
+# The fp32 GEMM has two kernels: split-bf16 on the bf16 matrix cores (the
+# default) and fp32 MFMA (GEMMA_HIP_GEMM_F32=mfma); both are held to TOL_F32.
+F32_KERNELS = ["split", "mfma"]
+
+
+@pytest.mark.parametrize("kern", F32_KERNELS)
+def test_f32_golden(gh, golden, oracle, monkeypatch, kern):
+    monkeypatch.setenv("GEMMA_HIP_GEMM_F32", kern)
     g = golden("fpx")
     n, k = g["gemv_w"].shape
     y = torch.empty(n, dtype=torch.float32, device="cuda")
@@ -449,8 +456,10 @@ def test_f32_golden(gh, golden, oracle):
 @pytest.mark.parametrize("m,n,k", [(1, 6912, 1152), (1, 1152, 6912), (1, 32768, 2560),
                                    (64, 1152, 588), (300, 640, 2048), (4096, 1152, 588),
                                    (5, 7, 9), (2048, 8192, 64), (1000, 9000, 100)])
-def test_f32_vs_oracle(gh, oracle, m, n, k):
-    note(f"f32 m={m} n={n} k={k}")
+@pytest.mark.parametrize("kern", F32_KERNELS)
+def test_f32_vs_oracle(gh, oracle, monkeypatch, kern, m, n, k):
+    monkeypatch.setenv("GEMMA_HIP_GEMM_F32", kern)
+    note(f"f32 {kern} m={m} n={n} k={k}")
     rng = np.random.default_rng(m + n + k)
     A = outlier_acts(rng, (m, k))
     B = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
