@@ -9,6 +9,7 @@
 // alike, so each of the 8 MFMA sub-steps pairs matching k.  The reference's
 // fp32 sum has no fixed order (vectorised, KC-chunked, gemma.c:3287-3299), so
 // parity for this path is a tolerance on |y - y_exact| / sum|a*b|.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 
@@ -135,15 +136,36 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(
 // column l%32; A and B fragments give lane l row l%32 and k 8 (l/32) .. + 7).
 // Per 32-float K step the workgroup splits its A and B rows once into three
 // bf16 planes each in LDS, while the next step's fp32 rows load into
-// registers; one buffer (60 KB at 128x128), two workgroups per CU.
-template <int WM, int WN>
+// registers; one buffer (60 KB at 128x128: two workgroups per CU), two
+// barriers per step.  Measured on the 4b prefill shapes and dropped: two
+// buffers with one barrier per step (16- or 32-float steps) ran 3-10%
+// slower at the same tiles.
+//
+// B comes as segments (F32Segs: q, k, v or gate, up side by side in the
+// output); each thread resolves the rows it loads to their segment once.
+// Split-K (SK, splits > 1): workgroup (x, y, z) computes K steps
+// [z nk / splits, (z + 1) nk / splits) of tile (x, y), stores its fp32
+// partial tile to the workspace, and counts itself in on the tile's counter;
+// the workgroup that arrives last sums the splits' partials in split order
+// (its own from registers), so the result does not depend on the order of
+// arrival, runs the epilogue and resets the counter.
+struct F32Split {
+  int splits;
+  int *ws;   // [tiles][splits][kThreads * WM * WN * 16] fp32 bits
+  int *cnt;  // [tiles], zero between launches
+};
+
+template <int WM, int WN, bool SK>
 __global__ __launch_bounds__(kThreads, 2) void gemm_bf3_kernel(
-    float *__restrict__ dst, int dstr, const float *__restrict__ mat, int mstr,
-    const float *__restrict__ src, int sstr, int m, int n, int k, F32Epilogue ep) {
+    float *__restrict__ dst, int dstr, F32Segs b, int mstr, const float *__restrict__ src,
+    int sstr, int m, int k, F32Epilogue ep, F32Split sk) {
   constexpr int kBM = 64 * WM, kBN = 64 * WN;
-  constexpr int BK = 32;      // floats of K per step
-  constexpr int RW = BK + 8;  // plane row (bf16): 8 consecutive rows in distinct banks
-  constexpr int HA = kBM / 32, HB = kBN / 32;  // rows per thread and step
+  constexpr int BK = 32;              // floats of K per step
+  constexpr int RW = BK + 8;          // plane row (bf16): 8 consecutive rows in distinct banks
+  constexpr int CPR = BK / 4;         // float4 chunks per row and step
+  constexpr int RPP = kThreads / CPR; // rows per load pass
+  constexpr int HA = kBM / RPP, HB = kBN / RPP;
+  static_assert(kBM % RPP == 0 && kBN % RPP == 0, "tile");
   __shared__ __attribute__((aligned(16))) uint16_t pa[3][kBM * RW];
   __shared__ __attribute__((aligned(16))) uint16_t pb[3][kBN * RW];
 
@@ -152,33 +174,42 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf3_kernel(
   const int wave = tid >> 6;
   const int wm = wave >> 1;
   const int wn = wave & 1;
+  const int n = b.end[b.nseg - 1];
   const int m0 = blockIdx.y * kBM;
   const int n0 = blockIdx.x * kBN;
-  const int ld_row = tid >> 3, ld_c = tid & 7;  // float4 chunk ld_c of rows ld_row + 32 h
+  const int ld_row = tid / CPR, ld_c = tid % CPR;  // chunk ld_c of rows ld_row + RPP h
+
+  // the B rows this thread loads (null past the last column)
+  const float *brow[HB];
+#pragma unroll
+  for (int h = 0; h < HB; ++h) {
+    const int gn = n0 + ld_row + RPP * h;
+    const int t = (b.nseg > 1 && gn >= b.end[0]) + (b.nseg > 2 && gn >= b.end[1]);
+    const int first = t == 0 ? 0 : t == 1 ? b.end[0] : b.end[1];
+    const float *w = t == 0 ? b.w[0] : t == 1 ? b.w[1] : b.w[2];
+    brow[h] = gn < n ? w + (size_t)(gn - first) * mstr : nullptr;
+  }
 
   v4f ra[HA], rb[HB];
   auto load = [&](int kt) {
     const int kb = kt * BK + 4 * ld_c;
 #pragma unroll
     for (int h = 0; h < HA; ++h) {
-      const int gm = m0 + ld_row + 32 * h;
+      const int gm = m0 + ld_row + RPP * h;
       ra[h] = (gm < m && kb < k)
                   ? *reinterpret_cast<const v4f *>(src + (size_t)gm * sstr + kb)
                   : v4f{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int h = 0; h < HB; ++h) {
-      const int gn = n0 + ld_row + 32 * h;
-      rb[h] = (gn < n && kb < k)
-                  ? *reinterpret_cast<const v4f *>(mat + (size_t)gn * mstr + kb)
-                  : v4f{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int h = 0; h < HB; ++h)
+      rb[h] = (brow[h] != nullptr && kb < k) ? *reinterpret_cast<const v4f *>(brow[h] + kb)
+                                             : v4f{0.f, 0.f, 0.f, 0.f};
   };
   auto split_store = [&]() {
 #pragma unroll
     for (int h = 0; h < HA; ++h) {
       const Bf3x2 lo = split3x2(ra[h][0], ra[h][1]), hi = split3x2(ra[h][2], ra[h][3]);
-      const int at = (ld_row + 32 * h) * RW + 4 * ld_c;
+      const int at = (ld_row + RPP * h) * RW + 4 * ld_c;
       *reinterpret_cast<u2 *>(&pa[0][at]) = u2{lo.q0, hi.q0};
       *reinterpret_cast<u2 *>(&pa[1][at]) = u2{lo.q1, hi.q1};
       *reinterpret_cast<u2 *>(&pa[2][at]) = u2{lo.q2, hi.q2};
@@ -186,7 +217,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf3_kernel(
 #pragma unroll
     for (int h = 0; h < HB; ++h) {
       const Bf3x2 lo = split3x2(rb[h][0], rb[h][1]), hi = split3x2(rb[h][2], rb[h][3]);
-      const int at = (ld_row + 32 * h) * RW + 4 * ld_c;
+      const int at = (ld_row + RPP * h) * RW + 4 * ld_c;
       *reinterpret_cast<u2 *>(&pb[0][at]) = u2{lo.q0, hi.q0};
       *reinterpret_cast<u2 *>(&pb[1][at]) = u2{lo.q1, hi.q1};
       *reinterpret_cast<u2 *>(&pb[2][at]) = u2{lo.q2, hi.q2};
@@ -199,16 +230,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf3_kernel(
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v16f{};
 
-  const int nk = (k + BK - 1) / BK;
   const int fr = lane & 31, half = lane >> 5;
-  load(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    split_store();
-    lds_barrier();  // the step's planes are complete
-    if (kt + 1 < nk) load(kt + 1);  // the next step's rows load during the MFMAs
+  auto mfmas = [&]() {
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
-      bf8 a[WM][3], b[WN][3];
+      bf8 a[WM][3], bb[WN][3];
 #pragma unroll
       for (int i = 0; i < WM; ++i) {
         const int at = (wm * 32 * WM + i * 32 + fr) * RW + 16 * s + 8 * half;
@@ -219,22 +245,77 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf3_kernel(
       for (int j = 0; j < WN; ++j) {
         const int at = (wn * 32 * WN + j * 32 + fr) * RW + 16 * s + 8 * half;
 #pragma unroll
-        for (int p = 0; p < 3; ++p) b[j][p] = *reinterpret_cast<const bf8 *>(&pb[p][at]);
+        for (int p = 0; p < 3; ++p) bb[j][p] = *reinterpret_cast<const bf8 *>(&pb[p][at]);
       }
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
           v16f c = acc[i][j];
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][2], b[j][0], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], b[j][1], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][2], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], b[j][0], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][1], c, 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][0], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][2], bb[j][0], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], bb[j][1], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], bb[j][2], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], bb[j][0], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], bb[j][1], c, 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], bb[j][0], c, 0, 0, 0);
         }
     }
+  };
+
+  const int nk = (k + BK - 1) / BK;
+  int kt0 = 0, kt1 = nk;
+  if constexpr (SK) {
+    kt0 = (int)((long)blockIdx.z * nk / sk.splits);
+    kt1 = (int)((long)(blockIdx.z + 1) * nk / sk.splits);
+  }
+  load(kt0);
+  for (int kt = kt0; kt < kt1; ++kt) {
+    split_store();
+    lds_barrier();  // the step's planes are complete
+    if (kt + 1 < kt1) load(kt + 1);  // the next step's rows load during the MFMAs
+    mfmas();
     lds_barrier();  // every wave is done with the planes
+  }
+
+  if constexpr (SK) {
+    // Partials go out and come back in with device-coherent (agent-scope)
+    // accesses, which write through and read past this XCD's L2.
+    constexpr int kTileInts = kThreads * WM * WN * 16;
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int z = blockIdx.z;
+    int *part = sk.ws + (size_t)tile * sk.splits * kTileInts;
+    int *mine = part + (size_t)z * kTileInts;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __hip_atomic_store(mine + ((i * WN + j) * 16 + r) * kThreads + tid,
+                             __float_as_int(acc[i][j][r]), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    __shared__ int last;
+    wait_vmcnt<0>();  // this thread's partial has reached the coherence point
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(sk.cnt + tile, 1) == sk.splits - 1;
+    __syncthreads();
+    if (!last) return;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int at = ((i * WN + j) * 16 + r) * kThreads + tid;
+          float t = 0.f;
+          for (int o = 0; o < sk.splits; ++o)
+            t += o == z ? acc[i][j][r]
+                        : __int_as_float(__hip_atomic_load(part + (size_t)o * kTileInts + at,
+                                                           __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT));
+          acc[i][j][r] = t;
+        }
+    if (tid == 0) sk.cnt[tile] = 0;
   }
 
 #pragma unroll
@@ -250,6 +331,29 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_bf3_kernel(
         if (row < m) dst[(size_t)row * dstr + col] = ep.apply(acc[i][j][r], row, col, dstr);
       }
   }
+}
+
+// One launch of the split kernel: tiles of (64 WM) x (64 WN), `splits`
+// workgroups per tile along z (1: no split-K).
+template <int WM, int WN>
+hipError_t launch_bf3(float *dst, int dstr, const F32Segs &b, int mstr, const float *src,
+                      int sstr, int m, int k, const F32Epilogue &ep, int splits,
+                      hipStream_t stream) {
+  const int n = b.end[b.nseg - 1];
+  const dim3 grid((n + 64 * WN - 1) / (64 * WN), (m + 64 * WM - 1) / (64 * WM), splits);
+  F32Split sk{splits, nullptr, nullptr};
+  if (splits > 1) {
+    const int tiles = (int)(grid.x * grid.y);
+    const hipError_t e = split_workspace(
+        stream, (size_t)tiles * splits * kThreads * WM * WN * 16, tiles, &sk.ws, &sk.cnt);
+    if (e != hipSuccess) return e;
+    gemm_bf3_kernel<WM, WN, true><<<grid, kThreads, 0, stream>>>(dst, dstr, b, mstr, src, sstr,
+                                                                m, k, ep, sk);
+  } else {
+    gemm_bf3_kernel<WM, WN, false><<<grid, kThreads, 0, stream>>>(dst, dstr, b, mstr, src, sstr,
+                                                                 m, k, ep, sk);
+  }
+  return hipGetLastError();
 }
 
 // Any shape, any alignment: one thread per output.
@@ -322,11 +426,67 @@ bool gemm_f32_split() {
   return e == nullptr || strcmp(e, "mfma") != 0;
 }
 
+// Block tile.  The fp32-MFMA kernel: 128x128 when that gives every CU at
+// least two workgroups, else 64x64 (k/v, o and down at the gemma-3-4b prefill
+// shapes leave most of the GPU idle at 128x128).  The split kernel (two
+// 128x128 or three 128x64 workgroups per CU): 128x128 from four 128x128
+// tiles per CU, else 128x64 (128 rows) from two of those per CU, else 64x64;
+// at the 4b prefill shapes q 165 -> 150 us and down 780 -> 735 against the
+// fp32-MFMA kernel's rule.  GEMMA_HIP_GEMM_F32_TILE=128, 128x64 or 64
+// (read at every launch) forces one for either kernel.
+enum Tile { kTile64, kTile128x64, kTile128 };
+Tile pick_tile(int m, int n, bool split, const DeviceInfo &dev) {
+  const char *e = getenv("GEMMA_HIP_GEMM_F32_TILE");
+  if (e != nullptr && strcmp(e, "128") == 0) return kTile128;
+  if (e != nullptr && strcmp(e, "128x64") == 0) return kTile128x64;
+  if (e != nullptr && strcmp(e, "64") == 0) return kTile64;
+  const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+  const long tiles128x64 = (long)((m + 127) / 128) * ((n + 63) / 64);
+  if (!split) return tiles128 >= 2L * dev.cus ? kTile128 : kTile64;
+  return tiles128 >= 4L * dev.cus ? kTile128 : tiles128x64 >= 2L * dev.cus ? kTile128x64 : kTile64;
+}
+
+// Split-K ways of the split kernel: none when the tiles give every CU two
+// workgroups, else enough for ~3 per CU, each split at least 8 K steps (256
+// floats), at most 16.  GEMMA_HIP_GEMM_F32_SPLIT=s (read at every launch)
+// forces s (clamped to 1..min(16, K steps)).
+int bf3_splits(long tiles, int k, const DeviceInfo &dev) {
+  const int nk = (k + 31) / 32;
+  long s;
+  const char *e = getenv("GEMMA_HIP_GEMM_F32_SPLIT");
+  if (e != nullptr)
+    s = atoi(e);
+  else if (tiles >= 2L * dev.cus)
+    s = 1;
+  else
+    s = std::min((3L * dev.cus + tiles - 1) / tiles, (long)(nk / 8));
+  return (int)std::max(1L, std::min({s, (long)nk, 16L}));
+}
+
+hipError_t launch_bf3_auto(float *dst, int dstr, const F32Segs &b, int mstr, const float *src,
+                           int sstr, int m, int k, const F32Epilogue &ep, const DeviceInfo &dev,
+                           hipStream_t stream) {
+  const int n = b.end[b.nseg - 1];
+  const Tile tile = pick_tile(m, n, true, dev);
+  const int bm = tile == kTile64 ? 64 : 128, bn = tile == kTile128 ? 128 : 64;
+  const long tiles = (long)((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+  const int splits = bf3_splits(tiles, k, dev);
+  if (tile == kTile128)
+    return launch_bf3<2, 2>(dst, dstr, b, mstr, src, sstr, m, k, ep, splits, stream);
+  if (tile == kTile128x64)
+    return launch_bf3<2, 1>(dst, dstr, b, mstr, src, sstr, m, k, ep, splits, stream);
+  return launch_bf3<1, 1>(dst, dstr, b, mstr, src, sstr, m, k, ep, splits, stream);
+}
+
+// float4 loads of both operands: K and the row strides multiples of 4
+// floats, the bases 16-byte aligned.
+bool f32_vec4(int k, int mstr, int sstr, const float *mat, const float *src) {
+  return k % 4 == 0 && mstr % 4 == 0 && sstr % 4 == 0 && (uintptr_t)mat % 16 == 0 &&
+         (uintptr_t)src % 16 == 0;
+}
+
 }  // namespace
 
-// Block tile: 128x128 when that gives every CU at least two workgroups,
-// else 64x64 (k/v, o and down at the gemma-3-4b prefill shapes leave most of
-// the GPU idle at 128x128).  GEMMA_HIP_GEMM_F32_TILE=128 or 64 forces one.
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const float *src, int sstr, int m, int n, int k,
                            const F32Epilogue &ep, const DeviceInfo &dev, hipStream_t stream,
@@ -336,32 +496,24 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
     gemm_f64_kernel<<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m, n, k, ep);
     return hipGetLastError();
   }
-  const bool fast = k % 4 == 0 && mstr % 4 == 0 && sstr % 4 == 0 &&
-                    (uintptr_t)mat % 16 == 0 && (uintptr_t)src % 16 == 0;
-  if (fast) {
-    static const int forced = [] {
-      const char *e = getenv("GEMMA_HIP_GEMM_F32_TILE");
-      return e != nullptr ? atoi(e) : 0;
-    }();
-    const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
-    const bool big = forced == 128 || (forced != 64 && tiles128 >= 2L * dev.cus);
-    const bool split = gemm_f32_split();
-    if (big) {
+  if (f32_vec4(k, mstr, sstr, mat, src)) {
+    if (gemm_f32_split()) {
+      const F32Segs b{{mat, nullptr, nullptr}, {n, n, n}, 1};
+      return launch_bf3_auto(dst, dstr, b, mstr, src, sstr, m, k, ep, dev, stream);
+    }
+    const Tile tile = pick_tile(m, n, false, dev);
+    if (tile == kTile128) {
       const dim3 grid((n + 127) / 128, (m + 127) / 128);
-      if (split)
-        gemm_bf3_kernel<2, 2><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
-                                                            n, k, ep);
-      else
-        gemm_f32_kernel<2, 2><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
-                                                            n, k, ep);
+      gemm_f32_kernel<2, 2><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
+                                                          n, k, ep);
+    } else if (tile == kTile128x64) {
+      const dim3 grid((n + 63) / 64, (m + 127) / 128);
+      gemm_f32_kernel<2, 1><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
+                                                          n, k, ep);
     } else {
       const dim3 grid((n + 63) / 64, (m + 63) / 64);
-      if (split)
-        gemm_bf3_kernel<1, 1><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
-                                                            n, k, ep);
-      else
-        gemm_f32_kernel<1, 1><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
-                                                            n, k, ep);
+      gemm_f32_kernel<1, 1><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
+                                                          n, k, ep);
     }
   } else {
     const dim3 grid((n + 63) / 64, (m + 3) / 4);
@@ -369,6 +521,29 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                                                            src, sstr, m, n, k, ep);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_f32_segs(float *dst, int dstr, const F32Segs &b, int mstr,
+                                const float *src, int sstr, int m, int k,
+                                const F32Epilogue &ep, const DeviceInfo &dev, hipStream_t stream,
+                                bool f64) {
+  bool vec4 = true;
+  for (int t = 0; t < b.nseg; ++t) vec4 = vec4 && f32_vec4(k, mstr, sstr, b.w[t], src);
+  if (!f64 && vec4 && gemm_f32_split())
+    return launch_bf3_auto(dst, dstr, b, mstr, src, sstr, m, k, ep, dev, stream);
+  // one launch per segment, the epilogue's column-indexed inputs shifted
+  // to the segment's first column
+  for (int t = 0; t < b.nseg; ++t) {
+    const int first = t ? b.end[t - 1] : 0;
+    F32Epilogue et = ep;
+    if (et.bias != nullptr) et.bias += first;
+    if (et.pos_q != nullptr) et.pos_q += first;
+    if (et.pos_f != nullptr) et.pos_f += first;
+    const hipError_t e = launch_gemm_f32(dst + first, dstr, b.w[t], mstr, src, sstr, m,
+                                         b.end[t] - first, k, et, dev, stream, f64);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,

@@ -317,12 +317,6 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[WM][WN],
 // kt+S-1 into the slot step kt-1 used, then compute step kt.
 
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
-}
-
 template <int kPerWave, int kMaxAhead>
 __device__ __forceinline__ void wait_ahead(int ahead) {
   // ahead in [0, kMaxAhead]: loads still allowed in flight = ahead*kPerWave
@@ -1104,6 +1098,14 @@ hipError_t split_ws(hipStream_t stream, size_t ws_ints, int ncnt, SplitK *sk) {
 }
 
 }  // namespace
+
+hipError_t split_workspace(hipStream_t stream, size_t ws_ints, int ncnt, int **ws, int **cnt) {
+  SplitK sk{};
+  const hipError_t e = split_ws(stream, ws_ints, ncnt, &sk);
+  *ws = sk.ws;
+  *cnt = sk.cnt;
+  return e;
+}
 
 hipError_t gemm_scratch_init(int device) {
   if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;

@@ -649,6 +649,36 @@ int gemma_hip_matmul_cols(float *dst, int dstr, const gemma_hip_job *jobs, int n
   return 0;
 }
 
+int gemma_hip_matmul_f32_cols(float *dst, int dstr, const gemma_hip_job *jobs, int njobs,
+                              const float *src, int sstr, int m, int k, void *stream) {
+  const char *name = "gemma_hip_matmul_f32_cols";
+  if (need_init()) return 1;
+  if (jobs == nullptr || njobs < 1 || njobs > gh::kMaxGemmSegs)
+    return fail("%s: njobs=%d outside 1..%d", name, njobs, gh::kMaxGemmSegs);
+  gh::F32Segs bs{};
+  long n = 0;
+  for (int j = 0; j < njobs; ++j) {
+    if (jobs[j].m <= 0) return fail("%s: job %d has m=%d rows", name, j, jobs[j].m);
+    if (jobs[j].w == nullptr) return fail("%s: job %d has a null weight pointer", name, j);
+    n += jobs[j].m;
+    if (n > (1l << 30)) return fail("%s: %ld output columns", name, n);
+    bs.w[j] = static_cast<const float *>(jobs[j].w);
+    bs.end[j] = (int)n;
+  }
+  bs.nseg = njobs;
+  if (dstr == 0) dstr = (int)n;
+  if (sstr == 0) sstr = k;
+  if (check_matmul_shape(name, m, (int)n, k, dstr, k, sstr)) return 1;
+  if (m == 0) return 0;
+  if (!dst || !src) return fail("%s: null pointer", name);
+  hipStream_t s = pick_stream(stream);
+  PerfScope perf(kOpGemmFpx, s);
+  GH_CHECK("gemma_hip_matmul_f32_cols: launch",
+           gh::launch_gemm_f32_segs(dst, dstr, bs, k, src, sstr, m, k, gh::F32Epilogue{},
+                                    g.info, s, false));
+  return 0;
+}
+
 int gemma_hip_matmul_heads(float *dst, const int8_t *mat, const float *matsc,
                            const int8_t *src, const float *ssc, int m,
                            int heads, int hdim, int k, void *stream) {
@@ -1471,6 +1501,12 @@ hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed,
     return GH_OP(kOpGemmFpx, gh::launch_gemm_f32(dst, dstr, w, k, src, sstr, n, nout, k, nullptr,
                                                  false, g.info, st));
   };
+  // adjacent output columns from several weight matrices of one K: one launch
+  auto gemm_cols = [&](float *dst, int dstr, const gh::F32Segs &b, const float *src, int sstr,
+                       int k) {
+    return GH_OP(kOpGemmFpx, gh::launch_gemm_f32_segs(dst, dstr, b, k, src, sstr, n, k,
+                                                      gh::F32Epilogue{}, g.info, st, false));
+  };
   if (embed && (e = gh::launch_pf_embed(d->pf_tok, n, nullptr, nullptr, d->emb_f, d->pf_x, dim,
                                         c.mlp_pre ? 1.0f : sqrtf((float)dim), st)) != hipSuccess)
     return e;
@@ -1481,11 +1517,8 @@ hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed,
                   dim, c.eps, d->pf_h};
     if ((e = GH_OP(kOpRmsnorm, gh::launch_pf_norm_rows(n1, n, st))) != hipSuccess) return e;
     // q, k, v into the fused rows (gemma.c:5079)
-    if ((e = gemm(d->pf_qkv, stride, L.wf[0], q_sz, d->pf_h, dim, dim)) != hipSuccess ||
-        (e = gemm(d->pf_qkv + q_sz, stride, L.wf[1], kv_sz, d->pf_h, dim, dim)) != hipSuccess ||
-        (e = gemm(d->pf_qkv + q_sz + kv_sz, stride, L.wf[2], kv_sz, d->pf_h, dim, dim)) !=
-            hipSuccess)
-      return e;
+    const gh::F32Segs qkv{{L.wf[0], L.wf[1], L.wf[2]}, {q_sz, q_sz + kv_sz, stride}, 3};
+    if ((e = gemm_cols(d->pf_qkv, stride, qkv, d->pf_h, dim, dim)) != hipSuccess) return e;
     const bool sliding = d->swa[l] != 0;
     float *kc = d->kv + (size_t)l * 2 * cache;
     const gh::PfRope rp{d->pf_qkv, stride, q_sz, c.qk_norm ? L.nq : nullptr,
@@ -1505,8 +1538,8 @@ hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed,
                         nullptr, nullptr, dim, c.eps, d->pf_h};
     if ((e = GH_OP(kOpRmsnorm, gh::launch_pf_norm_rows(n3, n, st))) != hipSuccess) return e;
     // gate (w2) and up (w1) side by side in pf_g (gemma.c:5358), GELU, down (5384)
-    if ((e = gemm(d->pf_g, 2 * mlp, L.wf[5], mlp, d->pf_h, dim, dim)) != hipSuccess ||
-        (e = gemm(d->pf_g + mlp, 2 * mlp, L.wf[4], mlp, d->pf_h, dim, dim)) != hipSuccess ||
+    const gh::F32Segs gu{{L.wf[5], L.wf[4], nullptr}, {mlp, 2 * mlp, 2 * mlp}, 2};
+    if ((e = gemm_cols(d->pf_g, 2 * mlp, gu, d->pf_h, dim, dim)) != hipSuccess ||
         (e = GH_OP(kOpGelu, gh::launch_gelu_mul_rows(d->pf_g, n, mlp, st))) != hipSuccess ||
         (e = gemm(d->pf_y, dim, L.wf[6], dim, d->pf_g, 2 * mlp, mlp)) != hipSuccess)
       return e;
@@ -2128,9 +2161,10 @@ hipError_t vision_enqueue_f32(gemma_hip_vision *v, hipStream_t st) {
     const gh::VisLn n1{v->x, l > 0 ? v->y : nullptr, l > 0 ? v->layers[l - 1].b2 : nullptr,
                        L.n1, L.n1b, nullptr, nullptr, v->hln, dim, c.eps};
     if ((e = GH_OP(kOpLayernorm, gh::launch_vis_ln_rows(n1, n, st))) != hipSuccess) return e;
-    if ((e = gemm(v->qkv, 3 * dim, L.wf[0], n, dim, v->hln, dim, dim)) != hipSuccess ||
-        (e = gemm(v->qkv + dim, 3 * dim, L.wf[1], n, dim, v->hln, dim, dim)) != hipSuccess ||
-        (e = gemm(v->qkv + 2 * dim, 3 * dim, L.wf[2], n, dim, v->hln, dim, dim)) != hipSuccess)
+    const gh::F32Segs qkv{{L.wf[0], L.wf[1], L.wf[2]}, {dim, 2 * dim, 3 * dim}, 3};
+    if ((e = GH_OP(kOpGemmFpx, gh::launch_gemm_f32_segs(v->qkv, 3 * dim, qkv, dim, v->hln, dim,
+                                                        n, dim, gh::F32Epilogue{}, g.info, st,
+                                                        f64))) != hipSuccess)
       return e;
     const gh::VisAttn at{v->qkv, 3 * dim, L.bqkv, v->att, n, c.n_heads, dim,
                          1.0f / sqrtf((float)v->hdim)};

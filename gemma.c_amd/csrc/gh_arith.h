@@ -123,6 +123,14 @@ __device__ __forceinline__ uint32_t pack4(int32_t a, int32_t b, int32_t c,
          ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
 }
 
+// s_waitcnt vmcnt(N): at most N of this wave's vector memory operations
+// still outstanding (lgkmcnt and expcnt not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // Workgroup barrier for LDS traffic only: this wave's LDS operations are
 // complete (lgkmcnt(0)) before the barrier, and nothing moves across it.
 // __syncthreads() also waits for the wave's outstanding global loads

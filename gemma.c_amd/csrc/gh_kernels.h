@@ -133,6 +133,27 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
                            const F32Epilogue &ep, const DeviceInfo &dev, hipStream_t stream,
                            bool f64);
 
+// B as up to kMaxGemmSegs separate fp32 [rows][mstr] matrices whose outputs
+// are adjacent column ranges of one dst (q, k, v; or gate, up): segment t
+// holds output columns [end[t-1], end[t]) (end[-1] = 0).  The split-bf16
+// kernel runs all segments in one launch (split-K when its tiles leave CUs
+// idle); the fp32-MFMA and fp64 kernels run one launch per segment.
+struct F32Segs {
+  const float *w[kMaxGemmSegs];
+  int end[kMaxGemmSegs];
+  int nseg;
+};
+hipError_t launch_gemm_f32_segs(float *dst, int dstr, const F32Segs &b, int mstr,
+                                const float *src, int sstr, int m, int k,
+                                const F32Epilogue &ep, const DeviceInfo &dev, hipStream_t stream,
+                                bool f64);
+
+// gemm_i8.hip: the split-K workspace of (device, stream) with at least
+// ws_ints ints of partials and ncnt tile counters (zero between launches;
+// each launch must leave them at zero), grown on demand (the stream is
+// synchronized first, so not while it is being captured).
+hipError_t split_workspace(hipStream_t stream, size_t ws_ints, int ncnt, int **ws, int **cnt);
+
 // patch.hip: a [npatch][3*psize*psize] = patches of the HWC image, in the K
 // order of the SigLIP patch-embedding weight [dim][3][psize][psize].
 hipError_t launch_im2col(float *a, const float *img, int img_px, int psize,

@@ -151,6 +151,7 @@ _SIGS = {
     "gemma_hip_matmul_multi": (_I, [ctypes.POINTER(Job), _I, _P, _P, _I, _P]),
     "gemma_hip_quantize_matmul": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P, _P, _P]),
     "gemma_hip_matmul_f32": (_I, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
+    "gemma_hip_matmul_f32_cols": (_I, [_P, _I, ctypes.POINTER(Job), _I, _P, _I, _I, _I, _P]),
     "gemma_hip_matmul_f32_multi": (_I, [ctypes.POINTER(Job), _I, _P, _I, _P]),
     "gemma_hip_quantize_act_host": (_I, [_P, _P, _P, _I]),
     "gemma_hip_quantize_acts_host": (_I, [_P, _P, _P, _I, _I, _I]),
@@ -295,6 +296,12 @@ class GemmaHip:
     def matmul_f32(self, dst, dstr, mat, mstr, src, sstr, m, n, k, stream=None):
         self._check(self.lib.gemma_hip_matmul_f32(_addr(dst), dstr, _addr(mat), mstr,
                                                   _addr(src), sstr, m, n, k, stream))
+
+    def matmul_f32_cols(self, dst, dstr, specs, src, sstr, m, k, stream=None):
+        """specs: (w, rows) per job; job j fills the next rows columns."""
+        arr, n = self.jobs((w, None, None, rows) for w, rows in specs)
+        self._check(self.lib.gemma_hip_matmul_f32_cols(_addr(dst), dstr, arr, n, _addr(src),
+                                                       sstr, m, k, stream))
 
     def matmul_f32_multi(self, specs, x, k, stream=None):
         arr, n = self.jobs(specs)

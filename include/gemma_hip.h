@@ -214,6 +214,17 @@ int gemma_hip_matmul_f32(float *dst, int dstr, const float *mat, int mstr,
                          const float *src, int sstr, int m, int n, int k,
                          void *stream);
 
+/* gemm_fpx (gemma.c:3304-3399) of one fp32 activation block against several
+ * fp32 weight matrices that share its K, as the unquantized prompt pass's
+ * adjacent call sites issue them (q, k and v at gemma.c:5079; gate and up at
+ * 5358): the fp32 form of gemma_hip_matmul_cols.  Job j (j < njobs <= 3)
+ * holds fp32 [jobs[j].m][k] dense weights jobs[j].w and fills dst columns
+ * [c_j, c_j + jobs[j].m), c_j the sum of the earlier jobs' m; jobs[j].sc and
+ * jobs[j].dst are not used.  src fp32 [m][sstr], dst fp32 [m][dstr] (0
+ * strides: dense).  Same tolerance as gemma_hip_matmul_f32. */
+int gemma_hip_matmul_f32_cols(float *dst, int dstr, const gemma_hip_job *jobs, int njobs,
+                              const float *src, int sstr, int m, int k, void *stream);
+
 /* gemv_fpx_multi (gemma.c:2839-2858). */
 int gemma_hip_matmul_f32_multi(const gemma_hip_job *jobs, int njobs,
                                const float *x, int k, void *stream);

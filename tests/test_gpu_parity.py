@@ -469,6 +469,69 @@ def test_f32_vs_oracle(gh, oracle, monkeypatch, kern, m, n, k):
     check_f32(host(d)[rows], B, A[rows], oracle)
 
 
+# Every block tile of both kernels (GEMMA_HIP_GEMM_F32_TILE forces one) on
+# shapes with tails in every dimension.
+@pytest.mark.parametrize("tile", ["128", "128x64", "64"])
+@pytest.mark.parametrize("kern", F32_KERNELS)
+@pytest.mark.parametrize("m,n,k", [(1000, 900, 100), (130, 70, 36)])
+def test_f32_tiles(gh, oracle, monkeypatch, kern, tile, m, n, k):
+    monkeypatch.setenv("GEMMA_HIP_GEMM_F32", kern)
+    monkeypatch.setenv("GEMMA_HIP_GEMM_F32_TILE", tile)
+    note(f"f32 {kern} tile {tile} m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * n + k)
+    A = outlier_acts(rng, (m, k))
+    B = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    d = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.matmul_f32(d, n, dev(B), k, dev(A), k, m, n, k, stream())
+    check_f32(host(d), B, A, oracle)
+
+
+# Several weight matrices side by side in one output (gemma_hip_matmul_f32_cols;
+# the split kernel runs them in one launch, the fp32-MFMA one per matrix):
+# the 1b prompt pass's q|k|v and gate|up at M=512 (split-K and 128x64 tiles)
+# and ragged segments whose boundaries cut through tiles.
+@pytest.mark.parametrize("kern", F32_KERNELS)
+@pytest.mark.parametrize("m,rows,k", [(512, (1024, 256, 256), 1152), (300, (6912, 6912), 1152),
+                                      (77, (100, 37, 5), 36), (130, (64,), 260)])
+def test_f32_cols(gh, oracle, monkeypatch, kern, m, rows, k):
+    monkeypatch.setenv("GEMMA_HIP_GEMM_F32", kern)
+    note(f"f32 cols {kern} m={m} rows={rows} k={k}")
+    rng = np.random.default_rng(m + sum(rows) + k)
+    A = outlier_acts(rng, (m, k))
+    Bs = [(rng.standard_normal((r, k)) * 0.02).astype(np.float32) for r in rows]
+    n = sum(rows)
+    d = torch.full((m, n + 3), 7.0, dtype=torch.float32, device="cuda")
+    gh.matmul_f32_cols(d, n + 3, [(dev(B), r) for B, r in zip(Bs, rows)], dev(A), k, m, k,
+                       stream())
+    got = host(d)
+    pick = np.unique(rng.integers(0, m, min(m, 48)))
+    check_f32(got[pick, :n], np.concatenate(Bs), A[pick], oracle)
+    assert np.all(got[:, n:] == 7.0)
+
+
+# Split-K of the split kernel (GEMMA_HIP_GEMM_F32_SPLIT forces the ways;
+# by default it runs when the tiles leave CUs idle, as at the 1b down shape
+# M=512 N=1152 K=6912): within TOL_F32 at every split, and the partials are
+# summed in split order, so a repeated launch is bit-identical.
+@pytest.mark.parametrize("splits", [None, 2, 3, 7, 16])
+@pytest.mark.parametrize("m,n,k", [(512, 1152, 6912), (130, 70, 100), (64, 640, 2048)])
+def test_f32_split_k(gh, oracle, monkeypatch, splits, m, n, k):
+    if splits is not None:
+        monkeypatch.setenv("GEMMA_HIP_GEMM_F32_SPLIT", str(splits))
+    note(f"f32 split-k {splits} m={m} n={n} k={k}")
+    rng = np.random.default_rng(m + n + k + (splits or 0))
+    A = outlier_acts(rng, (m, k))
+    B = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    d = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    gh.matmul_f32(d, n, dev(B), k, dev(A), k, m, n, k, stream())
+    first = host(d)
+    pick = np.unique(rng.integers(0, m, min(m, 48)))
+    check_f32(first[pick], B, A[pick], oracle)
+    d.fill_(0.0)
+    gh.matmul_f32(d, n, dev(B), k, dev(A), k, m, n, k, stream())
+    assert np.array_equal(bits(host(d)), bits(first))
+
+
 def test_f32_multi(gh, oracle):
     rng = np.random.default_rng(3)
     k = 1152
