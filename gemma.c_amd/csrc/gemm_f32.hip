@@ -426,56 +426,92 @@ bool gemm_f32_split() {
   return e == nullptr || strcmp(e, "mfma") != 0;
 }
 
-// Block tile.  The fp32-MFMA kernel: 128x128 when that gives every CU at
-// least two workgroups, else 64x64 (k/v, o and down at the gemma-3-4b prefill
-// shapes leave most of the GPU idle at 128x128).  The split kernel (two
-// 128x128 or three 128x64 workgroups per CU): 128x128 from four 128x128
-// tiles per CU, else 128x64 (128 rows) from two of those per CU, else 64x64;
-// at the 4b prefill shapes q 165 -> 150 us and down 780 -> 735 against the
-// fp32-MFMA kernel's rule.  GEMMA_HIP_GEMM_F32_TILE=128, 128x64 or 64
-// (read at every launch) forces one for either kernel.
+// Block tile of the fp32-MFMA kernel: 128x128 when that gives every CU at
+// least two workgroups, else 64x64 (k/v, o and down at the gemma-3-4b
+// prefill shapes leave most of the GPU idle at 128x128).
+// GEMMA_HIP_GEMM_F32_TILE=128, 128x64 or 64 (read at every launch) forces a
+// tile for either kernel.
 enum Tile { kTile64, kTile128x64, kTile128 };
-Tile pick_tile(int m, int n, bool split, const DeviceInfo &dev) {
+bool forced_tile(Tile *t) {
   const char *e = getenv("GEMMA_HIP_GEMM_F32_TILE");
-  if (e != nullptr && strcmp(e, "128") == 0) return kTile128;
-  if (e != nullptr && strcmp(e, "128x64") == 0) return kTile128x64;
-  if (e != nullptr && strcmp(e, "64") == 0) return kTile64;
-  const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
-  const long tiles128x64 = (long)((m + 127) / 128) * ((n + 63) / 64);
-  if (!split) return tiles128 >= 2L * dev.cus ? kTile128 : kTile64;
-  return tiles128 >= 4L * dev.cus ? kTile128 : tiles128x64 >= 2L * dev.cus ? kTile128x64 : kTile64;
+  if (e == nullptr) return false;
+  if (strcmp(e, "128") == 0) *t = kTile128;
+  else if (strcmp(e, "128x64") == 0) *t = kTile128x64;
+  else if (strcmp(e, "64") == 0) *t = kTile64;
+  else return false;
+  return true;
 }
 
-// Split-K ways of the split kernel: none when the tiles give every CU two
-// workgroups, else enough for ~3 per CU, each split at least 8 K steps (256
-// floats), at most 16.  GEMMA_HIP_GEMM_F32_SPLIT=s (read at every launch)
-// forces s (clamped to 1..min(16, K steps)).
-int bf3_splits(long tiles, int k, const DeviceInfo &dev) {
+Tile f32_tile(int m, int n, const DeviceInfo &dev) {
+  Tile t;
+  if (forced_tile(&t)) return t;
+  const long tiles128 = (long)((m + 127) / 128) * ((n + 127) / 128);
+  return tiles128 >= 2L * dev.cus ? kTile128 : kTile64;
+}
+
+long tile_count(int m, int n, Tile t) {
+  const int bm = t == kTile64 ? 64 : 128, bn = t == kTile128 ? 128 : 64;
+  return (long)((m + bm - 1) / bm) * ((n + bn - 1) / bn);
+}
+
+// Tile and split-K ways of the split kernel (two 128x128, three 128x64 or
+// four 64x64 workgroups per CU), from a sweep of the gemma-3 prefill and
+// SigLIP shapes (M = 512, 2048, 4096; T = the count of 128x128 tiles):
+//   T >= 1.5 per CU:           128x128, no split
+//   T >= 1 per CU:             128x128 in 3 splits when K >= 3072 floats
+//                              (4b down 743 -> 604 us, SigLIP fc2 315 -> 285);
+//                              else 128x128 in 2 when those fill two per CU
+//                              to within 10% (4b q 166 -> 140), else 128x64
+//                              in 2 (4b o 147)
+//   128x64 tiles >= 1 per CU:  128x64 in 2 (4b k/v 89 -> 83)
+//   fewer:                     64x64, splits for ~1.5 workgroups per CU
+//                              (1b down at M=512: 3 splits, 86 us; 6: 92)
+// Each split keeps at least 8 K steps (256 floats); at most 16 splits.
+// GEMMA_HIP_GEMM_F32_TILE forces the tile (the split then follows the last
+// rule for that tile's count), GEMMA_HIP_GEMM_F32_SPLIT=s the splits
+// (clamped to 1..min(16, K steps)); both are read at every launch.
+struct Bf3Plan {
+  Tile tile;
+  int splits;
+};
+Bf3Plan bf3_plan(int m, int n, int k, const DeviceInfo &dev) {
   const int nk = (k + 31) / 32;
-  long s;
+  Bf3Plan p{kTile64, 1};
+  const long t128 = tile_count(m, n, kTile128);
+  if (forced_tile(&p.tile)) {
+    const long t = tile_count(m, n, p.tile);
+    p.splits = t >= dev.cus ? 1 : (int)((3L * dev.cus + 2 * t - 1) / (2 * t));
+  } else if (2 * t128 >= 3L * dev.cus) {
+    p = {kTile128, 1};
+  } else if (t128 >= dev.cus) {
+    if (nk >= 96)
+      p = {kTile128, 3};
+    else if (10 * t128 <= 11L * dev.cus)
+      p = {kTile128, 2};
+    else
+      p = {kTile128x64, 2};
+  } else if (tile_count(m, n, kTile128x64) >= dev.cus) {
+    p = {kTile128x64, 2};
+  } else {
+    const long t = tile_count(m, n, kTile64);
+    p = {kTile64, (int)((3L * dev.cus + 2 * t - 1) / (2 * t))};
+  }
+  p.splits = std::min(p.splits, std::max(1, nk / 8));
   const char *e = getenv("GEMMA_HIP_GEMM_F32_SPLIT");
-  if (e != nullptr)
-    s = atoi(e);
-  else if (tiles >= 2L * dev.cus)
-    s = 1;
-  else
-    s = std::min((3L * dev.cus + tiles - 1) / tiles, (long)(nk / 8));
-  return (int)std::max(1L, std::min({s, (long)nk, 16L}));
+  if (e != nullptr) p.splits = atoi(e);
+  p.splits = std::max(1, std::min({p.splits, nk, 16}));
+  return p;
 }
 
 hipError_t launch_bf3_auto(float *dst, int dstr, const F32Segs &b, int mstr, const float *src,
                            int sstr, int m, int k, const F32Epilogue &ep, const DeviceInfo &dev,
                            hipStream_t stream) {
-  const int n = b.end[b.nseg - 1];
-  const Tile tile = pick_tile(m, n, true, dev);
-  const int bm = tile == kTile64 ? 64 : 128, bn = tile == kTile128 ? 128 : 64;
-  const long tiles = (long)((m + bm - 1) / bm) * ((n + bn - 1) / bn);
-  const int splits = bf3_splits(tiles, k, dev);
-  if (tile == kTile128)
-    return launch_bf3<2, 2>(dst, dstr, b, mstr, src, sstr, m, k, ep, splits, stream);
-  if (tile == kTile128x64)
-    return launch_bf3<2, 1>(dst, dstr, b, mstr, src, sstr, m, k, ep, splits, stream);
-  return launch_bf3<1, 1>(dst, dstr, b, mstr, src, sstr, m, k, ep, splits, stream);
+  const Bf3Plan p = bf3_plan(m, b.end[b.nseg - 1], k, dev);
+  if (p.tile == kTile128)
+    return launch_bf3<2, 2>(dst, dstr, b, mstr, src, sstr, m, k, ep, p.splits, stream);
+  if (p.tile == kTile128x64)
+    return launch_bf3<2, 1>(dst, dstr, b, mstr, src, sstr, m, k, ep, p.splits, stream);
+  return launch_bf3<1, 1>(dst, dstr, b, mstr, src, sstr, m, k, ep, p.splits, stream);
 }
 
 // float4 loads of both operands: K and the row strides multiples of 4
@@ -501,7 +537,7 @@ hipError_t launch_gemm_f32(float *dst, int dstr, const float *mat, int mstr,
       const F32Segs b{{mat, nullptr, nullptr}, {n, n, n}, 1};
       return launch_bf3_auto(dst, dstr, b, mstr, src, sstr, m, k, ep, dev, stream);
     }
-    const Tile tile = pick_tile(m, n, false, dev);
+    const Tile tile = f32_tile(m, n, dev);
     if (tile == kTile128) {
       const dim3 grid((n + 127) / 128, (m + 127) / 128);
       gemm_f32_kernel<2, 2><<<grid, kThreads, 0, stream>>>(dst, dstr, mat, mstr, src, sstr, m,
