@@ -282,6 +282,155 @@ __global__ __launch_bounds__(kNT) void dec_norm_stream_kernel(DecNorm na, GemvJo
   }
 }
 
+// The norm prologue + fp32 GEMV of the unquantized ('U') decode step
+// (forward_text_decode's !quant branches, gemma.c:4762-4768 and 4906-4915:
+// rmsnorm, then gemv_fpx_multi of q, k, v or of gate and up, then GELU(gate)
+// * up) in one launch, on gemv_f32_stream_kernel's schedule: an
+// all-resident grid deals groups of R = 64 / L rows to its waves round
+// robin; lane `sub` of a row takes 16-byte chunks sub, sub + L, ... in
+// `passes` passes of CPL chunks, fp32 FMAs in two chains, then the fixed
+// L-lane tree, the same sums as that kernel for the same L.  Every workgroup
+// computes the residual and norm itself (dec_final_norm_kernel's arithmetic)
+// into LDS as fp32, with its first weight loads issued before it; workgroup
+// 0 stores the new residual.
+//  GELU == false: rows are the flat row range of `jobs` (q, k, v).
+//  GELU == true:  group g covers outputs r = g R/2 .. g R/2 + R/2 - 1; row
+//                 rloc of the group is gate row r (jobs.w[0]) for even rloc
+//                 and up row r (jobs.w[1]) for odd, and the gate lanes store
+//                 gelu(gate) * up to jobs.dst[0][r] (jobs.end[0] = 2 x
+//                 outputs), rounded once as gelu_mul_rows_kernel does.
+// Loads are unconditional: a row past the end reads the job's last row and
+// a chunk past k reads chunk 0; neither is summed or stored.
+template <int L, int CPL, bool GELU, int NPT>
+__global__ __launch_bounds__(kNT) void dec_norm_f32_kernel(DecNorm na, GemvJobs jobs, int ngroups,
+                                                           int k, int passes) {
+  extern __shared__ v4f hf4[];
+  __shared__ double red[kWaves];
+  __shared__ float redf[kWaves];
+  __shared__ double etab[GELU ? 128 : 1];
+  hold_args(na);
+  hold_args(jobs);
+  asm volatile("" ::"s"(ngroups), "s"(k), "s"(passes));
+  const double etv = GELU ? kExp2Tab[threadIdx.x & 127] : 0.0;
+  const ExpConsts ec = exp_consts();
+  constexpr int R = 64 / L;
+  static_assert(!GELU || R >= 2, "gate and up rows must share a wave");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane % L, rloc = lane / L;
+  const int kc = k >> 2;
+  const int nwaves = gridDim.x * kWaves;
+  const int w0 = blockIdx.x * kWaves + wave;
+
+  int gend[kMaxJobs];  // groups up to the end of each job
+  {
+    int prev = 0, g = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxJobs; ++t) {
+      if (t < jobs.njobs) g += (jobs.end[t] - prev + R - 1) / R;
+      gend[t] = g;
+      prev = jobs.end[t];
+    }
+  }
+  struct At {
+    int job, row, out;  // job, row read (clamped), row of the output
+    bool ok;
+  };
+  auto where = [&](int g) {
+    At a;
+    if (GELU) {
+      const int m = jobs.end[0] >> 1;
+      a.out = g * (R / 2) + (rloc >> 1);
+      a.job = rloc & 1;
+      a.ok = g < ngroups && a.out < m;
+      a.row = a.ok ? a.out : m - 1;
+    } else {
+      int j = 0, gs = 0, rs = 0;
+#pragma unroll
+      for (int t = 0; t < kMaxJobs - 1; ++t)
+        if (t + 1 < jobs.njobs && g >= gend[t]) {
+          j = t + 1;
+          gs = gend[t];
+          rs = jobs.end[t];
+        }
+      const int m = pick4(jobs.end, j) - rs;
+      a.out = (g - gs) * R + rloc;
+      a.job = j;
+      a.ok = g < ngroups && a.out < m;
+      a.row = a.ok ? a.out : m - 1;
+    }
+    return a;
+  };
+  struct Slot {
+    v4f w[CPL];
+  };
+  auto load = [&](int g, int pass, Slot &s) {
+    const At a = where(g);
+    const gptr<const v4f> w4 =
+        as_global(static_cast<const v4f *>(pick4(jobs.w, a.job))) + (size_t)a.row * kc;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int c = sub + (pass * CPL + i) * L;
+      s.w[i] = __builtin_nontemporal_load(w4 + (c < kc ? c : 0));
+    }
+  };
+
+  const int mine = w0 < ngroups ? (ngroups - 1 - w0) / nwaves + 1 : 0;
+  const int items = mine * passes;
+  auto item_load = [&](int t, Slot &s) { load(w0 + (t / passes) * nwaves, t % passes, s); };
+
+  NormIn<NPT> in;
+  norm_load<NPT, kNT>(na, in);
+  Slot buf0, buf1;
+  item_load(0, buf0);
+  if (GELU && threadIdx.x < 128) etab[threadIdx.x] = etv;
+  norm_quant<NPT, kNT>(na, in, nullptr, red, redf);
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int c = threadIdx.x + j * kNT;
+    if (c < kc) hf4[c] = in.y[j];
+  }
+  lds_barrier();
+
+  float a0 = 0.0f, a1 = 0.0f;
+  auto item_sum = [&](int t, const Slot &s) {
+    const int pass = t % passes;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const int c = sub + (pass * CPL + u) * L;
+      if (c < kc) {
+        const v4f xv = hf4[c];
+        a0 = __builtin_fmaf(s.w[u].x, xv.x, a0);
+        a1 = __builtin_fmaf(s.w[u].y, xv.y, a1);
+        a0 = __builtin_fmaf(s.w[u].z, xv.z, a0);
+        a1 = __builtin_fmaf(s.w[u].w, xv.w, a1);
+      }
+    }
+    if (pass == passes - 1) {
+      const float acc = group_sum_f32<L>(a0 + a1);
+      const At a = where(w0 + (t / passes) * nwaves);
+      if (GELU) {
+        const float up = __shfl_xor(acc, L, 64);  // the up row's lanes
+        if (sub == 0 && (rloc & 1) == 0 && a.ok)
+          as_global(pick4(jobs.dst, 0))[a.out] =
+              (float)(gelu((double)acc, etab, ec) * (double)up);
+      } else if (sub == 0 && a.ok) {
+        as_global(pick4(jobs.dst, a.job))[a.out] = acc;
+      }
+      a0 = 0.0f;
+      a1 = 0.0f;
+    }
+  };
+  for (int t = 0; t < items; t += 2) {
+    item_load(t + 1, buf1);
+    item_sum(t, buf0);
+    if (t + 1 < items) {
+      item_load(t + 2, buf0);
+      item_sum(t + 1, buf1);
+    }
+  }
+}
+
 // x = dequantized embedding row of the step's token, or its fp32 row times
 // the embedding scale (gemma.c:5468-5493)
 __global__ __launch_bounds__(kNT) void dec_embed_kernel(DecEmbed a) {
@@ -847,6 +996,86 @@ NormStreamFn norm_stream_fn(int kc, bool gelu) {
 }
 
 }  // namespace
+
+namespace {
+
+constexpr int kNfCpl = 8;     // 16-byte chunks per lane and pass (as the fp32 stream GEMV)
+constexpr int kNfMaxNpt = 6;  // dim <= 6144
+
+template <int L, bool GELU, int NPT>
+hipError_t launch_norm_f32(const DecNorm &na, const GemvJobs &jobs, int ngroups, int k, int passes,
+                           const DeviceInfo &dev, hipStream_t stream) {
+  const auto kern = dec_norm_f32_kernel<L, kNfCpl, GELU, NPT>;
+  const size_t lds = (size_t)(k / 4) * 16;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kNT, lds) != hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const long need = (ngroups + kWaves - 1) / kWaves;
+  const long cap = (long)dev.cus * per_cu;
+  kern<<<dim3((unsigned)(need < cap ? need : cap)), kNT, lds, stream>>>(na, jobs, ngroups, k,
+                                                                       passes);
+  return hipGetLastError();
+}
+
+template <int L, bool GELU, int N = 1>
+hipError_t norm_f32_npt(int npt, const DecNorm &na, const GemvJobs &jobs, int ngroups, int k,
+                        int passes, const DeviceInfo &dev, hipStream_t stream) {
+  if (npt == N) return launch_norm_f32<L, GELU, N>(na, jobs, ngroups, k, passes, dev, stream);
+  if constexpr (N < kNfMaxNpt)
+    return norm_f32_npt<L, GELU, N + 1>(npt, na, jobs, ngroups, k, passes, dev, stream);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_dec_norm_gemv_f32(const DecNorm &na, const GemvJobs &jobs, int total, int k,
+                                    bool gelu, const DeviceInfo &dev, hipStream_t stream) {
+  if (total <= 0 || k <= 0 || k % 4 != 0 || k != na.dim || k > 4 * kNT * kNfMaxNpt)
+    return hipErrorInvalidValue;
+  for (int j = 0; j < (gelu ? 2 : jobs.njobs); ++j)
+    if ((uintptr_t)jobs.w[j] % 16 != 0) return hipErrorInvalidValue;
+  if (!gelu) {
+    for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
+      if (jobs.end[j] <= prev) return hipErrorInvalidValue;
+  } else if (total % 2 != 0 || jobs.end[0] != total) {
+    return hipErrorInvalidValue;
+  }
+  // lanes per row: the fewest (8 .. 64) that cover a row in at most two
+  // passes of kNfCpl chunks (as the fp32 stream GEMV), at most 32 for the
+  // gate/up pairing (two rows per wave)
+  const int kc = k / 4;
+  int lanes = 64;
+  for (int l = 8; l <= 64; l *= 2)
+    if ((kc + l * kNfCpl - 1) / (l * kNfCpl) <= 2) {
+      lanes = l;
+      break;
+    }
+  if (gelu && lanes > 32) lanes = 32;
+  const int passes = (kc + lanes * kNfCpl - 1) / (lanes * kNfCpl);
+  const int rows = 64 / lanes;
+  int ngroups = 0;
+  if (gelu) {
+    ngroups = (total / 2 + rows / 2 - 1) / (rows / 2);
+  } else {
+    for (int j = 0, prev = 0; j < jobs.njobs; prev = jobs.end[j], ++j)
+      ngroups += (jobs.end[j] - prev + rows - 1) / rows;
+  }
+  const int npt = (kc + kNT - 1) / kNT;
+  switch (lanes) {
+    case 8:
+      return gelu ? norm_f32_npt<8, true>(npt, na, jobs, ngroups, k, passes, dev, stream)
+                  : norm_f32_npt<8, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+    case 16:
+      return gelu ? norm_f32_npt<16, true>(npt, na, jobs, ngroups, k, passes, dev, stream)
+                  : norm_f32_npt<16, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+    case 32:
+      return gelu ? norm_f32_npt<32, true>(npt, na, jobs, ngroups, k, passes, dev, stream)
+                  : norm_f32_npt<32, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+    default:
+      return norm_f32_npt<64, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+  }
+}
 
 hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                                 bool gelu, const DeviceInfo &dev, hipStream_t stream) {

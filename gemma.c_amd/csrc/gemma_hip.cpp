@@ -1566,9 +1566,11 @@ hipError_t prefill_enqueue_f32(gemma_hip_decoder *d, int n, int pos, bool embed,
 }
 
 // The fp32 ('U') model's decode step: forward_text_decode's !quant branches
-// (gemma.c:4762, 4855, 4906, 4925, 4960).  Each norm is one workgroup that
-// stores the new residual and the normalized vector, which the fp32 GEMVs
-// (gemv_fpx / gemv_fpx_multi) read; GELU(gate) * up is its own launch.
+// (gemma.c:4762, 4855, 4906, 4925, 4960), launched as the W8A8 step is: the
+// pre-attention and pre-FFN norms are the prologues of the q/k/v and gate/up
+// fp32 GEMVs (every workgroup normalizes into LDS; workgroup 0 stores the new
+// residual), the gate/up launch stores GELU(gate) * up, and o, down and the
+// LM head are plain fp32 GEMVs (gemv_fpx / gemv_fpx_multi).
 hipError_t decoder_enqueue_f32(gemma_hip_decoder *d, hipStream_t st) {
   const gemma_hip_text_config &c = d->cfg;
   const int q_sz = c.n_heads * c.hdim, kv_sz = c.nkv * c.hdim, mlp = c.mlp_dim;
@@ -1589,17 +1591,19 @@ hipError_t decoder_enqueue_f32(gemma_hip_decoder *d, hipStream_t st) {
   int cur = 0;
   for (int l = 0; l < c.nl; ++l) {
     const auto &L = d->layers[l];
+    // residual of the previous MLP (post-FFN norm), pre-attention norm, q/k/v
     gh::DecNorm n1{d->x[cur], l > 0 ? d->ymlp : nullptr,
                    (l > 0 && c.mlp_pst) ? d->layers[l - 1].n4 : nullptr, L.n1,
-                   d->x[cur ^ 1], d->h, c.dim, c.eps};
-    if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(n1, st))) != hipSuccess) return e;
-    cur ^= 1;
+                   d->x[cur ^ 1], nullptr, c.dim, c.eps};
     gh::GemvJobs qkv{};
     qkv.w[0] = L.wf[0]; qkv.w[1] = L.wf[1]; qkv.w[2] = L.wf[2];
     qkv.dst[0] = d->xq; qkv.dst[1] = d->xk; qkv.dst[2] = d->xv;
     qkv.end[0] = q_sz; qkv.end[1] = q_sz + kv_sz; qkv.end[2] = qkv.end[3] = q_sz + 2 * kv_sz;
     qkv.njobs = 3;
-    if ((e = gemv(qkv, c.dim, d->h)) != hipSuccess) return e;
+    if ((e = GH_OP(kOpGemvFpx, gh::launch_dec_norm_gemv_f32(n1, qkv, q_sz + 2 * kv_sz, c.dim,
+                                                            false, g.info, st))) != hipSuccess)
+      return e;
+    cur ^= 1;
     const size_t cache = (size_t)d->clen * kv_sz;
     float *kc = d->kv + (size_t)l * 2 * cache;
     const bool sliding = d->swa[l] != 0;
@@ -1610,19 +1614,20 @@ hipError_t decoder_enqueue_f32(gemma_hip_decoder *d, hipStream_t st) {
                    c.eps};
     if ((e = GH_OP(kOpSoftmax, gh::launch_dec_attention(at, st))) != hipSuccess) return e;
     if ((e = gemv(one_job(L.wf[3], d->yattn, c.dim), q_sz, d->xo)) != hipSuccess) return e;
+    // residual of the attention (post-attention norm), pre-FFN norm, gate/up
+    // and GELU(gate) * up into gbuf (gemma.c:4906-4915)
     gh::DecNorm n3{d->x[cur], d->yattn, c.mlp_pre ? L.n2 : nullptr, c.mlp_pre ? L.n3 : L.n2,
-                   d->x[cur ^ 1], d->h, c.dim, c.eps};
-    if ((e = GH_OP(kOpRmsnorm, gh::launch_dec_final_norm(n3, st))) != hipSuccess) return e;
-    cur ^= 1;
+                   d->x[cur ^ 1], nullptr, c.dim, c.eps};
     gh::GemvJobs gu{};
     gu.w[0] = L.wf[5]; gu.w[1] = L.wf[4];  // gate (w2), up (w1): gemma.c:4906-4910
-    gu.dst[0] = d->gbuf; gu.dst[1] = d->gbuf + mlp;
-    gu.end[0] = mlp; gu.end[1] = gu.end[2] = gu.end[3] = 2 * mlp;
+    gu.dst[0] = d->gbuf; gu.dst[1] = d->gbuf;
+    gu.end[0] = gu.end[1] = gu.end[2] = gu.end[3] = 2 * mlp;
     gu.njobs = 2;
-    if ((e = gemv(gu, c.dim, d->h)) != hipSuccess ||
-        (e = GH_OP(kOpGelu, gh::launch_gelu_mul_rows(d->gbuf, 1, mlp, st))) != hipSuccess ||
-        (e = gemv(one_job(L.wf[6], d->ymlp, c.dim), mlp, d->gbuf)) != hipSuccess)
+    if ((e = GH_OP(kOpGemvFpx, gh::launch_dec_norm_gemv_f32(n3, gu, 2 * mlp, c.dim, true, g.info,
+                                                            st))) != hipSuccess)
       return e;
+    cur ^= 1;
+    if ((e = gemv(one_job(L.wf[6], d->ymlp, c.dim), mlp, d->gbuf)) != hipSuccess) return e;
   }
   gh::DecNorm fn{d->x[cur], d->ymlp, c.mlp_pst ? d->layers[c.nl - 1].n4 : nullptr, d->fnorm,
                  nullptr, d->h, c.dim, c.eps};

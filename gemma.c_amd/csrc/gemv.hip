@@ -492,18 +492,6 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(
 // staged in LDS as fp32.  The sum is fp32 FMAs in two chains per lane, then
 // a fixed tree over the L lanes (the reference's order is its compiler's;
 // the bound is the fp32 tolerance).  Requires every job's m * k * 4 < 2^31.
-template <int L>
-__device__ __forceinline__ float group_sum_f32(float v) {
-  static_assert(L == 8 || L == 16 || L == 32 || L == 64, "L is 8, 16, 32 or 64");
-  v += dpp_f32<kDppXor1>(v);
-  v += dpp_f32<kDppXor2>(v);
-  v += dpp_f32<kDppHalfMirror>(v);
-  if (L >= 16) v += dpp_f32<kDppMirror>(v);
-  if (L >= 32) v += __shfl_xor(v, 16, 64);
-  if (L >= 64) v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
 template <int L, int CPL, int NT>
 __global__ __launch_bounds__(NT) void gemv_f32_stream_kernel(GemvJobs jobs, int ngroups, int k,
                                                              int passes,

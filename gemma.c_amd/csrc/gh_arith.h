@@ -229,6 +229,20 @@ __device__ __forceinline__ float dpp_f32(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// Sum over the L consecutive lanes of a row group (L = 8, 16, 32 or 64), in
+// a fixed tree: every lane of the group ends with the sum.
+template <int L>
+__device__ __forceinline__ float group_sum_f32(float v) {
+  static_assert(L == 8 || L == 16 || L == 32 || L == 64, "L is 8, 16, 32 or 64");
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppHalfMirror>(v);
+  if (L >= 16) v += dpp_f32<kDppMirror>(v);
+  if (L >= 32) v += __shfl_xor(v, 16, 64);
+  if (L >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 // Sum over each aligned group of L lanes (L = 8, 16, 32 or 64), the same
 // value in every lane of the group.  Integer sums are exact, so the order
 // of the additions does not matter.

@@ -222,6 +222,11 @@ struct DecAttn {
 // k <= 6144 (k <= 4096 for gelu), rows 16-byte aligned
 hipError_t launch_dec_norm_gemv(const DecNorm &na, const GemvJobs &jobs, int total, int k,
                                 bool gelu, const DeviceInfo &dev, hipStream_t stream);
+// The same for fp32 weights (the unquantized decode step): jobs.w fp32 rows
+// (16-byte aligned), k = na.dim <= 6144 and a multiple of 4; gelu as above.
+// Every workgroup normalizes into LDS as fp32; workgroup 0 stores x_out.
+hipError_t launch_dec_norm_gemv_f32(const DecNorm &na, const GemvJobs &jobs, int total, int k,
+                                    bool gelu, const DeviceInfo &dev, hipStream_t stream);
 hipError_t launch_dec_embed(const DecEmbed &a, hipStream_t stream);
 hipError_t launch_dec_final_norm(const DecNorm &na, hipStream_t stream);
 hipError_t launch_dec_attention(const DecAttn &a, hipStream_t stream);

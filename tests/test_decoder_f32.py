@@ -178,6 +178,43 @@ def test_u_decoder_steps_match_oracle(gh, oracle, u_models, key):
         dec.close()
 
 
+# One layer at the real widths of gemma-3-1b (dim 1152: 32 lanes per row in
+# the norm-fused GEMVs) and gemma-3-4b (dim 2560: 64 lanes for q/k/v, 32 in
+# three passes for the gate/up pairing), decode steps and then a prompt pass
+# (the fp32 GEMMs at these widths split K).
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["gemma-3-1b", "gemma-3-4b"])
+def test_u_decoder_real_widths_match_oracle(gh, oracle, tmp_path, name):
+    path = model_bin.write_bin(str(tmp_path / "w.bin"), name, seed=5, nvocab=1024,
+                               norm_std=0.1, quant=False, layers=1, slide=8, flags=7)
+    model = model_bin.read_bin(path)
+    nv = model["config"]["nvocab"]
+    clen = 40
+    dec = gh.decoder(model, clen)
+    try:
+        ref = dorc.DecodeOracle(model, oracle, clen)
+        logits = np.empty(nv, np.float32)
+        token, worst = 3, 0.0
+        for pos in range(6):
+            nxt = dec.step(token, pos, logits)
+            want = ref.step(token, pos)
+            worst = max(worst, check(logits, want, nxt, f"{name} step {pos}"))
+            token = int(np.argmax(want))
+        prompt = np.random.default_rng(4).integers(0, nv, 20).astype(np.int32)
+        want = ref.prefill(prompt, 6)
+        nxt = dec.prefill(prompt, 6, logits)
+        worst = max(worst, check(logits, want, nxt, f"{name} prefill"))
+        token = int(np.argmax(want))
+        for pos in range(26, 30):
+            nxt = dec.step(token, pos, logits)
+            want = ref.step(token, pos)
+            worst = max(worst, check(logits, want, nxt, f"{name} step {pos}"))
+            token = int(np.argmax(want))
+        print(f"U decoder {name} (1 layer): worst |d|/max|logit| = {worst:.3g}", flush=True)
+    finally:
+        dec.close()
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("key", ["gemma3", "softcap", "plain", "odd"])
 @pytest.mark.parametrize("mode", [ATTN_F64, ATTN_F32])
@@ -236,8 +273,11 @@ def test_u_decoder_generate_and_perf(gh, u_models):
         assert calls["prefill"]["gemm_fpx"] == 4 * nl
         assert calls["prefill"]["gemv_fpx"] == 1 and calls["prefill"]["gelu"] == nl
         assert "gemm_int8" not in calls["prefill"] and "quantize_act" not in calls["prefill"]
+        # per token: the norm-fused q/k/v and gate/up GEMVs (GELU fused), o,
+        # down, the LM head; the final norm the only separate one
         assert calls["decode"]["gemv_fpx"] == 8 * (4 * nl + 1)
-        assert calls["decode"]["rmsnorm"] == 8 * (2 * nl + 1)
+        assert calls["decode"]["rmsnorm"] == 8
+        assert "gelu" not in calls["decode"]
         assert "gemv_int8" not in calls["decode"]
     finally:
         dec.close()
