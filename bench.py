@@ -43,10 +43,11 @@ The JSON line also carries, measured in the same run:
                 embedding, norms, q/k/v, RoPE, KV cache, attention, o, GELU,
                 down, LM head, argmax); "gemma-3-1b:U" is config 3 as an
                 unquantized ('U') model (gemma_hip_decoder_create_f32: fp32
-                GEMVs, ~4 GB of weights per token; fp32 matrix-core GEMMs in
+                GEMVs, ~4 GB of weights per token; split-bf16 fp32 GEMMs in
                 the prompt pass)
   vision        config 4 end to end: one 896x896 image through the SigLIP
-                tower on the GPU (gemma_hip_vision_forward), ms per image
+                tower on the GPU (gemma_hip_vision_forward), ms per image;
+                ms_per_image_u the same tower from fp32 weights ('U')
   cpu_baseline  the reference's own quantize_act + gemv_int8(_multi), compiled
                 from its source (oracle/_ref/gemma_ref_clang), on the host cores
 """
@@ -509,7 +510,9 @@ def bench_vision(torch, gh) -> dict:
     projection to the gemma-3-4b width), random weights of that shape; the
     median of five timed images after one untimed, with the attention on the
     fp32 matrix cores (the default) and on the fp64 matrix cores (the
-    verification mode, equal to the fp64 oracle; gemma_hip_vision_set_attention)."""
+    verification mode, equal to the fp64 oracle; gemma_hip_vision_set_attention);
+    then the same tower from fp32 weights (an unquantized 'U' file:
+    gemma_hip_vision_create_f32, fp32 GEMMs on the split-bf16 kernel)."""
     import statistics
     import time
 
@@ -518,18 +521,28 @@ def bench_vision(torch, gh) -> dict:
     vis = model_bin.synth_vision(seed=1234, text_dim=2560)
     img = model_bin.synth_image(vis["config"]["img_px"], seed=1234)
     c = vis["config"]
-    tower = gh.vision(vis)
     ms = {}
+
+    def timed(tower, name):
+        tower.forward(img)
+        ts = []
+        for _ in range(TIMING_RUNS):
+            t0 = time.perf_counter()
+            tower.forward(img)
+            ts.append(time.perf_counter() - t0)
+        ms[name] = statistics.median(ts) * 1e3
+
+    tower = gh.vision(vis)
     try:
         for name, mode in (("f64", tower.ATTN_F64), ("f32", tower.ATTN_F32)):
             tower.set_attention(mode)
-            tower.forward(img)
-            ts = []
-            for _ in range(TIMING_RUNS):
-                t0 = time.perf_counter()
-                tower.forward(img)
-                ts.append(time.perf_counter() - t0)
-            ms[name] = statistics.median(ts) * 1e3
+            timed(tower, name)
+    finally:
+        tower.close()
+    del vis
+    tower = gh.vision(model_bin.synth_vision(seed=1234, text_dim=2560, quant=False))
+    try:
+        timed(tower, "u")
     finally:
         tower.close()
     n = (c["img_px"] // c["psize"]) ** 2
@@ -539,7 +552,9 @@ def bench_vision(torch, gh) -> dict:
     return dict(model="siglip (27 layers, 896 px, 4096 patches -> 256 tokens)",
                 ms_per_image=round(ms["f32"], 2), images_s=round(1e3 / ms["f32"], 2),
                 ms_per_image_attn_f64=round(ms["f64"], 2),
-                int8_ops=ops, int8_tops_over_tower=round(ops / ms["f32"] / 1e9, 1))
+                int8_ops=ops, int8_tops_over_tower=round(ops / ms["f32"] / 1e9, 1),
+                ms_per_image_u=round(ms["u"], 2),
+                fp32_tflops_over_tower_u=round(ops / ms["u"] / 1e9, 1))
 
 
 def measured_traffic(kernel: str) -> dict | None:
