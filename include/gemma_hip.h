@@ -101,7 +101,10 @@ int gemma_hip_sync(void *stream);
  * quantize), "rope" (the prompt pass's q/k norm + RoPE + cache append),
  * "softmax" (the attention kernels, which also hold the reference's score
  * and value products and, in the decode step, its RoPE), "gemm_fpx" (the
- * tower's im2col + patch GEMM) and "sample_from_logits" (softcap + argmax,
+ * tower's im2col + patch GEMM; with 'U' weights every GEMM, q|k|v and
+ * gate|up one launch each), "gemv_fpx" (with 'U' weights the decode GEMVs,
+ * their norm-fused forms, GELU fused, and the LM head) and
+ * "sample_from_logits" (softcap + argmax,
  * counted in the decode phase as the reference does).  They set the phase
  * themselves as the reference's forward_gemma_* do: decoder_prefill and
  * prefill_rows with mask != 0 prefill; decoder_step and decoder_generate
@@ -339,9 +342,11 @@ typedef struct {
  * (decode gemma.c:4762, 4855, 4906, 4925, 4960; prefill 5079, 5297, 5358,
  * 5384, 5431) on the device: emb is the fp32 [nvocab][dim] table (also the
  * tied LM head), the projections run as fp32 GEMVs (gemv_fpx) in the step
- * and as fp32 matrix-core GEMMs (gemm_fpx) in the prompt pass, with no
- * activation quantize.  Every other decoder entry point takes the result as
- * it takes a W8A8 decoder. */
+ * (the norms fused into the q/k/v and gate/up GEMVs, GELU into gate/up, as
+ * in the W8A8 step) and as fp32 GEMMs (gemm_fpx: on the bf16 matrix cores in
+ * split precision, fp32 accuracy) in the prompt pass, with no activation
+ * quantize.  Every other decoder entry point takes the result as it takes a
+ * W8A8 decoder. */
 gemma_hip_decoder *gemma_hip_decoder_create_f32(const gemma_hip_text_config *cfg,
                                                 const gemma_hip_layer_f32 *layers,
                                                 const float *emb, const float *fnorm,
