@@ -506,7 +506,11 @@ Bf3Plan bf3_plan(int m, int n, int k, const DeviceInfo &dev) {
 hipError_t launch_bf3_auto(float *dst, int dstr, const F32Segs &b, int mstr, const float *src,
                            int sstr, int m, int k, const F32Epilogue &ep, const DeviceInfo &dev,
                            hipStream_t stream) {
-  const Bf3Plan p = bf3_plan(m, b.end[b.nseg - 1], k, dev);
+  Bf3Plan p = bf3_plan(m, b.end[b.nseg - 1], k, dev);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (p.splits > 1 &&
+      (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone))
+    p.splits = 1;  // the split-K workspace may have to be allocated: not under capture
   if (p.tile == kTile128)
     return launch_bf3<2, 2>(dst, dstr, b, mstr, src, sstr, m, k, ep, p.splits, stream);
   if (p.tile == kTile128x64)

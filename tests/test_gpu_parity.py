@@ -532,6 +532,40 @@ def test_f32_split_k(gh, oracle, monkeypatch, splits, m, n, k):
     assert np.array_equal(bits(host(d)), bits(first))
 
 
+def test_f32_gemm_in_a_graph(gh, oracle, monkeypatch):
+    """Captured into a graph, a launch that would split K runs unsplit (the
+    split-K workspace may have to be allocated, which capture forbids): every
+    replay equals the unsplit eager launch bit for bit, with eager split-K
+    launches of the same product between the replays."""
+    m, n, k = 512, 1152, 6912
+    note(f"f32 graph m={m} n={n} k={k}")
+    rng = np.random.default_rng(77)
+    A = outlier_acts(rng, (m, k))
+    B = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    a, b = dev(A), dev(B)
+    want = torch.empty((m, n), device="cuda")
+    monkeypatch.setenv("GEMMA_HIP_GEMM_F32_SPLIT", "1")
+    gh.matmul_f32(want, n, b, k, a, k, m, n, k, stream())
+    monkeypatch.delenv("GEMMA_HIP_GEMM_F32_SPLIT")
+    out = torch.empty((m, n), device="cuda")
+    eager = torch.empty((m, n), device="cuda")
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=side):
+        out.fill_(0.0)
+        gh.matmul_f32(out, n, b, k, a, k, m, n, k, side.cuda_stream)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int32), want.view(torch.int32)), f"replay {rep}"
+        gh.matmul_f32(eager, n, b, k, a, k, m, n, k, stream())  # split K, eagerly
+        torch.cuda.synchronize()
+    pick = np.unique(rng.integers(0, m, 32))
+    check_f32(host(eager)[pick], B, A[pick], oracle)
+    check_f32(host(want)[pick], B, A[pick], oracle)
+
+
 def test_f32_multi(gh, oracle):
     rng = np.random.default_rng(3)
     k = 1152
@@ -730,6 +764,17 @@ def test_argument_errors(gh):
         gh.matmul(1, 4, 1, 8, 1, 1, 16, 1, 2, 8, 16)
     with pytest.raises(gemma_hip.GemmaHipError, match="k="):
         gh.quantize_matmul([(1, 1, 1, 4)], 1, 70000)
+    # the fp32 column-grouped GEMM: job count, an empty job, a null weight
+    with pytest.raises(gemma_hip.GemmaHipError, match="njobs"):
+        gh.matmul_f32_cols(1, 0, [], 1, 0, 4, 8)
+    with pytest.raises(gemma_hip.GemmaHipError, match="njobs"):
+        gh.matmul_f32_cols(1, 0, [(1, 4)] * 4, 1, 0, 4, 8)
+    with pytest.raises(gemma_hip.GemmaHipError, match="m=0"):
+        gh.matmul_f32_cols(1, 0, [(1, 4), (1, 0)], 1, 0, 4, 8)
+    with pytest.raises(gemma_hip.GemmaHipError, match="null weight"):
+        gh.matmul_f32_cols(1, 0, [(1, 4), (None, 4)], 1, 0, 4, 8)
+    with pytest.raises(gemma_hip.GemmaHipError, match="stride"):
+        gh.matmul_f32_cols(1, 4, [(1, 4), (1, 4)], 1, 0, 4, 8)
 
 
 # --------------------------------------------------------------- SigLIP patch embedding
