@@ -999,13 +999,12 @@ NormStreamFn norm_stream_fn(int kc, bool gelu) {
 
 namespace {
 
-constexpr int kNfCpl = 8;     // 16-byte chunks per lane and pass (as the fp32 stream GEMV)
 constexpr int kNfMaxNpt = 6;  // dim <= 6144
 
-template <int L, bool GELU, int NPT>
+template <int L, int CPL, bool GELU, int NPT>
 hipError_t launch_norm_f32(const DecNorm &na, const GemvJobs &jobs, int ngroups, int k, int passes,
                            const DeviceInfo &dev, hipStream_t stream) {
-  const auto kern = dec_norm_f32_kernel<L, kNfCpl, GELU, NPT>;
+  const auto kern = dec_norm_f32_kernel<L, CPL, GELU, NPT>;
   const size_t lds = (size_t)(k / 4) * 16;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kNT, lds) != hipSuccess ||
@@ -1018,13 +1017,30 @@ hipError_t launch_norm_f32(const DecNorm &na, const GemvJobs &jobs, int ngroups,
   return hipGetLastError();
 }
 
-template <int L, bool GELU, int N = 1>
+// f32_stream_shape takes 8 or 16 lanes only for rows of at most 192 chunks
+// (one norm chunk per thread) and 32 lanes for plain rows only up to 384
+// chunks, so those kernels exist for the NPT they can meet
+template <int L, bool GELU>
+constexpr int kNfNpt = L <= 16 ? 1 : (L == 32 && !GELU) ? 2 : kNfMaxNpt;
+
+template <int L, int CPL, bool GELU, int N = 1>
 hipError_t norm_f32_npt(int npt, const DecNorm &na, const GemvJobs &jobs, int ngroups, int k,
                         int passes, const DeviceInfo &dev, hipStream_t stream) {
-  if (npt == N) return launch_norm_f32<L, GELU, N>(na, jobs, ngroups, k, passes, dev, stream);
-  if constexpr (N < kNfMaxNpt)
-    return norm_f32_npt<L, GELU, N + 1>(npt, na, jobs, ngroups, k, passes, dev, stream);
+  if (npt == N)
+    return launch_norm_f32<L, CPL, GELU, N>(na, jobs, ngroups, k, passes, dev, stream);
+  if constexpr (N < kNfNpt<L, GELU>)
+    return norm_f32_npt<L, CPL, GELU, N + 1>(npt, na, jobs, ngroups, k, passes, dev, stream);
   return hipErrorInvalidValue;
+}
+
+template <int L, bool GELU>
+hipError_t norm_f32_cpl(int cpl, int npt, const DecNorm &na, const GemvJobs &jobs, int ngroups,
+                        int k, int passes, const DeviceInfo &dev, hipStream_t stream) {
+  switch (cpl) {
+    case 8: return norm_f32_npt<L, 8, GELU>(npt, na, jobs, ngroups, k, passes, dev, stream);
+    case 10: return norm_f32_npt<L, 10, GELU>(npt, na, jobs, ngroups, k, passes, dev, stream);
+    default: return norm_f32_npt<L, 12, GELU>(npt, na, jobs, ngroups, k, passes, dev, stream);
+  }
 }
 
 }  // namespace
@@ -1041,18 +1057,11 @@ hipError_t launch_dec_norm_gemv_f32(const DecNorm &na, const GemvJobs &jobs, int
   } else if (total % 2 != 0 || jobs.end[0] != total) {
     return hipErrorInvalidValue;
   }
-  // lanes per row: the fewest (8 .. 64) that cover a row in at most two
-  // passes of kNfCpl chunks (as the fp32 stream GEMV), at most 32 for the
-  // gate/up pairing (two rows per wave)
+  // lanes per row and chunks per lane as the fp32 stream GEMV (at most 32
+  // lanes for the gate/up pairing: two rows per wave)
   const int kc = k / 4;
-  int lanes = 64;
-  for (int l = 8; l <= 64; l *= 2)
-    if ((kc + l * kNfCpl - 1) / (l * kNfCpl) <= 2) {
-      lanes = l;
-      break;
-    }
-  if (gelu && lanes > 32) lanes = 32;
-  const int passes = (kc + lanes * kNfCpl - 1) / (lanes * kNfCpl);
+  const F32StreamShape sh = f32_stream_shape(kc, gelu, total);
+  const int lanes = sh.lanes, passes = sh.passes;
   const int rows = 64 / lanes;
   int ngroups = 0;
   if (gelu) {
@@ -1062,18 +1071,19 @@ hipError_t launch_dec_norm_gemv_f32(const DecNorm &na, const GemvJobs &jobs, int
       ngroups += (jobs.end[j] - prev + rows - 1) / rows;
   }
   const int npt = (kc + kNT - 1) / kNT;
+  const int c = sh.cpl;
   switch (lanes) {
     case 8:
-      return gelu ? norm_f32_npt<8, true>(npt, na, jobs, ngroups, k, passes, dev, stream)
-                  : norm_f32_npt<8, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+      return gelu ? norm_f32_cpl<8, true>(c, npt, na, jobs, ngroups, k, passes, dev, stream)
+                  : norm_f32_cpl<8, false>(c, npt, na, jobs, ngroups, k, passes, dev, stream);
     case 16:
-      return gelu ? norm_f32_npt<16, true>(npt, na, jobs, ngroups, k, passes, dev, stream)
-                  : norm_f32_npt<16, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+      return gelu ? norm_f32_cpl<16, true>(c, npt, na, jobs, ngroups, k, passes, dev, stream)
+                  : norm_f32_cpl<16, false>(c, npt, na, jobs, ngroups, k, passes, dev, stream);
     case 32:
-      return gelu ? norm_f32_npt<32, true>(npt, na, jobs, ngroups, k, passes, dev, stream)
-                  : norm_f32_npt<32, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+      return gelu ? norm_f32_cpl<32, true>(c, npt, na, jobs, ngroups, k, passes, dev, stream)
+                  : norm_f32_cpl<32, false>(c, npt, na, jobs, ngroups, k, passes, dev, stream);
     default:
-      return norm_f32_npt<64, false>(npt, na, jobs, ngroups, k, passes, dev, stream);
+      return norm_f32_cpl<64, false>(c, npt, na, jobs, ngroups, k, passes, dev, stream);
   }
 }
 

@@ -16,6 +16,7 @@
 // Several weight matrices ("jobs": q/k/v or gate/up) are one flat row range,
 // as in gemma.c:2803-2811, so a fused projection is one launch.
 #include <cstdlib>
+#include <type_traits>
 
 #include "gh_arith.h"
 #include "gh_kernels.h"
@@ -874,12 +875,10 @@ hipError_t launch_gemv_i8(const GemvJobs &jobs, int k, const int8_t *xq,
 
 namespace {
 
-constexpr int kF32Cpl = 8;  // 16-byte chunks per lane and pass of the fp32 stream kernel
-
-template <int L>
+template <int L, int CPL>
 hipError_t launch_f32_stream(const DeviceInfo &dev, hipStream_t stream, const GemvJobs &jobs,
                              int ngroups, int k, int passes, const float *x) {
-  auto kern = gemv_f32_stream_kernel<L, kF32Cpl, kStreamNT>;
+  auto kern = gemv_f32_stream_kernel<L, CPL, kStreamNT>;
   const size_t lds = (size_t)(k / 4) * 16;
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStreamNT, lds) !=
@@ -926,25 +925,24 @@ hipError_t launch_gemv_f32(const GemvJobs &jobs, int k, const float *x,
   const bool vec = rows_aligned(jobs, k, 4, 16);
   GemvJobs sj;
   if (vec && ((uintptr_t)x & 15) == 0 && !tuning().force_loop && split_f32_jobs(jobs, k, &sj)) {
-    // lanes per row: the fewest (8 .. 64) that cover a row in at most two
-    // passes of kF32Cpl chunks, else 64 lanes and as many passes as needed
-    const int kc = k / 4;
-    int lanes = 64;
-    for (int l = 8; l <= 64; l *= 2)
-      if ((kc + l * kF32Cpl - 1) / (l * kF32Cpl) <= 2) {
-        lanes = l;
-        break;
-      }
-    const int passes = (kc + lanes * kF32Cpl - 1) / (lanes * kF32Cpl);
-    const int rows = 64 / lanes;
+    const F32StreamShape sh = f32_stream_shape(k / 4, false, total);
+    const int rows = 64 / sh.lanes;
     int ngroups = 0;
     for (int j = 0, prev = 0; j < sj.njobs; prev = sj.end[j], ++j)
       ngroups += (sj.end[j] - prev + rows - 1) / rows;
-    switch (lanes) {
-      case 8: return launch_f32_stream<8>(dev, stream, sj, ngroups, k, passes, x);
-      case 16: return launch_f32_stream<16>(dev, stream, sj, ngroups, k, passes, x);
-      case 32: return launch_f32_stream<32>(dev, stream, sj, ngroups, k, passes, x);
-      default: return launch_f32_stream<64>(dev, stream, sj, ngroups, k, passes, x);
+    auto go = [&](auto lanes) {
+      constexpr int L = decltype(lanes)::value;
+      switch (sh.cpl) {
+        case 8: return launch_f32_stream<L, 8>(dev, stream, sj, ngroups, k, sh.passes, x);
+        case 10: return launch_f32_stream<L, 10>(dev, stream, sj, ngroups, k, sh.passes, x);
+        default: return launch_f32_stream<L, 12>(dev, stream, sj, ngroups, k, sh.passes, x);
+      }
+    };
+    switch (sh.lanes) {
+      case 8: return go(std::integral_constant<int, 8>{});
+      case 16: return go(std::integral_constant<int, 16>{});
+      case 32: return go(std::integral_constant<int, 32>{});
+      default: return go(std::integral_constant<int, 64>{});
     }
   }
   const int lanes = vec ? lanes_for(k / 4) : 64;
