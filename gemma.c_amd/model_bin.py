@@ -41,6 +41,9 @@ CONFIGS = {
     # widths that are multiples of 16 but not of the GEMM tile (64/128) or of
     # 256-thread vectors: dim 208, mlp 1040, one q head per kv head
     "test-odd": dict(nl=2, n_heads=2, nkv=2, hdim=128, dim=208, mlp=1040, slide=512),
+    # rows of 176 and 352 16-byte chunks (dim 704, mlp 1408): the fp32 GEMVs
+    # take one pass of 12 chunks per lane at 16 and 32 lanes
+    "test-cpl12": dict(nl=2, n_heads=2, nkv=1, hdim=128, dim=704, mlp=1408, slide=512),
 }
 NVOCAB = 262144
 SPECIALS = ["<pad>", "<eos>", "<bos>", "<unk>", "<start_of_turn>", "<end_of_turn>"]

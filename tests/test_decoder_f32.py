@@ -180,10 +180,11 @@ def test_u_decoder_steps_match_oracle(gh, oracle, u_models, key):
 
 # One layer at the real widths of gemma-3-1b (dim 1152: 32 lanes per row in
 # the norm-fused GEMVs) and gemma-3-4b (dim 2560: 64 lanes for q/k/v, 32 in
-# three passes for the gate/up pairing), decode steps and then a prompt pass
-# (the fp32 GEMMs at these widths split K).
+# three passes for the gate/up pairing), and at dim 704 (one pass of 12
+# chunks per lane), decode steps and then a prompt pass (the fp32 GEMMs at
+# these widths split K).
 @pytest.mark.gpu
-@pytest.mark.parametrize("name", ["gemma-3-1b", "gemma-3-4b"])
+@pytest.mark.parametrize("name", ["gemma-3-1b", "gemma-3-4b", "test-cpl12"])
 def test_u_decoder_real_widths_match_oracle(gh, oracle, tmp_path, name):
     path = model_bin.write_bin(str(tmp_path / "w.bin"), name, seed=5, nvocab=1024,
                                norm_std=0.1, quant=False, layers=1, slide=8, flags=7)

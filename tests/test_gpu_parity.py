@@ -584,7 +584,8 @@ def test_f32_multi(gh, oracle):
 # 2.7 GB of fp32 rows the launcher splits into jobs below 2 GB.
 @pytest.mark.parametrize("rows,k", [((1024, 256, 256), 1152), ((1152,), 1024),
                                     ((6912, 6912), 1152), ((1152,), 6912),
-                                    ((262144,), 1152), ((2560,), 10240),
+                                    ((262144,), 1152), ((2560,), 10240), ((1000, 300), 1408),
+                                    ((999,), 720),
                                     ((3001, 5, 0, 2999), 2560), ((17,), 16)])
 def test_f32_stream_gemv_vs_oracle(gh, oracle, rows, k):
     note(f"f32 stream rows={rows} k={k}")
